@@ -1,0 +1,91 @@
+// CPU oracle for the token sampler: TEST INFRASTRUCTURE ONLY.
+//
+// A C++ restatement of the reference's CPU sampler (crates/engine/src/sample.rs, rng.rs,
+// logprobs.rs, spec/step.rs:340-385, kernels/src/twin/argmax.rs). Only tests/,
+// __graft_entry__.smoke() and bench.py's cpu_baseline leg may load it, as the checker or the
+// timed CPU baseline. The product (artemis_amd) never calls it.
+//
+// Penalties extend the reference's presence penalty (sample.rs:308-323, 351-356, 378-396) to a
+// history multiset with repetition and frequency penalties; with repetition 1 and frequency 0 they
+// are bit-equal to the reference (see oc_penalize in sampler_oracle.cc).
+#pragma once
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+// The reference's `Sampling` (sample.rs:38-49) plus the two new penalties.
+typedef struct {
+  float temp;
+  uint32_t top_k;
+  float top_p;
+  float min_p;
+  float presence;
+  float frequency;
+  float repetition;
+  uint32_t pad;
+} oc_params;
+
+// rng.rs: xoshiro256** seeded by splitmix64.
+void oc_rng_new(uint64_t seed, uint64_t state[4]);
+uint64_t oc_rng_next_u64(uint64_t state[4]);
+double oc_rng_unit(uint64_t state[4]);
+uint64_t oc_rng_below(uint64_t state[4], uint64_t n);  // n > 0
+
+// sample.rs:9-17, 22-34; kernels/src/twin/argmax.rs:8-16 (UINT32_MAX for none).
+uint32_t oc_greedy(const float* logits, size_t n);
+int64_t oc_first_non_finite(const float* logits, size_t n);  // -1 when all finite
+uint32_t oc_argmax_row(const float* logits, size_t n);
+
+// sample.rs:71-94. Returns 0 when accepted, else 1 with a one-line message naming the flag.
+int oc_check(const oc_params* p, char* msg, size_t cap);
+
+typedef struct oc_sampler oc_sampler;
+oc_sampler* oc_sampler_new(const oc_params* p, uint64_t seed);
+void oc_sampler_free(oc_sampler* s);
+// Adds ids to the penalty history (each occurrence counts once more).
+void oc_sampler_add_history(oc_sampler* s, const uint32_t* ids, size_t n);
+void oc_sampler_get_rng(const oc_sampler* s, uint64_t state[4]);
+void oc_sampler_set_rng(oc_sampler* s, const uint64_t state[4]);
+// sample.rs:122-153. Returns the token; the token joins the history.
+uint32_t oc_sampler_sample(oc_sampler* s, const float* logits, size_t n);
+// The last draw's kept set in rank order with probabilities w_i / sum(w) at the temperature
+// (empty after a greedy pick). Returns the kept count; writes at most `cap` entries.
+size_t oc_sampler_last_kept(const oc_sampler* s, uint32_t* ids, double* probs, size_t cap);
+// Which path the last sample took: 0 greedy, 1 greedy with penalties, 2 one-pass top-k + full sort,
+// 3 every candidate + full sort, 4 partial.
+int oc_sampler_last_path(const oc_sampler* s);
+
+// The two draws and the top-k selections on explicit candidates, for the equivalence tests
+// (sample.rs:157-198, 208-293, 308-323, 335-372). Candidates are (id, value) pairs.
+uint32_t oc_sampler_draw_full_sort(oc_sampler* s, const uint32_t* ids, const float* vals, size_t n);
+uint32_t oc_sampler_draw_partial(oc_sampler* s, const uint32_t* ids, const float* vals, size_t n);
+// One-pass top-k over logits with the sampler's history penalties; returns the count written.
+size_t oc_top_k(const oc_sampler* s, const float* logits, size_t n, size_t k, uint32_t* ids,
+                float* vals);
+// Selection over every penalized candidate, then sorted (the equivalence the one pass claims).
+size_t oc_selected(const oc_sampler* s, const float* logits, size_t n, size_t k, uint32_t* ids,
+                   float* vals);
+int oc_takes_one_pass(size_t k, size_t n);
+
+// spec/step.rs:340-385 with Picker's stop rule (turn.rs:344-352): rows 0..=k in order, each
+// picked by the sampler; stop at the first pick that is a stop id or differs from the next draft.
+// `rows` is [k+1][n]. Returns read (rows picked); picks[0..read) are written, *accepted = read-1
+// (drafts kept), *stopped = 1 when the last pick was a stop id.
+size_t oc_verify(oc_sampler* s, const float* rows, size_t n, const uint32_t* drafts, size_t k,
+                 const uint32_t* stop_ids, size_t n_stop, uint32_t* picks, uint32_t* accepted,
+                 uint32_t* stopped);
+
+// logprobs.rs:12-38: returns the token's log-probability; writes min(top, 20, n) (id, logprob).
+float oc_logprobs(const float* logits, size_t n, uint32_t token, uint32_t top, uint32_t* ids,
+                  float* lps, size_t* n_top);
+
+// The exact f64 weight the sampler uses, from the host libm: exp(x).
+double oc_exp(double x);
+double oc_log(double x);
+
+#ifdef __cplusplus
+}
+#endif
