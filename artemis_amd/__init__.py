@@ -1,0 +1,7 @@
+"""MI355X (gfx950) token sampler and speculative verify: HIP kernels behind a C ABI
+(include/artemis_sampler.h), with the reference's sampler interface in `artemis_amd.sampler`."""
+from .sampler import (AS_ROW_EXACT_PATH, AS_ROW_NONFINITE, AS_ROW_OK, NO_DRAFT, Context, Sampler,
+                      SamplerError, Sampling, greedy, rng_state, states_tensor)
+
+__all__ = ["AS_ROW_EXACT_PATH", "AS_ROW_NONFINITE", "AS_ROW_OK", "NO_DRAFT", "Context", "Sampler",
+           "SamplerError", "Sampling", "greedy", "rng_state", "states_tensor"]

@@ -1,0 +1,388 @@
+// The C ABI (include/artemis_sampler.h): context, argument checks, per-row parameter blocks and
+// the launches. No host synchronisation except as_sync and the staging-buffer reuse wait.
+#include <hip/hip_runtime.h>
+
+#include <cmath>
+#include <cstdio>
+#include <cstring>
+#include <string>
+#include <vector>
+
+#include "../../include/artemis_sampler.h"
+#include "launch.h"
+#include "sampler_device.h"
+
+using as_dev::RowParams;
+using as_dev::SegStats;
+
+struct as_ctx {
+  int device = 0;
+  hipStream_t stream = nullptr;
+  uint32_t max_rows = 0, max_vocab = 0, max_history = 0, max_seg = 0;
+  RowParams* d_params = nullptr;
+  RowParams* h_params[2] = {nullptr, nullptr};
+  hipEvent_t staged[2] = {nullptr, nullptr};
+  int next = 0;
+  SegStats* d_stats = nullptr;
+  uint64_t* d_cands = nullptr;
+  uint32_t* d_scratch = nullptr;
+  uint64_t scratch_stride = 0;
+  uint32_t* d_vstatus = nullptr;
+  std::string err;
+  // Profiling: events before the scan, between the kernels and after the finish, per call.
+  bool profile = false;
+  std::vector<hipEvent_t> ev;
+  size_t ev_used = 0;
+};
+
+namespace {
+
+int fail(as_ctx* c, int code, const std::string& msg) {
+  if (c) c->err = msg;
+  return code;
+}
+
+int hip_fail(as_ctx* c, hipError_t e, const char* what) {
+  return fail(c, AS_ERR_HIP, std::string(what) + ": " + hipGetErrorString(e));
+}
+
+#define AS_HIP(ctx, call)                                   \
+  do {                                                      \
+    hipError_t e_ = (call);                                 \
+    if (e_ != hipSuccess) return hip_fail(ctx, e_, #call);  \
+  } while (0)
+
+bool penalties_on(const as_sampling& s) {
+  return s.presence != 0.0f || s.frequency != 0.0f || s.repetition != 1.0f;
+}
+
+// The row's mode and parameter block (Sampler::sample's dispatch, sample.rs:129-150).
+RowParams make_row(const as_sampling& s, uint32_t n, uint32_t n_seg) {
+  RowParams r{};
+  r.temp = s.temp;
+  r.top_k = s.top_k;
+  r.top_p = s.top_p;
+  r.min_p = s.min_p;
+  r.presence = s.presence;
+  r.frequency = s.frequency;
+  r.repetition = s.repetition;
+  r.ln_min_p = s.min_p > 0.0f ? std::log((double)s.min_p) : 0.0;
+  r.flags = penalties_on(s) ? as_dev::kFlagPenalties : 0u;
+  if (s.temp <= 0.0f) {
+    r.mode = as_dev::kModeGreedy;
+    r.cand = 0;
+  } else if (s.top_k > 0 && s.top_k < n) {
+    if (s.top_k <= (uint32_t)as_launch::kPartialCand && (uint64_t)s.top_k * n_seg <= as_launch::kCandCap) {
+      r.mode = as_dev::kModeTopK;
+      r.cand = s.top_k;
+    } else {
+      r.mode = as_dev::kModeExactTopK;
+      r.cand = 0;
+    }
+  } else {
+    r.mode = as_dev::kModePartial;
+    uint32_t c = as_launch::kCandCap / n_seg;
+    r.cand = c < (uint32_t)as_launch::kPartialCand ? c : (uint32_t)as_launch::kPartialCand;
+    if (s.top_p < 1.0f)
+      r.flags |= as_dev::kFlagSumTop;
+    else if (!(s.min_p > 0.0f))
+      r.flags |= as_dev::kFlagSumTemp;
+  }
+  return r;
+}
+
+bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
+
+// Copies rows' parameter blocks to the device through a pinned staging buffer, waiting only if the
+// same buffer's previous copy has not finished.
+int upload_params(as_ctx* c, const RowParams* rows, uint32_t n) {
+  const int b = c->next;
+  c->next ^= 1;
+  AS_HIP(c, hipEventSynchronize(c->staged[b]));
+  std::memcpy(c->h_params[b], rows, sizeof(RowParams) * n);
+  AS_HIP(c, hipMemcpyAsync(c->d_params, c->h_params[b], sizeof(RowParams) * n,
+                           hipMemcpyHostToDevice, c->stream));
+  AS_HIP(c, hipEventRecord(c->staged[b], c->stream));
+  return AS_OK;
+}
+
+// The next profiling event (created on first use), or null when profiling is off.
+hipEvent_t next_event(as_ctx* c) {
+  if (!c->profile) return nullptr;
+  if (c->ev_used == c->ev.size()) {
+    if (c->ev.size() >= 3 * 4096) return nullptr;
+    hipEvent_t e;
+    if (hipEventCreate(&e) != hipSuccess) return nullptr;
+    c->ev.push_back(e);
+  }
+  return c->ev[c->ev_used++];
+}
+
+int run_rows(as_ctx* c, const float* logits, uint64_t row_stride, uint32_t n, uint32_t n_rows,
+             const uint32_t* hist_off, const uint32_t* hist_ids, const uint32_t* extra_ids,
+             uint64_t* rng, uint32_t* tokens, uint32_t* status, uint32_t* kept_count,
+             uint32_t* kept_ids, double* kept_probs, uint32_t kept_cap) {
+  const uint32_t n_seg = (n + as_launch::kSegment - 1) / as_launch::kSegment;
+  const bool vec = aligned16(logits) && (row_stride % 4 == 0);
+  hipEvent_t e0 = nullptr, e1 = nullptr, e2 = nullptr;
+  if (c->profile && c->ev_used + 3 <= 3 * 4096) {
+    e0 = next_event(c);
+    e1 = next_event(c);
+    e2 = next_event(c);
+  }
+  if (e0) AS_HIP(c, hipEventRecord(e0, c->stream));
+  AS_HIP(c, as_launch::scan(c->stream, vec, logits, row_stride, n, n_rows, n_seg, c->d_params,
+                            hist_off, hist_ids, extra_ids, c->d_stats, c->d_cands,
+                            as_launch::kPartialCand));
+  as_launch::FinishArgs a{};
+  a.logits = logits;
+  a.row_stride = row_stride;
+  a.n = n;
+  a.n_seg = n_seg;
+  a.params = c->d_params;
+  a.hist_off = hist_off;
+  a.hist_ids = hist_ids;
+  a.extra_ids = extra_ids;
+  a.stats = c->d_stats;
+  a.cands = c->d_cands;
+  a.cand_stride = as_launch::kPartialCand;
+  a.kept_cap = kept_cap;
+  a.rng_state = rng;
+  a.tokens = tokens;
+  a.status = status;
+  a.kept_count = kept_count;
+  a.kept_ids = kept_ids;
+  a.kept_probs = kept_probs;
+  a.scratch = c->d_scratch;
+  a.scratch_stride = c->scratch_stride;
+  if (e1) AS_HIP(c, hipEventRecord(e1, c->stream));
+  AS_HIP(c, as_launch::finish(c->stream, n_rows, a));
+  if (e2) AS_HIP(c, hipEventRecord(e2, c->stream));
+  return AS_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int as_check(const as_sampling* p, char* msg, size_t cap) {
+  char buf[160];
+  buf[0] = 0;
+  if (!p) {
+    std::snprintf(buf, sizeof buf, "no sampling settings");
+  } else if (!(std::isfinite(p->temp) && p->temp >= 0.0f)) {
+    std::snprintf(buf, sizeof buf, "--temp %g must be a finite number, 0 or more", p->temp);
+  } else if (!(p->top_p > 0.0f && p->top_p <= 1.0f)) {
+    std::snprintf(buf, sizeof buf, "--top-p %g must be above 0 and at most 1", p->top_p);
+  } else if (!(p->min_p >= 0.0f && p->min_p <= 1.0f)) {
+    std::snprintf(buf, sizeof buf, "--min-p %g must be from 0 to 1", p->min_p);
+  } else if (!std::isfinite(p->presence)) {
+    std::snprintf(buf, sizeof buf, "--presence-penalty %g must be a finite number", p->presence);
+  } else if (!std::isfinite(p->frequency)) {
+    std::snprintf(buf, sizeof buf, "--frequency-penalty %g must be a finite number", p->frequency);
+  } else if (!(std::isfinite(p->repetition) && p->repetition > 0.0f)) {
+    std::snprintf(buf, sizeof buf, "--repetition-penalty %g must be a finite number above 0",
+                  p->repetition);
+  }
+  if (msg && cap) {
+    std::strncpy(msg, buf, cap - 1);
+    msg[cap - 1] = 0;
+  }
+  return buf[0] ? AS_ERR_PARAMS : AS_OK;
+}
+
+void as_rng_seed(uint64_t seed, uint64_t state[4]) {
+  uint64_t x = seed;
+  for (int i = 0; i < 4; ++i) {
+    x += 0x9E3779B97F4A7C15ull;
+    uint64_t z = x;
+    z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+    z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+    state[i] = z ^ (z >> 31);
+  }
+}
+
+const char* as_last_error(const as_ctx* ctx) { return ctx ? ctx->err.c_str() : "no context"; }
+
+int as_destroy(as_ctx* c) {
+  if (!c) return AS_ERR_INVALID;
+  (void)hipSetDevice(c->device);
+  if (c->stream) (void)hipStreamSynchronize(c->stream);
+  (void)hipFree(c->d_params);
+  (void)hipFree(c->d_stats);
+  (void)hipFree(c->d_cands);
+  (void)hipFree(c->d_scratch);
+  (void)hipFree(c->d_vstatus);
+  for (hipEvent_t e : c->ev) (void)hipEventDestroy(e);
+  for (int b = 0; b < 2; ++b) {
+    if (c->h_params[b]) (void)hipHostFree(c->h_params[b]);
+    if (c->staged[b]) (void)hipEventDestroy(c->staged[b]);
+  }
+  delete c;
+  return AS_OK;
+}
+
+int as_create(int device, void* hip_stream, uint32_t max_rows, uint32_t max_vocab,
+              uint32_t max_history, as_ctx** out) {
+  if (!out) return AS_ERR_INVALID;
+  *out = nullptr;
+  if (max_rows == 0 || max_vocab == 0) return AS_ERR_INVALID;
+  const uint32_t max_seg = (max_vocab + as_launch::kSegment - 1) / as_launch::kSegment;
+  if (max_seg > 256) return AS_ERR_CAPACITY;
+  as_ctx* c = new as_ctx();
+  c->device = device;
+  c->stream = (hipStream_t)hip_stream;
+  c->max_rows = max_rows;
+  c->max_vocab = max_vocab;
+  c->max_history = max_history;
+  c->max_seg = max_seg;
+  c->scratch_stride = 5ull * max_vocab;
+  hipError_t e = hipSetDevice(device);
+  if (e == hipSuccess) e = hipMalloc(&c->d_params, sizeof(RowParams) * max_rows);
+  if (e == hipSuccess) e = hipMalloc(&c->d_stats, sizeof(SegStats) * (uint64_t)max_rows * max_seg);
+  if (e == hipSuccess)
+    e = hipMalloc(&c->d_cands, sizeof(uint64_t) * (uint64_t)max_rows * max_seg * as_launch::kPartialCand);
+  if (e == hipSuccess) e = hipMalloc(&c->d_scratch, sizeof(uint32_t) * (uint64_t)max_rows * c->scratch_stride);
+  if (e == hipSuccess) e = hipMalloc(&c->d_vstatus, sizeof(uint32_t) * max_rows);
+  for (int b = 0; b < 2 && e == hipSuccess; ++b) {
+    e = hipHostMalloc((void**)&c->h_params[b], sizeof(RowParams) * max_rows, hipHostMallocDefault);
+    if (e == hipSuccess) e = hipEventCreateWithFlags(&c->staged[b], hipEventDisableTiming);
+    if (e == hipSuccess) e = hipEventRecord(c->staged[b], c->stream);
+  }
+  if (e != hipSuccess) {
+    std::fprintf(stderr, "as_create: %s\n", hipGetErrorString(e));
+    as_destroy(c);
+    return AS_ERR_HIP;
+  }
+  *out = c;
+  return AS_OK;
+}
+
+int as_sync(as_ctx* c) {
+  if (!c) return AS_ERR_INVALID;
+  AS_HIP(c, hipStreamSynchronize(c->stream));
+  return AS_OK;
+}
+
+int as_sample(as_ctx* c, const as_batch* b, const as_sampling* params) {
+  if (!c) return AS_ERR_INVALID;
+  if (!b || !params) return fail(c, AS_ERR_INVALID, "as_sample: no batch or no params");
+  if (b->n_rows == 0) return AS_OK;
+  if (!b->logits || !b->rng_state || !b->tokens || !b->status)
+    return fail(c, AS_ERR_INVALID, "as_sample: logits, rng_state, tokens and status are required");
+  if (b->n_vocab == 0 || (b->row_stride != 0 && b->row_stride < b->n_vocab))
+    return fail(c, AS_ERR_INVALID, "as_sample: n_vocab must be at least 1 and at most row_stride");
+  if (b->n_rows > c->max_rows || b->n_vocab > c->max_vocab)
+    return fail(c, AS_ERR_CAPACITY, "as_sample: more rows or a larger vocabulary than the context holds");
+  if ((b->hist_ids == nullptr) != (b->hist_offsets == nullptr))
+    return fail(c, AS_ERR_INVALID, "as_sample: hist_offsets and hist_ids go together");
+  if (b->kept_ids && b->kept_cap == 0)
+    return fail(c, AS_ERR_INVALID, "as_sample: kept_ids needs kept_cap > 0");
+  const uint32_t n_seg = (b->n_vocab + as_launch::kSegment - 1) / as_launch::kSegment;
+  std::vector<RowParams> h(b->n_rows);
+  for (uint32_t r = 0; r < b->n_rows; ++r) {
+    char msg[160];
+    if (as_check(&params[r], msg, sizeof msg) != AS_OK)
+      return fail(c, AS_ERR_PARAMS, "row " + std::to_string(r) + ": " + msg);
+    h[r] = make_row(params[r], b->n_vocab, n_seg);
+    h[r].rng_index = r;
+    h[r].rng_skip = 0;
+    h[r].flags |= as_dev::kFlagRngWrite;
+  }
+  AS_HIP(c, hipSetDevice(c->device));
+  int rc = upload_params(c, h.data(), b->n_rows);
+  if (rc != AS_OK) return rc;
+  return run_rows(c, b->logits, b->row_stride, b->n_vocab, b->n_rows, b->hist_offsets, b->hist_ids,
+                  nullptr, b->rng_state, b->tokens, b->status, b->kept_count, b->kept_ids,
+                  b->kept_probs, b->kept_cap);
+}
+
+int as_verify(as_ctx* c, const float* rows, uint64_t row_stride, uint32_t n_vocab,
+              const uint32_t* drafts, uint32_t k, const uint32_t* history, uint32_t hist_len,
+              const uint32_t* stop_ids, uint32_t n_stop, const as_sampling* params,
+              uint64_t* rng_state, uint32_t* picks, uint32_t* result) {
+  if (!c) return AS_ERR_INVALID;
+  if (!rows || !params || !rng_state || !picks || !result)
+    return fail(c, AS_ERR_INVALID, "as_verify: rows, params, rng_state, picks and result are required");
+  if ((k > 0 && !drafts) || (hist_len > 0 && !history) || (n_stop > 0 && !stop_ids))
+    return fail(c, AS_ERR_INVALID, "as_verify: a list with a length has no pointer");
+  if (n_vocab == 0 || row_stride < n_vocab)
+    return fail(c, AS_ERR_INVALID, "as_verify: n_vocab must be at least 1 and at most row_stride");
+  if (k + 1 > c->max_rows || n_vocab > c->max_vocab)
+    return fail(c, AS_ERR_CAPACITY, "as_verify: more rows or a larger vocabulary than the context holds");
+  char msg[160];
+  if (as_check(params, msg, sizeof msg) != AS_OK) return fail(c, AS_ERR_PARAMS, msg);
+  const uint32_t n_seg = (n_vocab + as_launch::kSegment - 1) / as_launch::kSegment;
+  const bool draws = params->temp > 0.0f;
+  std::vector<RowParams> h(k + 1);
+  for (uint32_t i = 0; i <= k; ++i) {
+    h[i] = make_row(*params, n_vocab, n_seg);
+    h[i].rng_index = 0;
+    h[i].rng_skip = draws ? i : 0;
+    h[i].hist_begin = 0;
+    h[i].hist_len = hist_len;
+    h[i].extra = i;  // the drafts before row i were emitted when row i is sampled
+  }
+  AS_HIP(c, hipSetDevice(c->device));
+  int rc = upload_params(c, h.data(), k + 1);
+  if (rc != AS_OK) return rc;
+  rc = run_rows(c, rows, row_stride, n_vocab, k + 1, nullptr, hist_len ? history : nullptr,
+                k ? drafts : nullptr, rng_state, picks, c->d_vstatus, nullptr, nullptr, nullptr, 0);
+  if (rc != AS_OK) return rc;
+  AS_HIP(c, as_launch::accept(c->stream, picks, c->d_vstatus, drafts, k, stop_ids, n_stop, rng_state,
+                              draws ? 1u : 0u, result));
+  return AS_OK;
+}
+
+int as_argmax_rows(as_ctx* c, const float* logits, uint64_t row_stride, uint32_t n, uint32_t n_rows,
+                   uint32_t* ids, uint64_t* rows_out, uint64_t embd, uint32_t row_bytes,
+                   uint32_t slot) {
+  if (!c) return AS_ERR_INVALID;
+  if (n_rows == 0) return AS_OK;
+  if (!logits || !ids || !rows_out || row_stride < n)
+    return fail(c, AS_ERR_INVALID, "as_argmax_rows: bad pointers or row_stride < n");
+  AS_HIP(c, hipSetDevice(c->device));
+  const bool vec = aligned16(logits) && (row_stride % 4 == 0);
+  AS_HIP(c, as_launch::argmax_rows(c->stream, vec, logits, row_stride, n, n_rows, ids, rows_out,
+                                   embd, row_bytes, slot));
+  return AS_OK;
+}
+
+int as_profile(as_ctx* c, int enable) {
+  if (!c) return AS_ERR_INVALID;
+  c->profile = enable != 0;
+  c->ev_used = 0;
+  return AS_OK;
+}
+
+int as_profile_read(as_ctx* c, double* scan_ms, double* finish_ms, uint32_t* calls) {
+  if (!c || !scan_ms || !finish_ms || !calls) return AS_ERR_INVALID;
+  AS_HIP(c, hipSetDevice(c->device));
+  AS_HIP(c, hipStreamSynchronize(c->stream));
+  double s = 0.0, f = 0.0;
+  uint32_t k = 0;
+  for (size_t i = 0; i + 2 < c->ev_used; i += 3) {
+    float a = 0.0f, b = 0.0f;
+    AS_HIP(c, hipEventElapsedTime(&a, c->ev[i], c->ev[i + 1]));
+    AS_HIP(c, hipEventElapsedTime(&b, c->ev[i + 1], c->ev[i + 2]));
+    s += a;
+    f += b;
+    ++k;
+  }
+  *scan_ms = s;
+  *finish_ms = f;
+  *calls = k;
+  c->ev_used = 0;
+  return AS_OK;
+}
+
+int as_debug_exp(as_ctx* c, const double* x, double* y, uint32_t n) {
+  if (!c) return AS_ERR_INVALID;
+  if (n == 0) return AS_OK;
+  if (!x || !y) return fail(c, AS_ERR_INVALID, "as_debug_exp: no arrays");
+  AS_HIP(c, hipSetDevice(c->device));
+  AS_HIP(c, as_launch::debug_exp(c->stream, x, y, n));
+  return AS_OK;
+}
+
+}  // extern "C"

@@ -1,0 +1,688 @@
+// Pass 2, one workgroup per row: merges the segments' results and chooses the token.
+//
+// Top-k rows (0 < k < n with k segment candidates each): the union of the segments' top k holds
+// the row's top k; a bitonic sort in LDS orders it by rank and one thread runs draw_full_sort's f64
+// tail (sample.rs:157-198) in the reference's own order, so every sum and comparison is bit-exact.
+//
+// Rows without a top-k (draw_partial, sample.rs:208-293): the union of the segments' best 256 is a
+// complete rank prefix down to the best of the truncated segments' last candidates. The min-p cut
+// is an exact comparison. The top-p cut and the unfiltered draw depend on a sum over the whole row
+// in index order; that sum comes from the segments' partial sums with a rigorous error bound that
+// covers the reference's own left-to-right rounding, and a decision is taken only when the bound
+// cannot change it. The kept set's draw is then exact. A row whose decision falls within the bound,
+// or whose cut lies past the complete prefix, runs the exact-order path below: a stable radix sort
+// of the whole row in HBM scratch and the reference's sequential folds, so its token is the
+// reference's in every case.
+#include "sampler_device.h"
+#include "launch.h"
+#include "../../include/artemis_sampler.h"
+
+using namespace as_dev;
+using as_launch::FinishArgs;
+
+namespace {
+
+constexpr int kThreads = 1024;
+constexpr int kWaves = kThreads / kWave;
+constexpr int kCap = as_launch::kCandCap;
+constexpr int kMaxSeg = 256;
+constexpr int kStage = 4096;
+constexpr double kU = 1.1102230246251565e-16;  // 2^-53, the unit roundoff
+
+__device__ __forceinline__ double gamma_n(double n) { return n * kU / (1.0 - n * kU); }
+
+struct Shared {
+  uint64_t sk[kCap];  // candidates (exact path: per-wave digit counts)
+  double wd[kCap];    // weights and prefix sums (exact path: staging for sequential folds)
+  uint64_t tab[256];
+  uint32_t hist[256];
+  uint32_t base[256];
+  uint32_t tot[256];
+  uint32_t seg_off[kMaxSeg + 1];
+  uint32_t red_u[kWaves];
+  double red_d[kWaves];
+  // Row scalars.
+  uint32_t bad, gi, mk, total, trunc, keep, pick, done, exact, prefix;
+  uint64_t bound_key;
+  double u01, sum, x, eps;
+};
+
+// --- block helpers ------------------------------------------------------------------------------
+
+__device__ void bitonic_desc(uint64_t* s, uint32_t n) {
+  for (uint32_t k = 2; k <= n; k <<= 1) {
+    for (uint32_t j = k >> 1; j > 0; j >>= 1) {
+      for (uint32_t i = threadIdx.x; i < n; i += kThreads) {
+        const uint32_t ixj = i ^ j;
+        if (ixj > i) {
+          const uint64_t x = s[i], y = s[ixj];
+          const bool desc = (i & k) == 0;
+          if (desc ? (x < y) : (x > y)) {
+            s[i] = y;
+            s[ixj] = x;
+          }
+        }
+      }
+      __syncthreads();
+    }
+  }
+}
+
+// Exclusive prefix sum of one f64 per thread over the block.
+__device__ double block_exclusive_scan_f64(double x, double* wave_tot) {
+  const int lane = threadIdx.x & (kWave - 1), w = threadIdx.x / kWave;
+  double incl = x;
+  for (int o = 1; o < kWave; o <<= 1) {
+    const double y = __shfl_up(incl, o, kWave);
+    if (lane >= o) incl = __dadd_rn(incl, y);
+  }
+  __syncthreads();
+  if (lane == kWave - 1) wave_tot[w] = incl;
+  __syncthreads();
+  double before = 0.0;
+  for (int k = 0; k < w; ++k) before = __dadd_rn(before, wave_tot[k]);
+  // incl - x is not exact; recompute the exclusive value from the wave's shifted inclusive scan.
+  double excl_in_wave = __shfl_up(incl, 1, kWave);
+  if (lane == 0) excl_in_wave = 0.0;
+  return __dadd_rn(before, excl_in_wave);
+}
+
+__device__ __forceinline__ uint32_t history_bounds(const FinishArgs& a, const RowParams& p,
+                                                   uint32_t row, uint32_t* hb) {
+  uint32_t b = 0, e = 0;
+  if (a.hist_ids) {
+    if (a.hist_off) {
+      b = a.hist_off[row];
+      e = a.hist_off[row + 1];
+    } else {
+      b = p.hist_begin;
+      e = p.hist_begin + p.hist_len;
+    }
+  }
+  *hb = b;
+  return e;
+}
+
+// --- the exact-order path ---------------------------------------------------------------------
+
+// Thread 0's left-to-right f64 fold of term(i), i in [0, m), staged through LDS in tiles that all
+// threads fill. Returns the sum to every thread.
+template <class Term>
+__device__ double seq_fold(Shared& sh, uint32_t m, Term term) {
+  double* stage = sh.wd;
+  double acc = 0.0;
+  for (uint32_t t0 = 0; t0 < m; t0 += kStage) {
+    const uint32_t c = min((uint32_t)kStage, m - t0);
+    for (uint32_t i = threadIdx.x; i < c; i += kThreads) stage[i] = term(t0 + i);
+    __syncthreads();
+    if (threadIdx.x == 0)
+      for (uint32_t i = 0; i < c; ++i) acc = __dadd_rn(acc, stage[i]);
+    __syncthreads();
+  }
+  if (threadIdx.x == 0) sh.sum = acc;
+  __syncthreads();
+  const double r = sh.sum;
+  __syncthreads();
+  return r;
+}
+
+// One stable pass of an LSD radix sort on 8 bits: (src_key, src_id) -> (dst_key, dst_id).
+__device__ void radix_pass(Shared& sh, uint32_t n, int shift, const uint32_t* src_key,
+                           const uint32_t* src_id, uint32_t* dst_key, uint32_t* dst_id) {
+  uint32_t* wcnt = reinterpret_cast<uint32_t*>(sh.sk);  // [kWaves][256]
+  const uint32_t tid = threadIdx.x, lane = tid & (kWave - 1), w = tid / kWave;
+  if (tid < 256) sh.hist[tid] = 0;
+  __syncthreads();
+  for (uint32_t i = tid; i < n; i += kThreads) atomicAdd(&sh.hist[(src_key[i] >> shift) & 255u], 1u);
+  __syncthreads();
+  if (tid == 0) {
+    uint32_t run = 0;
+    for (int d = 0; d < 256; ++d) {
+      sh.base[d] = run;
+      run += sh.hist[d];
+    }
+  }
+  for (uint32_t i = tid; i < kWaves * 256; i += kThreads) wcnt[i] = 0;
+  __syncthreads();
+  const uint64_t below = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
+  for (uint32_t t0 = 0; t0 < n; t0 += kThreads) {
+    const uint32_t i = t0 + tid;
+    const bool valid = i < n;
+    const uint32_t k = valid ? src_key[i] : 0u, id = valid ? src_id[i] : 0u;
+    const uint32_t d = (k >> shift) & 255u;
+    uint64_t peers = __ballot(valid);
+#pragma unroll
+    for (int b = 0; b < 8; ++b) {
+      const uint64_t bb = __ballot(valid && ((d >> b) & 1u));
+      peers &= ((d >> b) & 1u) ? bb : ~bb;
+    }
+    const uint32_t rank = __popcll(peers & below), count = __popcll(peers);
+    if (valid && rank == count - 1) wcnt[w * 256 + d] = count;
+    __syncthreads();
+    if (tid < 256) {
+      uint32_t run = 0;
+      for (int ww = 0; ww < kWaves; ++ww) {
+        const uint32_t c = wcnt[ww * 256 + tid];
+        wcnt[ww * 256 + tid] = run;
+        run += c;
+      }
+      sh.tot[tid] = run;
+    }
+    __syncthreads();
+    if (valid) {
+      const uint32_t pos = sh.base[d] + wcnt[w * 256 + d] + rank;
+      dst_key[pos] = k;
+      dst_id[pos] = id;
+    }
+    __syncthreads();
+    if (tid < 256) sh.base[tid] += sh.tot[tid];
+    for (uint32_t j = tid; j < kWaves * 256; j += kThreads) wcnt[j] = 0;
+    __syncthreads();
+  }
+}
+
+// The reference's algorithm in its own order: Sampler::sample's dispatch (sample.rs:136-149),
+// draw_full_sort (157-198) for top-k rows and draw_partial (208-293) otherwise.
+__device__ void exact_row(const FinishArgs& a, const RowParams& p, uint32_t row, Shared& sh) {
+  const uint32_t n = a.n, tid = threadIdx.x;
+  uint32_t* S = a.scratch + (uint64_t)row * a.scratch_stride;
+  uint32_t* cnt = S;
+  uint32_t* keyA = S + n;
+  uint32_t* idA = S + 2 * (uint64_t)n;
+  uint32_t* keyB = S + 3 * (uint64_t)n;
+  uint32_t* idB = S + 4 * (uint64_t)n;
+  const float* x = a.logits + (uint64_t)row * a.row_stride;
+
+  uint32_t hb;
+  const uint32_t he = history_bounds(a, p, row, &hb);
+  const uint32_t extra = a.extra_ids ? p.extra : 0;
+  const bool pen = (p.flags & kFlagPenalties) && (he > hb || extra > 0);
+  if (pen) {
+    for (uint32_t i = tid; i < n; i += kThreads) cnt[i] = 0;
+    __syncthreads();
+    for (uint32_t h = hb + tid; h < he; h += kThreads) {
+      const uint32_t id = a.hist_ids[h];
+      if (id < n) atomicAdd(&cnt[id], 1u);
+    }
+    for (uint32_t h = tid; h < extra; h += kThreads) {
+      const uint32_t id = a.extra_ids[h];
+      if (id < n) atomicAdd(&cnt[id], 1u);
+    }
+    __syncthreads();
+  }
+  auto value = [&](uint32_t i) -> float {
+    float v = x[i];
+    if (pen) {
+      const uint32_t c = cnt[i];
+      if (c) v = penalize(v, c, p);
+    }
+    return v;
+  };
+  for (uint32_t i = tid; i < n; i += kThreads) {
+    keyA[i] = ~total_key(value(i));
+    idA[i] = i;
+  }
+  __syncthreads();
+  radix_pass(sh, n, 0, keyA, idA, keyB, idB);
+  radix_pass(sh, n, 8, keyB, idB, keyA, idA);
+  radix_pass(sh, n, 16, keyA, idA, keyB, idB);
+  radix_pass(sh, n, 24, keyB, idB, keyA, idA);
+  // Rank j: id idA[j], value key_value(~keyA[j]).
+  auto rv = [&](uint32_t j) -> double { return (double)key_value(~keyA[j]); };
+  const double top = rv(0);
+  const double temp = (double)p.temp;
+  const bool has_floor = p.min_p > 0.0f;
+  const double floor = __dadd_rn(top, p.ln_min_p);
+  const double top_p = (double)p.top_p;
+  const uint64_t* tab = sh.tab;
+  auto w_temp = [&](double v) { return as_exp::exp_with(tab, __ddiv_rn(__dsub_rn(v, top), temp)); };
+  auto w_one = [&](double v) { return as_exp::exp_with(tab, __dsub_rn(v, top)); };
+
+  uint32_t keep = 0;
+  bool unfiltered = false;
+  if (p.mode == kModeExactTopK) {
+    const uint32_t k = p.top_k;
+    keep = k;
+    if (p.top_p < 1.0f) {
+      const double total = seq_fold(sh, k, [&](uint32_t j) { return w_one(rv(j)); });
+      // The cumulative walk, thread 0 over staged weights.
+      if (tid == 0) sh.done = 0;
+      for (uint32_t t0 = 0; t0 < k; t0 += kStage) {
+        const uint32_t c = min((uint32_t)kStage, k - t0);
+        for (uint32_t i = tid; i < c; i += kThreads) sh.wd[i] = w_one(rv(t0 + i));
+        __syncthreads();
+        if (tid == 0) {
+          double cum = sh.sum;  // carried between tiles
+          if (t0 == 0) cum = 0.0;
+          for (uint32_t i = 0; i < c; ++i) {
+            cum = __dadd_rn(cum, __ddiv_rn(sh.wd[i], total));
+            if (cum >= top_p) {
+              sh.keep = t0 + i + 1;
+              sh.done = 1;
+              break;
+            }
+          }
+          sh.sum = cum;
+        }
+        __syncthreads();
+        if (sh.done) break;
+      }
+      if (sh.done) keep = sh.keep;
+      __syncthreads();
+    }
+    if (has_floor) {
+      uint32_t first = keep;
+      for (uint32_t j = tid; j < keep; j += kThreads)
+        if (!(rv(j) >= floor)) first = min(first, j);
+      keep = block_min_u32<kWaves>(first, sh.red_u);
+    }
+  } else if (p.top_p < 1.0f || has_floor) {
+    double total1 = 0.0;
+    if (p.top_p < 1.0f) total1 = seq_fold(sh, n, [&](uint32_t i) { return w_one((double)value(i)); });
+    keep = n;
+    if (tid == 0) {
+      sh.done = 0;
+      sh.sum = 0.0;
+    }
+    __syncthreads();
+    for (uint32_t t0 = 0; t0 < n; t0 += kStage) {
+      const uint32_t c = min((uint32_t)kStage, n - t0);
+      for (uint32_t i = tid; i < c; i += kThreads) {
+        const double v = rv(t0 + i);
+        // -1 marks the first token min-p drops (tested before top-p, sample.rs:237-251).
+        sh.wd[i] = (has_floor && v < floor) ? -1.0 : (p.top_p < 1.0f ? w_one(v) : 0.0);
+      }
+      __syncthreads();
+      if (tid == 0) {
+        double cum = sh.sum;
+        for (uint32_t i = 0; i < c; ++i) {
+          if (sh.wd[i] < 0.0) {
+            sh.keep = t0 + i;
+            sh.done = 1;
+            break;
+          }
+          if (p.top_p < 1.0f) {
+            cum = __dadd_rn(cum, __ddiv_rn(sh.wd[i], total1));
+            if (cum >= top_p) {
+              sh.keep = t0 + i + 1;
+              sh.done = 1;
+              break;
+            }
+          }
+        }
+        sh.sum = cum;
+      }
+      __syncthreads();
+      if (sh.done) break;
+    }
+    if (sh.done) keep = sh.keep;
+    __syncthreads();
+  } else {
+    unfiltered = true;
+    keep = n;
+  }
+
+  // The draw: u = unit() * total, then the first rank whose cumulative weight exceeds u.
+  double total;
+  if (unfiltered)
+    total = seq_fold(sh, n, [&](uint32_t i) { return w_temp((double)value(i)); });
+  else
+    total = seq_fold(sh, keep, [&](uint32_t j) { return w_temp(rv(j)); });
+  const double u = __dmul_rn(sh.u01, total);
+  if (tid == 0) {
+    sh.done = 0;
+    sh.sum = 0.0;
+    sh.pick = keep - 1;  // sample.rs:197, 272, 288: the last kept when u is never passed
+  }
+  __syncthreads();
+  for (uint32_t t0 = 0; t0 < keep; t0 += kStage) {
+    const uint32_t c = min((uint32_t)kStage, keep - t0);
+    for (uint32_t i = tid; i < c; i += kThreads) sh.wd[i] = w_temp(rv(t0 + i));
+    __syncthreads();
+    if (tid == 0) {
+      double cum = sh.sum;
+      for (uint32_t i = 0; i < c; ++i) {
+        cum = __dadd_rn(cum, sh.wd[i]);
+        if (u < cum) {
+          sh.pick = t0 + i;
+          sh.done = 1;
+          break;
+        }
+      }
+      sh.sum = cum;
+    }
+    __syncthreads();
+    if (sh.done) break;
+  }
+  const uint32_t pick = sh.pick;
+  if (tid == 0) {
+    a.tokens[row] = idA[pick];
+    a.status[row] = AS_ROW_OK | AS_ROW_EXACT_PATH;
+    if (a.kept_count) a.kept_count[row] = keep;
+  }
+  if (a.kept_ids) {
+    const uint32_t m = min(keep, a.kept_cap);
+    for (uint32_t j = tid; j < m; j += kThreads) {
+      a.kept_ids[(uint64_t)row * a.kept_cap + j] = idA[j];
+      if (a.kept_probs) a.kept_probs[(uint64_t)row * a.kept_cap + j] = __ddiv_rn(w_temp(rv(j)), total);
+    }
+  }
+}
+
+// --- the kernel ---------------------------------------------------------------------------------
+
+__global__ __launch_bounds__(kThreads) void finish_kernel(FinishArgs a) {
+  __shared__ Shared sh;
+  const uint32_t row = blockIdx.x, tid = threadIdx.x;
+  const RowParams p = a.params[row];
+  const SegStats* st = a.stats + (uint64_t)row * a.n_seg;
+  const uint32_t n = a.n;
+  if (tid < 256) sh.tab[tid] = as_exp::kTable[tid];
+
+  if (tid == 0) {
+    uint32_t bad = kNone, gi = kNone, mk = 0, total = 0, trunc = 0, long_hist = 0;
+    float gv = 0.0f;
+    uint64_t bound = 0;
+    for (uint32_t s = 0; s < a.n_seg; ++s) {
+      const SegStats t = st[s];
+      bad = min(bad, t.nonfinite);
+      greedy_merge(gv, gi, t.greedy_val, t.greedy_idx);
+      mk = max(mk, t.max_key);
+      sh.seg_off[s] = total;
+      total += t.n_cand;
+      if (t.truncated & 1u) {
+        trunc = 1;
+        bound = max(bound, t.min_cand);
+      }
+      if (t.truncated & 2u) long_hist = 1;
+    }
+    sh.seg_off[a.n_seg] = total;
+    sh.bad = bad;
+    sh.gi = gi;
+    sh.mk = mk;
+    sh.total = total;
+    sh.trunc = trunc;
+    sh.bound_key = bound;
+    sh.exact = long_hist;
+    sh.u01 = 0.0;
+    if (bad == kNone && p.mode != kModeGreedy) {
+      // One unit() per sampled row (sample.rs:189, 264, 276), after the row's skipped draws.
+      uint64_t s4[4];
+      uint64_t* src = a.rng_state + 4ull * p.rng_index;
+      for (int k = 0; k < 4; ++k) s4[k] = src[k];
+      for (uint32_t k = 0; k < p.rng_skip; ++k) rng_next(s4);
+      sh.u01 = rng_unit(s4);
+      if (p.flags & kFlagRngWrite)
+        for (int k = 0; k < 4; ++k) src[k] = s4[k];
+    }
+  }
+  __syncthreads();
+
+  if (sh.bad != kNone) {
+    if (tid == 0) {
+      a.tokens[row] = kNone;
+      a.status[row] = AS_ROW_NONFINITE;
+      if (a.kept_count) a.kept_count[row] = sh.bad;
+    }
+    return;
+  }
+  if (p.mode == kModeGreedy && !sh.exact) {
+    if (tid == 0) {
+      a.tokens[row] = sh.gi;
+      a.status[row] = AS_ROW_OK;
+      if (a.kept_count) a.kept_count[row] = 1;
+      if (a.kept_ids && a.kept_cap > 0) {
+        a.kept_ids[(uint64_t)row * a.kept_cap] = sh.gi;
+        if (a.kept_probs) a.kept_probs[(uint64_t)row * a.kept_cap] = 1.0;
+      }
+    }
+    return;
+  }
+
+  if ((p.mode == kModeTopK || p.mode == kModePartial) && !sh.exact) {
+    const uint32_t total = sh.total;
+    uint32_t N = 2;
+    while (N < total) N <<= 1;
+    for (uint32_t s = 0; s < a.n_seg; ++s) {
+      const uint32_t off = sh.seg_off[s], c = sh.seg_off[s + 1] - off;
+      const uint64_t* src = a.cands + ((uint64_t)row * a.n_seg + s) * a.cand_stride;
+      for (uint32_t j = tid; j < c; j += kThreads) sh.sk[off + j] = src[j];
+    }
+    for (uint32_t i = total + tid; i < N; i += kThreads) sh.sk[i] = 0;
+    __syncthreads();
+    bitonic_desc(sh.sk, N);
+
+    const double top = (double)packed_value(sh.sk[0]);
+    const double temp = (double)p.temp;
+    const double top_p = (double)p.top_p;
+    const bool has_floor = p.min_p > 0.0f;
+    const double floor = __dadd_rn(top, p.ln_min_p);
+    const uint64_t* tab = sh.tab;
+    auto val = [&](uint32_t i) -> double { return (double)packed_value(sh.sk[i]); };
+    auto w_temp = [&](double v) { return as_exp::exp_with(tab, __ddiv_rn(__dsub_rn(v, top), temp)); };
+    auto w_one = [&](double v) { return as_exp::exp_with(tab, __dsub_rn(v, top)); };
+
+    uint32_t keep = 0;
+    bool unfiltered = false;
+    if (p.mode == kModeTopK) {
+      // draw_full_sort over the k best (sample.rs:157-183).
+      const uint32_t k = p.top_k;
+      keep = k;
+      if (p.top_p < 1.0f) {
+        for (uint32_t i = tid; i < k; i += kThreads) sh.wd[i] = w_one(val(i));
+        __syncthreads();
+        if (tid == 0) {
+          double tot = 0.0;
+          for (uint32_t i = 0; i < k; ++i) tot = __dadd_rn(tot, sh.wd[i]);
+          double cum = 0.0;
+          uint32_t kk = k;
+          for (uint32_t i = 0; i < k; ++i) {
+            cum = __dadd_rn(cum, __ddiv_rn(sh.wd[i], tot));
+            if (cum >= top_p) {
+              kk = i + 1;
+              break;
+            }
+          }
+          sh.keep = kk;
+        }
+        __syncthreads();
+        keep = sh.keep;
+      }
+      if (has_floor) {
+        uint32_t first = keep;
+        for (uint32_t i = tid; i < keep; i += kThreads)
+          if (!(val(i) >= floor)) first = min(first, i);
+        keep = block_min_u32<kWaves>(first, sh.red_u);
+      }
+    } else {
+      // draw_partial: the complete rank prefix first.
+      uint32_t P = total;
+      if (sh.trunc) {
+        uint32_t c = 0;
+        for (uint32_t i = tid; i < total; i += kThreads) c += (sh.sk[i] >= sh.bound_key) ? 1u : 0u;
+        P = block_sum_u32<kWaves>(c, sh.red_u);
+      }
+      if (tid == 0) sh.prefix = P;
+      const bool complete = !sh.trunc;  // every value of the row is a candidate
+      uint32_t im = P;
+      if (has_floor) {
+        uint32_t first = P;
+        for (uint32_t i = tid; i < P; i += kThreads)
+          if (!(val(i) >= floor)) first = min(first, i);
+        im = block_min_u32<kWaves>(first, sh.red_u);
+      }
+      const bool cuts = p.top_p < 1.0f || has_floor;
+      if (cuts) {
+        uint32_t jl = P, jh = P;
+        bool ok = true;
+        if (p.top_p < 1.0f) {
+          // total1 = sum of exp(l - top) over the row in index order (sample.rs:218-222): the
+          // segments' sums rescaled, with |result - reference's left fold| <= eps.
+          if (tid == 0) {
+            double X = 0.0, babs = 0.0;
+            for (uint32_t s = 0; s < a.n_seg; ++s) {
+              const SegStats t = st[s];
+              const double ms = (double)key_value(t.max_key);
+              const double dm = __dsub_rn(top, ms);
+              const double sc = as_exp::exp_with(tab, __dsub_rn(ms, top));
+              X = __dadd_rn(X, __dmul_rn(t.sum, sc));
+              babs = __dadd_rn(babs, __dmul_rn(sc, __dadd_rn(t.sum_abs, __dmul_rn(dm, t.sum))));
+            }
+            const double terms = (double)n + (double)a.n_seg + 64.0;
+            sh.x = X;
+            sh.eps = kU * 1.02 * (2.1 * babs + terms * X);
+          }
+          __syncthreads();
+          const double X = sh.x, eps = sh.eps;
+          ok = (X - eps > 0.0) && (eps == eps);
+          if (ok) {
+            // Inclusive prefix sums of the exact weights in rank order, 8 per thread.
+            const uint32_t i0 = tid * 8;
+            double loc[8];
+            double run = 0.0;
+#pragma unroll
+            for (int q = 0; q < 8; ++q) {
+              const uint32_t i = i0 + q;
+              const double w = (i < P) ? w_one(val(i)) : 0.0;
+              run = __dadd_rn(run, w);
+              loc[q] = run;
+            }
+            const double off = block_exclusive_scan_f64(run, sh.red_d);
+            const double g31 = 2.0 * gamma_n(40.0);
+            uint32_t fl = P, fh = P;
+#pragma unroll
+            for (int q = 0; q < 8; ++q) {
+              const uint32_t i = i0 + q;
+              if (i < P) {
+                const double R = __dadd_rn(off, loc[q]);
+                const double rel = g31 + gamma_n((double)i + 2.0) + 10.0 * kU;
+                const double hi = R * (1.0 + rel) / (X - eps);
+                const double lo = R * (1.0 - rel) / (X + eps);
+                if (hi >= top_p) fl = min(fl, i);
+                if (lo >= top_p) fh = min(fh, i);
+              }
+            }
+            jl = block_min_u32<kWaves>(fl, sh.red_u);
+            jh = block_min_u32<kWaves>(fh, sh.red_u);
+          }
+        }
+        if (!ok)
+          keep = kNone;
+        else if (im < P && im <= jl)
+          keep = im;
+        else if (jl < P && jl == jh)
+          keep = jh + 1;
+        else if (jl == P && im == P && complete)
+          keep = n;
+        else
+          keep = kNone;
+      } else {
+        unfiltered = true;
+        // The unfiltered draw's total over the row in index order (sample.rs:275).
+        if (tid == 0) {
+          double X = 0.0, babs = 0.0;
+          for (uint32_t s = 0; s < a.n_seg; ++s) {
+            const SegStats t = st[s];
+            const double ms = (double)key_value(t.max_key);
+            const double dm = __ddiv_rn(__dsub_rn(top, ms), temp);
+            const double sc = as_exp::exp_with(tab, __ddiv_rn(__dsub_rn(ms, top), temp));
+            X = __dadd_rn(X, __dmul_rn(t.sum, sc));
+            babs = __dadd_rn(babs, __dmul_rn(sc, __dadd_rn(t.sum_abs, __dmul_rn(dm, t.sum))));
+          }
+          const double terms = (double)n + (double)a.n_seg + 64.0;
+          sh.x = X;
+          sh.eps = kU * 1.02 * (4.2 * babs + terms * X);
+        }
+        for (uint32_t i = tid; i < P; i += kThreads) sh.wd[i] = w_temp(val(i));
+        __syncthreads();
+        const double X = sh.x, eps = sh.eps;
+        if (tid == 0) {
+          uint32_t pick = kNone;
+          if (X - eps > 0.0 && eps == eps) {
+            const double ulo = sh.u01 * (X - eps) * (1.0 - 3.0 * kU);
+            const double uhi = sh.u01 * (X + eps) * (1.0 + 3.0 * kU);
+            uint32_t jp = P, jc = P;
+            double cum = 0.0;
+            for (uint32_t i = 0; i < P; ++i) {
+              cum = __dadd_rn(cum, sh.wd[i]);
+              if (jp == P && cum > ulo) jp = i;
+              if (cum > uhi) {
+                jc = i;
+                break;
+              }
+            }
+            if (jp == jc && jc < P)
+              pick = jc;
+            else if (jp == P && complete)
+              pick = n - 1;
+          }
+          sh.pick = pick;
+          sh.sum = X;
+        }
+        __syncthreads();
+        keep = (sh.pick == kNone) ? kNone : n;
+      }
+    }
+
+    if (keep == kNone) {
+      if (tid == 0) sh.exact = 1;
+    } else if (!unfiltered) {
+      // The draw over the kept prefix, in the reference's order (sample.rs:184-197, 260-272).
+      for (uint32_t i = tid; i < keep; i += kThreads) sh.wd[i] = w_temp(val(i));
+      __syncthreads();
+      if (tid == 0) {
+        double tot = 0.0;
+        for (uint32_t i = 0; i < keep; ++i) tot = __dadd_rn(tot, sh.wd[i]);
+        const double u = __dmul_rn(sh.u01, tot);
+        double cum = 0.0;
+        uint32_t pick = keep - 1;
+        for (uint32_t i = 0; i < keep; ++i) {
+          cum = __dadd_rn(cum, sh.wd[i]);
+          if (u < cum) {
+            pick = i;
+            break;
+          }
+        }
+        sh.pick = pick;
+        sh.sum = tot;
+      }
+      __syncthreads();
+    }
+    if (keep != kNone) {
+      const uint32_t pick = sh.pick;
+      const double tot = sh.sum;
+      if (tid == 0) {
+        a.tokens[row] = packed_id(sh.sk[pick]);
+        a.status[row] = AS_ROW_OK;
+        if (a.kept_count) a.kept_count[row] = keep;
+      }
+      if (a.kept_ids) {
+        const uint32_t m = min(min(keep, a.kept_cap), unfiltered ? sh.prefix : keep);
+        for (uint32_t j = tid; j < m; j += kThreads) {
+          a.kept_ids[(uint64_t)row * a.kept_cap + j] = packed_id(sh.sk[j]);
+          if (a.kept_probs) a.kept_probs[(uint64_t)row * a.kept_cap + j] = __ddiv_rn(sh.wd[j], tot);
+        }
+      }
+    }
+    __syncthreads();
+  } else {
+    if (tid == 0) sh.exact = 1;
+    __syncthreads();
+  }
+
+  if (sh.exact) {
+    __syncthreads();
+    exact_row(a, p, row, sh);
+  }
+}
+
+}  // namespace
+
+namespace as_launch {
+
+hipError_t finish(hipStream_t stream, uint32_t n_rows, const FinishArgs& a) {
+  hipLaunchKernelGGL(finish_kernel, dim3(n_rows), dim3(kThreads), 0, stream, a);
+  return hipGetLastError();
+}
+
+}  // namespace as_launch

@@ -1,0 +1,199 @@
+// Device-side building blocks of the sampler kernels: the rank order as integer keys, the penalty,
+// the seed stream, the per-row parameter block and wave64 reductions.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "exp_f64.h"
+
+namespace as_dev {
+
+constexpr int kWave = 64;
+constexpr uint32_t kNone = 0xFFFFFFFFu;
+
+// Row modes, chosen on the host from the sampling settings (sample.rs:129-150).
+enum : uint32_t {
+  kModeGreedy = 0,     // temp <= 0: greedy / greedy_penalized
+  kModeTopK = 1,       // 0 < k < n, k small enough for the segment candidates: draw_full_sort
+  kModePartial = 2,    // k == 0 or k >= n: draw_partial
+  kModeExactTopK = 3,  // 0 < k < n with a k too large for the segment candidates
+};
+
+// RowParams.flags
+enum : uint32_t {
+  kFlagPenalties = 1u,  // some penalty acts (the reference's `pen != 0.0`)
+  kFlagSumTop = 2u,     // partial with top_p < 1: segment sums of exp(l - m)
+  kFlagSumTemp = 4u,    // partial with no filter: segment sums of exp((l - m) / T)
+  kFlagRngWrite = 8u,   // write the advanced RNG state back (batch rows; verify defers it)
+  kFlagKept = 16u,      // the caller wants kept lists
+};
+
+struct RowParams {
+  float temp;
+  uint32_t top_k;
+  float top_p;
+  float min_p;
+  float presence;
+  float frequency;
+  float repetition;
+  uint32_t mode;
+  double ln_min_p;      // log((double)min_p) from the host libm, as f64::ln (sample.rs:181, 217)
+  uint32_t flags;
+  uint32_t cand;        // candidates each segment keeps (top-k rows: k)
+  uint32_t rng_index;   // which 4-word state the row draws from
+  uint32_t rng_skip;    // draws to skip first (verify row i skips i)
+  uint32_t hist_begin;  // history range when no CSR offsets are given
+  uint32_t hist_len;
+  uint32_t extra;       // ids of the extra list appended to the history (verify drafts)
+  uint32_t pad;
+};
+
+// Per (row, segment) results of the scan.
+struct SegStats {
+  uint32_t nonfinite;   // first index holding NaN/inf in the raw logits, or kNone
+  uint32_t greedy_idx;  // IEEE-greater argmax, lowest index on ties, NaN skipped; kNone if none
+  float greedy_val;
+  uint32_t max_key;     // largest rank key of the penalised values
+  uint32_t n_cand;
+  uint32_t truncated;   // bit 0: the segment held more values than it kept as candidates;
+                        // bit 1: the row's history is too long for the scan's u16 counts
+  uint64_t min_cand;    // smallest packed candidate kept
+  double sum;           // sum of exp(d), d = l - m (or (l - m) / T), m = key_value(max_key)
+  double sum_abs;       // sum of exp(d) * |d|
+};
+
+// f32::total_cmp as an unsigned key (sample.rs:106-108): larger key = higher rank; +0 above -0.
+__device__ __forceinline__ uint32_t total_key(float x) {
+  uint32_t b = __float_as_uint(x);
+  return b ^ ((b >> 31) ? 0xFFFFFFFFu : 0x80000000u);
+}
+__device__ __forceinline__ float key_value(uint32_t k) {
+  return __uint_as_float((k & 0x80000000u) ? (k ^ 0x80000000u) : ~k);
+}
+// Rank order as one descending u64: key, then the lower id.
+__device__ __forceinline__ uint64_t pack(uint32_t key, uint32_t id) {
+  return ((uint64_t)key << 32) | (uint64_t)(~id);
+}
+__device__ __forceinline__ uint32_t packed_id(uint64_t p) { return ~(uint32_t)p; }
+__device__ __forceinline__ float packed_value(uint64_t p) { return key_value((uint32_t)(p >> 32)); }
+
+__device__ __forceinline__ bool is_finite_bits(float x) {
+  return (__float_as_uint(x) & 0x7F800000u) != 0x7F800000u;
+}
+
+// The history penalty for an id seen c >= 1 times, in f32, each operation rounded on its own.
+__device__ __forceinline__ float penalize(float x, uint32_t c, const RowParams& p) {
+  float t = x;
+  if (p.repetition != 1.0f) t = (x > 0.0f) ? __fdiv_rn(x, p.repetition) : __fmul_rn(x, p.repetition);
+  float d = __fmul_rn((float)c, p.frequency);
+  d = __fadd_rn(d, p.presence);
+  return __fsub_rn(t, d);
+}
+
+// xoshiro256** (rng.rs:26-37) and unit() (rng.rs:55-57).
+__device__ __forceinline__ uint64_t rotl64(uint64_t x, int k) { return (x << k) | (x >> (64 - k)); }
+__device__ __forceinline__ uint64_t rng_next(uint64_t s[4]) {
+  uint64_t out = rotl64(s[1] * 5, 7) * 9;
+  uint64_t t = s[1] << 17;
+  s[2] ^= s[0];
+  s[3] ^= s[1];
+  s[1] ^= s[2];
+  s[0] ^= s[3];
+  s[2] ^= t;
+  s[3] = rotl64(s[3], 45);
+  return out;
+}
+__device__ __forceinline__ double rng_unit(uint64_t s[4]) {
+  return (double)(rng_next(s) >> 11) * (1.0 / 9007199254740992.0);
+}
+
+// ---- wave64 / block reductions ----------------------------------------------------------------
+
+__device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
+  for (int o = 32; o > 0; o >>= 1) v = max(v, (uint32_t)__shfl_xor((int)v, o, kWave));
+  return v;
+}
+__device__ __forceinline__ uint32_t wave_min_u32(uint32_t v) {
+  for (int o = 32; o > 0; o >>= 1) v = min(v, (uint32_t)__shfl_xor((int)v, o, kWave));
+  return v;
+}
+__device__ __forceinline__ uint32_t wave_sum_u32(uint32_t v) {
+  for (int o = 32; o > 0; o >>= 1) v += (uint32_t)__shfl_xor((int)v, o, kWave);
+  return v;
+}
+__device__ __forceinline__ double wave_sum_f64(double v) {
+  for (int o = 32; o > 0; o >>= 1) v = __dadd_rn(v, __shfl_xor(v, o, kWave));
+  return v;
+}
+__device__ __forceinline__ uint64_t wave_max_u64(uint64_t v) {
+  for (int o = 32; o > 0; o >>= 1) {
+    uint64_t w = __shfl_xor(v, o, kWave);
+    v = w > v ? w : v;
+  }
+  return v;
+}
+
+// Greedy's order (sample.rs:9-17): a larger value by IEEE `>`, equal values to the lower index;
+// kNone loses to anything.
+__device__ __forceinline__ void greedy_merge(float& v, uint32_t& i, float v2, uint32_t i2) {
+  if (i2 == kNone) return;
+  if (i == kNone || v2 > v || (v2 == v && i2 < i)) {
+    v = v2;
+    i = i2;
+  }
+}
+__device__ __forceinline__ void wave_greedy(float& v, uint32_t& i) {
+  for (int o = 32; o > 0; o >>= 1) {
+    float v2 = __shfl_xor(v, o, kWave);
+    uint32_t i2 = (uint32_t)__shfl_xor((int)i, o, kWave);
+    greedy_merge(v, i, v2, i2);
+  }
+}
+
+// Block reductions through a small LDS array `red` (one slot per wave); all threads get the result.
+template <int NW>
+__device__ __forceinline__ uint32_t block_max_u32(uint32_t v, uint32_t* red) {
+  v = wave_max_u32(v);
+  const int w = threadIdx.x / kWave;
+  __syncthreads();
+  if ((threadIdx.x & (kWave - 1)) == 0) red[w] = v;
+  __syncthreads();
+  uint32_t r = red[0];
+  for (int k = 1; k < NW; ++k) r = max(r, red[k]);
+  return r;
+}
+template <int NW>
+__device__ __forceinline__ uint32_t block_min_u32(uint32_t v, uint32_t* red) {
+  v = wave_min_u32(v);
+  const int w = threadIdx.x / kWave;
+  __syncthreads();
+  if ((threadIdx.x & (kWave - 1)) == 0) red[w] = v;
+  __syncthreads();
+  uint32_t r = red[0];
+  for (int k = 1; k < NW; ++k) r = min(r, red[k]);
+  return r;
+}
+template <int NW>
+__device__ __forceinline__ uint32_t block_sum_u32(uint32_t v, uint32_t* red) {
+  v = wave_sum_u32(v);
+  const int w = threadIdx.x / kWave;
+  __syncthreads();
+  if ((threadIdx.x & (kWave - 1)) == 0) red[w] = v;
+  __syncthreads();
+  uint32_t r = 0;
+  for (int k = 0; k < NW; ++k) r += red[k];
+  return r;
+}
+template <int NW>
+__device__ __forceinline__ double block_sum_f64(double v, double* red) {
+  v = wave_sum_f64(v);
+  const int w = threadIdx.x / kWave;
+  __syncthreads();
+  if ((threadIdx.x & (kWave - 1)) == 0) red[w] = v;
+  __syncthreads();
+  double r = red[0];
+  for (int k = 1; k < NW; ++k) r = __dadd_rn(r, red[k]);
+  return r;
+}
+
+}  // namespace as_dev

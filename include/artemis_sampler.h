@@ -1,0 +1,137 @@
+/* MI355X (gfx950) token sampler and speculative verify: the C ABI.
+ *
+ * Replaces the reference's CPU sampler (crates/engine/src/sample.rs), its seed stream
+ * (crates/engine/src/rng.rs), the speculative accept loop (crates/engine/src/spec/step.rs:340-385)
+ * and the greedy draft kernel (crates/kernels/shaders/argmax_rows.comp) with HIP kernels that read
+ * the logits where the output head wrote them, in HBM.
+ *
+ * Conventions: device pointers are plain `void*`-compatible addresses on the context's device;
+ * host pointers are marked `host`. Every launch is ordered on the context's stream and nothing
+ * blocks the host except as_sync(). Calls return AS_OK or an AS_ERR_* code, and never throw;
+ * as_last_error() gives a one-line message. A context is thread-compatible: one per engine thread
+ * (the reference samples on its single worker thread, crates/engine/src/worker.rs:1-5).
+ */
+#ifndef ARTEMIS_SAMPLER_H
+#define ARTEMIS_SAMPLER_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define AS_OK 0
+#define AS_ERR_INVALID 1  /* a null pointer, a zero size, or sizes that do not fit together */
+#define AS_ERR_PARAMS 2   /* a row's sampling settings fail as_check (as Sampling::check refuses) */
+#define AS_ERR_CAPACITY 3 /* more rows, vocabulary or history than the context was made for */
+#define AS_ERR_HIP 4      /* a HIP runtime call failed */
+
+/* Per-row status written by as_sample / as_verify. */
+#define AS_ROW_OK 0u
+#define AS_ROW_NONFINITE 1u /* the row holds a NaN or an infinity: no token, the RNG is not advanced;
+                               kept_count holds the first such index (Error::NonFinite,
+                               crates/engine/src/decode.rs:439-444) */
+/* OR-ed into the status: the row was settled by the exact-order path (the reference's own
+ * summation order), because a fast-path decision fell within its rounding bound or its cut lay
+ * deeper than the fast path's candidates. Informational; the token is the same either way. */
+#define AS_ROW_EXACT_PATH 0x100u
+
+/* The draft id argmax_rows writes for a row with no finite value
+ * (crates/kernels/src/dispatch.rs:61, NO_DRAFT). */
+#define AS_NO_DRAFT 0xFFFFFFFFu
+
+/* How the sampler chooses: the reference's Sampling (sample.rs:38-49) plus two penalties it
+ * accepts and ignores today (crates/server/src/params.rs:298-328).
+ * temp 0 is greedy; top_k 0, top_p 1 and min_p 0 turn their filters off.
+ * Penalties act on every id in the row's history with count c >= 1, in f32:
+ *   t = (repetition != 1) ? (x > 0 ? x / repetition : x * repetition) : x
+ *   x' = t - ((float)c * frequency + presence)
+ * With repetition 1 and frequency 0 this is the reference's presence penalty, x - presence
+ * (sample.rs:315-321). */
+typedef struct {
+  float temp;
+  uint32_t top_k;
+  float top_p;
+  float min_p;
+  float presence;
+  float frequency;
+  float repetition;
+  uint32_t reserved; /* 0 */
+} as_sampling;
+
+typedef struct as_ctx as_ctx;
+
+/* Context: device ordinal, the HIP stream to order work on (NULL = the null stream), and the
+ * largest batch, vocabulary and per-row history it must take. The context owns all scratch. */
+int as_create(int device, void* hip_stream, uint32_t max_rows, uint32_t max_vocab,
+              uint32_t max_history, as_ctx** out);
+int as_destroy(as_ctx* ctx);
+const char* as_last_error(const as_ctx* ctx);
+/* Waits for the context's stream. */
+int as_sync(as_ctx* ctx);
+
+/* Sampling::check (sample.rs:71-94): 0 when the settings are usable, else AS_ERR_PARAMS and a
+ * one-line message naming the flag in msg (host). */
+int as_check(const as_sampling* s, char* msg, size_t cap);
+/* Rng::new (rng.rs:11-23): the 4-word xoshiro256** state for a seed (host). */
+void as_rng_seed(uint64_t seed, uint64_t state[4]);
+
+/* One batch of independent rows: Sampler::sample (sample.rs:122-153) on each.
+ * Replaces Picker::pick's self.sampler.sample(logits) (crates/engine/src/turn.rs:346) and the
+ * non-finite check before it (sample.rs:22-34 via decode.rs:437-447). */
+typedef struct {
+  const float* logits;          /* [n_rows][row_stride] f32, n_vocab used per row */
+  uint64_t row_stride;          /* in floats, >= n_vocab; 0: every row reads the same row */
+  uint32_t n_vocab;
+  uint32_t n_rows;
+  const uint32_t* hist_offsets; /* [n_rows + 1] CSR offsets into hist_ids, or NULL: no history */
+  const uint32_t* hist_ids;     /* penalty history per row: ids the sampler returned before */
+  uint64_t* rng_state;          /* [n_rows][4] xoshiro256** states, advanced by one draw per
+                                   row that draws (temp > 0 and finite) */
+  uint32_t* tokens;             /* [n_rows] out */
+  uint32_t* status;             /* [n_rows] out: AS_ROW_* */
+  uint32_t* kept_count;         /* [n_rows] out or NULL: tokens the draw chose among */
+  uint32_t* kept_ids;           /* [n_rows][kept_cap] out or NULL: kept ids in rank order */
+  double* kept_probs;           /* [n_rows][kept_cap] out or NULL: w_i / sum(w) at temp */
+  uint32_t kept_cap;
+} as_batch;
+
+/* params: host array [n_rows]. */
+int as_sample(as_ctx* ctx, const as_batch* batch, const as_sampling* params);
+
+/* Speculative verify (spec/step.rs:340-385 with Picker's stop rule, turn.rs:344-352): row i of
+ * rows ([k+1][row_stride]) is sampled as the sampler would after emitting drafts[0..i), on the
+ * i-th draw of the stream, so all k+1 rows run at once. read = 1 + the first i whose pick is a stop
+ * id or differs from drafts[i] (k+1 when none does); accepted = read - 1; bonus = picks[read-1].
+ * The stream advances by `read` draws (when temp > 0).
+ * history/hist_len: the request's history (device); stop_ids/n_stop (device, may be 0).
+ * out: picks [k+1]; result [4] = {read, accepted, bonus, flags} with flags bit 0 = stopped on a
+ * stop id, bit 1 = a row was non-finite (read stops before it), bit 8 = the exact-order path ran. */
+int as_verify(as_ctx* ctx, const float* rows, uint64_t row_stride, uint32_t n_vocab,
+              const uint32_t* drafts, uint32_t k, const uint32_t* history, uint32_t hist_len,
+              const uint32_t* stop_ids, uint32_t n_stop, const as_sampling* params,
+              uint64_t* rng_state, uint32_t* picks, uint32_t* result);
+
+/* argmax_rows (crates/kernels/src/dispatch.rs:121-153, shaders/argmax_rows.comp): for each of
+ * n_rows rows, ids[slot + r] = the largest finite value's index (ties to the lower index) or
+ * AS_NO_DRAFT, rows_out[slot + r] = embd + id * row_bytes (id 0 for AS_NO_DRAFT). */
+int as_argmax_rows(as_ctx* ctx, const float* logits, uint64_t row_stride, uint32_t n,
+                   uint32_t n_rows, uint32_t* ids, uint64_t* rows_out, uint64_t embd,
+                   uint32_t row_bytes, uint32_t slot);
+
+/* Profiling: while enabled, each as_sample / as_verify records HIP events on the context's stream
+ * around its scan and finish kernels (no counterpart in the reference, which samples on the CPU;
+ * for benchmarks). as_profile_read waits for the stream and returns the summed kernel times of the
+ * calls since as_profile and how many calls there were, then starts a new count. */
+int as_profile(as_ctx* ctx, int enable);
+int as_profile_read(as_ctx* ctx, double* scan_ms, double* finish_ms, uint32_t* calls);
+
+/* Diagnostics: y[i] = exp(x[i]) on the GPU with the sampler's f64 exp (device arrays). */
+int as_debug_exp(as_ctx* ctx, const double* x, double* y, uint32_t n);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* ARTEMIS_SAMPLER_H */

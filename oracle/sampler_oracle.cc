@@ -6,6 +6,8 @@
 #include "sampler_oracle.h"
 
 #include <algorithm>
+#include <atomic>
+#include <thread>
 #include <cmath>
 #include <cstdio>
 #include <cstring>
@@ -552,5 +554,37 @@ float oc_logprobs(const float* logits, size_t n, uint32_t token, uint32_t top, u
 
 double oc_exp(double x) { return std::exp(x); }
 double oc_log(double x) { return std::log(x); }
+void oc_exp_array(const double* x, double* y, size_t n) {
+  for (size_t i = 0; i < n; ++i) y[i] = std::exp(x[i]);
+}
+
+void oc_sample_rows(const oc_params* params, const uint64_t* seeds, const float* logits,
+                    size_t stride, size_t n, size_t rows, const uint32_t* hist_off,
+                    const uint32_t* hist_ids, unsigned threads, uint32_t* tokens,
+                    uint64_t* rng_out) {
+  std::atomic<size_t> next{0};
+  auto work = [&]() {
+    for (;;) {
+      const size_t r = next.fetch_add(1);
+      if (r >= rows) break;
+      const float* row = logits + r * stride;
+      oc_sampler smp;
+      smp.s = params[r];
+      rng_new(seeds[r], smp.rng);
+      if (hist_off)
+        for (uint32_t h = hist_off[r]; h < hist_off[r + 1]; ++h) smp.seen[hist_ids[h]] += 1;
+      // The engine's check before the sampler (decode.rs:437-447, sample.rs:22-34).
+      tokens[r] = oc_first_non_finite(row, n) >= 0 ? 0xFFFFFFFFu : sample(smp, row, n);
+      if (rng_out) std::memcpy(rng_out + 4 * r, smp.rng, 32);
+    }
+  };
+  if (threads <= 1) {
+    work();
+  } else {
+    std::vector<std::thread> pool;
+    for (unsigned t = 0; t < threads; ++t) pool.emplace_back(work);
+    for (auto& t : pool) t.join();
+  }
+}
 
 }  // extern "C"

@@ -85,6 +85,17 @@ float oc_logprobs(const float* logits, size_t n, uint32_t token, uint32_t top, u
 // The exact f64 weight the sampler uses, from the host libm: exp(x).
 double oc_exp(double x);
 double oc_log(double x);
+void oc_exp_array(const double* x, double* y, size_t n);
+
+// A batch of independent rows, each a fresh Sampler(params[r], seeds[r]) with history
+// hist_ids[hist_off[r] .. hist_off[r+1]) taking one draw from row r (logits + r * stride; stride 0
+// shares one row). Rows are spread over `threads` host threads (1 = this thread). tokens[r] gets
+// the draw, or UINT32_MAX for a row holding a non-finite value (the engine refuses such rows
+// before sampling). rng_out, when given, gets each row's state after the draw ([rows][4]).
+void oc_sample_rows(const oc_params* params, const uint64_t* seeds, const float* logits,
+                    size_t stride, size_t n, size_t rows, const uint32_t* hist_off,
+                    const uint32_t* hist_ids, unsigned threads, uint32_t* tokens,
+                    uint64_t* rng_out);
 
 #ifdef __cplusplus
 }

@@ -98,6 +98,9 @@ def lib():
         L.oc_exp.restype = C.c_double
         L.oc_log.argtypes = [C.c_double]
         L.oc_log.restype = C.c_double
+        L.oc_exp_array.argtypes = [f64p, f64p, C.c_size_t]
+        L.oc_sample_rows.argtypes = [C.POINTER(Params), u64p, f32p, C.c_size_t, C.c_size_t,
+                                     C.c_size_t, u32p, u32p, C.c_uint, u32p, u64p]
         _lib = L
     return _lib
 
@@ -255,3 +258,30 @@ def host_exp(x: float) -> float:
 
 def host_log(x: float) -> float:
     return lib().oc_log(x)
+
+
+def exp_array(x):
+    x = np.ascontiguousarray(x, dtype=np.float64)
+    y = np.empty_like(x)
+    lib().oc_exp_array(x.ctypes.data_as(f64p), y.ctypes.data_as(f64p), x.size)
+    return y
+
+
+def sample_rows(rows_params, seeds, logits, hist_off=None, hist_ids=None, threads=1, shared=False):
+    """oc_sample_rows: one fresh-sampler draw per row. Returns (tokens u32, rng states [rows, 4])."""
+    logits = np.ascontiguousarray(logits, dtype=np.float32)
+    n = logits.shape[-1]
+    rows = len(rows_params)
+    P = (Params * rows)(*[params(**p) if isinstance(p, dict) else p for p in rows_params])
+    s = np.ascontiguousarray(seeds, dtype=np.uint64)
+    toks = np.zeros(rows, np.uint32)
+    rng = np.zeros((rows, 4), np.uint64)
+    if hist_off is not None:
+        ho = np.ascontiguousarray(hist_off, dtype=np.uint32)
+        hi = np.ascontiguousarray(hist_ids if len(hist_ids) else [0], dtype=np.uint32)
+        hop, hip = ho.ctypes.data_as(u32p), hi.ctypes.data_as(u32p)
+    else:
+        hop = hip = None
+    lib().oc_sample_rows(P, s.ctypes.data_as(u64p), logits.ctypes.data_as(f32p), 0 if shared else n, n,
+                         rows, hop, hip, threads, toks.ctypes.data_as(u32p), rng.ctypes.data_as(u64p))
+    return toks, rng

@@ -1,0 +1,75 @@
+"""The C-ABI library without a GPU: it loads, exports every entry point include/artemis_sampler.h
+declares, and its host-only functions (as_check, as_rng_seed) agree with the oracle."""
+import ctypes as C
+import os
+import re
+
+import pytest
+
+import oracle_lib
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "artemis_sampler.h")
+
+
+@pytest.fixture(scope="module")
+def L():
+    from artemis_amd import sampler
+    if not os.path.exists(sampler.LIB_PATH):
+        from artemis_amd import build
+        build.build()
+    return sampler.lib()
+
+
+def declared():
+    text = open(HEADER).read()
+    return sorted(set(re.findall(r"^\s*(?:int|void|const char\*)\s+(as_\w+)\(", text, re.M)))
+
+
+def test_the_library_exports_every_declared_entry_point(L):
+    names = declared()
+    assert len(names) >= 10, names
+    for name in names:
+        assert hasattr(L, name), name
+
+
+def test_check_matches_the_oracle(L):
+    from artemis_amd import Sampling
+    nan, inf = float("nan"), float("inf")
+    cases = [
+        dict(), dict(temp=-0.1), dict(temp=nan), dict(temp=inf), dict(top_p=0.0), dict(top_p=1.1),
+        dict(top_p=nan), dict(min_p=-0.1), dict(min_p=1.5), dict(presence=nan), dict(presence=-inf),
+        dict(frequency=nan), dict(repetition=0.0), dict(repetition=-1.0), dict(repetition=inf),
+        dict(temp=0.0, top_k=2, top_p=0.1, min_p=0.9),
+    ]
+    for kw in cases:
+        want = oracle_lib.check(**{**oracle_lib.PLAIN, **kw})
+        s = Sampling(temp=kw.get("temp", 1.0), top_k=kw.get("top_k", 0), top_p=kw.get("top_p", 1.0),
+                     min_p=kw.get("min_p", 0.0), presence_penalty=kw.get("presence", 0.0),
+                     frequency_penalty=kw.get("frequency", 0.0), repetition_penalty=kw.get("repetition", 1.0))
+        if want is None:
+            s.check()
+        else:
+            with pytest.raises(ValueError) as e:
+                s.check()
+            assert str(e.value) == want
+
+
+def test_defaults_are_productions():
+    from artemis_amd import Sampling
+    assert Sampling.DEFAULT == Sampling(0.6, 20, 0.95, 0.0, 0.0)
+    assert Sampling.GREEDY == Sampling(0.0, 0, 1.0, 0.0, 0.0)
+    Sampling.DEFAULT.check()
+    Sampling.GREEDY.check()
+
+
+def test_rng_seed_matches_the_oracle(L):
+    from artemis_amd import rng_state
+    for seed in [0, 1, 7, 1234, 2**64 - 1]:
+        assert rng_state(seed) == oracle_lib.Rng(seed).state()
+
+
+def test_calls_without_a_context_fail_cleanly(L):
+    assert L.as_sample(None, None, None) != 0
+    assert L.as_sync(None) != 0
+    assert L.as_destroy(None) != 0

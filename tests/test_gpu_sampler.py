@@ -1,0 +1,349 @@
+"""Parity of the HIP sampler with the CPU oracle on the GPU, through the C ABI.
+
+Token ids, kept counts, RNG states and accepted-draft counts must be bit-exact; kept-set
+probabilities within 1e-5 relative (the unfiltered fast path divides by a total that is itself
+within ~1e-11 of the reference's, every other path by the same f64 value).
+"""
+import numpy as np
+import pytest
+
+import oracle_lib as O
+
+pytestmark = pytest.mark.gpu
+
+torch = pytest.importorskip("torch")
+
+PROB_RTOL = 1e-5
+VOCAB = 248_320
+
+
+@pytest.fixture(scope="module")
+def ctx():
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU")
+    from artemis_amd import Context
+    c = Context(max_rows=1024, max_vocab=VOCAB)
+    yield c
+    c.close()
+
+
+def as_sampling(p):
+    from artemis_amd import Sampling
+    return Sampling(p["temp"], p["top_k"], p["top_p"], p["min_p"], p.get("presence", 0.0),
+                    p.get("frequency", 0.0), p.get("repetition", 1.0))
+
+
+def csr(histories, rows):
+    hs = histories if histories is not None else [np.zeros(0, np.uint32)] * rows
+    off = np.zeros(rows + 1, np.int32)
+    off[1:] = np.cumsum([len(h) for h in hs])
+    ids = np.concatenate([np.asarray(h, np.uint32) for h in hs]) if off[-1] else np.zeros(0, np.uint32)
+    return off, ids.astype(np.int32)
+
+
+def gpu_batch(ctx, logits, params, seeds, histories=None, kept_cap=0):
+    from artemis_amd import states_tensor
+    rows = len(params)
+    dev = torch.device("cuda:0")
+    lg = torch.from_numpy(np.ascontiguousarray(logits, np.float32)).to(dev)
+    if lg.dim() == 1:
+        lg = lg.view(1, -1)
+    stride = 0 if lg.shape[0] == 1 and rows > 1 else lg.stride(0)
+    off, ids = csr(histories, rows)
+    rng = states_tensor(seeds, dev)
+    tok, st, kc, ki, kp = ctx.sample_batch(lg, [as_sampling(p) for p in params], rng,
+                                           torch.from_numpy(off).to(dev), torch.from_numpy(ids).to(dev),
+                                           kept_cap=kept_cap, row_stride=stride, n_vocab=lg.shape[1])
+    torch.cuda.synchronize()
+    return dict(tokens=tok.cpu().numpy().astype(np.uint32), status=st.cpu().numpy().astype(np.uint32),
+                kept=kc.cpu().numpy().astype(np.uint32), kept_ids=ki.cpu().numpy().astype(np.uint32),
+                kept_probs=kp.cpu().numpy(), rng=rng.cpu().numpy().view(np.uint64))
+
+
+def oracle_rows(logits, params, seeds, histories=None, kept_cap=0):
+    """Per row: a fresh oracle Sampler with the history, one draw; token, kept set, RNG state."""
+    out = []
+    lg = np.asarray(logits, np.float32)
+    for r, p in enumerate(params):
+        row = lg[0] if lg.ndim == 1 or lg.shape[0] == 1 else lg[r]
+        row = lg if lg.ndim == 1 else row
+        s = O.Sampler(seeds[r], **p)
+        if histories is not None and len(histories[r]):
+            s.add_history(histories[r])
+        if O.first_non_finite(row) is not None:
+            out.append(None)
+            continue
+        t = s.sample(row)
+        ids, probs = s.last_kept(kept_cap if kept_cap else 1)
+        out.append(dict(token=t, kept_ids=ids, kept_probs=probs, path=s.last_path(),
+                        rng=s.rng_state(), n_kept=len(s.last_kept(1 << 30)[0])))
+    return out
+
+
+def check_rows(g, want, params, kept_cap=0, label=""):
+    for r, w in enumerate(want):
+        if w is None:
+            assert g["status"][r] & 1, (label, r)
+            continue
+        assert g["status"][r] & 1 == 0, (label, r, g["status"][r])
+        assert g["tokens"][r] == w["token"], (label, r, params[r], g["tokens"][r], w["token"], g["status"][r])
+        assert list(g["rng"][r]) == w["rng"], (label, r, "rng")
+        cuts = params[r]["top_p"] < 1 or params[r]["min_p"] > 0
+        if params[r]["temp"] > 0 and not (w["path"] == 4 and not cuts):
+            assert g["kept"][r] == w["n_kept"], (label, r, params[r], g["kept"][r], w["n_kept"])
+        if kept_cap and params[r]["temp"] > 0:
+            m = min(kept_cap, len(w["kept_ids"]))
+            assert (g["kept_ids"][r][:m] == w["kept_ids"][:m]).all(), (label, r)
+            np.testing.assert_allclose(g["kept_probs"][r][:m], w["kept_probs"][:m], rtol=PROB_RTOL)
+
+
+def test_gpu_exp_is_the_hosts(ctx):
+    rng = np.random.default_rng(11)
+    parts = [-rng.random(400000) * 40, -rng.random(200000) * 800, (rng.random(200000) - 0.5) * 4,
+             -708 - rng.random(100000) * 40, rng.integers(0, 2**64, 100000, dtype=np.uint64).view(np.float64),
+             np.array([0.0, -0.0, np.inf, -np.inf, np.nan, 709.7, -745.2, -745.1, 1e-300, -1e-300])]
+    x = np.concatenate(parts)
+    want = O.exp_array(x)
+    got = ctx.debug_exp(torch.from_numpy(x).cuda()).cpu().numpy()
+    same = (got.view(np.uint64) == want.view(np.uint64)) | (np.isnan(got) & np.isnan(want))
+    assert same.all(), x[~same][:5]
+
+
+GRID = []
+for temp in [0.0, 0.6, 1.0, 5.0, 1e-6]:
+    for top_k in [0, 1, 2, 20, 300]:
+        for top_p, min_p in [(1.0, 0.0), (0.95, 0.0), (0.5, 0.05), (0.99999, 0.0), (1.0, 1.0), (0.9, 0.001)]:
+            GRID.append(dict(temp=temp, top_k=top_k, top_p=top_p, min_p=min_p))
+
+
+def random_logits(rng, n, shape):
+    x = (rng.random(n) * 12 - 6).astype(np.float32)
+    if shape == 1:  # heavy ties
+        x = np.round(x * 2) / 2
+    elif shape == 2:  # signed zeros on top
+        i = np.arange(n)
+        x = np.where(i % 3 == 0, np.where(i % 2 == 0, 0.0, -0.0), -np.abs(x) - 0.5).astype(np.float32)
+    return x.astype(np.float32)
+
+
+@pytest.mark.parametrize("n", [1, 2, 5, 63, 64, 65, 300, 5000, 8193, 20000])
+def test_small_rows_match_the_oracle(ctx, n):
+    rng = np.random.default_rng(n)
+    params, logits, seeds, hists = [], [], [], []
+    for i, p in enumerate(GRID):
+        shape = i % 3
+        q = dict(p)
+        if i % 4 == 1:
+            q.update(presence=1.5)
+        if i % 4 == 2:
+            q.update(presence=0.5, frequency=0.3, repetition=1.05)
+        params.append(q)
+        logits.append(random_logits(rng, n, shape))
+        seeds.append(i)
+        hists.append(rng.integers(0, n, size=min(n, 17)).astype(np.uint32) if i % 4 else np.zeros(0, np.uint32))
+    logits = np.stack(logits)
+    g = gpu_batch(ctx, logits, params, seeds, hists, kept_cap=64)
+    want = oracle_rows(logits, params, seeds, hists, kept_cap=64)
+    check_rows(g, want, params, kept_cap=64, label=f"n={n}")
+
+
+def test_nonfinite_rows_report_their_first_index_and_keep_the_stream(ctx):
+    n = 20000
+    rng = np.random.default_rng(3)
+    rows = np.tile((rng.standard_normal(n) * 2.5).astype(np.float32), (6, 1))
+    plants = [(0, np.nan), (1023, np.inf), (1024, -np.inf), (8191, np.nan), (n - 1, -np.inf)]
+    for r, (i, v) in enumerate(plants):
+        rows[r, i] = v
+        if r == 3:
+            rows[r, 15000] = np.nan  # two of them: the first is named
+    params = [dict(temp=0.6, top_k=20, top_p=0.95, min_p=0.0)] * 6
+    g = gpu_batch(ctx, rows, params, list(range(6)), kept_cap=0)
+    for r, (i, _) in enumerate(plants):
+        assert g["status"][r] == 1 and g["kept"][r] == i, (r, g["status"][r], g["kept"][r])
+        assert list(g["rng"][r]) == O.Rng(r).state(), "a refused row draws nothing"
+    assert g["status"][5] == 0
+
+
+def test_config1_greedy(ctx):
+    from artemis_amd import workloads
+    w = workloads.config1()
+    g = gpu_batch(ctx, w.logits, [dict(temp=0.0, top_k=0, top_p=1.0, min_p=0.0)], [0])
+    assert g["tokens"][0] == O.greedy(w.logits[0])
+
+
+def test_config2_thousand_seeds(ctx):
+    from artemis_amd import workloads
+    w = workloads.config2()
+    params = [dict(temp=0.6, top_k=20, top_p=0.95, min_p=0.0)] * len(w.seeds)
+    g = gpu_batch(ctx, w.logits, params, w.seeds, kept_cap=20)
+    want = oracle_rows(w.logits, params, w.seeds, kept_cap=20)
+    check_rows(g, want, params, kept_cap=20, label="config2")
+
+
+def test_config3_penalised(ctx):
+    from artemis_amd import workloads
+    w = workloads.config3(draws=64)
+    params = [dict(temp=0.7, top_k=40, top_p=0.9, min_p=0.05, presence=0.5, frequency=0.3, repetition=1.05)] * 64
+    g = gpu_batch(ctx, w.logits, params, w.seeds, w.histories, kept_cap=40)
+    want = oracle_rows(w.logits, params, w.seeds, w.histories, kept_cap=40)
+    check_rows(g, want, params, kept_cap=40, label="config3")
+
+
+def test_config5_batch(ctx):
+    from artemis_amd import workloads
+    w = workloads.config5()
+    params = [dict(temp=p.temp, top_k=p.top_k, top_p=p.top_p, min_p=p.min_p, presence=p.presence,
+                   frequency=p.frequency, repetition=p.repetition) for p in w.params]
+    g = gpu_batch(ctx, w.logits, params, w.seeds, w.histories)
+    off, ids = w.hist_csr()
+    want, rng = O.sample_rows(params, w.seeds, w.logits, off, ids, threads=8)
+    bad = np.nonzero(g["tokens"] != want)[0]
+    assert len(bad) == 0, [(int(r), params[r], int(g["tokens"][r]), int(want[r])) for r in bad[:5]]
+    assert (g["rng"] == rng).all()
+
+
+def test_whole_vocabulary_plants(ctx):
+    # sample.rs:807-885's plants at the model's vocabulary: ties with the k-th best in later runs,
+    # penalised ids in low runs, top values on run edges, signed zeros, all equal, spread highs.
+    N = VOCAB
+    gen = np.random.default_rng(77)
+    base = (gen.random(N).astype(np.float32) * 4 - 8).astype(np.float32)
+    params, rows, hists, seeds = [], [], [], []
+    for plant in range(5):
+        l = base.copy()
+        if plant == 0:
+            for i in range(20):
+                l[i * 7] = 10.0 - i * 0.25
+            for i in [1024, 1087, 1151, 200000, N - 1]:
+                l[i] = 10.0 - 19 * 0.25
+        elif plant == 1:
+            for j, i in enumerate([63, 64, 127, 128, 4095, 4096, N - 2, N - 1]):
+                l[i] = 12.0 - j
+        elif plant == 2:
+            l[::9973] = 0.0
+            l[9973::2 * 9973] = -0.0
+        elif plant == 3:
+            l[:] = 1.5
+        else:
+            l[::1009] = 5.0 + gen.random(len(l[::1009])).astype(np.float32)
+        for k in [1, 2, 20, 256, 0, 1000]:
+            for pen in [0.0, 1.5, -6.0]:
+                params.append(dict(temp=0.6, top_k=k, top_p=0.95, min_p=0.0, presence=pen))
+                rows.append(l)
+                hists.append(np.array([5, 640, 100003, N - 1], np.uint32))
+                seeds.append(3 + len(seeds))
+    rows = np.stack(rows)
+    g = gpu_batch(ctx, rows, params, seeds, hists, kept_cap=32)
+    want = oracle_rows(rows, params, seeds, hists, kept_cap=32)
+    check_rows(g, want, params, kept_cap=32, label="plants")
+
+
+def test_argmax_rows_matches_its_twin(ctx):
+    # kernels/tests/gpu_kernels.rs:1565-1618.
+    gen = np.random.default_rng(41)
+    embd, row_bytes = 0x3_0000_1000, 1 << 20
+    for n in [512, VOCAB, 1001]:
+        rows = (gen.random((6, n)) * 16 - 8).astype(np.float32)
+        m = np.float32(9.0)
+        for i in [n - 1, n // 2, 3, 3 + min(1024, n - 4)]:
+            rows[1, i] = m
+        rows[2, 0] = np.nan
+        rows[2, n // 3] = np.nan
+        rows[2, 7] = 8.5
+        rows[3, 5] = np.inf
+        rows[3, 9] = -np.inf
+        rows[3, n - 2] = 8.25
+        rows[4, :] = np.nan
+        rows[5, :] = np.where(np.arange(n) % 2 == 0, np.inf, -np.inf)
+        rows[0, n - 1] = rows[0].max()
+        ids = torch.full((8,), 0x2AAAAAAA, dtype=torch.int32, device="cuda")
+        out = torch.full((8,), 0x3BBBBBBB, dtype=torch.int64, device="cuda")
+        ctx.argmax_rows(torch.from_numpy(rows).cuda(), ids, out, embd, row_bytes, slot=1)
+        torch.cuda.synchronize()
+        gi = ids.cpu().numpy().astype(np.uint32)
+        go = out.cpu().numpy().view(np.uint64)
+        for r in range(6):
+            want = O.argmax_row(rows[r])
+            assert gi[1 + r] == (0xFFFFFFFF if want is None else want), (n, r)
+            assert go[1 + r] == embd + (0 if want is None else want) * row_bytes, (n, r)
+        assert gi[0] == 0x2AAAAAAA and gi[7] == 0x2AAAAAAA and go[0] == 0x3BBBBBBB and go[7] == 0x3BBBBBBB
+
+
+def gpu_verify(ctx, rows, drafts, p, seed, history=(), stops=()):
+    from artemis_amd import states_tensor
+    dev = torch.device("cuda:0")
+    rng = states_tensor([seed], dev)
+    picks, result = ctx.verify(torch.from_numpy(np.ascontiguousarray(rows, np.float32)).to(dev),
+                               torch.tensor(np.asarray(drafts, np.int64).astype(np.int32), device=dev),
+                               as_sampling(p), rng,
+                               torch.tensor(np.asarray(history, np.int64).astype(np.int32), device=dev) if len(history) else None,
+                               torch.tensor(np.asarray(stops, np.int64).astype(np.int32), device=dev) if len(stops) else None)
+    torch.cuda.synchronize()
+    return picks.cpu().numpy().astype(np.uint32), result.cpu().numpy().astype(np.uint32), rng.cpu().numpy().view(np.uint64)[0]
+
+
+def test_verify_matches_the_plain_loop(ctx):
+    gen = np.random.default_rng(9)
+    n = 3000
+    cases = 0
+    for p in [dict(temp=0.0, top_k=0, top_p=1.0, min_p=0.0), dict(temp=0.6, top_k=20, top_p=0.95, min_p=0.0),
+              dict(temp=0.8, top_k=0, top_p=0.9, min_p=0.02, presence=0.5),
+              dict(temp=0.7, top_k=40, top_p=0.9, min_p=0.05, presence=0.5, frequency=0.3, repetition=1.05)]:
+        for k in [0, 1, 3, 5, 15]:
+            for mode in range(3):
+                rows = (gen.standard_normal((k + 1, n)) * 2.5).astype(np.float32)
+                rows[np.arange(k + 1), gen.integers(n, size=k + 1)] += 6.0
+                hist = gen.integers(0, n, size=30).astype(np.uint32)
+                # Drafts: all equal to the plain loop's picks, half of them, or none.
+                o = O.Sampler(77, **p)
+                o.add_history(hist)
+                truth = []
+                for i in range(k + 1):
+                    truth.append(o.sample(rows[i]))
+                drafts = np.array(truth[:k], np.uint32)
+                if mode == 1 and k:
+                    drafts[k // 2] = (drafts[k // 2] + 1) % n
+                if mode == 2 and k:
+                    drafts[:] = (drafts + 7) % n
+                stops = [int(truth[2])] if (mode == 0 and k >= 3) else []
+                want = O.Sampler(77, **p)
+                want.add_history(hist)
+                wpicks, wacc, wstop = want.verify(rows, drafts, stops)
+                picks, result, rng = gpu_verify(ctx, rows, drafts, p, 77, hist, stops)
+                read = len(wpicks)
+                assert result[0] == read and result[1] == wacc, (p, k, mode, result, wpicks)
+                assert (picks[:read] == np.array(wpicks, np.uint32)).all(), (p, k, mode)
+                assert result[2] == wpicks[-1] and bool(result[3] & 1) == wstop
+                assert list(rng) == want.rng_state(), (p, k, mode, "rng")
+                cases += 1
+    assert cases == 60
+
+
+def test_config4_verify(ctx):
+    from artemis_amd import workloads
+    w = workloads.config4()
+    p = dict(temp=0.6, top_k=0, top_p=0.95, min_p=0.0)
+    o = O.Sampler(w.seeds[0], **p)
+    wpicks, wacc, _ = o.verify(w.logits, w.drafts)
+    picks, result, rng = gpu_verify(ctx, w.logits, w.drafts, p, w.seeds[0])
+    assert result[0] == len(wpicks) and result[1] == wacc
+    assert (picks[: len(wpicks)] == np.array(wpicks, np.uint32)).all()
+    assert list(rng) == o.rng_state()
+
+
+def test_sampler_object_follows_the_reference_sequence(ctx):
+    from artemis_amd import Sampler, Sampling
+    # sample.rs:563-578: greedy with presence 0.5 over [1.0, 0.9, 0.0] gives [0, 1, 0].
+    l = torch.tensor([1.0, 0.9, 0.0], device="cuda")
+    s = Sampler(Sampling(0.0, 0, 1.0, 0.0, 0.5), 0)
+    assert [s.sample(l), s.sample(l), s.sample(l)] == [0, 1, 0]
+    # A run of draws with the history growing, against the oracle's Sampler.
+    gen = np.random.default_rng(4)
+    base = (gen.random(3000) * 12 - 6).astype(np.float32)
+    for top_k in [0, 20]:
+        p = dict(temp=0.8, top_k=top_k, top_p=0.9, min_p=0.0, presence=0.7)
+        a = Sampler(as_sampling(p), 3)
+        b = O.Sampler(3, **p)
+        lt = torch.from_numpy(base).cuda()
+        for step in range(30):
+            assert a.sample(lt) == b.sample(base), (top_k, step)
