@@ -68,11 +68,13 @@ RowParams make_row(const as_sampling& s, uint32_t n, uint32_t n_seg) {
   r.repetition = s.repetition;
   r.ln_min_p = s.min_p > 0.0f ? std::log((double)s.min_p) : 0.0;
   r.flags = penalties_on(s) ? as_dev::kFlagPenalties : 0u;
+  const uint32_t cap_all = as_launch::kCandCap / n_seg;
+  r.cap = cap_all < (uint32_t)as_launch::kPartialCand ? cap_all : (uint32_t)as_launch::kPartialCand;
   if (s.temp <= 0.0f) {
     r.mode = as_dev::kModeGreedy;
     r.cand = 0;
   } else if (s.top_k > 0 && s.top_k < n) {
-    if (s.top_k <= (uint32_t)as_launch::kPartialCand && (uint64_t)s.top_k * n_seg <= as_launch::kCandCap) {
+    if (s.top_k <= r.cap) {
       r.mode = as_dev::kModeTopK;
       r.cand = s.top_k;
     } else {
@@ -81,8 +83,8 @@ RowParams make_row(const as_sampling& s, uint32_t n, uint32_t n_seg) {
     }
   } else {
     r.mode = as_dev::kModePartial;
-    uint32_t c = as_launch::kCandCap / n_seg;
-    r.cand = c < (uint32_t)as_launch::kPartialCand ? c : (uint32_t)as_launch::kPartialCand;
+    // The rank among the segment's 256 per-thread maxima that sets its candidate threshold.
+    r.cand = r.cap < (uint32_t)as_launch::kPartialRank ? r.cap : (uint32_t)as_launch::kPartialRank;
     if (s.top_p < 1.0f)
       r.flags |= as_dev::kFlagSumTop;
     else if (!(s.min_p > 0.0f))

@@ -39,6 +39,9 @@ struct Shared {
   uint32_t base[256];
   uint32_t tot[256];
   uint32_t seg_off[kMaxSeg + 1];
+  SegStats seg[kMaxSeg];
+  uint32_t bcnt[1024];
+  uint32_t bstart[1024];
   uint32_t red_u[kWaves];
   double red_d[kWaves];
   // Row scalars.
@@ -240,7 +243,7 @@ __device__ void exact_row(const FinishArgs& a, const RowParams& p, uint32_t row,
 
   uint32_t keep = 0;
   bool unfiltered = false;
-  if (p.mode == kModeExactTopK) {
+  if (p.mode == kModeExactTopK || p.mode == kModeTopK) {
     const uint32_t k = p.top_k;
     keep = k;
     if (p.top_p < 1.0f) {
@@ -369,15 +372,159 @@ __device__ void exact_row(const FinishArgs& a, const RowParams& p, uint32_t row,
   }
 }
 
+// --- the fast path's sort and certified draw --------------------------------------------------
+
+constexpr uint32_t kBuckets = 1024;
+
+// Exclusive prefix sum of one u32 per thread over the block; *total gets the sum.
+__device__ uint32_t block_exclusive_scan_u32(uint32_t x, uint32_t* wave_tot, uint32_t* total) {
+  const int lane = threadIdx.x & (kWave - 1), w = threadIdx.x / kWave;
+  uint32_t incl = x;
+  for (int o = 1; o < kWave; o <<= 1) {
+    const uint32_t y = (uint32_t)__shfl_up((int)incl, o, kWave);
+    if (lane >= o) incl += y;
+  }
+  __syncthreads();
+  if (lane == kWave - 1) wave_tot[w] = incl;
+  __syncthreads();
+  uint32_t before = 0, all = 0;
+  for (int k = 0; k < kWaves; ++k) {
+    if (k < w) before += wave_tot[k];
+    all += wave_tot[k];
+  }
+  *total = all;
+  return before + incl - x;
+}
+
+// The smallest f32 whose f64 value is >= f (IEEE, so a floor of 0 admits -0 as well).
+__device__ __forceinline__ float floor_f32(double f) {
+  float x = __double2float_rn(f);
+  if ((double)x < f) x = nextafterf(x, __builtin_inff());
+  if (x == 0.0f) x = -0.0f;
+  return x;
+}
+
+// Sorts the candidates sh.sk[0..total) whose packed rank is >= R into rank order (packed
+// descending) and returns how many there are, P. Only the first `need` ranks are guaranteed placed:
+// a bucket that starts at or past `need` is left unsorted. A bucket sort: buckets by distance from
+// the row's largest key kmax, then each value's place inside its bucket by counting the bucket's
+// values above it (quadratic in a bucket's size, which heavy ties make large).
+__device__ __forceinline__ uint32_t sort_candidates(Shared& sh, uint32_t total, uint64_t R,
+                                                    uint32_t kmax, uint32_t need) {
+  const uint32_t tid = threadIdx.x;
+  uint64_t* out2 = reinterpret_cast<uint64_t*>(sh.wd);
+  constexpr int kPerT = kCap / kThreads;
+  uint64_t xs[kPerT];
+  uint32_t kmin = 0xFFFFFFFFu, mine = 0;
+#pragma unroll
+  for (int q = 0; q < kPerT; ++q) {
+    const uint32_t i = tid + q * kThreads;
+    xs[q] = (i < total) ? sh.sk[i] : 0ull;
+    if (i < total && xs[q] >= R) {
+      kmin = min(kmin, (uint32_t)(xs[q] >> 32));
+      ++mine;
+    }
+  }
+  kmin = block_min_u32<kWaves>(kmin, sh.red_u);
+  const uint32_t P = block_sum_u32<kWaves>(mine, sh.red_u);
+  const uint32_t range = kmax - kmin;
+  uint32_t shift = 0;
+  while ((range >> shift) >= kBuckets) ++shift;
+  sh.bcnt[tid] = 0;
+  __syncthreads();
+  uint32_t slot[kPerT];
+#pragma unroll
+  for (int q = 0; q < kPerT; ++q) {
+    const uint32_t i = tid + q * kThreads;
+    slot[q] = 0;
+    if (i < total && xs[q] >= R) slot[q] = atomicAdd(&sh.bcnt[(kmax - (uint32_t)(xs[q] >> 32)) >> shift], 1u);
+  }
+  __syncthreads();
+  const uint32_t c = sh.bcnt[tid];
+  uint32_t all;
+  sh.bstart[tid] = block_exclusive_scan_u32(c, sh.red_u, &all);
+  __syncthreads();
+#pragma unroll
+  for (int q = 0; q < kPerT; ++q) {
+    const uint32_t i = tid + q * kThreads;
+    if (i < total && xs[q] >= R) {
+      const uint32_t b = (kmax - (uint32_t)(xs[q] >> 32)) >> shift;
+      out2[sh.bstart[b] + slot[q]] = xs[q];
+    }
+  }
+  __syncthreads();
+  for (uint32_t i = tid; i < P; i += kThreads) {
+    const uint64_t x = out2[i];
+    const uint32_t b = (kmax - (uint32_t)(x >> 32)) >> shift;
+    const uint32_t s0 = sh.bstart[b], nb = sh.bcnt[b];
+    if (s0 >= need) continue;
+    uint32_t r = 0;
+    for (uint32_t j = 0; j < nb; ++j) r += (out2[s0 + j] > x) ? 1u : 0u;
+    sh.sk[s0 + r] = x;
+  }
+  __syncthreads();
+  return P;
+}
+
+// Inclusive prefix sums of sh.wd[0..m) (m <= kCap), eight per thread in loc[], the thread's
+// offset in *off; returns the sum of all m to every thread. Parallel: each sum is within
+// gamma(40) of the exact sum of its (positive) terms.
+__device__ __forceinline__ double prefix_scan(Shared& sh, uint32_t m, double loc[8], double* off) {
+  const uint32_t i0 = threadIdx.x * 8;
+  double run = 0.0;
+#pragma unroll
+  for (int q = 0; q < 8; ++q) {
+    run = __dadd_rn(run, (i0 + q < m) ? sh.wd[i0 + q] : 0.0);
+    loc[q] = run;
+  }
+  *off = block_exclusive_scan_f64(run, sh.red_d);
+#pragma unroll
+  for (int q = 0; q < 8; ++q)
+    if (i0 + q == m - 1) sh.x = __dadd_rn(*off, loc[q]);
+  __syncthreads();
+  const double s = sh.x;
+  __syncthreads();
+  return s;
+}
+
+// The draw's decision from bounds: u (the reference's unit() * total) lies in [ulo, uhi], and the
+// reference's cumulative c_j (its left fold of w_0..w_j) is within gamma(j+1) + gamma(40) of our
+// scanned prefix. Returns the first j < m with c_j > u when the bounds settle it, m when u is
+// certainly past every c_j of the m, kNone when they cannot decide.
+__device__ __forceinline__ uint32_t decide_draw(Shared& sh, uint32_t m, const double loc[8], double off, double ulo,
+                                double uhi) {
+  const uint32_t i0 = threadIdx.x * 8;
+  const double g40 = gamma_n(40.0);
+  uint32_t fp = m, fc = m;
+#pragma unroll
+  for (int q = 0; q < 8; ++q) {
+    const uint32_t i = i0 + q;
+    if (i < m) {
+      const double Rv = __dadd_rn(off, loc[q]);
+      const double rel = gamma_n((double)i + 1.0) + g40 + 4.0 * kU;
+      if (Rv * (1.0 + rel) > ulo) fp = min(fp, i);
+      if (Rv * (1.0 - rel) > uhi) fc = min(fc, i);
+    }
+  }
+  const uint32_t jp = block_min_u32<kWaves>(fp, sh.red_u);
+  const uint32_t jc = block_min_u32<kWaves>(fc, sh.red_u);
+  if (jp == jc) return jc;  // jc < m, or both m: past every c_j
+  return kNone;
+}
+
 // --- the kernel ---------------------------------------------------------------------------------
 
 __global__ __launch_bounds__(kThreads) void finish_kernel(FinishArgs a) {
   __shared__ Shared sh;
   const uint32_t row = blockIdx.x, tid = threadIdx.x;
   const RowParams p = a.params[row];
-  const SegStats* st = a.stats + (uint64_t)row * a.n_seg;
+  const SegStats* gst = a.stats + (uint64_t)row * a.n_seg;
   const uint32_t n = a.n;
   if (tid < 256) sh.tab[tid] = as_exp::kTable[tid];
+  // The segments' results, all loads in flight at once.
+  for (uint32_t s = tid; s < a.n_seg; s += kThreads) sh.seg[s] = gst[s];
+  __syncthreads();
+  const SegStats* st = sh.seg;
 
   if (tid == 0) {
     uint32_t bad = kNone, gi = kNone, mk = 0, total = 0, trunc = 0, long_hist = 0;
@@ -392,7 +539,7 @@ __global__ __launch_bounds__(kThreads) void finish_kernel(FinishArgs a) {
       total += t.n_cand;
       if (t.truncated & 1u) {
         trunc = 1;
-        bound = max(bound, t.min_cand);
+        bound = max(bound, t.bound);
       }
       if (t.truncated & 2u) long_hist = 1;
     }
@@ -441,18 +588,31 @@ __global__ __launch_bounds__(kThreads) void finish_kernel(FinishArgs a) {
 
   if ((p.mode == kModeTopK || p.mode == kModePartial) && !sh.exact) {
     const uint32_t total = sh.total;
-    uint32_t N = 2;
-    while (N < total) N <<= 1;
-    for (uint32_t s = 0; s < a.n_seg; ++s) {
-      const uint32_t off = sh.seg_off[s], c = sh.seg_off[s + 1] - off;
-      const uint64_t* src = a.cands + ((uint64_t)row * a.n_seg + s) * a.cand_stride;
-      for (uint32_t j = tid; j < c; j += kThreads) sh.sk[off + j] = src[j];
+    {
+      // Every segment's candidates at once: slot g is candidate g % cap of segment g / cap. The
+      // loads are unconditional (clamped into the row's own candidate area) so that all of them
+      // are in flight together; slots past a segment's count are dropped afterwards.
+      const uint32_t C = p.cap, slots = a.n_seg * C;
+      const uint64_t* src = a.cands + (uint64_t)row * a.n_seg * a.cand_stride;
+      uint64_t tmp[kCap / kThreads];
+#pragma unroll
+      for (int q = 0; q < kCap / kThreads; ++q) {
+        const uint32_t g = min(tid + q * kThreads, slots - 1);
+        const uint32_t s = g / C, j = g - s * C;
+        tmp[q] = src[(uint64_t)s * a.cand_stride + j];
+      }
+#pragma unroll
+      for (int q = 0; q < kCap / kThreads; ++q) {
+        const uint32_t g = tid + q * kThreads;
+        if (g < slots) {
+          const uint32_t s = g / C, j = g - s * C;
+          if (j < sh.seg[s].n_cand) sh.sk[sh.seg_off[s] + j] = tmp[q];
+        }
+      }
     }
-    for (uint32_t i = total + tid; i < N; i += kThreads) sh.sk[i] = 0;
     __syncthreads();
-    bitonic_desc(sh.sk, N);
 
-    const double top = (double)packed_value(sh.sk[0]);
+    const double top = (double)key_value(sh.mk);
     const double temp = (double)p.temp;
     const double top_p = (double)p.top_p;
     const bool has_floor = p.min_p > 0.0f;
@@ -462,8 +622,27 @@ __global__ __launch_bounds__(kThreads) void finish_kernel(FinishArgs a) {
     auto w_temp = [&](double v) { return as_exp::exp_with(tab, __ddiv_rn(__dsub_rn(v, top), temp)); };
     auto w_one = [&](double v) { return as_exp::exp_with(tab, __dsub_rn(v, top)); };
 
-    uint32_t keep = 0;
-    bool unfiltered = false;
+    // The values that can matter, sorted: every value of the row ranking at or above R is a
+    // candidate (R is the largest bound of a truncated segment; for a top-k row that segment also
+    // holds k values >= R), and nothing below min-p's floor is ever kept.
+    uint64_t R = sh.trunc ? sh.bound_key : 0ull;
+    bool floor_cut = false;  // R is the floor: the value after the sorted ones is below it
+    if (p.mode == kModePartial && has_floor) {
+      const uint64_t F = (uint64_t)total_key(floor_f32(floor)) << 32;
+      if (F >= R) {
+        R = F;
+        floor_cut = true;
+      }
+    }
+    const uint32_t P = sort_candidates(sh, total, R, sh.mk, p.mode == kModeTopK ? p.top_k : kNone);
+    if (tid == 0) sh.prefix = P;
+    const bool complete = (P == n);  // every value of the row is sorted
+
+    uint32_t keep = kNone;
+    uint32_t status = AS_ROW_OK;
+    bool drawn = false;
+    double r_prefix = 0.0;  // the top-p scan's sum of exp(l - top) over the P sorted values
+    double x1 = 0.0, eps1 = 0.0;  // total1 and its bound
     if (p.mode == kModeTopK) {
       // draw_full_sort over the k best (sample.rs:157-183).
       const uint32_t k = p.top_k;
@@ -494,170 +673,209 @@ __global__ __launch_bounds__(kThreads) void finish_kernel(FinishArgs a) {
           if (!(val(i) >= floor)) first = min(first, i);
         keep = block_min_u32<kWaves>(first, sh.red_u);
       }
-    } else {
-      // draw_partial: the complete rank prefix first.
-      uint32_t P = total;
-      if (sh.trunc) {
-        uint32_t c = 0;
-        for (uint32_t i = tid; i < total; i += kThreads) c += (sh.sk[i] >= sh.bound_key) ? 1u : 0u;
-        P = block_sum_u32<kWaves>(c, sh.red_u);
-      }
-      if (tid == 0) sh.prefix = P;
-      const bool complete = !sh.trunc;  // every value of the row is a candidate
-      uint32_t im = P;
-      if (has_floor) {
+    } else if (p.top_p < 1.0f || has_floor) {
+      // draw_partial's cut (sample.rs:230-259): the first rank below min-p's floor, or the rank at
+      // which the top-p cumulative reaches top_p, whichever comes first.
+      uint32_t im = P;  // first sorted rank below the floor (P: none among the sorted)
+      if (has_floor && !floor_cut) {
         uint32_t first = P;
         for (uint32_t i = tid; i < P; i += kThreads)
           if (!(val(i) >= floor)) first = min(first, i);
         im = block_min_u32<kWaves>(first, sh.red_u);
       }
-      const bool cuts = p.top_p < 1.0f || has_floor;
-      if (cuts) {
-        uint32_t jl = P, jh = P;
-        bool ok = true;
-        if (p.top_p < 1.0f) {
-          // total1 = sum of exp(l - top) over the row in index order (sample.rs:218-222): the
-          // segments' sums rescaled, with |result - reference's left fold| <= eps.
-          if (tid == 0) {
-            double X = 0.0, babs = 0.0;
-            for (uint32_t s = 0; s < a.n_seg; ++s) {
-              const SegStats t = st[s];
-              const double ms = (double)key_value(t.max_key);
-              const double dm = __dsub_rn(top, ms);
-              const double sc = as_exp::exp_with(tab, __dsub_rn(ms, top));
-              X = __dadd_rn(X, __dmul_rn(t.sum, sc));
-              babs = __dadd_rn(babs, __dmul_rn(sc, __dadd_rn(t.sum_abs, __dmul_rn(dm, t.sum))));
-            }
-            const double terms = (double)n + (double)a.n_seg + 64.0;
-            sh.x = X;
-            sh.eps = kU * 1.02 * (2.1 * babs + terms * X);
-          }
-          __syncthreads();
-          const double X = sh.x, eps = sh.eps;
-          ok = (X - eps > 0.0) && (eps == eps);
-          if (ok) {
-            // Inclusive prefix sums of the exact weights in rank order, 8 per thread.
-            const uint32_t i0 = tid * 8;
-            double loc[8];
-            double run = 0.0;
-#pragma unroll
-            for (int q = 0; q < 8; ++q) {
-              const uint32_t i = i0 + q;
-              const double w = (i < P) ? w_one(val(i)) : 0.0;
-              run = __dadd_rn(run, w);
-              loc[q] = run;
-            }
-            const double off = block_exclusive_scan_f64(run, sh.red_d);
-            const double g31 = 2.0 * gamma_n(40.0);
-            uint32_t fl = P, fh = P;
-#pragma unroll
-            for (int q = 0; q < 8; ++q) {
-              const uint32_t i = i0 + q;
-              if (i < P) {
-                const double R = __dadd_rn(off, loc[q]);
-                const double rel = g31 + gamma_n((double)i + 2.0) + 10.0 * kU;
-                const double hi = R * (1.0 + rel) / (X - eps);
-                const double lo = R * (1.0 - rel) / (X + eps);
-                if (hi >= top_p) fl = min(fl, i);
-                if (lo >= top_p) fh = min(fh, i);
-              }
-            }
-            jl = block_min_u32<kWaves>(fl, sh.red_u);
-            jh = block_min_u32<kWaves>(fh, sh.red_u);
-          }
-        }
-        if (!ok)
-          keep = kNone;
-        else if (im < P && im <= jl)
-          keep = im;
-        else if (jl < P && jl == jh)
-          keep = jh + 1;
-        else if (jl == P && im == P && complete)
-          keep = n;
-        else
-          keep = kNone;
-      } else {
-        unfiltered = true;
-        // The unfiltered draw's total over the row in index order (sample.rs:275).
+      // min-p's cut is known exactly when it falls among the sorted values, or right after them.
+      const bool im_exact = (im < P) || floor_cut;
+      uint32_t jl = P, jh = P;  // top-p: possible and certain trigger ranks among the sorted
+      bool ok = true;
+      if (p.top_p < 1.0f) {
+        // total1 = sum of exp(l - top) over the row in index order (sample.rs:218-222): the
+        // segments' sums rescaled, with |result - reference's left fold| <= eps.
         if (tid == 0) {
           double X = 0.0, babs = 0.0;
           for (uint32_t s = 0; s < a.n_seg; ++s) {
             const SegStats t = st[s];
             const double ms = (double)key_value(t.max_key);
-            const double dm = __ddiv_rn(__dsub_rn(top, ms), temp);
-            const double sc = as_exp::exp_with(tab, __ddiv_rn(__dsub_rn(ms, top), temp));
+            const double dm = __dsub_rn(top, ms);
+            const double sc = as_exp::exp_with(tab, __dsub_rn(ms, top));
             X = __dadd_rn(X, __dmul_rn(t.sum, sc));
             babs = __dadd_rn(babs, __dmul_rn(sc, __dadd_rn(t.sum_abs, __dmul_rn(dm, t.sum))));
           }
           const double terms = (double)n + (double)a.n_seg + 64.0;
           sh.x = X;
-          sh.eps = kU * 1.02 * (4.2 * babs + terms * X);
+          sh.eps = kU * 1.02 * (2.1 * babs + terms * X);
         }
-        for (uint32_t i = tid; i < P; i += kThreads) sh.wd[i] = w_temp(val(i));
         __syncthreads();
         const double X = sh.x, eps = sh.eps;
-        if (tid == 0) {
-          uint32_t pick = kNone;
-          if (X - eps > 0.0 && eps == eps) {
-            const double ulo = sh.u01 * (X - eps) * (1.0 - 3.0 * kU);
-            const double uhi = sh.u01 * (X + eps) * (1.0 + 3.0 * kU);
-            uint32_t jp = P, jc = P;
-            double cum = 0.0;
-            for (uint32_t i = 0; i < P; ++i) {
-              cum = __dadd_rn(cum, sh.wd[i]);
-              if (jp == P && cum > ulo) jp = i;
-              if (cum > uhi) {
-                jc = i;
-                break;
-              }
+        __syncthreads();
+        x1 = X;
+        eps1 = eps;
+        ok = (X - eps > 0.0) && (eps == eps);
+        if (ok) {
+          for (uint32_t i = tid; i < P; i += kThreads) sh.wd[i] = w_one(val(i));
+          __syncthreads();
+          double loc[8], off;
+          r_prefix = prefix_scan(sh, P, loc, &off);
+          const double g40 = 2.0 * gamma_n(40.0);
+          uint32_t fl = P, fh = P;
+          const uint32_t i0 = tid * 8;
+#pragma unroll
+          for (int q = 0; q < 8; ++q) {
+            const uint32_t i = i0 + q;
+            if (i < P) {
+              const double Rv = __dadd_rn(off, loc[q]);
+              const double rel = g40 + gamma_n(2.0 * (double)i + 4.0) + 10.0 * kU;
+              const double hi = Rv * (1.0 + rel) / (X - eps);
+              const double lo = Rv * (1.0 - rel) / (X + eps);
+              if (hi >= top_p) fl = min(fl, i);
+              if (lo >= top_p) fh = min(fh, i);
             }
-            if (jp == jc && jc < P)
-              pick = jc;
-            else if (jp == P && complete)
-              pick = n - 1;
           }
-          sh.pick = pick;
-          sh.sum = X;
+          jl = block_min_u32<kWaves>(fl, sh.red_u);
+          jh = block_min_u32<kWaves>(fh, sh.red_u);
+        }
+      }
+      if (!ok) {
+        keep = kNone;
+      } else if (im_exact && im <= jl) {
+        keep = im;  // min-p's cut, at or before any rank top-p could stop at
+      } else if (jl < P && jl == jh) {
+        keep = jh + 1;  // top-p's cut, certainly, and min-p's comes later
+      } else if (jl == P && complete) {
+        keep = n;  // neither filter stops: every value
+      } else if (jl == P && !im_exact && !a.kept_ids) {
+        // Neither filter stops among the P sorted values: the kept set runs past them. The draw is
+        // still settled when u falls among the sorted values with the unsorted tail's weight
+        // bounded: it is at most (n - P) times the last sorted weight.
+        for (uint32_t i = tid; i < P; i += kThreads) sh.wd[i] = w_temp(val(i));
+        __syncthreads();
+        double loc[8], off;
+        const double SP = prefix_scan(sh, P, loc, &off);
+        // Each unsorted weight is at most the last sorted one. For T <= 1 with top-p's total known,
+        // also w = e^(1/T) <= e * e_last^(1/T - 1) with e = exp(l - top) <= e_last, so the tail is
+        // at most e_last^(1/T - 1) times total1's unsorted part.
+        double tail = (double)(n - P) * sh.wd[P - 1] * (1.0 + 4.0 * kU);
+        if (p.top_p < 1.0f && p.temp <= 1.0f) {
+          const double e_last = w_one(val(P - 1));
+          const double rest = (x1 + eps1) - r_prefix * (1.0 - 2.0 * gamma_n(40.0));
+          const double t2 = pow(e_last, 1.0 / temp - 1.0) * (1.0 + 1e-9) * (rest > 0.0 ? rest : 0.0);
+          if (t2 < tail) tail = t2;
+        }
+        const double g40 = gamma_n(40.0), gn = gamma_n((double)n);
+        const double slo = SP * (1.0 - g40 - 4.0 * kU) * (1.0 - gn);
+        const double shi = (SP * (1.0 + g40 + 4.0 * kU) + tail) * (1.0 + gn);
+        const uint32_t j = decide_draw(sh, P, loc, off, sh.u01 * slo * (1.0 - 3.0 * kU),
+                                       sh.u01 * shi * (1.0 + 3.0 * kU));
+        if (j != kNone && j < P) {
+          if (tid == 0) {
+            sh.pick = j;
+            sh.sum = SP;
+          }
+          drawn = true;
+          keep = P;  // a lower bound: the kept set's full size is not known
+          status |= AS_ROW_KEPT_PARTIAL;
+        } else {
+          keep = kNone;
         }
         __syncthreads();
-        keep = (sh.pick == kNone) ? kNone : n;
+      } else {
+        keep = kNone;
+      }
+    } else {
+      // No filter (sample.rs:274-292): the total over the row in index order, from the segments'
+      // sums with an error bound, then the first rank whose cumulative weight passes u.
+      if (tid == 0) {
+        double X = 0.0, babs = 0.0;
+        for (uint32_t s = 0; s < a.n_seg; ++s) {
+          const SegStats t = st[s];
+          const double ms = (double)key_value(t.max_key);
+          const double dm = __ddiv_rn(__dsub_rn(top, ms), temp);
+          const double sc = as_exp::exp_with(tab, __ddiv_rn(__dsub_rn(ms, top), temp));
+          X = __dadd_rn(X, __dmul_rn(t.sum, sc));
+          babs = __dadd_rn(babs, __dmul_rn(sc, __dadd_rn(t.sum_abs, __dmul_rn(dm, t.sum))));
+        }
+        const double terms = (double)n + (double)a.n_seg + 64.0;
+        sh.x = X;
+        sh.eps = kU * 1.02 * (4.2 * babs + terms * X);
+      }
+      for (uint32_t i = tid; i < P; i += kThreads) sh.wd[i] = w_temp(val(i));
+      __syncthreads();
+      const double X = sh.x, eps = sh.eps;
+      __syncthreads();
+      keep = kNone;
+      if (X - eps > 0.0 && eps == eps) {
+        double loc[8], off;
+        prefix_scan(sh, P, loc, &off);
+        const uint32_t j = decide_draw(sh, P, loc, off, sh.u01 * (X - eps) * (1.0 - 3.0 * kU),
+                                       sh.u01 * (X + eps) * (1.0 + 3.0 * kU));
+        uint32_t pick = kNone;
+        if (j != kNone && j < P) pick = j;
+        else if (j == P && complete) pick = n - 1;  // u past every cumulative: the last value
+        if (pick != kNone) {
+          if (tid == 0) {
+            sh.pick = pick;
+            sh.sum = X;
+          }
+          drawn = true;
+          keep = n;
+        }
+        __syncthreads();
+      }
+    }
+
+    if (keep != kNone && !drawn) {
+      // The draw over the kept prefix (sample.rs:184-197, 260-272): u = unit() * sum(w), then the
+      // first rank whose cumulative weight exceeds u. Both sums are the reference's left folds in
+      // rank order; past a few hundred tokens they come from a parallel scan with an error bound,
+      // and the sequential folds run only when the bound cannot decide.
+      for (uint32_t i = tid; i < keep; i += kThreads) sh.wd[i] = w_temp(val(i));
+      __syncthreads();
+      if (keep > 256) {
+        double loc[8], off;
+        const double S = prefix_scan(sh, keep, loc, &off);
+        const double d = gamma_n((double)keep) + gamma_n(40.0) + 4.0 * kU;
+        const uint32_t j = decide_draw(sh, keep, loc, off, sh.u01 * S * (1.0 - d), sh.u01 * S * (1.0 + d));
+        if (j != kNone) {
+          if (tid == 0) {
+            sh.pick = (j < keep) ? j : keep - 1;  // past every cumulative: the last kept
+            sh.sum = S;
+          }
+          drawn = true;
+        }
+        __syncthreads();
+      }
+      if (!drawn) {
+        if (tid == 0) {
+          double tot = 0.0;
+          for (uint32_t i = 0; i < keep; ++i) tot = __dadd_rn(tot, sh.wd[i]);
+          const double u = __dmul_rn(sh.u01, tot);
+          double cum = 0.0;
+          uint32_t pick = keep - 1;
+          for (uint32_t i = 0; i < keep; ++i) {
+            cum = __dadd_rn(cum, sh.wd[i]);
+            if (u < cum) {
+              pick = i;
+              break;
+            }
+          }
+          sh.pick = pick;
+          sh.sum = tot;
+        }
+        __syncthreads();
       }
     }
 
     if (keep == kNone) {
       if (tid == 0) sh.exact = 1;
-    } else if (!unfiltered) {
-      // The draw over the kept prefix, in the reference's order (sample.rs:184-197, 260-272).
-      for (uint32_t i = tid; i < keep; i += kThreads) sh.wd[i] = w_temp(val(i));
-      __syncthreads();
-      if (tid == 0) {
-        double tot = 0.0;
-        for (uint32_t i = 0; i < keep; ++i) tot = __dadd_rn(tot, sh.wd[i]);
-        const double u = __dmul_rn(sh.u01, tot);
-        double cum = 0.0;
-        uint32_t pick = keep - 1;
-        for (uint32_t i = 0; i < keep; ++i) {
-          cum = __dadd_rn(cum, sh.wd[i]);
-          if (u < cum) {
-            pick = i;
-            break;
-          }
-        }
-        sh.pick = pick;
-        sh.sum = tot;
-      }
-      __syncthreads();
-    }
-    if (keep != kNone) {
+    } else {
       const uint32_t pick = sh.pick;
       const double tot = sh.sum;
       if (tid == 0) {
         a.tokens[row] = packed_id(sh.sk[pick]);
-        a.status[row] = AS_ROW_OK;
+        a.status[row] = status;
         if (a.kept_count) a.kept_count[row] = keep;
       }
       if (a.kept_ids) {
-        const uint32_t m = min(min(keep, a.kept_cap), unfiltered ? sh.prefix : keep);
+        const uint32_t m = min(min(keep, a.kept_cap), sh.prefix);
         for (uint32_t j = tid; j < m; j += kThreads) {
           a.kept_ids[(uint64_t)row * a.kept_cap + j] = packed_id(sh.sk[j]);
           if (a.kept_probs) a.kept_probs[(uint64_t)row * a.kept_cap + j] = __ddiv_rn(sh.wd[j], tot);

@@ -11,8 +11,11 @@ namespace as_launch {
 constexpr int kSegment = 8192;
 // Candidates the finish kernel sorts in LDS: segments x per-segment candidates must fit.
 constexpr int kCandCap = 8192;
-// Per-segment candidate budget for rows without a top-k.
+// Per-segment candidate budget (the finish kernel takes segments x budget <= kCandCap).
 constexpr int kPartialCand = 256;
+// Rows without a top-k keep each segment's values at or above the 192nd largest of its threads'
+// two largest values (about 200 values of a segment of normally spread logits).
+constexpr int kPartialRank = 192;
 
 struct FinishArgs {
   const float* logits;

@@ -45,7 +45,7 @@ struct RowParams {
   uint32_t hist_begin;  // history range when no CSR offsets are given
   uint32_t hist_len;
   uint32_t extra;       // ids of the extra list appended to the history (verify drafts)
-  uint32_t pad;
+  uint32_t cap;         // most candidates a segment may keep (segments x cap fit the finish LDS)
 };
 
 // Per (row, segment) results of the scan.
@@ -57,7 +57,8 @@ struct SegStats {
   uint32_t n_cand;
   uint32_t truncated;   // bit 0: the segment held more values than it kept as candidates;
                         // bit 1: the row's history is too long for the scan's u16 counts
-  uint64_t min_cand;    // smallest packed candidate kept
+  uint64_t bound;       // a truncated segment kept every value whose packed rank is >= bound,
+                        // and at least `cand` of its values are >= bound
   double sum;           // sum of exp(d), d = l - m (or (l - m) / T), m = key_value(max_key)
   double sum_abs;       // sum of exp(d) * |d|
 };
@@ -108,30 +109,21 @@ __device__ __forceinline__ double rng_unit(uint64_t s[4]) {
 }
 
 // ---- wave64 / block reductions ----------------------------------------------------------------
+// The device library's wavefront reductions (DPP lane moves, a fixed order).
 
-__device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
-  for (int o = 32; o > 0; o >>= 1) v = max(v, (uint32_t)__shfl_xor((int)v, o, kWave));
-  return v;
-}
-__device__ __forceinline__ uint32_t wave_min_u32(uint32_t v) {
-  for (int o = 32; o > 0; o >>= 1) v = min(v, (uint32_t)__shfl_xor((int)v, o, kWave));
-  return v;
-}
-__device__ __forceinline__ uint32_t wave_sum_u32(uint32_t v) {
-  for (int o = 32; o > 0; o >>= 1) v += (uint32_t)__shfl_xor((int)v, o, kWave);
-  return v;
-}
-__device__ __forceinline__ double wave_sum_f64(double v) {
-  for (int o = 32; o > 0; o >>= 1) v = __dadd_rn(v, __shfl_xor(v, o, kWave));
-  return v;
-}
-__device__ __forceinline__ uint64_t wave_max_u64(uint64_t v) {
-  for (int o = 32; o > 0; o >>= 1) {
-    uint64_t w = __shfl_xor(v, o, kWave);
-    v = w > v ? w : v;
-  }
-  return v;
-}
+}  // namespace as_dev
+extern "C" __device__ __attribute__((const)) unsigned int __ockl_wfred_add_u32(unsigned int);
+extern "C" __device__ __attribute__((const)) unsigned int __ockl_wfred_min_u32(unsigned int);
+extern "C" __device__ __attribute__((const)) unsigned int __ockl_wfred_max_u32(unsigned int);
+extern "C" __device__ __attribute__((const)) double __ockl_wfred_add_f64(double);
+extern "C" __device__ __attribute__((const)) unsigned long long __ockl_wfred_max_u64(unsigned long long);
+namespace as_dev {
+
+__device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) { return __ockl_wfred_max_u32(v); }
+__device__ __forceinline__ uint32_t wave_min_u32(uint32_t v) { return __ockl_wfred_min_u32(v); }
+__device__ __forceinline__ uint32_t wave_sum_u32(uint32_t v) { return __ockl_wfred_add_u32(v); }
+__device__ __forceinline__ double wave_sum_f64(double v) { return __ockl_wfred_add_f64(v); }
+__device__ __forceinline__ uint64_t wave_max_u64(uint64_t v) { return __ockl_wfred_max_u64(v); }
 
 // Greedy's order (sample.rs:9-17): a larger value by IEEE `>`, equal values to the lower index;
 // kNone loses to anything.

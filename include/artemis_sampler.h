@@ -36,6 +36,10 @@ extern "C" {
  * summation order), because a fast-path decision fell within its rounding bound or its cut lay
  * deeper than the fast path's candidates. Informational; the token is the same either way. */
 #define AS_ROW_EXACT_PATH 0x100u
+/* OR-ed into the status: the kept set runs deeper than the values the fast path sorted; the token
+ * is exact (the unsorted tail's weight is bounded and cannot change it), kept_count is a lower
+ * bound and the kept lists hold the first kept_count ids with weights over that prefix. */
+#define AS_ROW_KEPT_PARTIAL 0x200u
 
 /* The draft id argmax_rows writes for a row with no finite value
  * (crates/kernels/src/dispatch.rs:61, NO_DRAFT). */
