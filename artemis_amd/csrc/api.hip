@@ -19,8 +19,10 @@ struct as_ctx {
   int device = 0;
   hipStream_t stream = nullptr;
   uint32_t max_rows = 0, max_vocab = 0, max_history = 0, max_seg = 0;
-  RowParams* d_params = nullptr;
-  RowParams* h_params[2] = {nullptr, nullptr};
+  RowParams* d_params = nullptr;           // after the FinishArgs slot of d_block
+  as_launch::FinishArgs* d_args = nullptr;  // the start of d_block
+  void* d_block = nullptr;
+  void* h_block[2] = {nullptr, nullptr};
   hipEvent_t staged[2] = {nullptr, nullptr};
   int next = 0;
   SegStats* d_stats = nullptr;
@@ -95,18 +97,8 @@ RowParams make_row(const as_sampling& s, uint32_t n, uint32_t n_seg) {
 
 bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
 
-// Copies rows' parameter blocks to the device through a pinned staging buffer, waiting only if the
-// same buffer's previous copy has not finished.
-int upload_params(as_ctx* c, const RowParams* rows, uint32_t n) {
-  const int b = c->next;
-  c->next ^= 1;
-  AS_HIP(c, hipEventSynchronize(c->staged[b]));
-  std::memcpy(c->h_params[b], rows, sizeof(RowParams) * n);
-  AS_HIP(c, hipMemcpyAsync(c->d_params, c->h_params[b], sizeof(RowParams) * n,
-                           hipMemcpyHostToDevice, c->stream));
-  AS_HIP(c, hipEventRecord(c->staged[b], c->stream));
-  return AS_OK;
-}
+constexpr size_t kArgsSlot = 256;
+static_assert(sizeof(as_launch::FinishArgs) <= kArgsSlot, "FinishArgs slot");
 
 // The next profiling event (created on first use), or null when profiling is off.
 hipEvent_t next_event(as_ctx* c) {
@@ -120,22 +112,15 @@ hipEvent_t next_event(as_ctx* c) {
   return c->ev[c->ev_used++];
 }
 
-int run_rows(as_ctx* c, const float* logits, uint64_t row_stride, uint32_t n, uint32_t n_rows,
-             const uint32_t* hist_off, const uint32_t* hist_ids, const uint32_t* extra_ids,
-             uint64_t* rng, uint32_t* tokens, uint32_t* status, uint32_t* kept_count,
-             uint32_t* kept_ids, double* kept_probs, uint32_t kept_cap) {
+// One call over n_rows rows: the finish kernel's arguments and the rows' parameter blocks go to the
+// device in one copy through a pinned staging buffer (waiting only if the same buffer's previous
+// copy has not finished), then the scan and finish kernels.
+int run_rows(as_ctx* c, const RowParams* rows, const float* logits, uint64_t row_stride, uint32_t n,
+             uint32_t n_rows, const uint32_t* hist_off, const uint32_t* hist_ids,
+             const uint32_t* extra_ids, uint64_t* rng, uint32_t* tokens, uint32_t* status,
+             uint32_t* kept_count, uint32_t* kept_ids, double* kept_probs, uint32_t kept_cap) {
   const uint32_t n_seg = (n + as_launch::kSegment - 1) / as_launch::kSegment;
   const bool vec = aligned16(logits) && (row_stride % 4 == 0);
-  hipEvent_t e0 = nullptr, e1 = nullptr, e2 = nullptr;
-  if (c->profile && c->ev_used + 3 <= 3 * 4096) {
-    e0 = next_event(c);
-    e1 = next_event(c);
-    e2 = next_event(c);
-  }
-  if (e0) AS_HIP(c, hipEventRecord(e0, c->stream));
-  AS_HIP(c, as_launch::scan(c->stream, vec, logits, row_stride, n, n_rows, n_seg, c->d_params,
-                            hist_off, hist_ids, extra_ids, c->d_stats, c->d_cands,
-                            as_launch::kPartialCand));
   as_launch::FinishArgs a{};
   a.logits = logits;
   a.row_stride = row_stride;
@@ -155,10 +140,32 @@ int run_rows(as_ctx* c, const float* logits, uint64_t row_stride, uint32_t n, ui
   a.kept_count = kept_count;
   a.kept_ids = kept_ids;
   a.kept_probs = kept_probs;
+  a.vec = vec ? 1u : 0u;
   a.scratch = c->d_scratch;
   a.scratch_stride = c->scratch_stride;
+
+  const int b = c->next;
+  c->next ^= 1;
+  AS_HIP(c, hipEventSynchronize(c->staged[b]));
+  char* h = static_cast<char*>(c->h_block[b]);
+  std::memcpy(h, &a, sizeof a);
+  std::memcpy(h + kArgsSlot, rows, sizeof(RowParams) * n_rows);
+  AS_HIP(c, hipMemcpyAsync(c->d_block, h, kArgsSlot + sizeof(RowParams) * n_rows, hipMemcpyHostToDevice,
+                           c->stream));
+  AS_HIP(c, hipEventRecord(c->staged[b], c->stream));
+
+  hipEvent_t e0 = nullptr, e1 = nullptr, e2 = nullptr;
+  if (c->profile && c->ev_used + 3 <= 3 * 4096) {
+    e0 = next_event(c);
+    e1 = next_event(c);
+    e2 = next_event(c);
+  }
+  if (e0) AS_HIP(c, hipEventRecord(e0, c->stream));
+  AS_HIP(c, as_launch::scan(c->stream, vec, logits, row_stride, n, n_rows, n_seg, c->d_params,
+                            hist_off, hist_ids, extra_ids, c->d_stats, c->d_cands,
+                            as_launch::kPartialCand));
   if (e1) AS_HIP(c, hipEventRecord(e1, c->stream));
-  AS_HIP(c, as_launch::finish(c->stream, n_rows, a));
+  AS_HIP(c, as_launch::finish(c->stream, n_rows, c->d_args));
   if (e2) AS_HIP(c, hipEventRecord(e2, c->stream));
   return AS_OK;
 }
@@ -210,14 +217,14 @@ int as_destroy(as_ctx* c) {
   if (!c) return AS_ERR_INVALID;
   (void)hipSetDevice(c->device);
   if (c->stream) (void)hipStreamSynchronize(c->stream);
-  (void)hipFree(c->d_params);
+  (void)hipFree(c->d_block);
   (void)hipFree(c->d_stats);
   (void)hipFree(c->d_cands);
   (void)hipFree(c->d_scratch);
   (void)hipFree(c->d_vstatus);
   for (hipEvent_t e : c->ev) (void)hipEventDestroy(e);
   for (int b = 0; b < 2; ++b) {
-    if (c->h_params[b]) (void)hipHostFree(c->h_params[b]);
+    if (c->h_block[b]) (void)hipHostFree(c->h_block[b]);
     if (c->staged[b]) (void)hipEventDestroy(c->staged[b]);
   }
   delete c;
@@ -238,16 +245,22 @@ int as_create(int device, void* hip_stream, uint32_t max_rows, uint32_t max_voca
   c->max_vocab = max_vocab;
   c->max_history = max_history;
   c->max_seg = max_seg;
-  c->scratch_stride = 5ull * max_vocab;
+  // Per row: u32 counts [n], then (8-byte aligned) two u64 buffers [n] each for the deep and
+  // exact-order paths; rounded to 4 words so every row's scratch starts 16-byte aligned.
+  c->scratch_stride = (5ull * max_vocab + 2 + 3) & ~3ull;
   hipError_t e = hipSetDevice(device);
-  if (e == hipSuccess) e = hipMalloc(&c->d_params, sizeof(RowParams) * max_rows);
+  if (e == hipSuccess) e = hipMalloc(&c->d_block, kArgsSlot + sizeof(RowParams) * max_rows);
+  if (e == hipSuccess) {
+    c->d_args = static_cast<as_launch::FinishArgs*>(c->d_block);
+    c->d_params = reinterpret_cast<RowParams*>(static_cast<char*>(c->d_block) + kArgsSlot);
+  }
   if (e == hipSuccess) e = hipMalloc(&c->d_stats, sizeof(SegStats) * (uint64_t)max_rows * max_seg);
   if (e == hipSuccess)
     e = hipMalloc(&c->d_cands, sizeof(uint64_t) * (uint64_t)max_rows * max_seg * as_launch::kPartialCand);
   if (e == hipSuccess) e = hipMalloc(&c->d_scratch, sizeof(uint32_t) * (uint64_t)max_rows * c->scratch_stride);
   if (e == hipSuccess) e = hipMalloc(&c->d_vstatus, sizeof(uint32_t) * max_rows);
   for (int b = 0; b < 2 && e == hipSuccess; ++b) {
-    e = hipHostMalloc((void**)&c->h_params[b], sizeof(RowParams) * max_rows, hipHostMallocDefault);
+    e = hipHostMalloc(&c->h_block[b], kArgsSlot + sizeof(RowParams) * max_rows, hipHostMallocDefault);
     if (e == hipSuccess) e = hipEventCreateWithFlags(&c->staged[b], hipEventDisableTiming);
     if (e == hipSuccess) e = hipEventRecord(c->staged[b], c->stream);
   }
@@ -292,11 +305,9 @@ int as_sample(as_ctx* c, const as_batch* b, const as_sampling* params) {
     h[r].flags |= as_dev::kFlagRngWrite;
   }
   AS_HIP(c, hipSetDevice(c->device));
-  int rc = upload_params(c, h.data(), b->n_rows);
-  if (rc != AS_OK) return rc;
-  return run_rows(c, b->logits, b->row_stride, b->n_vocab, b->n_rows, b->hist_offsets, b->hist_ids,
-                  nullptr, b->rng_state, b->tokens, b->status, b->kept_count, b->kept_ids,
-                  b->kept_probs, b->kept_cap);
+  return run_rows(c, h.data(), b->logits, b->row_stride, b->n_vocab, b->n_rows, b->hist_offsets,
+                  b->hist_ids, nullptr, b->rng_state, b->tokens, b->status, b->kept_count,
+                  b->kept_ids, b->kept_probs, b->kept_cap);
 }
 
 int as_verify(as_ctx* c, const float* rows, uint64_t row_stride, uint32_t n_vocab,
@@ -326,10 +337,8 @@ int as_verify(as_ctx* c, const float* rows, uint64_t row_stride, uint32_t n_voca
     h[i].extra = i;  // the drafts before row i were emitted when row i is sampled
   }
   AS_HIP(c, hipSetDevice(c->device));
-  int rc = upload_params(c, h.data(), k + 1);
-  if (rc != AS_OK) return rc;
-  rc = run_rows(c, rows, row_stride, n_vocab, k + 1, nullptr, hist_len ? history : nullptr,
-                k ? drafts : nullptr, rng_state, picks, c->d_vstatus, nullptr, nullptr, nullptr, 0);
+  int rc = run_rows(c, h.data(), rows, row_stride, n_vocab, k + 1, nullptr, hist_len ? history : nullptr,
+                    k ? drafts : nullptr, rng_state, picks, c->d_vstatus, nullptr, nullptr, nullptr, 0);
   if (rc != AS_OK) return rc;
   AS_HIP(c, as_launch::accept(c->stream, picks, c->d_vstatus, drafts, k, stop_ids, n_stop, rng_state,
                               draws ? 1u : 0u, result));

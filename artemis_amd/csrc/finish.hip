@@ -186,7 +186,7 @@ __device__ void radix_pass(Shared& sh, uint32_t n, int shift, const uint32_t* sr
 
 // The reference's algorithm in its own order: Sampler::sample's dispatch (sample.rs:136-149),
 // draw_full_sort (157-198) for top-k rows and draw_partial (208-293) otherwise.
-__device__ void exact_row(const FinishArgs& a, const RowParams& p, uint32_t row, Shared& sh) {
+__device__ __noinline__ void exact_row(const FinishArgs& a, const RowParams& p, uint32_t row, Shared& sh) {
   const uint32_t n = a.n, tid = threadIdx.x;
   uint32_t* S = a.scratch + (uint64_t)row * a.scratch_stride;
   uint32_t* cnt = S;
@@ -512,10 +512,471 @@ __device__ __forceinline__ uint32_t decide_draw(Shared& sh, uint32_t m, const do
   return kNone;
 }
 
+// --- the deep path ------------------------------------------------------------------------------
+//
+// For a row whose cut or draw lies past the fast path's sorted candidates: one pass over the row
+// histograms its keys (with f32 weight sums per bin), which fixes the lowest bin that can hold the
+// cut (or the draw), with slack; a second pass collects every value down to that bin; a bucket
+// sort in HBM scratch puts them in rank order; and the same certified decisions as the fast path
+// run while streaming through them. When a bound still cannot decide, the exact-order path runs.
+
+constexpr uint32_t kDeepBins = 4096;
+constexpr uint32_t kDeepBucketMax = 4096;
+
+// Streams the sorted values buf[c0 .. c0+m) through LDS in chunks: sh.sk gets the values, sh.wd
+// their weight(value), then a block prefix scan; f(chunk_start, count, loc, base) sees the chunk,
+// with the global inclusive prefix of chunk value q at base + loc[q], and returns true to stop.
+// Returns the sum of every weight streamed (within gamma(80) of the exact sum).
+template <class W, class F>
+__device__ __forceinline__ double stream_scan(Shared& sh, const uint64_t* buf, uint32_t m, W weight, F f) {
+  double carry = 0.0;
+  for (uint32_t c0 = 0; c0 < m; c0 += kCap) {
+    const uint32_t cn = min((uint32_t)kCap, m - c0);
+    for (uint32_t i = threadIdx.x; i < cn; i += kThreads) {
+      const uint64_t x = buf[c0 + i];
+      sh.sk[i] = x;
+      sh.wd[i] = weight((double)packed_value(x));
+    }
+    __syncthreads();
+    double loc[8], off;
+    const double tot = prefix_scan(sh, cn, loc, &off);
+    const bool stop = f(c0, cn, loc, __dadd_rn(carry, off));
+    carry = __dadd_rn(carry, tot);
+    __syncthreads();
+    if (stop) break;
+  }
+  return carry;
+}
+
+// First rank j with lo/hi bounds of the reference's cumulative crossing `target`: fills *jl (first
+// j whose upper bound reaches it) and *jh (first j whose lower bound does), over m streamed values.
+// cum_j = R_j / total with total in [x - eps, x + eps]; rel(j) bounds the rank-order fold.
+template <class W>
+__device__ __forceinline__ void stream_cross(Shared& sh, const uint64_t* buf, uint32_t m, W weight,
+                                             double x, double eps, double target, uint32_t* jl,
+                                             uint32_t* jh) {
+  uint32_t fl = kNone, fh = kNone;
+  stream_scan(sh, buf, m, weight, [&](uint32_t c0, uint32_t cn, const double loc[8], double base) {
+    const uint32_t i0 = threadIdx.x * 8;
+    uint32_t a = kNone, b = kNone;
+#pragma unroll
+    for (int q = 0; q < 8; ++q) {
+      const uint32_t i = i0 + q;
+      if (i < cn) {
+        const double Rv = __dadd_rn(base, loc[q]);
+        const double rel = 2.0 * gamma_n(80.0) + gamma_n(2.0 * (double)(c0 + i) + 4.0) + 10.0 * kU;
+        if (Rv * (1.0 + rel) / (x - eps) >= target) a = min(a, c0 + i);
+        if (Rv * (1.0 - rel) / (x + eps) >= target) b = min(b, c0 + i);
+      }
+    }
+    a = block_min_u32<kWaves>(a, sh.red_u);
+    b = block_min_u32<kWaves>(b, sh.red_u);
+    if (fl == kNone) fl = a;
+    if (fh == kNone) fh = b;
+    return fl != kNone && fh != kNone;
+  });
+  *jl = (fl == kNone) ? m : fl;
+  *jh = (fh == kNone) ? m : fh;
+}
+
+// The draw over the first m streamed values with u in [ulo, uhi]: the first j with the
+// reference's cumulative c_j > u when the bounds settle it, m when u is certainly past all of
+// them, kNone when they cannot decide.
+template <class W>
+__device__ __forceinline__ uint32_t stream_draw(Shared& sh, const uint64_t* buf, uint32_t m, W weight,
+                                                double ulo, double uhi) {
+  uint32_t res = m;
+  bool done = false;
+  stream_scan(sh, buf, m, weight, [&](uint32_t c0, uint32_t cn, const double loc[8], double base) {
+    const uint32_t i0 = threadIdx.x * 8;
+    uint32_t a = kNone, b = kNone;
+#pragma unroll
+    for (int q = 0; q < 8; ++q) {
+      const uint32_t i = i0 + q;
+      if (i < cn) {
+        const double Rv = __dadd_rn(base, loc[q]);
+        const double rel = gamma_n((double)(c0 + i) + 1.0) + gamma_n(80.0) + 4.0 * kU;
+        if (Rv * (1.0 + rel) > ulo) a = min(a, c0 + i);
+        if (Rv * (1.0 - rel) > uhi) b = min(b, c0 + i);
+      }
+    }
+    a = block_min_u32<kWaves>(a, sh.red_u);
+    b = block_min_u32<kWaves>(b, sh.red_u);
+    if (a != kNone) {
+      res = (a == b) ? a : kNone;
+      done = true;
+    }
+    return done;
+  });
+  return res;
+}
+
+// The totals of the row from the segments' sums: total1 (by_temp false) or the unfiltered total,
+// with the bound eps on the distance to the reference's index-order left fold.
+__device__ __forceinline__ void stats_total(const FinishArgs& a, Shared& sh, double top, double temp,
+                                            bool by_temp, double* X, double* eps) {
+  if (threadIdx.x == 0) {
+    double x = 0.0, babs = 0.0;
+    for (uint32_t s = 0; s < a.n_seg; ++s) {
+      const SegStats& t = sh.seg[s];
+      const double ms = (double)key_value(t.max_key);
+      double dm = __dsub_rn(top, ms), dd = __dsub_rn(ms, top);
+      if (by_temp) {
+        dm = __ddiv_rn(dm, temp);
+        dd = __ddiv_rn(dd, temp);
+      }
+      const double sc = as_exp::exp_with(sh.tab, dd);
+      x = __dadd_rn(x, __dmul_rn(t.sum, sc));
+      babs = __dadd_rn(babs, __dmul_rn(sc, __dadd_rn(t.sum_abs, __dmul_rn(dm, t.sum))));
+    }
+    sh.x = x;
+    sh.eps = kU * 1.02 * ((by_temp ? 4.2 : 2.1) * babs + ((double)a.n + (double)a.n_seg + 64.0) * x);
+  }
+  __syncthreads();
+  *X = sh.x;
+  *eps = sh.eps;
+  __syncthreads();
+}
+
+// The deep path's passes over a row: 16 values per thread per step, four 16-byte loads in flight
+// (scalar loads for an unaligned row or the ragged end). f(i, v) runs for each value.
+template <class F>
+__device__ __forceinline__ void for_each_value(const float* x, uint32_t n, bool vec, F f) {
+  typedef float f32x4 __attribute__((ext_vector_type(4)));
+  constexpr uint32_t kStep = 16 * kThreads;
+  const uint32_t tid = threadIdx.x;
+  for (uint32_t b0 = 0; b0 < n; b0 += kStep) {
+    if (vec && b0 + kStep <= n) {
+      f32x4 q[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) q[j] = *reinterpret_cast<const f32x4*>(x + b0 + (j * kThreads + tid) * 4);
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+#pragma unroll
+        for (int c = 0; c < 4; ++c) f(b0 + (j * kThreads + tid) * 4 + c, q[j][c]);
+    } else {
+      float q[16];
+#pragma unroll
+      for (int j = 0; j < 16; ++j) {
+        const uint32_t i = b0 + j * kThreads + tid;
+        q[j] = (i < n) ? x[i] : 0.0f;
+      }
+#pragma unroll
+      for (int j = 0; j < 16; ++j) {
+        const uint32_t i = b0 + j * kThreads + tid;
+        if (i < n) f(i, q[j]);
+      }
+    }
+  }
+}
+
+// Returns true when it settled the row.
+__device__ __noinline__ bool deep_row(const FinishArgs& a, const RowParams& p, uint32_t row, Shared& sh) {
+  const uint32_t n = a.n, tid = threadIdx.x, lane = tid & (kWave - 1);
+  uint32_t* S = a.scratch + (uint64_t)row * a.scratch_stride;
+  uint32_t* cnt = S;
+  uint64_t* bufA = reinterpret_cast<uint64_t*>(S + ((n + 1) & ~1u));
+  uint64_t* bufB = bufA + n;
+  const float* x = a.logits + (uint64_t)row * a.row_stride;
+
+  uint32_t hb;
+  const uint32_t he = history_bounds(a, p, row, &hb);
+  const uint32_t extra = a.extra_ids ? p.extra : 0;
+  const bool pen = (p.flags & kFlagPenalties) && (he > hb || extra > 0);
+  if (pen) {
+    for (uint32_t i = tid; i < n; i += kThreads) cnt[i] = 0;
+    __syncthreads();
+    for (uint32_t h = hb + tid; h < he; h += kThreads) {
+      const uint32_t id = a.hist_ids[h];
+      if (id < n) atomicAdd(&cnt[id], 1u);
+    }
+    for (uint32_t h = tid; h < extra; h += kThreads) {
+      const uint32_t id = a.extra_ids[h];
+      if (id < n) atomicAdd(&cnt[id], 1u);
+    }
+    __syncthreads();
+  }
+  auto pvalue = [&](uint32_t i, float v) -> float {
+    if (pen) {
+      const uint32_t c = cnt[i];
+      if (c) v = penalize(v, c, p);
+    }
+    return v;
+  };
+  const bool vec = a.vec && a.row_stride % 4 == 0;
+
+  if (p.mode == kModeGreedy) {
+    // greedy / greedy_penalized (sample.rs:9-17, 378-396) over the whole row.
+    float gv = 0.0f;
+    uint32_t gi = kNone;
+    for_each_value(x, n, vec, [&](uint32_t i, float v) { greedy_merge(gv, gi, pvalue(i, v), i); });
+    wave_greedy(gv, gi);
+    if (lane == 0) {
+      sh.wd[tid / kWave] = (double)gv;
+      sh.red_u[tid / kWave] = gi;
+    }
+    __syncthreads();
+    if (tid == 0) {
+      for (int w = 1; w < kWaves; ++w) greedy_merge(gv, gi, (float)sh.wd[w], sh.red_u[w]);
+      a.tokens[row] = gi;
+      a.status[row] = AS_ROW_OK | AS_ROW_DEEP_PATH;
+      if (a.kept_count) a.kept_count[row] = 1;
+      if (a.kept_ids && a.kept_cap > 0) {
+        a.kept_ids[(uint64_t)row * a.kept_cap] = gi;
+        if (a.kept_probs) a.kept_probs[(uint64_t)row * a.kept_cap] = 1.0;
+      }
+    }
+    return true;
+  }
+
+  // A history too long for the scan's u16 counts left its maxima and sums unpenalised: the
+  // exact-order path recomputes everything.
+  if ((uint64_t)(he - hb) + extra > 0xFFFFu) return false;
+
+  const uint32_t mk = sh.mk;
+  const double top = (double)key_value(mk);
+  const double temp = (double)p.temp, top_p = (double)p.top_p;
+  const bool has_floor = p.min_p > 0.0f;
+  const double floor = __dadd_rn(top, p.ln_min_p);
+  const uint32_t fk = total_key(floor_f32(floor));
+  const bool topk = (p.mode == kModeTopK || p.mode == kModeExactTopK);
+  const uint32_t k = p.top_k;
+  const bool cuts = p.top_p < 1.0f || has_floor;
+  const bool unfiltered = !topk && !cuts;
+  const uint64_t* tab = sh.tab;
+  auto w_temp = [&](double v) { return as_exp::exp_with(tab, __ddiv_rn(__dsub_rn(v, top), temp)); };
+  auto w_one = [&](double v) { return as_exp::exp_with(tab, __dsub_rn(v, top)); };
+
+  double X = 0.0, eps = 0.0;
+  if (!topk && (p.top_p < 1.0f || unfiltered)) stats_total(a, sh, top, temp, unfiltered, &X, &eps);
+  if (!topk && (p.top_p < 1.0f || unfiltered) && !(X - eps > 0.0 && eps == eps)) return false;
+
+  // Pass 1: a histogram of the keys by distance from the largest, with f32 weight sums.
+  uint32_t s1 = 0;
+  while ((mk >> s1) >= kDeepBins) ++s1;
+  uint32_t* hc = reinterpret_cast<uint32_t*>(sh.wd);
+  float* hm = reinterpret_cast<float*>(sh.wd) + kDeepBins;
+  for (uint32_t b = tid; b < kDeepBins; b += kThreads) {
+    hc[b] = 0;
+    hm[b] = 0.0f;
+  }
+  __syncthreads();
+  const bool masses = !topk && (p.top_p < 1.0f || unfiltered);
+  const float topf = key_value(mk), inv_t = 1.0f / p.temp;
+  for_each_value(x, n, vec, [&](uint32_t i, float v0) {
+    const float v = pvalue(i, v0);
+    const uint32_t b = (mk - total_key(v)) >> s1;
+    atomicAdd(&hc[b], 1u);
+    if (masses) atomicAdd(&hm[b], unfiltered ? __expf((v - topf) * inv_t) : __expf(v - topf));
+  });
+  __syncthreads();
+  if (tid == 0) {
+    uint32_t bc = kDeepBins - 1;
+    if (topk) {
+      uint32_t c = 0;
+      for (uint32_t b = 0; b < kDeepBins; ++b) {
+        c += hc[b];
+        if (c >= k) {
+          bc = b;
+          break;
+        }
+      }
+    } else {
+      const double target = unfiltered ? sh.u01 * (X + eps) * 1.05 : (p.top_p < 1.0f ? top_p * (X + eps) * 1.05 : 0.0);
+      if (masses) {
+        double c = 0.0;
+        for (uint32_t b = 0; b < kDeepBins; ++b) {
+          c += (double)hm[b];
+          if (c >= target) {
+            bc = b;
+            break;
+          }
+        }
+      }
+      if (has_floor) bc = min(bc, (mk - fk) >> s1);
+    }
+    sh.keep = bc;
+    sh.pick = 0;
+  }
+  __syncthreads();
+  const uint32_t bc = sh.keep;
+
+  // Pass 2: every value in bins 0..bc, into bufA (any order): 16 values per thread per step,
+  // placed by ballots with one LDS atomic per wave and step.
+  {
+    constexpr uint32_t kStep = 16 * kThreads;
+    const uint64_t below = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
+    for (uint32_t b0 = 0; b0 < n; b0 += kStep) {
+      float q[16];
+      uint32_t idx[16];
+      if (vec && b0 + kStep <= n) {
+        typedef float f32x4 __attribute__((ext_vector_type(4)));
+        f32x4 t[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) t[j] = *reinterpret_cast<const f32x4*>(x + b0 + (j * kThreads + tid) * 4);
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+#pragma unroll
+          for (int c = 0; c < 4; ++c) {
+            q[4 * j + c] = t[j][c];
+            idx[4 * j + c] = b0 + (j * kThreads + tid) * 4 + c;
+          }
+      } else {
+#pragma unroll
+        for (int j = 0; j < 16; ++j) {
+          idx[j] = b0 + j * kThreads + tid;
+          q[j] = (idx[j] < n) ? x[idx[j]] : 0.0f;
+        }
+      }
+      uint32_t keys[16];
+      uint64_t m[16];
+      uint32_t tot = 0;
+#pragma unroll
+      for (int j = 0; j < 16; ++j) {
+        keys[j] = (idx[j] < n) ? total_key(pvalue(idx[j], q[j])) : 0u;
+        const bool take = idx[j] < n && ((mk - keys[j]) >> s1) <= bc;
+        m[j] = __ballot(take);
+        tot += (uint32_t)__popcll(m[j]);
+      }
+      uint32_t base = 0;
+      if (lane == 0 && tot) base = atomicAdd(&sh.pick, tot);
+      base = __shfl(base, 0, kWave);
+#pragma unroll
+      for (int j = 0; j < 16; ++j) {
+        if ((m[j] >> lane) & 1ull) bufA[base + __popcll(m[j] & below)] = pack(keys[j], idx[j]);
+        base += (uint32_t)__popcll(m[j]);
+      }
+    }
+  }
+  __syncthreads();
+  const uint32_t D = sh.pick;
+  const bool complete = (D == n);
+
+  // Bucket sort of bufA[0..D) into rank order (through bufB).
+  {
+    uint32_t kmin = 0xFFFFFFFFu;
+    for (uint32_t i = tid; i < D; i += kThreads) kmin = min(kmin, (uint32_t)(bufA[i] >> 32));
+    kmin = block_min_u32<kWaves>(kmin, sh.red_u);
+    uint32_t s2 = 0;
+    while (((mk - kmin) >> s2) >= kDeepBins) ++s2;
+    for (uint32_t b = tid; b < kDeepBins; b += kThreads) hc[b] = 0;
+    __syncthreads();
+    for (uint32_t i = tid; i < D; i += kThreads) atomicAdd(&hc[(mk - (uint32_t)(bufA[i] >> 32)) >> s2], 1u);
+    __syncthreads();
+    // Exclusive scan of the 4096 counts: four per thread, then the block.
+    uint32_t* bs = hc + kDeepBins;  // bucket starts (over hm's space)
+    uint32_t c4[4], run = 0, big = 0;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      c4[q] = hc[tid * 4 + q];
+      big = max(big, c4[q]);
+      run += c4[q];
+    }
+    uint32_t all;
+    uint32_t off = block_exclusive_scan_u32(run, sh.red_u, &all);
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      bs[tid * 4 + q] = off;
+      off += c4[q];
+    }
+    big = block_max_u32<kWaves>(big, sh.red_u);
+    if (big > kDeepBucketMax) return false;  // heavy ties: the exact-order path's stable sort
+    // Scatter: a value's slot in its bucket from an LDS counter (reusing the counts, now zeroed
+    // by subtraction as slots are taken).
+    for (uint32_t i = tid; i < D; i += kThreads) {
+      const uint64_t v = bufA[i];
+      const uint32_t b = (mk - (uint32_t)(v >> 32)) >> s2;
+      const uint32_t slot = atomicSub(&hc[b], 1u) - 1u;
+      bufB[bs[b] + slot] = v;
+    }
+    __syncthreads();
+    for (uint32_t i = tid; i < D; i += kThreads) {
+      const uint64_t v = bufB[i];
+      const uint32_t b = (mk - (uint32_t)(v >> 32)) >> s2;
+      const uint32_t s0 = bs[b];
+      const uint32_t e0 = (b + 1 < kDeepBins) ? bs[b + 1] : D;
+      uint32_t r = 0;
+      for (uint32_t j = s0; j < e0; ++j) r += (bufB[j] > v) ? 1u : 0u;
+      bufA[s0 + r] = v;
+    }
+    __syncthreads();
+  }
+  auto val_at = [&](uint32_t j) -> double { return (double)packed_value(bufA[j]); };
+
+  // The cut.
+  uint32_t keep = kNone;
+  if (topk) {
+    keep = k;
+    if (p.top_p < 1.0f) {
+      const double Tk = stream_scan(sh, bufA, k, w_one, [](uint32_t, uint32_t, const double*, double) { return false; });
+      const double ek = Tk * (gamma_n((double)k) + 2.0 * gamma_n(80.0) + 4.0 * kU);
+      uint32_t jl, jh;
+      stream_cross(sh, bufA, k, w_one, Tk, ek, top_p, &jl, &jh);
+      if (jl == jh) keep = (jl < k) ? jl + 1 : k;
+      else return false;
+    }
+    if (has_floor) {
+      uint32_t first = keep;
+      for (uint32_t j = tid; j < keep; j += kThreads)
+        if (!(val_at(j) >= floor)) first = min(first, j);
+      keep = block_min_u32<kWaves>(first, sh.red_u);
+    }
+  } else if (cuts) {
+    uint32_t im = D;
+    if (has_floor) {
+      uint32_t first = D;
+      for (uint32_t j = tid; j < D; j += kThreads)
+        if (!(val_at(j) >= floor)) first = min(first, j);
+      im = block_min_u32<kWaves>(first, sh.red_u);
+    }
+    const bool im_exact = (im < D) || complete;
+    uint32_t jl = D, jh = D;
+    if (p.top_p < 1.0f) stream_cross(sh, bufA, D, w_one, X, eps, top_p, &jl, &jh);
+    if (im_exact && im <= jl) keep = im;
+    else if (jl < D && jl == jh) keep = jh + 1;
+    else if (jl == D && complete) keep = n;
+    else return false;
+  }
+
+  // The draw.
+  uint32_t pick;
+  double tot;
+  if (unfiltered) {
+    const uint32_t j = stream_draw(sh, bufA, D, w_temp, sh.u01 * (X - eps) * (1.0 - 3.0 * kU),
+                                   sh.u01 * (X + eps) * (1.0 + 3.0 * kU));
+    if (j != kNone && j < D) pick = j;
+    else if (j == D && complete) pick = n - 1;
+    else return false;
+    keep = n;
+    tot = X;
+  } else {
+    const double Sk = stream_scan(sh, bufA, keep, w_temp, [](uint32_t, uint32_t, const double*, double) { return false; });
+    const double d = gamma_n((double)keep) + 2.0 * gamma_n(80.0) + 4.0 * kU;
+    const uint32_t j = stream_draw(sh, bufA, keep, w_temp, sh.u01 * Sk * (1.0 - d), sh.u01 * Sk * (1.0 + d));
+    if (j == kNone) return false;
+    pick = (j < keep) ? j : keep - 1;
+    tot = Sk;
+  }
+  if (tid == 0) {
+    a.tokens[row] = packed_id(bufA[pick]);
+    a.status[row] = AS_ROW_OK | AS_ROW_DEEP_PATH;
+    if (a.kept_count) a.kept_count[row] = keep;
+  }
+  if (a.kept_ids) {
+    const uint32_t m = min(min(keep, a.kept_cap), D);
+    for (uint32_t j = tid; j < m; j += kThreads) {
+      a.kept_ids[(uint64_t)row * a.kept_cap + j] = packed_id(bufA[j]);
+      if (a.kept_probs) a.kept_probs[(uint64_t)row * a.kept_cap + j] = __ddiv_rn(w_temp(val_at(j)), tot);
+    }
+  }
+  return true;
+}
+
 // --- the kernel ---------------------------------------------------------------------------------
 
-__global__ __launch_bounds__(kThreads) void finish_kernel(FinishArgs a) {
+__global__ __launch_bounds__(kThreads) void finish_kernel(const FinishArgs* __restrict__ ap) {
   __shared__ Shared sh;
+  const FinishArgs& a = *ap;
   const uint32_t row = blockIdx.x, tid = threadIdx.x;
   const RowParams p = a.params[row];
   const SegStats* gst = a.stats + (uint64_t)row * a.n_seg;
@@ -890,7 +1351,10 @@ __global__ __launch_bounds__(kThreads) void finish_kernel(FinishArgs a) {
 
   if (sh.exact) {
     __syncthreads();
-    exact_row(a, p, row, sh);
+    if (!deep_row(a, a.params[row], row, sh)) {
+      __syncthreads();
+      exact_row(a, a.params[row], row, sh);
+    }
   }
 }
 
@@ -898,7 +1362,7 @@ __global__ __launch_bounds__(kThreads) void finish_kernel(FinishArgs a) {
 
 namespace as_launch {
 
-hipError_t finish(hipStream_t stream, uint32_t n_rows, const FinishArgs& a) {
+hipError_t finish(hipStream_t stream, uint32_t n_rows, const FinishArgs* a) {
   hipLaunchKernelGGL(finish_kernel, dim3(n_rows), dim3(kThreads), 0, stream, a);
   return hipGetLastError();
 }

@@ -36,7 +36,8 @@ struct FinishArgs {
   uint32_t* kept_count;
   uint32_t* kept_ids;
   double* kept_probs;
-  uint32_t* scratch;        // exact path: 5 x n u32 per row
+  uint32_t vec;             // the rows are 16-byte aligned (float4 loads)
+  uint32_t* scratch;        // deep and exact paths: 5 x n u32 (+ alignment) per row
   uint64_t scratch_stride;  // u32 per row
 };
 
@@ -45,7 +46,7 @@ hipError_t scan(hipStream_t stream, bool vec, const float* logits, uint64_t row_
                 const uint32_t* hist_off, const uint32_t* hist_ids, const uint32_t* extra_ids,
                 as_dev::SegStats* stats, uint64_t* cands, uint32_t cand_stride);
 
-hipError_t finish(hipStream_t stream, uint32_t n_rows, const FinishArgs& a);
+hipError_t finish(hipStream_t stream, uint32_t n_rows, const FinishArgs* a);
 
 hipError_t accept(hipStream_t stream, const uint32_t* picks, const uint32_t* status,
                   const uint32_t* drafts, uint32_t k, const uint32_t* stop_ids, uint32_t n_stop,

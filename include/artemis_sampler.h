@@ -40,6 +40,9 @@ extern "C" {
  * is exact (the unsorted tail's weight is bounded and cannot change it), kept_count is a lower
  * bound and the kept lists hold the first kept_count ids with weights over that prefix. */
 #define AS_ROW_KEPT_PARTIAL 0x200u
+/* OR-ed into the status: the cut or the draw lay past the fast path's candidates and a second pass
+ * over the row settled it (informational; the token is the reference's either way). */
+#define AS_ROW_DEEP_PATH 0x400u
 
 /* The draft id argmax_rows writes for a row with no finite value
  * (crates/kernels/src/dispatch.rs:61, NO_DRAFT). */
