@@ -49,14 +49,18 @@ class Workload:
         ids = np.concatenate(hs) if off[-1] else np.zeros(0, np.uint32)
         return off.astype(np.int32), ids.astype(np.int32)
 
-    def digest(self) -> str:
+    def sha256(self) -> str:
+        """SHA-256 of the logits, then each history, then the drafts (u32), as raw bytes."""
         h = hashlib.sha256()
         h.update(np.ascontiguousarray(self.logits).tobytes())
         for x in self.histories:
             h.update(np.ascontiguousarray(x, dtype=np.uint32).tobytes())
         if self.drafts is not None:
             h.update(np.ascontiguousarray(self.drafts, dtype=np.uint32).tobytes())
-        return h.hexdigest()[:16]
+        return h.hexdigest()
+
+    def digest(self) -> str:
+        return self.sha256()[:16]
 
 
 def _zipf_weights(n: int, s: float) -> np.ndarray:

@@ -21,6 +21,8 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
 
 HBM_PEAK_GBS = 8000.0  # MI355X HBM3E, 8 TB/s
+CAL_FLOATS = 64 << 20  # the calibration copy: 256 MiB read, 256 MiB written
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "scan_kernel_config5_traffic.json")
 
 
 def log(msg):
@@ -44,6 +46,12 @@ def gpu_config5(steps, warmup, copies=3):
     rng = states_tensor(w.seeds, dev)
     ctx = Context(max_rows=rows, max_vocab=n)
     log(f"bench: config5 rows={rows} vocab={n} history={len(ids) // rows} digest={w.digest()}")
+    # A plain elementwise kernel of known traffic (reads and writes 256 MiB), untimed: under
+    # rocprofv3 --pmc its FETCH_SIZE / WRITE_SIZE calibrate the counters against known bytes.
+    cal = torch.empty(CAL_FLOATS, dtype=torch.float32, device=dev).uniform_()
+    torch.neg(cal, out=torch.empty_like(cal))
+    torch.cuda.synchronize()
+    del cal
 
     for i in range(warmup):
         ctx.sample_batch(sets[i % copies], params, rng, d_off, d_ids)
@@ -179,6 +187,11 @@ def main():
     ms_per_step = g["wall"] / a.steps * 1e3
     rows_per_s = g["rows"] / (ms_per_step / 1e3)
     achieved = g["alg_bytes"] / (g["scan_ms"] / 1e3) / 1e9
+    traffic = None
+    if os.path.exists(TRAFFIC_FILE):
+        # HBM bytes per scan launch from the committed rocprofv3 --pmc passes over this same command.
+        with open(TRAFFIC_FILE) as f:
+            traffic = json.load(f).get("scan_kernel_bytes_per_launch")
     cpu = None
     if not a.no_cpu:
         log("bench: CPU baseline")
@@ -214,7 +227,7 @@ def main():
         "exact_path_rows": g["exact_rows"],
         "batch1": b1,
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,
                      "kernel": "scan_kernel", "bytes_per_launch": g["alg_bytes"]},
         "cpu_baseline": cpu,
     }

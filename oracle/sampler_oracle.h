@@ -8,6 +8,21 @@
 // Penalties extend the reference's presence penalty (sample.rs:308-323, 351-356, 378-396) to a
 // history multiset with repetition and frequency penalties; with repetition 1 and frequency 0 they
 // are bit-equal to the reference (see oc_penalize in sampler_oracle.cc).
+//
+// How each part is pinned (tests/test_oracle_*.py):
+//   - rng: the reference's known-answer streams (rng.rs:64-87), an independent restatement, and the
+//     below/unit invariants (rng.rs:90-144).
+//   - greedy, first_non_finite, argmax_row, check, top_k, draw_full_sort, draw_partial, logprobs:
+//     the reference's own sampler tests restated case for case (sample.rs:398-1086), including
+//     draw_partial == draw_full_sort and the distribution tests.
+//   - verify: the reference's accept-loop tests on integer-valued rows (spec/step.rs:972-1059).
+//   - exp / log: the host libm (glibc), compared with Python's math module.
+// Parity unpinned:
+//   - repetition and frequency penalties: the reference has none; they are pinned only by their
+//     definition here, a brute-force recomputation and the reduction to the presence penalty.
+//   - absolute token ids on large seeded rows: no reference test fixes them; they rest on following
+//     sample.rs line by line.
+//   - the libm boundary: no reference test pins exp/ln bits.
 #pragma once
 #include <stddef.h>
 #include <stdint.h>

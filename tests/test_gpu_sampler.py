@@ -4,6 +4,8 @@ Token ids, kept counts, RNG states and accepted-draft counts must be bit-exact; 
 probabilities within 1e-5 relative (the unfiltered fast path divides by a total that is itself
 within ~1e-11 of the reference's, every other path by the same f64 value).
 """
+import os
+
 import numpy as np
 import pytest
 
@@ -347,3 +349,46 @@ def test_sampler_object_follows_the_reference_sequence(ctx):
         lt = torch.from_numpy(base).cuda()
         for step in range(30):
             assert a.sample(lt) == b.sample(base), (top_k, step)
+
+
+GOLDEN_PATH = os.path.join(os.path.dirname(__file__), "golden", "configs.json")
+
+
+@pytest.mark.parametrize("name", ["config2", "config3", "config5"])
+def test_batches_match_the_committed_goldens(ctx, name):
+    import hashlib
+    import json
+    from artemis_amd import workloads
+    g = json.load(open(GOLDEN_PATH))[name]
+    w = {"config2": workloads.config2, "config3": lambda: workloads.config3(draws=64),
+         "config5": workloads.config5}[name]()
+    assert w.sha256() == g["sha256"]
+    rows = len(w.seeds)
+    params = [g["params"]] * rows if isinstance(g["params"], dict) else g["params"]
+    cap = 64
+    out = gpu_batch(ctx, w.logits, params, w.seeds, w.histories or None, kept_cap=cap)
+    assert out["tokens"].tolist() == g["tokens"], name
+    assert hashlib.sha256(out["rng"].astype("<u8").tobytes()).hexdigest() == g["rng_sha256"], name
+    for r, k in enumerate(g["kept"]):
+        st = int(out["status"][r])
+        if st & 0x200:  # the kept list holds a prefix of the kept set
+            continue
+        assert int(out["kept"][r]) == k["kept_count"], (name, r)
+        m = min(len(k["ids"]), cap)
+        assert out["kept_ids"][r][:m].tolist() == k["ids"][:m], (name, r)
+        np.testing.assert_allclose(out["kept_probs"][r][:m], k["probs"][:m], rtol=PROB_RTOL)
+
+
+def test_verify_and_greedy_match_the_committed_goldens(ctx):
+    import json
+    from artemis_amd import workloads
+    gold = json.load(open(GOLDEN_PATH))
+    g, w = gold["config4"], workloads.config4()
+    picks, result, rng = gpu_verify(ctx, w.logits, w.drafts, g["params"], g["seed"])
+    read = int(result[0])
+    assert read == g["read"] and int(result[1]) == g["accepted"] and int(result[2]) == g["bonus"]
+    assert picks[:read].tolist() == g["picks"]
+    assert ["%016x" % int(x) for x in rng] == g["rng"]
+    g1, w1 = gold["config1"], workloads.config1()
+    out = gpu_batch(ctx, w1.logits, [dict(temp=0.0, top_k=0, top_p=1.0, min_p=0.0)], [0])
+    assert int(out["tokens"][0]) == g1["greedy"]
