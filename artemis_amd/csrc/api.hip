@@ -2,6 +2,7 @@
 // the launches. No host synchronisation except as_sync and the staging-buffer reuse wait.
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <cmath>
 #include <cstdio>
 #include <cstring>
@@ -30,6 +31,7 @@ struct as_ctx {
   uint32_t* d_scratch = nullptr;
   uint64_t scratch_stride = 0;
   uint32_t* d_vstatus = nullptr;
+  float* d_zero = nullptr;  // 1,024 zeros the scan's idle loads read
   std::string err;
   // Profiling: events before the scan, between the kernels and after the finish, per call.
   bool profile = false;
@@ -58,8 +60,41 @@ bool penalties_on(const as_sampling& s) {
   return s.presence != 0.0f || s.frequency != 0.0f || s.repetition != 1.0f;
 }
 
+// The candidates each wave of a slice keeps for a row: top_k for a top-k row the fast path can take
+// (a wave holding k values at or above a threshold proves that nothing below it is among the row's
+// k best), kPartialRank for rows without a top-k, 0 for rows that keep none.
+uint32_t wave_cand(uint32_t top_k) { return top_k; }
+uint32_t wanted_cand(const as_sampling& s, uint32_t n) {
+  if (s.temp <= 0.0f) return 0;
+  if (s.top_k > 0 && s.top_k < n) return s.top_k <= as_launch::kTopKMax ? wave_cand(s.top_k) : 0;
+  return as_launch::kPartialRank;
+}
+
+// How a call splits its rows: n_seg slices of slice_len values, and `stride` candidate slots per
+// slice. Enough slices to give the GPU about kTargetGroups workgroups, no more than the finish
+// kernel's candidate room allows for the largest per-wave count, and slices of at most kSliceMax.
+struct Plan {
+  uint32_t n_seg, slice_len, stride, limit;
+};
+Plan plan_slices(uint32_t n, uint32_t n_rows, uint32_t c_max) {
+  const uint32_t s_min = (n + as_launch::kSliceMax - 1) / as_launch::kSliceMax;
+  uint32_t s = (as_launch::kTargetGroups + n_rows - 1) / n_rows;
+  s = std::min(s, std::max(1u, n / (4 * as_launch::kSliceAlign)));
+  if (c_max > 0) s = std::min(s, as_launch::kCandCap / (4 * c_max + as_launch::kHistReserve));
+  s = std::min(s, as_launch::kMaxSlices);
+  s = std::max(s, std::max(s_min, 1u));
+  uint32_t len = (n + s - 1) / s;
+  len = (len + as_launch::kSliceAlign - 1) / as_launch::kSliceAlign * as_launch::kSliceAlign;
+  Plan p;
+  p.slice_len = len;
+  p.n_seg = (n + len - 1) / len;
+  p.stride = as_launch::kCandCap / p.n_seg;
+  p.limit = p.stride > as_launch::kHistReserve ? (p.stride - as_launch::kHistReserve) / 4 : 0;
+  return p;
+}
+
 // The row's mode and parameter block (Sampler::sample's dispatch, sample.rs:129-150).
-RowParams make_row(const as_sampling& s, uint32_t n, uint32_t n_seg) {
+RowParams make_row(const as_sampling& s, uint32_t n, const Plan& pl) {
   RowParams r{};
   r.temp = s.temp;
   r.top_k = s.top_k;
@@ -70,23 +105,25 @@ RowParams make_row(const as_sampling& s, uint32_t n, uint32_t n_seg) {
   r.repetition = s.repetition;
   r.ln_min_p = s.min_p > 0.0f ? std::log((double)s.min_p) : 0.0;
   r.flags = penalties_on(s) ? as_dev::kFlagPenalties : 0u;
-  const uint32_t cap_all = as_launch::kCandCap / n_seg;
-  r.cap = cap_all < (uint32_t)as_launch::kPartialCand ? cap_all : (uint32_t)as_launch::kPartialCand;
+  r.cap = pl.stride;
+  const uint32_t limit = pl.limit;
   if (s.temp <= 0.0f) {
     r.mode = as_dev::kModeGreedy;
     r.cand = 0;
   } else if (s.top_k > 0 && s.top_k < n) {
-    if (s.top_k <= r.cap) {
+    if (s.top_k <= as_launch::kTopKMax && wave_cand(s.top_k) <= limit) {
       r.mode = as_dev::kModeTopK;
-      r.cand = s.top_k;
+      r.cand = wave_cand(s.top_k);
     } else {
       r.mode = as_dev::kModeExactTopK;
       r.cand = 0;
     }
   } else {
     r.mode = as_dev::kModePartial;
-    // The rank among the segment's 256 per-thread maxima that sets its candidate threshold.
-    r.cand = r.cap < (uint32_t)as_launch::kPartialRank ? r.cap : (uint32_t)as_launch::kPartialRank;
+    // A min-p row keeps every value above its floor: each wave keeps as many as its buffer and the
+    // slice's candidate room allow, so that a floor set of a few thousand values stays whole.
+    const uint32_t c = s.min_p > 0.0f ? as_launch::kFloorRank : as_launch::kPartialRank;
+    r.cand = std::max(1u, std::min(c, limit));
     if (s.top_p < 1.0f)
       r.flags |= as_dev::kFlagSumTop;
     else if (!(s.min_p > 0.0f))
@@ -115,11 +152,11 @@ hipEvent_t next_event(as_ctx* c) {
 // One call over n_rows rows: the finish kernel's arguments and the rows' parameter blocks go to the
 // device in one copy through a pinned staging buffer (waiting only if the same buffer's previous
 // copy has not finished), then the scan and finish kernels.
-int run_rows(as_ctx* c, const RowParams* rows, const float* logits, uint64_t row_stride, uint32_t n,
-             uint32_t n_rows, const uint32_t* hist_off, const uint32_t* hist_ids,
+int run_rows(as_ctx* c, const Plan& pl, const RowParams* rows, const float* logits, uint64_t row_stride,
+             uint32_t n, uint32_t n_rows, const uint32_t* hist_off, const uint32_t* hist_ids,
              const uint32_t* extra_ids, uint64_t* rng, uint32_t* tokens, uint32_t* status,
              uint32_t* kept_count, uint32_t* kept_ids, double* kept_probs, uint32_t kept_cap) {
-  const uint32_t n_seg = (n + as_launch::kSegment - 1) / as_launch::kSegment;
+  const uint32_t n_seg = pl.n_seg;
   const bool vec = aligned16(logits) && (row_stride % 4 == 0);
   as_launch::FinishArgs a{};
   a.logits = logits;
@@ -132,7 +169,7 @@ int run_rows(as_ctx* c, const RowParams* rows, const float* logits, uint64_t row
   a.extra_ids = extra_ids;
   a.stats = c->d_stats;
   a.cands = c->d_cands;
-  a.cand_stride = as_launch::kPartialCand;
+  a.cand_stride = pl.stride;
   a.kept_cap = kept_cap;
   a.rng_state = rng;
   a.tokens = tokens;
@@ -161,9 +198,9 @@ int run_rows(as_ctx* c, const RowParams* rows, const float* logits, uint64_t row
     e2 = next_event(c);
   }
   if (e0) AS_HIP(c, hipEventRecord(e0, c->stream));
-  AS_HIP(c, as_launch::scan(c->stream, vec, logits, row_stride, n, n_rows, n_seg, c->d_params,
-                            hist_off, hist_ids, extra_ids, c->d_stats, c->d_cands,
-                            as_launch::kPartialCand));
+  AS_HIP(c, as_launch::scan(c->stream, vec, logits, c->d_zero, row_stride, n, n_rows, n_seg, pl.slice_len,
+                            c->d_params, hist_off, hist_ids, extra_ids, c->d_stats, c->d_cands,
+                            pl.stride));
   if (e1) AS_HIP(c, hipEventRecord(e1, c->stream));
   AS_HIP(c, as_launch::finish(c->stream, n_rows, c->d_args));
   if (e2) AS_HIP(c, hipEventRecord(e2, c->stream));
@@ -222,6 +259,7 @@ int as_destroy(as_ctx* c) {
   (void)hipFree(c->d_cands);
   (void)hipFree(c->d_scratch);
   (void)hipFree(c->d_vstatus);
+  (void)hipFree(c->d_zero);
   for (hipEvent_t e : c->ev) (void)hipEventDestroy(e);
   for (int b = 0; b < 2; ++b) {
     if (c->h_block[b]) (void)hipHostFree(c->h_block[b]);
@@ -236,8 +274,8 @@ int as_create(int device, void* hip_stream, uint32_t max_rows, uint32_t max_voca
   if (!out) return AS_ERR_INVALID;
   *out = nullptr;
   if (max_rows == 0 || max_vocab == 0) return AS_ERR_INVALID;
-  const uint32_t max_seg = (max_vocab + as_launch::kSegment - 1) / as_launch::kSegment;
-  if (max_seg > 256) return AS_ERR_CAPACITY;
+  const uint32_t max_seg = as_launch::kMaxSlices;
+  if ((uint64_t)max_vocab > (uint64_t)as_launch::kMaxSlices * as_launch::kSliceMax) return AS_ERR_CAPACITY;
   as_ctx* c = new as_ctx();
   c->device = device;
   c->stream = (hipStream_t)hip_stream;
@@ -256,9 +294,11 @@ int as_create(int device, void* hip_stream, uint32_t max_rows, uint32_t max_voca
   }
   if (e == hipSuccess) e = hipMalloc(&c->d_stats, sizeof(SegStats) * (uint64_t)max_rows * max_seg);
   if (e == hipSuccess)
-    e = hipMalloc(&c->d_cands, sizeof(uint64_t) * (uint64_t)max_rows * max_seg * as_launch::kPartialCand);
+    e = hipMalloc(&c->d_cands, sizeof(uint64_t) * (uint64_t)max_rows * as_launch::kCandCap);
   if (e == hipSuccess) e = hipMalloc(&c->d_scratch, sizeof(uint32_t) * (uint64_t)max_rows * c->scratch_stride);
   if (e == hipSuccess) e = hipMalloc(&c->d_vstatus, sizeof(uint32_t) * max_rows);
+  if (e == hipSuccess) e = hipMalloc(&c->d_zero, sizeof(float) * 1024);
+  if (e == hipSuccess) e = hipMemset(c->d_zero, 0, sizeof(float) * 1024);
   for (int b = 0; b < 2 && e == hipSuccess; ++b) {
     e = hipHostMalloc(&c->h_block[b], kArgsSlot + sizeof(RowParams) * max_rows, hipHostMallocDefault);
     if (e == hipSuccess) e = hipEventCreateWithFlags(&c->staged[b], hipEventDisableTiming);
@@ -293,19 +333,23 @@ int as_sample(as_ctx* c, const as_batch* b, const as_sampling* params) {
     return fail(c, AS_ERR_INVALID, "as_sample: hist_offsets and hist_ids go together");
   if (b->kept_ids && b->kept_cap == 0)
     return fail(c, AS_ERR_INVALID, "as_sample: kept_ids needs kept_cap > 0");
-  const uint32_t n_seg = (b->n_vocab + as_launch::kSegment - 1) / as_launch::kSegment;
-  std::vector<RowParams> h(b->n_rows);
+  uint32_t c_max = 0;
   for (uint32_t r = 0; r < b->n_rows; ++r) {
     char msg[160];
     if (as_check(&params[r], msg, sizeof msg) != AS_OK)
       return fail(c, AS_ERR_PARAMS, "row " + std::to_string(r) + ": " + msg);
-    h[r] = make_row(params[r], b->n_vocab, n_seg);
+    c_max = std::max(c_max, wanted_cand(params[r], b->n_vocab));
+  }
+  const Plan pl = plan_slices(b->n_vocab, b->n_rows, c_max);
+  std::vector<RowParams> h(b->n_rows);
+  for (uint32_t r = 0; r < b->n_rows; ++r) {
+    h[r] = make_row(params[r], b->n_vocab, pl);
     h[r].rng_index = r;
     h[r].rng_skip = 0;
     h[r].flags |= as_dev::kFlagRngWrite;
   }
   AS_HIP(c, hipSetDevice(c->device));
-  return run_rows(c, h.data(), b->logits, b->row_stride, b->n_vocab, b->n_rows, b->hist_offsets,
+  return run_rows(c, pl, h.data(), b->logits, b->row_stride, b->n_vocab, b->n_rows, b->hist_offsets,
                   b->hist_ids, nullptr, b->rng_state, b->tokens, b->status, b->kept_count,
                   b->kept_ids, b->kept_probs, b->kept_cap);
 }
@@ -325,11 +369,11 @@ int as_verify(as_ctx* c, const float* rows, uint64_t row_stride, uint32_t n_voca
     return fail(c, AS_ERR_CAPACITY, "as_verify: more rows or a larger vocabulary than the context holds");
   char msg[160];
   if (as_check(params, msg, sizeof msg) != AS_OK) return fail(c, AS_ERR_PARAMS, msg);
-  const uint32_t n_seg = (n_vocab + as_launch::kSegment - 1) / as_launch::kSegment;
+  const Plan pl = plan_slices(n_vocab, k + 1, wanted_cand(*params, n_vocab));
   const bool draws = params->temp > 0.0f;
   std::vector<RowParams> h(k + 1);
   for (uint32_t i = 0; i <= k; ++i) {
-    h[i] = make_row(*params, n_vocab, n_seg);
+    h[i] = make_row(*params, n_vocab, pl);
     h[i].rng_index = 0;
     h[i].rng_skip = draws ? i : 0;
     h[i].hist_begin = 0;
@@ -337,7 +381,7 @@ int as_verify(as_ctx* c, const float* rows, uint64_t row_stride, uint32_t n_voca
     h[i].extra = i;  // the drafts before row i were emitted when row i is sampled
   }
   AS_HIP(c, hipSetDevice(c->device));
-  int rc = run_rows(c, h.data(), rows, row_stride, n_vocab, k + 1, nullptr, hist_len ? history : nullptr,
+  int rc = run_rows(c, pl, h.data(), rows, row_stride, n_vocab, k + 1, nullptr, hist_len ? history : nullptr,
                     k ? drafts : nullptr, rng_state, picks, c->d_vstatus, nullptr, nullptr, nullptr, 0);
   if (rc != AS_OK) return rc;
   AS_HIP(c, as_launch::accept(c->stream, picks, c->d_vstatus, drafts, k, stop_ids, n_stop, rng_state,
@@ -393,6 +437,15 @@ int as_debug_exp(as_ctx* c, const double* x, double* y, uint32_t n) {
   if (!x || !y) return fail(c, AS_ERR_INVALID, "as_debug_exp: no arrays");
   AS_HIP(c, hipSetDevice(c->device));
   AS_HIP(c, as_launch::debug_exp(c->stream, x, y, n));
+  return AS_OK;
+}
+
+int as_debug_exp2f(as_ctx* c, const float* x, float* y, uint32_t n) {
+  if (!c) return AS_ERR_INVALID;
+  if (n == 0) return AS_OK;
+  if (!x || !y) return fail(c, AS_ERR_INVALID, "as_debug_exp2f: no arrays");
+  AS_HIP(c, hipSetDevice(c->device));
+  AS_HIP(c, as_launch::debug_exp2f(c->stream, x, y, n));
   return AS_OK;
 }
 

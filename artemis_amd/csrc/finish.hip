@@ -24,7 +24,7 @@ namespace {
 
 constexpr int kThreads = 1024;
 constexpr int kWaves = kThreads / kWave;
-constexpr int kCap = as_launch::kCandCap;
+constexpr int kCap = as_launch::kFinishCap;
 constexpr int kMaxSeg = 256;
 constexpr int kStage = 4096;
 constexpr double kU = 1.1102230246251565e-16;  // 2^-53, the unit roundoff
@@ -45,7 +45,7 @@ struct Shared {
   uint32_t red_u[kWaves];
   double red_d[kWaves];
   // Row scalars.
-  uint32_t bad, gi, mk, total, trunc, keep, pick, done, exact, prefix;
+  uint32_t bad, gi, mk, total, trunc, keep, pick, done, exact, prefix, stats_bad, nsk;
   uint64_t bound_key;
   double u01, sum, x, eps;
 };
@@ -396,13 +396,46 @@ __device__ uint32_t block_exclusive_scan_u32(uint32_t x, uint32_t* wave_tot, uin
   return before + incl - x;
 }
 
-// The smallest f32 whose f64 value is >= f (IEEE, so a floor of 0 admits -0 as well).
-__device__ __forceinline__ float floor_f32(double f) {
-  float x = __double2float_rn(f);
-  if ((double)x < f) x = nextafterf(x, __builtin_inff());
-  if (x == 0.0f) x = -0.0f;
-  return x;
+// The row's total from the slices' sums: total1 (by_temp false: sum of exp(l - top)) or the
+// unfiltered total (sum of exp((l - top) / T)), with a bound eps on its distance to the reference's
+// left fold in index order (sample.rs:218-222, 274-282). Each slice's sum is rescaled from its own
+// reference (sum_ref) to the row's largest value (a host-exact exp and a product). The bound adds up:
+//   - the reference's own fold of n terms and its exp: (n + 1) * 2^-53 per unit of X, with the
+//     fold of the slices (n_seg) and 64 to spare;
+//   - each slice's own evaluation, at most err_rel * sum + err_abs * sum_abs (sum_abs moved to the
+//     row's largest value by adding |dm| * sum), and 4 * 2^-53 per unit for its rescale;
+//   - the reference's argument roundings, 2^-53 * |d| per term and per rounding (babs);
+//   - terms the scan's exp flushed to 0: below 2^-126 each.
+__device__ __forceinline__ void slices_total(const FinishArgs& a, Shared& sh, double top, double temp,
+                                             bool by_temp, double* X, double* eps) {
+  if (threadIdx.x == 0) {
+    double x = 0.0, babs = 0.0, own = 0.0;
+    for (uint32_t s = 0; s < a.n_seg; ++s) {
+      const SegStats& t = sh.seg[s];
+      if (t.sum == 0.0) continue;
+      const double ms = (double)t.sum_ref;
+      double dm = fabs(__dsub_rn(top, ms)), dd = __dsub_rn(ms, top);
+      if (by_temp) {
+        dm = __ddiv_rn(dm, temp);
+        dd = __ddiv_rn(dd, temp);
+      }
+      const double sc = as_exp::exp_with(sh.tab, dd);
+      const double part = __dmul_rn(t.sum, sc);
+      const double pabs = __dmul_rn(sc, __dadd_rn(t.sum_abs, __dmul_rn(dm, t.sum)));
+      x = __dadd_rn(x, part);
+      babs = __dadd_rn(babs, pabs);
+      own = __dadd_rn(own, __dadd_rn(__dmul_rn(part, (double)t.err_rel + 4.0 * kU), __dmul_rn(pabs, (double)t.err_abs)));
+    }
+    const double terms = (double)a.n + (double)a.n_seg + 64.0;
+    sh.x = x;
+    sh.eps = 1.02 * (kU * ((by_temp ? 2.1 : 1.1) * babs + terms * x) + own) + (double)a.n * 0x1p-126;
+  }
+  __syncthreads();
+  *X = sh.x;
+  *eps = sh.eps;
+  __syncthreads();
 }
+
 
 // Sorts the candidates sh.sk[0..total) whose packed rank is >= R into rank order (packed
 // descending) and returns how many there are, P. Only the first `need` ranks are guaranteed placed:
@@ -611,33 +644,6 @@ __device__ __forceinline__ uint32_t stream_draw(Shared& sh, const uint64_t* buf,
   return res;
 }
 
-// The totals of the row from the segments' sums: total1 (by_temp false) or the unfiltered total,
-// with the bound eps on the distance to the reference's index-order left fold.
-__device__ __forceinline__ void stats_total(const FinishArgs& a, Shared& sh, double top, double temp,
-                                            bool by_temp, double* X, double* eps) {
-  if (threadIdx.x == 0) {
-    double x = 0.0, babs = 0.0;
-    for (uint32_t s = 0; s < a.n_seg; ++s) {
-      const SegStats& t = sh.seg[s];
-      const double ms = (double)key_value(t.max_key);
-      double dm = __dsub_rn(top, ms), dd = __dsub_rn(ms, top);
-      if (by_temp) {
-        dm = __ddiv_rn(dm, temp);
-        dd = __ddiv_rn(dd, temp);
-      }
-      const double sc = as_exp::exp_with(sh.tab, dd);
-      x = __dadd_rn(x, __dmul_rn(t.sum, sc));
-      babs = __dadd_rn(babs, __dmul_rn(sc, __dadd_rn(t.sum_abs, __dmul_rn(dm, t.sum))));
-    }
-    sh.x = x;
-    sh.eps = kU * 1.02 * ((by_temp ? 4.2 : 2.1) * babs + ((double)a.n + (double)a.n_seg + 64.0) * x);
-  }
-  __syncthreads();
-  *X = sh.x;
-  *eps = sh.eps;
-  __syncthreads();
-}
-
 // The deep path's passes over a row: 16 values per thread per step, four 16-byte loads in flight
 // (scalar loads for an unaligned row or the ragged end). f(i, v) runs for each value.
 template <class F>
@@ -729,9 +735,9 @@ __device__ __noinline__ bool deep_row(const FinishArgs& a, const RowParams& p, u
     return true;
   }
 
-  // A history too long for the scan's u16 counts left its maxima and sums unpenalised: the
-  // exact-order path recomputes everything.
-  if ((uint64_t)(he - hb) + extra > 0xFFFFu) return false;
+  // A slice whose statistics the scan could not finish (too many distinct history ids or
+  // candidates) leaves the maxima and sums incomplete: the exact-order path recomputes everything.
+  if (sh.stats_bad) return false;
 
   const uint32_t mk = sh.mk;
   const double top = (double)key_value(mk);
@@ -747,9 +753,12 @@ __device__ __noinline__ bool deep_row(const FinishArgs& a, const RowParams& p, u
   auto w_temp = [&](double v) { return as_exp::exp_with(tab, __ddiv_rn(__dsub_rn(v, top), temp)); };
   auto w_one = [&](double v) { return as_exp::exp_with(tab, __dsub_rn(v, top)); };
 
+  // The row's total, when the cut or the draw needs it, is summed here in pass 1 from the host-exact
+  // exp of the reference's own f64 arguments: every term has the reference's bits, so the sum is
+  // within (n + this fold's depth) * 2^-53 of the reference's left fold (the slices' f32 sums are too
+  // loose for a cut this deep, where neighbouring cumulative weights differ by ~1e-5 of the total).
+  const bool need_total = !topk && (p.top_p < 1.0f || unfiltered);
   double X = 0.0, eps = 0.0;
-  if (!topk && (p.top_p < 1.0f || unfiltered)) stats_total(a, sh, top, temp, unfiltered, &X, &eps);
-  if (!topk && (p.top_p < 1.0f || unfiltered) && !(X - eps > 0.0 && eps == eps)) return false;
 
   // Pass 1: a histogram of the keys by distance from the largest, with f32 weight sums.
   uint32_t s1 = 0;
@@ -761,14 +770,24 @@ __device__ __noinline__ bool deep_row(const FinishArgs& a, const RowParams& p, u
     hm[b] = 0.0f;
   }
   __syncthreads();
-  const bool masses = !topk && (p.top_p < 1.0f || unfiltered);
+  const bool masses = need_total;
   const float topf = key_value(mk), inv_t = 1.0f / p.temp;
+  double tsum = 0.0;
   for_each_value(x, n, vec, [&](uint32_t i, float v0) {
     const float v = pvalue(i, v0);
     const uint32_t b = (mk - total_key(v)) >> s1;
     atomicAdd(&hc[b], 1u);
-    if (masses) atomicAdd(&hm[b], unfiltered ? __expf((v - topf) * inv_t) : __expf(v - topf));
+    if (masses) {
+      atomicAdd(&hm[b], unfiltered ? __expf((v - topf) * inv_t) : __expf(v - topf));
+      const double d = __dsub_rn((double)v, top);
+      tsum = __dadd_rn(tsum, as_exp::exp_with(tab, unfiltered ? __ddiv_rn(d, temp) : d));
+    }
   });
+  if (need_total) {
+    X = block_sum_f64<kWaves>(tsum, sh.red_d);
+    eps = kU * 1.02 * ((double)n + (double)(n / kThreads) + 32.0) * X;
+    if (!(X - eps > 0.0 && eps == eps)) return false;
+  }
   __syncthreads();
   if (tid == 0) {
     uint32_t bc = kDeepBins - 1;
@@ -1012,6 +1031,8 @@ __global__ __launch_bounds__(kThreads) void finish_kernel(const FinishArgs* __re
     sh.trunc = trunc;
     sh.bound_key = bound;
     sh.exact = long_hist;
+    sh.stats_bad = long_hist;
+    sh.nsk = 0;
     sh.u01 = 0.0;
     if (bad == kNone && p.mode != kModeGreedy) {
       // One unit() per sampled row (sample.rs:189, 264, 276), after the row's skipped draws.
@@ -1048,31 +1069,6 @@ __global__ __launch_bounds__(kThreads) void finish_kernel(const FinishArgs* __re
   }
 
   if ((p.mode == kModeTopK || p.mode == kModePartial) && !sh.exact) {
-    const uint32_t total = sh.total;
-    {
-      // Every segment's candidates at once: slot g is candidate g % cap of segment g / cap. The
-      // loads are unconditional (clamped into the row's own candidate area) so that all of them
-      // are in flight together; slots past a segment's count are dropped afterwards.
-      const uint32_t C = p.cap, slots = a.n_seg * C;
-      const uint64_t* src = a.cands + (uint64_t)row * a.n_seg * a.cand_stride;
-      uint64_t tmp[kCap / kThreads];
-#pragma unroll
-      for (int q = 0; q < kCap / kThreads; ++q) {
-        const uint32_t g = min(tid + q * kThreads, slots - 1);
-        const uint32_t s = g / C, j = g - s * C;
-        tmp[q] = src[(uint64_t)s * a.cand_stride + j];
-      }
-#pragma unroll
-      for (int q = 0; q < kCap / kThreads; ++q) {
-        const uint32_t g = tid + q * kThreads;
-        if (g < slots) {
-          const uint32_t s = g / C, j = g - s * C;
-          if (j < sh.seg[s].n_cand) sh.sk[sh.seg_off[s] + j] = tmp[q];
-        }
-      }
-    }
-    __syncthreads();
-
     const double top = (double)key_value(sh.mk);
     const double temp = (double)p.temp;
     const double top_p = (double)p.top_p;
@@ -1095,16 +1091,58 @@ __global__ __launch_bounds__(kThreads) void finish_kernel(const FinishArgs* __re
         floor_cut = true;
       }
     }
+    {
+      // The slices' candidates ranking >= R into sh.sk, in any order: candidate g of the row is
+      // slot g - seg_off[s] of slice s. Those below R (spilled before a slice's bound rose) drop.
+      const uint64_t* src = a.cands + (uint64_t)row * a.n_seg * a.cand_stride;
+      const uint32_t all = sh.total, lane = tid & (kWave - 1);
+      constexpr int kLoad = 4;
+      for (uint32_t g0 = 0; g0 < all; g0 += kLoad * kThreads) {
+        uint64_t tmp[kLoad];
+#pragma unroll
+        for (int q = 0; q < kLoad; ++q) {
+          const uint32_t g = g0 + tid + q * kThreads;
+          tmp[q] = 0ull;
+          if (g < all) {
+            uint32_t lo = 0, hi = a.n_seg;  // seg_off[lo] <= g < seg_off[hi]
+            while (hi - lo > 1) {
+              const uint32_t mid = (lo + hi) / 2;
+              if (sh.seg_off[mid] <= g) lo = mid;
+              else hi = mid;
+            }
+            tmp[q] = src[(uint64_t)lo * a.cand_stride + (g - sh.seg_off[lo])];
+          }
+        }
+#pragma unroll
+        for (int q = 0; q < kLoad; ++q) {
+          const bool keep = tmp[q] != 0ull && tmp[q] >= R;
+          const uint64_t m = __ballot(keep);
+          uint32_t base = 0;
+          if (lane == 0 && m) base = atomicAdd(&sh.nsk, (uint32_t)__popcll(m));
+          base = __builtin_amdgcn_readfirstlane(base);
+          const uint32_t pos = base + __builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32),
+                                                                 __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0u));
+          if (keep && pos < (uint32_t)kCap) sh.sk[pos] = tmp[q];
+        }
+      }
+      __syncthreads();
+    }
+    const uint32_t total = min(sh.nsk, (uint32_t)kCap);
+    const bool too_many = sh.nsk > (uint32_t)kCap;  // more candidates >= R than the finish holds
     const uint32_t P = sort_candidates(sh, total, R, sh.mk, p.mode == kModeTopK ? p.top_k : kNone);
     if (tid == 0) sh.prefix = P;
     const bool complete = (P == n);  // every value of the row is sorted
+    // A top-k row's k best are among the sorted values only when at least k rank at or above R.
+    const bool short_topk = p.mode == kModeTopK && P < p.top_k;
 
     uint32_t keep = kNone;
     uint32_t status = AS_ROW_OK;
     bool drawn = false;
     double r_prefix = 0.0;  // the top-p scan's sum of exp(l - top) over the P sorted values
     double x1 = 0.0, eps1 = 0.0;  // total1 and its bound
-    if (p.mode == kModeTopK) {
+    if (short_topk || too_many) {
+      keep = kNone;
+    } else if (p.mode == kModeTopK) {
       // draw_full_sort over the k best (sample.rs:157-183).
       const uint32_t k = p.top_k;
       keep = k;
@@ -1151,23 +1189,8 @@ __global__ __launch_bounds__(kThreads) void finish_kernel(const FinishArgs* __re
       if (p.top_p < 1.0f) {
         // total1 = sum of exp(l - top) over the row in index order (sample.rs:218-222): the
         // segments' sums rescaled, with |result - reference's left fold| <= eps.
-        if (tid == 0) {
-          double X = 0.0, babs = 0.0;
-          for (uint32_t s = 0; s < a.n_seg; ++s) {
-            const SegStats t = st[s];
-            const double ms = (double)key_value(t.max_key);
-            const double dm = __dsub_rn(top, ms);
-            const double sc = as_exp::exp_with(tab, __dsub_rn(ms, top));
-            X = __dadd_rn(X, __dmul_rn(t.sum, sc));
-            babs = __dadd_rn(babs, __dmul_rn(sc, __dadd_rn(t.sum_abs, __dmul_rn(dm, t.sum))));
-          }
-          const double terms = (double)n + (double)a.n_seg + 64.0;
-          sh.x = X;
-          sh.eps = kU * 1.02 * (2.1 * babs + terms * X);
-        }
-        __syncthreads();
-        const double X = sh.x, eps = sh.eps;
-        __syncthreads();
+        double X, eps;
+        slices_total(a, sh, top, temp, false, &X, &eps);
         x1 = X;
         eps1 = eps;
         ok = (X - eps > 0.0) && (eps == eps);
@@ -1244,23 +1267,9 @@ __global__ __launch_bounds__(kThreads) void finish_kernel(const FinishArgs* __re
     } else {
       // No filter (sample.rs:274-292): the total over the row in index order, from the segments'
       // sums with an error bound, then the first rank whose cumulative weight passes u.
-      if (tid == 0) {
-        double X = 0.0, babs = 0.0;
-        for (uint32_t s = 0; s < a.n_seg; ++s) {
-          const SegStats t = st[s];
-          const double ms = (double)key_value(t.max_key);
-          const double dm = __ddiv_rn(__dsub_rn(top, ms), temp);
-          const double sc = as_exp::exp_with(tab, __ddiv_rn(__dsub_rn(ms, top), temp));
-          X = __dadd_rn(X, __dmul_rn(t.sum, sc));
-          babs = __dadd_rn(babs, __dmul_rn(sc, __dadd_rn(t.sum_abs, __dmul_rn(dm, t.sum))));
-        }
-        const double terms = (double)n + (double)a.n_seg + 64.0;
-        sh.x = X;
-        sh.eps = kU * 1.02 * (4.2 * babs + terms * X);
-      }
+      double X, eps;
+      slices_total(a, sh, top, temp, true, &X, &eps);
       for (uint32_t i = tid; i < P; i += kThreads) sh.wd[i] = w_temp(val(i));
-      __syncthreads();
-      const double X = sh.x, eps = sh.eps;
       __syncthreads();
       keep = kNone;
       if (X - eps > 0.0 && eps == eps) {

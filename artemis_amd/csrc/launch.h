@@ -7,15 +7,31 @@
 
 namespace as_launch {
 
-// Values one scan workgroup covers (256 threads x 32 values).
-constexpr int kSegment = 8192;
-// Candidates the finish kernel sorts in LDS: segments x per-segment candidates must fit.
-constexpr int kCandCap = 8192;
-// Per-segment candidate budget (the finish kernel takes segments x budget <= kCandCap).
-constexpr int kPartialCand = 256;
-// Rows without a top-k keep each segment's values at or above the 192nd largest of its threads'
-// two largest values (about 200 values of a segment of normally spread logits).
-constexpr int kPartialRank = 192;
+// The scan splits each row into slices, one 256-thread workgroup each, and streams a slice through
+// registers. A slice holds at most kSliceMax values (its history bitmap lives in LDS) and starts at
+// a multiple of kSliceAlign.
+constexpr uint32_t kSliceMax = 98304;
+constexpr uint32_t kSliceAlign = 1024;
+constexpr uint32_t kMaxSlices = 256;
+// The scan aims for about this many workgroups per call: three per CU, which its registers allow
+// at once, so that a call runs in one round.
+constexpr uint32_t kTargetGroups = 768;
+// Candidate slots per row in HBM (the slices share them evenly), and how many of a row's candidates
+// at or above its bound the finish kernel sorts in LDS.
+constexpr uint32_t kCandCap = 16384;
+constexpr uint32_t kFinishCap = 8192;
+// Each wave of a slice keeps the values at or above its threshold in an LDS buffer of kWaveCap
+// entries, and at most its best C once the buffer fills (C = top_k; kPartialRank for rows without a
+// top-k; kFloorRank for those with min-p, whose buffer should hold every value above the floor); a
+// slice writes at most 4 C of them plus the history values that rank at or above its bound, for
+// which kHistReserve slots are kept.
+constexpr uint32_t kWaveCap = 768;
+constexpr uint32_t kPartialRank = 192;
+constexpr uint32_t kFloorRank = 384;
+constexpr uint32_t kTopKMax = 256;
+constexpr uint32_t kHistReserve = 64;
+// Distinct history ids a slice can count (an LDS hash); more send the row to the exact path.
+constexpr uint32_t kHistSlots = 512;
 
 struct FinishArgs {
   const float* logits;
@@ -41,8 +57,10 @@ struct FinishArgs {
   uint64_t scratch_stride;  // u32 per row
 };
 
-hipError_t scan(hipStream_t stream, bool vec, const float* logits, uint64_t row_stride, uint32_t n,
-                uint32_t n_rows, uint32_t n_seg, const as_dev::RowParams* params,
+// n_seg slices of slice_len values per row (the last one shorter).
+// zero: 1,024 readable floats (the loads of a wave with no full chunk of its slice read there).
+hipError_t scan(hipStream_t stream, bool vec, const float* logits, const float* zero, uint64_t row_stride,
+                uint32_t n, uint32_t n_rows, uint32_t n_seg, uint32_t slice_len, as_dev::RowParams* params,
                 const uint32_t* hist_off, const uint32_t* hist_ids, const uint32_t* extra_ids,
                 as_dev::SegStats* stats, uint64_t* cands, uint32_t cand_stride);
 
@@ -57,5 +75,6 @@ hipError_t argmax_rows(hipStream_t stream, bool vec, const float* logits, uint64
                        uint64_t embd, uint32_t row_bytes, uint32_t slot);
 
 hipError_t debug_exp(hipStream_t stream, const double* x, double* y, uint32_t n);
+hipError_t debug_exp2f(hipStream_t stream, const float* x, float* y, uint32_t n);
 
 }  // namespace as_launch

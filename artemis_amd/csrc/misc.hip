@@ -94,6 +94,12 @@ __global__ void exp_kernel(const double* __restrict__ x, double* __restrict__ y,
   if (i < n) y[i] = as_exp::exp(x[i]);
 }
 
+// The hardware 2^x (V_EXP_F32) the scan's sums are built on.
+__global__ void exp2f_kernel(const float* __restrict__ x, float* __restrict__ y, uint32_t n) {
+  const uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) y[i] = __builtin_amdgcn_exp2f(x[i]);
+}
+
 }  // namespace
 
 namespace as_launch {
@@ -120,6 +126,11 @@ hipError_t argmax_rows(hipStream_t stream, bool vec, const float* logits, uint64
 
 hipError_t debug_exp(hipStream_t stream, const double* x, double* y, uint32_t n) {
   hipLaunchKernelGGL(exp_kernel, dim3((n + 255) / 256), dim3(256), 0, stream, x, y, n);
+  return hipGetLastError();
+}
+
+hipError_t debug_exp2f(hipStream_t stream, const float* x, float* y, uint32_t n) {
+  hipLaunchKernelGGL(exp2f_kernel, dim3((n + 255) / 256), dim3(256), 0, stream, x, y, n);
   return hipGetLastError();
 }
 

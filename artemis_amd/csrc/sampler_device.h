@@ -14,16 +14,16 @@ constexpr uint32_t kNone = 0xFFFFFFFFu;
 // Row modes, chosen on the host from the sampling settings (sample.rs:129-150).
 enum : uint32_t {
   kModeGreedy = 0,     // temp <= 0: greedy / greedy_penalized
-  kModeTopK = 1,       // 0 < k < n, k small enough for the segment candidates: draw_full_sort
+  kModeTopK = 1,       // 0 < k < n, k small enough for the slice candidates: draw_full_sort
   kModePartial = 2,    // k == 0 or k >= n: draw_partial
-  kModeExactTopK = 3,  // 0 < k < n with a k too large for the segment candidates
+  kModeExactTopK = 3,  // 0 < k < n with a k too large for the slice candidates
 };
 
 // RowParams.flags
 enum : uint32_t {
   kFlagPenalties = 1u,  // some penalty acts (the reference's `pen != 0.0`)
-  kFlagSumTop = 2u,     // partial with top_p < 1: segment sums of exp(l - m)
-  kFlagSumTemp = 4u,    // partial with no filter: segment sums of exp((l - m) / T)
+  kFlagSumTop = 2u,     // partial with top_p < 1: slice sums of exp(l - m)
+  kFlagSumTemp = 4u,    // partial with no filter: slice sums of exp((l - m) / T)
   kFlagRngWrite = 8u,   // write the advanced RNG state back (batch rows; verify defers it)
   kFlagKept = 16u,      // the caller wants kept lists
 };
@@ -39,28 +39,37 @@ struct RowParams {
   uint32_t mode;
   double ln_min_p;      // log((double)min_p) from the host libm, as f64::ln (sample.rs:181, 217)
   uint32_t flags;
-  uint32_t cand;        // candidates each segment keeps (top-k rows: k)
+  uint32_t cand;        // candidates each wave of a slice keeps (top-k rows: k)
   uint32_t rng_index;   // which 4-word state the row draws from
   uint32_t rng_skip;    // draws to skip first (verify row i skips i)
   uint32_t hist_begin;  // history range when no CSR offsets are given
   uint32_t hist_len;
   uint32_t extra;       // ids of the extra list appended to the history (verify drafts)
-  uint32_t cap;         // most candidates a segment may keep (segments x cap fit the finish LDS)
+  uint32_t cap;         // candidate slots per slice (slices x cap fit the finish LDS)
+  // Written by the scan during a call (uploaded as zero): the largest wave threshold's key any
+  // slice of the row has published, and the largest key any slice has seen (min-p rows).
+  uint32_t share_bound;
+  uint32_t share_top;
 };
 
-// Per (row, segment) results of the scan.
+// Per (row, slice) results of the scan.
 struct SegStats {
   uint32_t nonfinite;   // first index holding NaN/inf in the raw logits, or kNone
   uint32_t greedy_idx;  // IEEE-greater argmax, lowest index on ties, NaN skipped; kNone if none
   float greedy_val;
   uint32_t max_key;     // largest rank key of the penalised values
   uint32_t n_cand;
-  uint32_t truncated;   // bit 0: the segment held more values than it kept as candidates;
-                        // bit 1: the row's history is too long for the scan's u16 counts
-  uint64_t bound;       // a truncated segment kept every value whose packed rank is >= bound,
+  uint32_t truncated;   // bit 0: the slice held more values than it kept as candidates;
+                        // bit 1: the scan could not finish the slice's statistics (more distinct
+                        // history ids than its hash holds, or more candidates than its slots)
+  float err_rel;        // sum's error from its own evaluation: at most err_rel * sum
+  float err_abs;        //   + err_abs * sum_abs
+  uint64_t bound;       // a truncated slice kept every value whose packed rank is >= bound,
                         // and at least `cand` of its values are >= bound
-  double sum;           // sum of exp(d), d = l - m (or (l - m) / T), m = key_value(max_key)
+  double sum;           // sum of exp(d), d = l - m (or (l - m) / T), m = sum_ref
   double sum_abs;       // sum of exp(d) * |d|
+  float sum_ref;        // the sums' reference m: at least every value they hold
+  uint32_t pad_;
 };
 
 // f32::total_cmp as an unsigned key (sample.rs:106-108): larger key = higher rank; +0 above -0.
@@ -80,6 +89,15 @@ __device__ __forceinline__ float packed_value(uint64_t p) { return key_value((ui
 
 __device__ __forceinline__ bool is_finite_bits(float x) {
   return (__float_as_uint(x) & 0x7F800000u) != 0x7F800000u;
+}
+
+// The smallest f32 whose f64 value is >= f (IEEE, so a floor of 0 admits -0 as well): a value x
+// passes min-p's test f64(x) >= f (sample.rs:181, 237) exactly when x >= floor_f32(f).
+__device__ __forceinline__ float floor_f32(double f) {
+  float x = __double2float_rn(f);
+  if ((double)x < f) x = nextafterf(x, __builtin_inff());
+  if (x == 0.0f) x = -0.0f;
+  return x;
 }
 
 // The history penalty for an id seen c >= 1 times, in f32, each operation rounded on its own.

@@ -1,14 +1,32 @@
-// Pass 1 over the logits: one workgroup per 8,192-value segment of a row, the only kernel that
-// reads the rows from HBM. Each thread holds 32 values in registers (eight 16-byte loads, all in
-// flight at once), applies the history penalties from an LDS count table, and produces the
-// segment's share of everything the finish kernel decides from:
-//   - the first non-finite index (sample.rs:22-34),
-//   - greedy's argmax (sample.rs:9-17, 378-396),
-//   - the largest rank key (the `top` of sample.rs:164, 212-216),
-//   - the segment's best candidates in rank order (its top k, or a fixed budget for rows without a
-//     top-k), found by a binary search on the key threshold and compacted to HBM,
-//   - for rows without a top-k, f64 sums of exp(l - m) or exp((l - m) / T) with m the segment's
-//     max, each term with the host-exact exp, and sums of exp(d) * |d| for the error bound.
+// Pass 1 over the logits, the only kernel that streams the rows from HBM: one 256-thread workgroup
+// per slice of a row (about a quarter of a 248,320-value row at batch 256, smaller slices for small
+// batches). Each wave walks its own 1,024-value chunks of the slice (chunks w, w+4, w+8, ...) with
+// the loads of the next chunk in flight while it works on the current one, and with no barrier until
+// the slice ends. Per value it does only what every value needs; what few values need is done when
+// they occur:
+//   - the first non-finite index (sample.rs:22-34): fma(x, 0, acc) turns NaN once any raw value is
+//     NaN or infinite; only then is the slice searched for the index;
+//   - rows with penalties: the history's ids in this slice are marked in an LDS bitmap and counted
+//     in an LDS hash; the stream leaves them out, and at the end of the slice each one's penalised
+//     value (sample.rs:308-323, extended to a count) joins the candidates, the maximum and the sums;
+//   - greedy rows: each lane's running argmax by IEEE `>`, lowest index (sample.rs:9-17, 378-396),
+//     updated value by value only in the chunks whose maximum beats it;
+//   - rows that draw: each wave keeps, in an LDS buffer, every value of its stream that ranks at or
+//     above its threshold tau; values are tested four at a time by their maximum. tau rises when the
+//     buffer holds a few times C values (C = top_k, or a fixed depth for rows without a top-k) to the
+//     C-th best it holds, and the wave publishes that key to the row's shared word with a
+//     device-wide atomic max. Every wave of the row reads the word once per two chunks and raises its
+//     own tau to it: for a top-k row a wave holding k values at or above a key proves that no value
+//     below it is among the row's k best (sample.rs:157-166), so all slices filter with the best
+//     bound any of them has found. Rows with min-p also share the largest value seen, and no wave
+//     keeps a value below that value plus ln(min_p) (sample.rs:181, 237);
+//   - rows without a top-k whose cut or draw needs the row's total (sample.rs:218-222, 274-282):
+//     sums of exp(l - ref) or exp((l - ref) / T), ref each lane's running maximum of the raw values
+//     (moved once per chunk), each term from the hardware's f32 exp2, a chunk's 16 terms added in a
+//     tree in f32 and then into f64, with a per-slice bound on their error and sums of exp(d) * |d|
+//     for the finish kernel's error bound.
+// At the end of the slice every kept value ranking at or above the slice's bound (the highest wave
+// threshold and the row's shared one) goes to HBM.
 #include "sampler_device.h"
 #include "launch.h"
 
@@ -18,75 +36,604 @@ namespace {
 
 constexpr int kThreads = 256;
 constexpr int kWaves = kThreads / kWave;
-constexpr int kPer = 32;
-constexpr int kVec = kPer / 4;
+constexpr int kU = 4;                           // 16-byte loads per lane per chunk
+constexpr uint32_t kChunk = kWave * 4 * kU;     // values per wave chunk (1,024)
+constexpr uint32_t kGroupStep = kWaves * kChunk;
+constexpr uint32_t kCapW = as_launch::kWaveCap;
+constexpr int kQ = kCapW / kWave;               // buffer entries per lane when a wave reads it whole
+constexpr uint32_t kRoom = 4 * kWave;           // the most one 16-byte group per lane appends
+constexpr uint32_t kHash = as_launch::kHistSlots;
+constexpr int kHashPer = kHash / kThreads;
+constexpr int kHashShift = 32 - __builtin_ctz(kHash);  // the multiplicative hash's top bits
+static_assert((kHash & (kHash - 1)) == 0, "a power of two");
+constexpr uint32_t kEmpty = 0xFFFFFFFFu;
 typedef float f32x4 __attribute__((ext_vector_type(4)));
-static_assert(kThreads * kPer == as_launch::kSegment, "segment size");
+static_assert(kCapW % kWave == 0 && kHash % kThreads == 0, "sizes");
+static_assert(as_launch::kSliceAlign % kChunk == 0, "slices start on a chunk");
+static_assert(as_launch::kTopKMax + kRoom <= kCapW, "a select always frees room");
 
-// Exclusive prefix sum over the block (in thread order) of one u32 per thread; *total gets the sum.
-__device__ uint32_t block_exclusive_scan(uint32_t x, uint32_t* wave_tot, uint32_t* total) {
-  const int lane = threadIdx.x & (kWave - 1), w = threadIdx.x / kWave;
-  uint32_t incl = x;
-  for (int o = 1; o < kWave; o <<= 1) {
-    uint32_t y = (uint32_t)__shfl_up((int)incl, o, kWave);
-    if (lane >= o) incl += y;
+// What a slice computes besides the non-finite check.
+enum Kind : int {
+  kKindPlain = 0,      // greedy rows (and rows the finish kernel settles on its own)
+  kKindCand = 1,       // candidates (with min-p's floor when the row has one)
+  kKindSumTop = 2,     // candidates and sums of exp(l - m)
+  kKindSumTemp = 3,    // candidates and sums of exp((l - m) / T)
+};
+
+struct Shared {
+  uint64_t buf[kWaves][kCapW];
+  uint32_t bitmap[as_launch::kSliceMax / 32];
+  uint32_t hid[kHash];
+  uint32_t hcnt[kHash];
+  uint64_t red_p[kWaves];
+  uint32_t red_u[kWaves];
+  uint32_t red_u2[kWaves];
+  uint32_t red_u3[kWaves];
+  float red_f[kWaves];
+  double red_d[kWaves];
+  double red_d2[kWaves];
+  uint32_t hist_out;
+  uint32_t overflow;
+  uint32_t out_n;  // candidates the waves have written to HBM during the stream
+};
+// The workgroup's LDS, at file scope so that the out-of-line helpers below address it directly.
+__shared__ Shared g_sh;
+
+__device__ __forceinline__ uint32_t lanes_below(uint64_t m) {
+  return __builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0u));
+}
+__device__ __forceinline__ uint64_t wave_min_u64(uint64_t v) {
+  for (int o = 32; o > 0; o >>= 1) {
+    const uint64_t u = __shfl_xor(v, o, kWave);
+    v = u < v ? u : v;
   }
-  __syncthreads();
-  if (lane == kWave - 1) wave_tot[w] = incl;
-  __syncthreads();
-  uint32_t before = 0, all = 0;
-  for (int k = 0; k < kWaves; ++k) {
-    if (k < w) before += wave_tot[k];
-    all += wave_tot[k];
-  }
-  *total = all;
-  return before + incl - x;
+  return v;
 }
 
-template <bool kVecLoad>
-__global__ __launch_bounds__(kThreads) void scan_kernel(
-    const float* __restrict__ logits, uint64_t row_stride, uint32_t n, uint32_t n_seg,
-    const RowParams* __restrict__ params, const uint32_t* __restrict__ hist_off,
-    const uint32_t* __restrict__ hist_ids, const uint32_t* __restrict__ extra_ids,
-    SegStats* __restrict__ stats, uint64_t* __restrict__ cands, uint32_t cand_stride) {
-  __shared__ uint32_t cnt[as_launch::kSegment / 2];  // u16 history counts, two per word
-  __shared__ uint64_t tab[256];
-  __shared__ uint32_t red_u[kWaves];
-  __shared__ uint32_t red_u2[kWaves];
-  __shared__ double red_d[kWaves];
-  __shared__ uint32_t tm[2 * kThreads];
-  __shared__ uint32_t slot;
+// The row's shared words (RowParams::share_bound, share_top), at device scope: the slices of a row
+// run on different XCDs.
+__device__ __forceinline__ void publish(uint32_t* word, uint32_t key) {
+  if (word && (threadIdx.x & (kWave - 1)) == 0)
+    __hip_atomic_fetch_max(word, key, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ uint64_t read_shared(uint32_t* words) {
+  return __hip_atomic_load(reinterpret_cast<uint64_t*>(words), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
 
-  const uint32_t row = blockIdx.y, seg = blockIdx.x, tid = threadIdx.x;
-  const RowParams p = params[row];
-  const uint32_t base = seg * (uint32_t)as_launch::kSegment;
-  const uint32_t len = min((uint32_t)as_launch::kSegment, n - base);
-  const float* src = logits + (uint64_t)row * row_stride + base;
+// A wave's candidate buffer (g_sh.buf[wave]): it holds every value of the wave's stream so far
+// whose packed rank is >= tau (tau 0: every value), `cnt` entries, some of which may rank below tau.
+// The same in every lane; passed and returned by value so that the out-of-line helpers keep it in
+// registers.
+struct WaveState {
+  uint32_t cnt;
+  float tau_f;   // the value of tau's key: a value below it cannot rank >= tau
+  uint64_t tau;
+  uint32_t top;  // min-p rows: the largest key the wave knows the row to hold (0: none yet)
+  uint32_t C;    // the count a select keeps (at most C + C / 4 of them)
+  uint32_t sel;  // the buffer count at which a chunk ends with a select
+  bool spill;    // min-p rows keeping every value above the floor: a full buffer goes to HBM
+};
 
-  float v[kPer];
-  if (kVecLoad && len == (uint32_t)as_launch::kSegment) {
-    // A full segment: eight unconditional 16-byte loads, all in flight before the first use.
-    f32x4 q[kVec];
+// Selects run once the buffer holds twice C (at least C + 64), and whenever it might overflow.
+__device__ __forceinline__ uint32_t select_at(uint32_t C) { return min(max(2 * C, C + 64), kCapW - kRoom); }
+
+__device__ __forceinline__ void raise_tau(WaveState& ws, uint64_t t) {
+  if (t > ws.tau) {
+    ws.tau = t;
+    ws.tau_f = key_value((uint32_t)(t >> 32));
+  }
+}
+
+// min-p's floor for a row whose largest value has key `top`: the smallest value that can be kept.
+__device__ __forceinline__ uint64_t floor_tau(uint32_t top, double ln_min_p) {
+  return (uint64_t)total_key(floor_f32((double)key_value(top) + ln_min_p)) << 32;
+}
+
+// A packed rank t with at least C and at most C + slack of the kN values per lane (0: none) at or
+// above it, as high as that allows: by ballot counts on the key, halving the key range until the
+// count at its low end is within the slack, then (slack 0, or heavy ties) among ties at that key on
+// the low word. 0 when fewer than C values are given. Every given value's key must be >= lo.
+template <int kN>
+__device__ __forceinline__ uint64_t wave_kth(const uint64_t (&ent)[kN], uint32_t C, uint32_t lo, uint32_t slack) {
+  uint32_t kmax = 0, total = 0;
 #pragma unroll
-    for (int j = 0; j < kVec; ++j)
-      q[j] = __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(src + (j * kThreads + tid) * 4));
+  for (int q = 0; q < kN; ++q) {
+    if (ent[q] != 0ull) kmax = max(kmax, (uint32_t)(ent[q] >> 32));
+    total += (uint32_t)__popcll(__ballot(ent[q] != 0ull));
+  }
+  if (total < C || C == 0) return 0ull;
+  if (total <= C + slack) return (uint64_t)lo << 32;
+  kmax = wave_max_u32(kmax);
+  uint64_t hi = (uint64_t)kmax + 1;  // count(key >= hi) = 0 < C; count(key >= lo) >= C
+  uint32_t c_hi = 0;
+  while (hi - lo > 1) {
+    const uint32_t mid = (uint32_t)(lo + ((hi - lo) >> 1));
+    uint32_t c = 0;
 #pragma unroll
-    for (int j = 0; j < kVec; ++j) {
-      v[4 * j + 0] = q[j][0];
-      v[4 * j + 1] = q[j][1];
-      v[4 * j + 2] = q[j][2];
-      v[4 * j + 3] = q[j][3];
-    }
-  } else {
-#pragma unroll
-    for (int j = 0; j < kVec; ++j) {
-      const uint32_t e = (j * kThreads + tid) * 4;
-#pragma unroll
-      for (int c = 0; c < 4; ++c) v[4 * j + c] = (e + c < len) ? src[e + c] : 0.0f;
+    for (int q = 0; q < kN; ++q) c += (uint32_t)__popcll(__ballot(ent[q] != 0ull && (uint32_t)(ent[q] >> 32) >= mid));
+    if (c >= C) {
+      lo = mid;
+      if (c <= C + slack) return (uint64_t)lo << 32;
+    } else {
+      hi = mid;
+      c_hi = c;
     }
   }
-  // History ids are loaded now, while the logits are in flight: the first 8 per thread (a
-  // 2,048-id history in one go), the rest later.
+  uint32_t c_ge = 0;
+#pragma unroll
+  for (int q = 0; q < kN; ++q) c_ge += (uint32_t)__popcll(__ballot(ent[q] != 0ull && (uint32_t)(ent[q] >> 32) >= lo));
+  if (c_ge <= C + slack && c_ge != C) return (uint64_t)lo << 32;
+  if (c_ge == C) {
+    uint64_t mn = ~0ull;
+#pragma unroll
+    for (int q = 0; q < kN; ++q)
+      if (ent[q] != 0ull && (uint32_t)(ent[q] >> 32) >= lo && ent[q] < mn) mn = ent[q];
+    return wave_min_u64(mn);
+  }
+  // c_hi < C < c_ge: the C - c_hi ties at lo with the largest low words (the lowest ids).
+  const uint32_t need = C - c_hi;
+  uint64_t l2 = 0, h2 = 1ull << 32;
+  while (h2 - l2 > 1) {
+    const uint32_t mid = (uint32_t)(l2 + ((h2 - l2) >> 1));
+    uint32_t c = 0;
+#pragma unroll
+    for (int q = 0; q < kN; ++q)
+      c += (uint32_t)__popcll(__ballot(ent[q] != 0ull && (uint32_t)(ent[q] >> 32) == lo && (uint32_t)ent[q] >= mid));
+    if (c >= need) l2 = mid;
+    else h2 = mid;
+  }
+  return ((uint64_t)lo << 32) | l2;
+}
+
+// Drops the entries below tau (which may have risen since they were appended) and, when more than
+// C remain, keeps the best C to C + slack, raises tau to the last kept and publishes its key to the
+// row (share null: not). Every value the wave streams later has a larger id than those held, so the
+// buffer stays exactly the wave's values >= tau. kN: entries read per lane (cnt <= kN * 64). Out of
+// line: it runs a few times a slice.
+template <int kN>
+__device__ __noinline__ WaveState wave_select(WaveState ws, uint32_t C, uint32_t slack, uint32_t* share) {
+  const uint32_t lane = threadIdx.x & (kWave - 1);
+  uint64_t* buf = g_sh.buf[threadIdx.x / kWave];
+  uint64_t ent[kN];
+  uint32_t n_ge = 0;
+#pragma unroll
+  for (int q = 0; q < kN; ++q) {
+    const uint32_t i = lane + q * kWave;
+    const uint64_t e = (i < ws.cnt) ? buf[i] : 0ull;
+    ent[q] = e >= ws.tau ? e : 0ull;
+    n_ge += (uint32_t)__popcll(__ballot(ent[q] != 0ull));
+  }
+  if (n_ge > C) {
+    const uint64_t t = wave_kth<kN>(ent, C, (uint32_t)(ws.tau >> 32), slack);
+    raise_tau(ws, t);
+    publish(share, (uint32_t)(t >> 32));
+  }
+  uint32_t run = 0;
+#pragma unroll
+  for (int q = 0; q < kN; ++q) {
+    const bool keep = ent[q] != 0ull && ent[q] >= ws.tau;
+    const uint64_t m = __ballot(keep);
+    if (keep) buf[run + lanes_below(m)] = ent[q];
+    run += (uint32_t)__popcll(m);
+  }
+  ws.cnt = run;
+  return ws;
+}
+
+__device__ __forceinline__ void select_now(WaveState& ws, uint32_t C, uint32_t slack, uint32_t* share) {
+  if (ws.cnt <= 2 * kWave) ws = wave_select<2>(ws, C, slack, share);
+  else if (ws.cnt <= 6 * kWave) ws = wave_select<6>(ws, C, slack, share);
+  else ws = wave_select<kQ>(ws, C, slack, share);
+  static_assert(kQ > 6, "three sizes");
+}
+
+// A min-p row's full buffer: the entries >= tau (the floor may have risen since they were appended)
+// stay when they are at most C; otherwise they go to the slice's candidates in HBM, after those
+// already there, and the buffer empties. When they would pass `room`, the floor set is too large to
+// keep whole: the wave keeps its best kPartialRank from then on, like a row without min-p (the floor
+// still applies). Out of line: it runs when a min-p row's buffer fills.
+__device__ __noinline__ WaveState spill(WaveState ws, uint64_t* out, uint32_t room, uint32_t* share) {
+  const uint32_t lane = threadIdx.x & (kWave - 1);
+  uint64_t* buf = g_sh.buf[threadIdx.x / kWave];
+  uint64_t ent[kQ];
+  uint32_t n_ge = 0;
+#pragma unroll
+  for (int q = 0; q < kQ; ++q) {
+    const uint32_t i = lane + q * kWave;
+    const uint64_t e = (i < ws.cnt) ? buf[i] : 0ull;
+    ent[q] = e >= ws.tau ? e : 0ull;
+    n_ge += (uint32_t)__popcll(__ballot(ent[q] != 0ull));
+  }
+  if (n_ge <= ws.C) {
+    uint32_t run = 0;
+#pragma unroll
+    for (int q = 0; q < kQ; ++q) {
+      const bool keep = ent[q] != 0ull;
+      const uint64_t m = __ballot(keep);
+      if (keep) buf[run + lanes_below(m)] = ent[q];
+      run += (uint32_t)__popcll(m);
+    }
+    ws.cnt = run;
+    return ws;
+  }
+  uint32_t base = kNone;
+  if (lane == 0) {
+    uint32_t old = g_sh.out_n;
+    while (old + n_ge <= room) {
+      const uint32_t prev = atomicCAS(&g_sh.out_n, old, old + n_ge);
+      if (prev == old) {
+        base = old;
+        break;
+      }
+      old = prev;
+    }
+  }
+  base = __builtin_amdgcn_readfirstlane(base);
+  if (base == kNone) {
+    ws.spill = false;
+    ws.C = as_launch::kPartialRank;
+    ws.sel = select_at(ws.C);
+    select_now(ws, ws.C, ws.C / 4, share);
+    return ws;
+  }
+  uint32_t run = base;
+#pragma unroll
+  for (int q = 0; q < kQ; ++q) {
+    const bool keep = ent[q] != 0ull;
+    const uint64_t m = __ballot(keep);
+    if (keep) out[run + lanes_below(m)] = ent[q];
+    run += (uint32_t)__popcll(m);
+  }
+  ws.cnt = 0;
+  return ws;
+}
+
+// The starting threshold from the wave's first chunk (16 values per lane, those with a bit set in
+// `masked` left out): the lane's two best by rank, then the wave's C-th best of those 128, which at
+// least C values of the chunk meet (with C above 128, the 128th); published to the row. Fewer valid
+// values leave it at 0. Out of line: it runs once a slice.
+__device__ __noinline__ WaveState first_tau(WaveState ws, f32x4 v0, f32x4 v1, f32x4 v2, f32x4 v3,
+                                            uint32_t masked, uint32_t e0, uint32_t C, uint32_t* share) {
+  const f32x4 v[kU] = {v0, v1, v2, v3};
+  uint64_t top[2] = {0ull, 0ull};
+#pragma unroll
+  for (int j = 0; j < kU; ++j) {
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      if ((masked >> (4 * j + c)) & 1u || !is_finite_bits(v[j][c])) continue;
+      const uint64_t pk = pack(total_key(v[j][c]), e0 + j * (kWave * 4) + c);
+      if (pk > top[0]) {
+        top[1] = top[0];
+        top[0] = pk;
+      } else if (pk > top[1]) {
+        top[1] = pk;
+      }
+    }
+  }
+  const uint64_t t = wave_kth<2>(top, min(C, 2u * kWave), 0u, 0u);
+  if (t != 0ull) {
+    raise_tau(ws, t);
+    publish(share, (uint32_t)(t >> 32));
+  }
+  return ws;
+}
+
+// The largest unmasked value of the wave's first chunk sets min-p's first floor. When two in five
+// of the chunk's values pass it (min_p so small that the floor bounds nothing), the wave keeps its
+// best kPartialRank like a row without min-p instead of every value above the floor (which still
+// applies). Out of line.
+__device__ __noinline__ WaveState first_floor(WaveState ws, f32x4 v0, f32x4 v1, f32x4 v2, f32x4 v3,
+                                              uint32_t masked, uint32_t e0, double ln_min_p, uint32_t* share) {
+  const f32x4 v[kU] = {v0, v1, v2, v3};
+  uint32_t k = 0;
+#pragma unroll
+  for (int j = 0; j < kU; ++j)
+#pragma unroll
+    for (int c = 0; c < 4; ++c)
+      if (!((masked >> (4 * j + c)) & 1u) && is_finite_bits(v[j][c])) k = max(k, total_key(v[j][c]));
+  k = wave_max_u32(k);
+  if (k > ws.top) {
+    ws.top = k;
+    publish(share + 1, k);
+    raise_tau(ws, floor_tau(k, ln_min_p));
+  }
+  uint32_t n_f = 0, n_v = 0;
+#pragma unroll
+  for (int j = 0; j < kU; ++j)
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      const bool valid = !((masked >> (4 * j + c)) & 1u);
+      n_v += (uint32_t)__popcll(__ballot(valid));
+      n_f += (uint32_t)__popcll(__ballot(valid && v[j][c] >= ws.tau_f));
+    }
+  if (5 * n_f > 2 * n_v && ws.C > as_launch::kPartialRank) {
+    ws.spill = false;
+    ws.C = as_launch::kPartialRank;
+    ws.sel = select_at(ws.C);
+    ws = first_tau(ws, v0, v1, v2, v3, masked, e0, ws.C, share);
+  }
+  return ws;
+}
+
+struct Slice {
+  const float* x;       // the row
+  const float* zero;    // kChunk readable zeros, for the loads of a wave with no full chunk
+  uint32_t* share;      // the row's shared words
+  uint32_t b0, b1;      // the slice's values [b0, b1)
+  uint32_t C;           // candidates per wave
+  uint64_t* out;        // the slice's candidates in HBM
+  uint32_t room;        // how many of them the stream may write
+  bool first;           // the first chunk sets tau
+  bool pen;             // history values are left out of the stream
+  bool floor_on;        // min-p's floor applies to the candidates (a row without a top-k)
+  float scale;          // log2(e), or log2(e) / T for sums of exp((l - m) / T)
+  double ln_min_p;
+};
+
+// The bits of values e0 .. e0+3 (e0 - b0 a multiple of 4, e0 < b1) in the slice's history bitmap.
+__device__ __forceinline__ uint32_t hist_nibble(const Slice& sl, uint32_t e0) {
+  const uint32_t off = e0 - sl.b0;
+  return (g_sh.bitmap[off >> 5] >> (off & 31u)) & 15u;
+}
+// The values of a 16-byte group the stream leaves out: history ids and, in the tail, those past b1.
+template <bool kTail>
+__device__ __forceinline__ uint32_t group_mask(const Slice& sl, uint32_t e0) {
+  uint32_t m = 0;
+  if (sl.pen && (!kTail || e0 < sl.b1)) m = hist_nibble(sl, e0);
+  if (kTail) {
+#pragma unroll
+    for (int c = 0; c < 4; ++c)
+      if (e0 + c >= sl.b1) m |= 1u << c;
+  }
+  return m;
+}
+
+struct Lane {
+  float nfa;        // fma(x, 0, nfa) over the raw values: NaN once one is NaN or infinite
+  float gv;         // greedy
+  uint32_t gi;
+  uint32_t amax;    // the largest key this lane appended
+  float ref;        // the lane's largest raw value so far (-inf before any)
+  double s;         // sum of exp2(t), t = (l - ref) * scale
+  float sa;         // sum of exp2(t) * |t|: an error-bound term, kept roughly
+  uint32_t moves;   // times ref moved while s held terms
+};
+
+// Appends the values e0 .. e0+3 of one 16-byte group that reach tau's value and are not masked to
+// the wave's buffer, first making room when it might not take four more per lane.
+__device__ __forceinline__ void append4(WaveState& ws, Lane& ln, const f32x4& v, uint32_t e0, uint32_t mask,
+                                        const Slice& sl) {
+  if (ws.cnt > kCapW - kRoom) {
+    if (ws.spill) ws = spill(ws, sl.out, sl.room, sl.share);
+    else select_now(ws, ws.C, ws.C / 4, sl.share);
+  }
+  uint64_t* buf = g_sh.buf[threadIdx.x / kWave];
+#pragma unroll
+  for (int c = 0; c < 4; ++c) {
+    const bool take = v[c] >= ws.tau_f && !((mask >> c) & 1u);
+    const uint64_t m = __ballot(take);
+    if (m == 0ull) continue;
+    if (take) {
+      const uint32_t key = total_key(v[c]);
+      buf[ws.cnt + lanes_below(m)] = pack(key, e0 + c);
+      ln.amax = max(ln.amax, key);
+    }
+    ws.cnt += (uint32_t)__popcll(m);
+  }
+}
+
+// exp2 through the hardware (V_EXP_F32). Its error is bounded per term by the callers: the
+// instruction's own (kExpUlp units of 2^-23), plus at most 4 * 2^-24 * |t| for the roundings of t
+// (the difference, the rounded scale and the product).
+constexpr float kLog2e = 1.44269502f;
+constexpr float kExpUlp = 2.0f;
+
+// Moves the lane's reference up to m (> ref): the sums are rescaled by exp2(-dt) and every |t| they
+// hold grows by dt.
+__device__ __forceinline__ void move_ref(Lane& ln, float m, float scale) {
+  if (ln.s != 0.0) {
+    const float dt = (m - ln.ref) * scale;
+    const float sc = __builtin_amdgcn_exp2f(-dt);
+    ln.sa = sc * fmaf((float)ln.s, dt, ln.sa);
+    ln.s = ln.s * (double)sc;
+    ++ln.moves;
+  }
+  ln.ref = m;
+}
+
+// One wave chunk: kU 16-byte groups per lane, group j of lane l at e = c0 + j*256 + l*4. kFirst: the
+// wave's first chunk, which sets the starting threshold.
+template <int kKind, bool kTail, bool kFirst>
+__device__ __forceinline__ void chunk(Lane& ln, WaveState& ws, const Slice& sl,
+                                      const f32x4 (&q)[kU], uint32_t c0) {
+  const uint32_t lane = threadIdx.x & (kWave - 1);
+  constexpr bool kSums = kKind == kKindSumTop || kKind == kKindSumTemp;
+#pragma unroll
+  for (int j = 0; j < kU; ++j)
+#pragma unroll
+    for (int c = 0; c < 4; ++c) ln.nfa = fmaf(q[j][c], 0.0f, ln.nfa);
+
+  if (kKind == kKindPlain) {
+    float cm = q[0][0];
+#pragma unroll
+    for (int j = 0; j < kU; ++j)
+#pragma unroll
+      for (int c = 0; c < 4; ++c) cm = fmaxf(cm, q[j][c]);
+    if (cm > ln.gv || ln.gi == kNone || kTail) {
+#pragma unroll
+      for (int j = 0; j < kU; ++j) {
+        const uint32_t e0 = c0 + j * (kWave * 4) + lane * 4;
+        const uint32_t m = group_mask<kTail>(sl, e0);
+#pragma unroll
+        for (int c = 0; c < 4; ++c)
+          if (!((m >> c) & 1u) && (q[j][c] > ln.gv || ln.gi == kNone)) {
+            ln.gv = q[j][c];
+            ln.gi = e0 + c;
+          }
+      }
+    }
+    return;
+  }
+
+  constexpr bool kMasks = kFirst || kSums || kTail;
+  uint32_t mask[kU];
+#pragma unroll
+  for (int j = 0; j < kU; ++j) mask[j] = kMasks ? group_mask<kTail>(sl, c0 + j * (kWave * 4) + lane * 4) : 0u;
+
+  if (kFirst) {
+    const uint32_t all = mask[0] | mask[1] << 4 | mask[2] << 8 | mask[3] << 12;
+    if (sl.floor_on) ws = first_floor(ws, q[0], q[1], q[2], q[3], all, c0 + lane * 4, sl.ln_min_p, sl.share);
+    else if (sl.first) ws = first_tau(ws, q[0], q[1], q[2], q[3], all, c0 + lane * 4, ws.C, sl.share);
+  }
+  float m4[kU];
+#pragma unroll
+  for (int j = 0; j < kU; ++j) {
+    const f32x4 v = q[j];
+    m4[j] = fmaxf(fmaxf(v[0], v[1]), fmaxf(v[2], v[3]));
+    if (__builtin_expect(__ballot(m4[j] >= ws.tau_f) != 0ull, 0)) {
+      const uint32_t e0 = c0 + j * (kWave * 4) + lane * 4;
+      append4(ws, ln, v, e0, kMasks ? mask[j] : group_mask<kTail>(sl, e0), sl);
+    }
+  }
+  // min-p: a new largest value raises the floor.
+  if (sl.floor_on && __ballot(ln.amax > ws.top) != 0ull) {
+    const uint32_t k = wave_max_u32(ln.amax);
+    ws.top = k;
+    publish(sl.share + 1, k);
+    raise_tau(ws, floor_tau(k, sl.ln_min_p));
+  }
+  if (ws.cnt >= ws.sel && !ws.spill) select_now(ws, ws.C, ws.C / 4, sl.share);
+
+  if (kSums) {
+    const float cm = fmaxf(fmaxf(m4[0], m4[1]), fmaxf(m4[2], m4[3]));
+    if (cm > ln.ref) move_ref(ln, cm, sl.scale);
+    float g[kU], ga = ln.sa;
+#pragma unroll
+    for (int j = 0; j < kU; ++j) {
+      float e[4];
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        const float t = (q[j][c] - ln.ref) * sl.scale;
+        e[c] = ((mask[j] >> c) & 1u) ? 0.0f : __builtin_amdgcn_exp2f(t);
+        ga = fmaf(e[c], -t, ga);
+      }
+      g[j] = (e[0] + e[1]) + (e[2] + e[3]);
+    }
+    ln.s = ln.s + (double)((g[0] + g[1]) + (g[2] + g[3]));
+    ln.sa = ga;
+  }
+}
+
+template <bool kVec>
+__device__ __forceinline__ void load_chunk(f32x4 (&q)[kU], const float* x, uint32_t c0) {
+#pragma unroll
+  for (int j = 0; j < kU; ++j) {
+    const uint32_t e0 = c0 + j * (kWave * 4) + (threadIdx.x & (kWave - 1)) * 4;
+    if (kVec) {
+      q[j] = __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(x + e0));
+    } else {
+#pragma unroll
+      for (int c = 0; c < 4; ++c) q[j][c] = x[e0 + c];
+    }
+  }
+}
+__device__ __forceinline__ void load_tail(f32x4 (&q)[kU], const float* x, uint32_t c0, uint32_t b1) {
+#pragma unroll
+  for (int j = 0; j < kU; ++j) {
+    const uint32_t e0 = c0 + j * (kWave * 4) + (threadIdx.x & (kWave - 1)) * 4;
+#pragma unroll
+    for (int c = 0; c < 4; ++c) q[j][c] = (e0 + c < b1) ? x[e0 + c] : 0.0f;
+  }
+}
+
+// The wave's chunks c(i) = c0 + i*kGroupStep, nfull of them full. A load index past the last full
+// chunk is clamped to it (or to the zero buffer when there is none), so that every load is issued
+// unconditionally and the waits stay exact.
+struct Walk {
+  uint32_t c0, nfull;
+};
+
+template <bool kVec>
+__device__ __forceinline__ void load_at(f32x4 (&q)[kU], const Slice& sl, const Walk& wk, uint32_t i) {
+  if (wk.nfull) load_chunk<kVec>(q, sl.x, wk.c0 + min(i, wk.nfull - 1) * kGroupStep);
+  else load_chunk<kVec>(q, sl.zero, 0);
+}
+
+// The row's shared words as read: the published bound, and min-p's largest key.
+__device__ __forceinline__ void apply_shared(WaveState& ws, const Slice& sl, uint64_t w) {
+  const uint32_t b = __builtin_amdgcn_readfirstlane((uint32_t)w);
+  raise_tau(ws, (uint64_t)b << 32);
+  if (sl.floor_on) {
+    const uint32_t top = __builtin_amdgcn_readfirstlane((uint32_t)(w >> 32));
+    if (top > ws.top) {
+      ws.top = top;
+      raise_tau(ws, floor_tau(top, sl.ln_min_p));
+    }
+  }
+}
+
+// The walk: qa and qb hold chunks 0 and 1 (as loaded); chunk i+1 is in flight while chunk i is
+// worked on, and the row's shared words are read once per two chunks; then the partial chunk at the
+// slice's end.
+template <int kKind, bool kVec>
+__device__ __forceinline__ void stream(Lane& ln, WaveState& ws, const Slice& sl,
+                                       const Walk& wk, f32x4 (&qa)[kU], f32x4 (&qb)[kU]) {
+  constexpr bool kShare = kKind != kKindPlain;
+  const uint32_t nfull = wk.nfull;
+  if (nfull > 0) {
+    chunk<kKind, false, true>(ln, ws, sl, qa, wk.c0);
+    for (uint32_t i = 1; i < nfull; i += 2) {
+      const uint64_t w = kShare ? read_shared(sl.share) : 0ull;
+      load_at<kVec>(qa, sl, wk, i + 1);
+      chunk<kKind, false, false>(ln, ws, sl, qb, wk.c0 + i * kGroupStep);
+      if (kShare) apply_shared(ws, sl, w);
+      if (i + 1 >= nfull) break;
+      load_at<kVec>(qb, sl, wk, i + 2);
+      chunk<kKind, false, false>(ln, ws, sl, qa, wk.c0 + (i + 1) * kGroupStep);
+    }
+  }
+  const uint32_t ct = wk.c0 + nfull * kGroupStep;
+  if (ct < sl.b1) {
+    f32x4 q[kU];
+    load_tail(q, sl.x, ct, sl.b1);
+    if (nfull == 0) chunk<kKind, true, true>(ln, ws, sl, q, ct);
+    else chunk<kKind, true, false>(ln, ws, sl, q, ct);
+  }
+}
+
+template <bool kVec>
+__global__ __launch_bounds__(kThreads, 3) void scan_kernel(
+    const float* __restrict__ logits, const float* __restrict__ zero, uint64_t row_stride, uint32_t n,
+    uint32_t n_seg, uint32_t slice_len, RowParams* params,
+    const uint32_t* __restrict__ hist_off, const uint32_t* __restrict__ hist_ids,
+    const uint32_t* __restrict__ extra_ids, SegStats* __restrict__ stats, uint64_t* __restrict__ cands,
+    uint32_t cand_stride) {
+  Shared& sh = g_sh;
+  const uint32_t row = blockIdx.y, seg = blockIdx.x, tid = threadIdx.x;
+  const uint32_t lane = tid & (kWave - 1), w = tid / kWave;
+  const RowParams& p = params[row];
+
+  Slice sl;
+  sl.x = logits + (uint64_t)row * row_stride;
+  sl.zero = zero;
+  sl.share = &params[row].share_bound;
+  sl.b0 = seg * slice_len;
+  sl.out = cands + ((uint64_t)row * n_seg + seg) * cand_stride;
+  sl.room = cand_stride > as_launch::kHistReserve ? cand_stride - as_launch::kHistReserve : 0u;
+  sl.b1 = min(sl.b0 + slice_len, n);
+  const uint32_t mode = p.mode, flags = p.flags;
+  sl.floor_on = mode == kModePartial && p.min_p > 0.0f;
+  sl.ln_min_p = p.ln_min_p;
+  int kind = kKindPlain;
+  if (mode == kModeTopK || mode == kModePartial) {
+    kind = (flags & kFlagSumTemp) ? kKindSumTemp : (flags & kFlagSumTop) ? kKindSumTop : kKindCand;
+  }
+  sl.scale = kind == kKindSumTemp ? (1.0f / p.temp) * kLog2e : kLog2e;
+  sl.C = (kind == kKindPlain) ? 0u : max(p.cand, 1u);
+  // A top-k row's tau must have k values at or above it; rows without a top-k take the best the
+  // first chunk gives.
+  sl.first = mode == kModeTopK ? sl.C <= 2u * kWave : true;
+
   uint32_t hb = 0, he = 0;
   if (hist_ids) {
     if (hist_off) {
@@ -98,259 +645,300 @@ __global__ __launch_bounds__(kThreads) void scan_kernel(
     }
   }
   const uint32_t extra = extra_ids ? p.extra : 0;
-  // Counts are u16 here; a longer history is left to the exact path's u32 counts.
-  const bool long_history = (uint64_t)(he - hb) + extra > 0xFFFFu;
-  const bool pen = (p.flags & kFlagPenalties) && (he > hb || extra > 0) && !long_history;
+  sl.pen = (flags & kFlagPenalties) && (he > hb || extra > 0);
+  const uint32_t len = sl.b1 - sl.b0;
+
+  // In flight together: the first history ids (kHistRegs per thread), then the wave's first two
+  // chunks; the ids come back first and the LDS tables are built while the chunks arrive.
   constexpr int kHistRegs = 8;
   uint32_t hreg[kHistRegs];
-  if (pen && he > hb) {
 #pragma unroll
-    for (int q = 0; q < kHistRegs; ++q) hreg[q] = hist_ids[min(hb + tid + q * kThreads, he - 1)];
+  for (int k = 0; k < kHistRegs; ++k) {
+    const uint32_t h = hb + tid + k * kThreads;
+    hreg[k] = (sl.pen && h < he) ? hist_ids[h] : kEmpty;
   }
-  tab[tid] = as_exp::kTable[tid];
+  Walk wk;
+  wk.c0 = sl.b0 + w * kChunk;
+  wk.nfull = (wk.c0 + kChunk <= sl.b1) ? (sl.b1 - wk.c0 - kChunk) / kGroupStep + 1 : 0;
+  f32x4 qa[kU], qb[kU];
+  load_at<kVec>(qa, sl, wk, 0);
+  load_at<kVec>(qb, sl, wk, 1);
 
-  // The raw row's first non-finite value.
-  uint32_t bad = kNone;
-#pragma unroll
-  for (int q = 0; q < kPer; ++q) {
-    const uint32_t e = ((q / 4) * kThreads + tid) * 4 + (q & 3);
-    if (e < len && !is_finite_bits(v[q])) bad = min(bad, base + e);
+  if (tid == 0) {
+    sh.hist_out = 0;
+    sh.overflow = 0;
+    sh.out_n = 0;
   }
-  bad = block_min_u32<kWaves>(bad, red_u);
-
-  // Penalties from the history (and, for verify rows, the drafts before the row).
-  if (pen && bad == kNone) {
-    for (int i = tid; i < as_launch::kSegment / 2; i += kThreads) cnt[i] = 0;
+  if (sl.pen) {
+    for (uint32_t i = tid; i < (len + 31) / 32; i += kThreads) sh.bitmap[i] = 0;
+    for (uint32_t i = tid; i < kHash; i += kThreads) {
+      sh.hid[i] = kEmpty;
+      sh.hcnt[i] = 0;
+    }
     __syncthreads();
-    if (he > hb) {
+    auto mark = [&](uint32_t id) {
+      const uint32_t off = id - sl.b0;
+      if (off >= len) return;
+      atomicOr(&sh.bitmap[off >> 5], 1u << (off & 31u));
+      uint32_t h = (id * 0x9E3779B1u) >> kHashShift;
+      for (uint32_t probe = 0; probe < kHash; ++probe) {
+        const uint32_t prev = atomicCAS(&sh.hid[h], kEmpty, id);
+        if (prev == kEmpty || prev == id) {
+          atomicAdd(&sh.hcnt[h], 1u);
+          return;
+        }
+        h = (h + 1) & (kHash - 1);
+      }
+      sh.overflow = 1;
+    };
 #pragma unroll
-      for (int q = 0; q < kHistRegs; ++q) {
-        const uint32_t off = hreg[q] - base;
-        if (hb + tid + q * kThreads < he && off < len) atomicAdd(&cnt[off >> 1], 1u << ((off & 1) * 16));
+    for (int k = 0; k < kHistRegs; ++k)
+      if (hreg[k] != kEmpty) mark(hreg[k]);
+    for (uint32_t h = hb + tid + kHistRegs * kThreads; h < he; h += kThreads) mark(hist_ids[h]);
+    for (uint32_t h = tid; h < extra; h += kThreads) mark(extra_ids[h]);
+  }
+  __syncthreads();
+
+  // The raw values of the slice's history ids, in flight during the stream.
+  uint32_t hidv[kHashPer];
+  float hx[kHashPer];
+#pragma unroll
+  for (int k = 0; k < kHashPer; ++k) {
+    hidv[k] = sl.pen ? sh.hid[tid + k * kThreads] : kEmpty;
+    hx[k] = (hidv[k] != kEmpty) ? sl.x[hidv[k]] : 0.0f;
+  }
+
+  Lane ln;
+  ln.nfa = 0.0f;
+  ln.gv = 0.0f;
+  ln.gi = kNone;
+  ln.amax = 0;
+  ln.ref = -__builtin_inff();
+  ln.s = 0.0;
+  ln.sa = 0.0f;
+  ln.moves = 0;
+  WaveState ws;
+  ws.cnt = 0;
+  ws.tau = 0;
+  ws.tau_f = -__builtin_inff();
+  ws.top = 0;
+  ws.C = sl.C;
+  ws.sel = select_at(sl.C);
+  ws.spill = sl.floor_on && sl.C > as_launch::kPartialRank;
+
+  switch (kind) {
+    case kKindPlain: stream<kKindPlain, kVec>(ln, ws, sl, wk, qa, qb); break;
+    case kKindCand: stream<kKindCand, kVec>(ln, ws, sl, wk, qa, qb); break;
+    case kKindSumTop: stream<kKindSumTop, kVec>(ln, ws, sl, wk, qa, qb); break;
+    default: stream<kKindSumTemp, kVec>(ln, ws, sl, wk, qa, qb); break;
+  }
+
+  // The first non-finite index, searched for only when the slice holds one.
+  uint32_t nf = kNone;
+  if (__syncthreads_or(ln.nfa != ln.nfa)) {
+    for (uint32_t e = sl.b0 + tid; e < sl.b1; e += kThreads)
+      if (!is_finite_bits(sl.x[e])) {
+        nf = e;
+        break;
+      }
+    nf = block_min_u32<kWaves>(nf, sh.red_u);
+  }
+
+  // The slice's history values, penalised.
+  const bool sums = kind == kKindSumTop || kind == kKindSumTemp;
+  uint64_t hpk[kHashPer];
+  uint32_t hkey_max = 0;
+#pragma unroll
+  for (int k = 0; k < kHashPer; ++k) {
+    hpk[k] = 0;
+    if (hidv[k] != kEmpty) {
+      const float v = penalize(hx[k], sh.hcnt[tid + k * kThreads], p);
+      const uint32_t key = total_key(v);
+      hpk[k] = pack(key, hidv[k]);
+      hkey_max = max(hkey_max, key);
+      if (kind == kKindPlain) {
+        if (is_finite_bits(v)) greedy_merge(ln.gv, ln.gi, v, hidv[k]);
+      } else if (sums) {
+        if (v > ln.ref) move_ref(ln, v, sl.scale);
+        const float t = (v - ln.ref) * sl.scale;
+        const float e = __builtin_amdgcn_exp2f(t);
+        ln.s = ln.s + (double)e;
+        ln.sa = fmaf(e, -t, ln.sa);
       }
     }
-    for (uint32_t h = hb + tid + kHistRegs * kThreads; h < he; h += kThreads) {
-      const uint32_t off = hist_ids[h] - base;
-      if (off < len) atomicAdd(&cnt[off >> 1], 1u << ((off & 1) * 16));
-    }
-    for (uint32_t h = tid; h < extra; h += kThreads) {
-      const uint32_t off = extra_ids[h] - base;
-      if (off < len) atomicAdd(&cnt[off >> 1], 1u << ((off & 1) * 16));
-    }
-    __syncthreads();
-#pragma unroll
-    for (int j = 0; j < kVec; ++j) {
-      const uint32_t e = (j * kThreads + tid) * 4;
-      const uint32_t w0 = cnt[e >> 1], w1 = cnt[(e >> 1) + 1];
-      const uint32_t c4[4] = {w0 & 0xFFFFu, w0 >> 16, w1 & 0xFFFFu, w1 >> 16};
-#pragma unroll
-      for (int c = 0; c < 4; ++c)
-        if (c4[c] != 0 && e + c < len) v[4 * j + c] = penalize(v[4 * j + c], c4[c], p);
-    }
-  }
-
-  // Rank keys from here on; 0 marks a slot past the segment's end (no finite value has key 0).
-  uint32_t k[kPer];
-#pragma unroll
-  for (int q = 0; q < kPer; ++q) {
-    const uint32_t e = ((q / 4) * kThreads + tid) * 4 + (q & 3);
-    k[q] = (e < len) ? total_key(v[q]) : 0u;
-  }
-
-  // The two largest keys of each thread, and the segment's largest.
-  uint32_t tmax = 0, tmax2 = 0;
-#pragma unroll
-  for (int q = 0; q < kPer; ++q) {
-    tmax2 = max(tmax2, min(tmax, k[q]));
-    tmax = max(tmax, k[q]);
-  }
-  const uint32_t mk = block_max_u32<kWaves>(tmax, red_u);
-
-  // Greedy (sample.rs:9-17, 378-396): the lowest index holding the largest value by IEEE `>`,
-  // so +0 and -0 tie. Only greedy rows need it.
-  uint32_t gi = kNone;
-  float gv = 0.0f;
-  if (p.mode == kModeGreedy && bad == kNone) {
-    gv = key_value(mk);
-    uint32_t first = kNone;
-#pragma unroll
-    for (int q = 0; q < kPer; ++q) {
-      const uint32_t e = ((q / 4) * kThreads + tid) * 4 + (q & 3);
-      if (k[q] != 0u && key_value(k[q]) == gv) first = min(first, base + e);
-    }
-    gi = block_min_u32<kWaves>(first, red_u);
   }
 
   SegStats st;
-  st.nonfinite = bad;
-  st.greedy_idx = gi;
-  st.greedy_val = gv;
-  st.max_key = mk;
+  st.nonfinite = nf;
+  st.greedy_idx = kNone;
+  st.greedy_val = 0.0f;
+  st.max_key = 0;
   st.n_cand = 0;
-  st.truncated = ((p.flags & kFlagPenalties) && long_history) ? 2u : 0u;
+  st.err_rel = 0.0f;
+  st.err_abs = 0.0f;
   st.bound = 0;
   st.sum = 0.0;
   st.sum_abs = 0.0;
+  st.sum_ref = 0.0f;
+  st.pad_ = 0;
 
-  const uint32_t C = p.cand;
-  if (bad == kNone && C > 0) {
-    uint64_t* out = cands + ((uint64_t)row * n_seg + seg) * cand_stride;
-    const int lane = tid & (kWave - 1), w = tid / kWave;
-    if (len <= C) {
-      // The whole segment, in index order.
-      uint32_t wc = 0;
-#pragma unroll
-      for (int q = 0; q < kPer; ++q) wc += (uint32_t)__popcll(__ballot(k[q] != 0u));
-      if (lane == 0) red_u2[w] = wc;
+  if (kind == kKindPlain) {
+    wave_greedy(ln.gv, ln.gi);
+    if (lane == 0) {
+      sh.red_f[w] = ln.gv;
+      sh.red_u2[w] = ln.gi;
+    }
+    __syncthreads();
+    float gv = sh.red_f[0];
+    uint32_t gi = sh.red_u2[0];
+    for (int k = 1; k < kWaves; ++k) greedy_merge(gv, gi, sh.red_f[k], sh.red_u2[k]);
+    st.greedy_idx = gi;
+    st.greedy_val = gv;
+    st.max_key = (gi == kNone) ? 0u : total_key(gv);
+    st.truncated = sh.overflow ? 2u : 0u;
+  } else {
+    // One barrier for the slice's bound (the highest wave threshold and the row's shared one), its
+    // largest key and its sums' reference.
+    const uint64_t* wbuf = sh.buf[w];
+    const uint32_t shared_b = __builtin_amdgcn_readfirstlane((uint32_t)read_shared(sl.share));
+    const uint32_t kmax = wave_max_u32(max(hkey_max, ln.amax));
+    const uint32_t rk = wave_max_u32(ln.ref > -__builtin_inff() ? total_key(ln.ref) : 0u);
+    if (lane == 0) {
+      sh.red_p[w] = max(ws.tau, (uint64_t)shared_b << 32);
+      sh.red_u2[w] = kmax;
+      sh.red_u[w] = rk;
+    }
+    __syncthreads();
+    uint64_t bound = sh.red_p[0];
+    uint32_t mk = sh.red_u2[0], rkey = sh.red_u[0];
+    for (int k = 1; k < kWaves; ++k) {
+      bound = max(bound, sh.red_p[k]);
+      mk = max(mk, sh.red_u2[k]);
+      rkey = max(rkey, sh.red_u[k]);
+    }
+    st.max_key = mk;
+
+    // Candidates: those spilled during the stream that rank >= bound (compacted in place, a tile at a
+    // time: every write lands before the tile being read), every buffered value >= bound, wave by
+    // wave, then the history values >= bound. When they would not fit the slice's slots, each wave
+    // first keeps only its share.
+    uint32_t spilled = sh.out_n;
+    if (spilled) {
       __syncthreads();
-      uint32_t run = 0;
-      for (int x = 0; x < w; ++x) run += red_u2[x];
-#pragma unroll
-      for (int q = 0; q < kPer; ++q) {
-        const uint64_t m = __ballot(k[q] != 0u);
-        const uint32_t e = ((q / 4) * kThreads + tid) * 4 + (q & 3);
-        if (k[q] != 0u) out[run + __popcll(m & ((1ull << lane) - 1))] = pack(k[q], base + e);
-        run += (uint32_t)__popcll(m);
-      }
-      st.n_cand = len;
-    } else {
-      // tau = the C-th largest of the 512 values that are some thread's largest or second largest:
-      // they are distinct values, so at least C values are >= tau and the segment's C best are
-      // among the values >= tau. Each wave finds tau on its own from the 512 in LDS (eight per
-      // lane, counted by ballots).
-      tm[tid] = tmax;
-      tm[tid + kThreads] = tmax2;
+      if (tid == 0) sh.out_n = 0;
       __syncthreads();
-      uint32_t a[8];
+      for (uint32_t t0 = 0; t0 < spilled; t0 += 4 * kThreads) {
+        uint64_t e[4];
 #pragma unroll
-      for (int x = 0; x < 8; ++x) a[x] = tm[lane + 64 * x];
-      uint64_t lo = 0, hi = (uint64_t)mk + 1;
-      while (hi - lo > 1) {
-        const uint32_t mid = (uint32_t)(lo + ((hi - lo) >> 1));
-        uint32_t c = 0;
-#pragma unroll
-        for (int x = 0; x < 8; ++x) c += (uint32_t)__popcll(__ballot(a[x] >= mid));
-        if (c >= C) lo = mid; else hi = mid;
-      }
-      const uint32_t tau = (uint32_t)lo;
-      uint32_t wc = 0;
-#pragma unroll
-      for (int q = 0; q < kPer; ++q) wc += (uint32_t)__popcll(__ballot(k[q] >= tau));
-      if (lane == 0) red_u2[w] = wc;
-      __syncthreads();
-      uint32_t M = 0, run = 0;
-      for (int x = 0; x < kWaves; ++x) {
-        if (x < w) run += red_u2[x];
-        M += red_u2[x];
-      }
-      if (M <= p.cap) {
-        // Every value >= tau, compacted by ballots in (load, lane) order.
-#pragma unroll
-        for (int q = 0; q < kPer; ++q) {
-          const uint64_t m = __ballot(k[q] >= tau);
-          const uint32_t e = ((q / 4) * kThreads + tid) * 4 + (q & 3);
-          if (k[q] >= tau) out[run + __popcll(m & ((1ull << lane) - 1))] = pack(k[q], base + e);
-          run += (uint32_t)__popcll(m);
-        }
-        st.n_cand = M;
-        st.truncated |= (M < len) ? 1u : 0u;
-        st.bound = (uint64_t)tau << 32;
-      } else {
-        // Too many values tie near tau (a flat or coarse row): the exact C best instead. Largest t
-        // with at least C keys >= t, by ballot counts; the keys > t, then the lowest ids equal to t.
-        if (tid == 0) slot = 0;
-        uint64_t lo2 = 0, hi2 = (uint64_t)mk + 1;
-        uint32_t cnt_lo = len, cnt_hi = 0;
-        int parity = 0;
-        while (hi2 - lo2 > 1 && cnt_lo != C) {
-          const uint32_t mid = (uint32_t)(lo2 + ((hi2 - lo2) >> 1));
-          uint32_t c = 0;
-#pragma unroll
-          for (int q = 0; q < kPer; ++q) c += (uint32_t)__popcll(__ballot(k[q] >= mid));
-          uint32_t* buf = parity ? red_u2 : red_u;
-          __syncthreads();
-          if (lane == 0) buf[w] = c;
-          __syncthreads();
-          c = 0;
-#pragma unroll
-          for (int x = 0; x < kWaves; ++x) c += buf[x];
-          parity ^= 1;
-          if (c >= C) {
-            lo2 = mid;
-            cnt_lo = c;
-          } else {
-            hi2 = mid;
-            cnt_hi = c;
-          }
+        for (int q = 0; q < 4; ++q) {
+          const uint32_t i = t0 + tid + q * kThreads;
+          e[q] = (i < spilled) ? sl.out[i] : 0ull;
         }
         __syncthreads();
-        const uint32_t t = (uint32_t)lo2;
-        uint32_t tie_max = 0;
-        if (cnt_lo == C) {
 #pragma unroll
-          for (int q = 0; q < kPer; ++q) {
-            const uint32_t e = ((q / 4) * kThreads + tid) * 4 + (q & 3);
-            if (k[q] >= t) {
-              out[atomicAdd(&slot, 1u)] = pack(k[q], base + e);
-              if (k[q] == t) tie_max = max(tie_max, base + e);
-            }
-          }
-        } else {
-          const uint32_t need = C - cnt_hi;
-          // Ties in index order: the index of value q is ((q/4)*kThreads + tid)*4 + q%4, so the
-          // order is (load j, thread, lane of the float4).
-          uint32_t running = 0;
-          for (int j = 0; j < kVec; ++j) {
-            uint32_t mine = 0;
-#pragma unroll
-            for (int c = 0; c < 4; ++c) mine += (k[4 * j + c] == t) ? 1u : 0u;
-            uint32_t total;
-            uint32_t r = running + block_exclusive_scan(mine, red_u2, &total);
-#pragma unroll
-            for (int c = 0; c < 4; ++c) {
-              const uint32_t e = (j * kThreads + tid) * 4 + c;
-              const uint32_t kk = k[4 * j + c];
-              if (kk > t) {
-                out[atomicAdd(&slot, 1u)] = pack(kk, base + e);
-              } else if (kk == t) {
-                if (r < need) {
-                  out[atomicAdd(&slot, 1u)] = pack(kk, base + e);
-                  tie_max = max(tie_max, base + e);
-                }
-                ++r;
-              }
-            }
-            running += total;
-          }
+        for (int q = 0; q < 4; ++q) {
+          const bool keep = e[q] != 0ull && e[q] >= bound;
+          const uint64_t m = __ballot(keep);
+          uint32_t base = 0;
+          if (lane == 0 && m) base = atomicAdd(&sh.out_n, (uint32_t)__popcll(m));
+          base = __builtin_amdgcn_readfirstlane(base);
+          if (keep) sl.out[base + lanes_below(m)] = e[q];
         }
-        tie_max = block_max_u32<kWaves>(tie_max, red_u);
-        st.n_cand = C;
-        st.truncated |= 1u;
-        st.bound = pack(t, tie_max);
+      }
+      __syncthreads();
+      spilled = sh.out_n;
+    }
+    uint32_t all = 0, hall = 0;
+    for (int pass = 0; pass < 2; ++pass) {
+      uint32_t mine = 0;
+      for (uint32_t i = lane; i < ws.cnt; i += kWave) mine += wbuf[i] >= bound ? 1u : 0u;
+      mine = wave_sum_u32(mine);
+      uint32_t hmine = 0;
+#pragma unroll
+      for (int k = 0; k < kHashPer; ++k) hmine += (hpk[k] != 0ull && hpk[k] >= bound) ? 1u : 0u;
+      hmine = wave_sum_u32(hmine);
+      __syncthreads();
+      if (lane == 0) {
+        sh.red_u3[w] = mine;
+        sh.red_u[w] = hmine;
+      }
+      __syncthreads();
+      all = 0;
+      hall = 0;
+      for (int k = 0; k < kWaves; ++k) {
+        all += sh.red_u3[k];
+        hall += sh.red_u[k];
+      }
+      if (pass == 1 || spilled + all + hall <= cand_stride) break;
+      const uint32_t used = spilled + hall;
+      const uint32_t share = cand_stride > used + 4u * kWaves ? (cand_stride - used) / kWaves : 1u;
+      if (ws.cnt > share) select_now(ws, share, 0u, nullptr);
+      __syncthreads();
+      if (lane == 0) sh.red_p[w] = ws.tau;
+      __syncthreads();
+      for (int k = 0; k < kWaves; ++k) bound = max(bound, sh.red_p[k]);
+    }
+    uint32_t run = spilled;
+    for (int k = 0; k < (int)w; ++k) run += sh.red_u3[k];
+    uint64_t* out = sl.out;
+    for (uint32_t i0 = 0; i0 < ws.cnt; i0 += kWave) {
+      const uint32_t i = i0 + lane;
+      const bool take = i < ws.cnt && wbuf[i] >= bound;
+      const uint64_t m = __ballot(take);
+      const uint32_t pos = run + lanes_below(m);
+      if (take && pos < cand_stride) out[pos] = wbuf[i];
+      run += (uint32_t)__popcll(m);
+    }
+#pragma unroll
+    for (int k = 0; k < kHashPer; ++k) {
+      if (hpk[k] != 0ull && hpk[k] >= bound) {
+        const uint32_t pos = spilled + all + atomicAdd(&sh.hist_out, 1u);
+        if (pos < cand_stride) out[pos] = hpk[k];
       }
     }
-  }
+    st.bound = bound;
+    st.n_cand = min(spilled + all + hall, cand_stride);
+    st.truncated = ((sh.overflow || spilled + all + hall > cand_stride) ? 2u : 0u) | (bound != 0 ? 1u : 0u);
 
-  if (bad == kNone && (p.flags & (kFlagSumTop | kFlagSumTemp))) {
-    const double m = (double)key_value(mk);
-    const bool by_temp = (p.flags & kFlagSumTemp) != 0;
-    const double temp = (double)p.temp;
-    double s = 0.0, sa = 0.0;
-    __syncthreads();  // tab[] is written
-#pragma unroll 4
-    for (int q = 0; q < kPer; ++q) {
-      if (k[q] != 0u) {
-        double d = __dsub_rn((double)key_value(k[q]), m);
-        if (by_temp) d = __ddiv_rn(d, temp);
-        const double x = as_exp::exp_with(tab, d);
-        s = __dadd_rn(s, x);
-        if (x != 0.0) sa = __dadd_rn(sa, __dmul_rn(x, fabs(d)));
+    if (sums) {
+      // Each lane's sums moved from its reference to the slice's largest one, m.
+      const float m = rkey ? key_value(rkey) : 0.0f;
+      double s = 0.0, sa = 0.0;
+      if (ln.s != 0.0) {
+        const float dt = (ln.ref - m) * sl.scale;
+        const float sc = __builtin_amdgcn_exp2f(dt);
+        s = ln.s * (double)sc;
+        sa = (double)(sc * fmaf((float)ln.s, fabsf(dt), ln.sa));
       }
+      s = wave_sum_f64(s);
+      sa = wave_sum_f64(sa);
+      const uint32_t moves = wave_max_u32(ln.moves);
+      if (lane == 0) {
+        sh.red_d[w] = s;
+        sh.red_d2[w] = sa;
+        sh.red_u2[w] = moves;
+      }
+      __syncthreads();
+      double ts = sh.red_d[0], tsa = sh.red_d2[0];
+      uint32_t tm = sh.red_u2[0];
+      for (int k = 1; k < kWaves; ++k) {
+        ts = __dadd_rn(ts, sh.red_d[k]);
+        tsa = __dadd_rn(tsa, sh.red_d2[k]);
+        tm = max(tm, sh.red_u2[k]);
+      }
+      st.sum = ts;
+      st.sum_ref = m;
+      // sum_abs in units of d = t * ln(2); it was kept in f32 (a lane folds a few hundred terms): a
+      // 2^-10 margin covers its roundings.
+      st.sum_abs = tsa * 0.69314718055994531 * (1.0 + 0x1p-10);
+      // Per term: the exp's own error once for the term, once per move of its lane's reference and
+      // once for the move to m; the chunk's f32 tree (4 levels); the f64 folds (the lane's chunks
+      // one by one, then 10 levels of wave and block adds) are far below that.
+      st.err_rel = kExpUlp * 0x1p-23f * (float)(tm + 2) + 4.0f * 0x1p-24f +
+                   0x1p-53f * (float)((len + kChunk - 1) / kChunk + 16);
+      st.err_abs = 5.0f * 0x1p-24f * 1.01f;
     }
-    st.sum = block_sum_f64<kWaves>(s, red_d);
-    st.sum_abs = block_sum_f64<kWaves>(sa, red_d);
   }
-
   if (tid == 0) stats[(uint64_t)row * n_seg + seg] = st;
 }
 
@@ -358,17 +946,17 @@ __global__ __launch_bounds__(kThreads) void scan_kernel(
 
 namespace as_launch {
 
-hipError_t scan(hipStream_t stream, bool vec, const float* logits, uint64_t row_stride, uint32_t n,
-                uint32_t n_rows, uint32_t n_seg, const as_dev::RowParams* params,
+hipError_t scan(hipStream_t stream, bool vec, const float* logits, const float* zero, uint64_t row_stride,
+                uint32_t n, uint32_t n_rows, uint32_t n_seg, uint32_t slice_len, as_dev::RowParams* params,
                 const uint32_t* hist_off, const uint32_t* hist_ids, const uint32_t* extra_ids,
                 as_dev::SegStats* stats, uint64_t* cands, uint32_t cand_stride) {
   dim3 grid(n_seg, n_rows);
   if (vec)
-    hipLaunchKernelGGL(scan_kernel<true>, grid, dim3(kThreads), 0, stream, logits, row_stride, n,
-                       n_seg, params, hist_off, hist_ids, extra_ids, stats, cands, cand_stride);
+    hipLaunchKernelGGL(scan_kernel<true>, grid, dim3(kThreads), 0, stream, logits, zero, row_stride, n, n_seg,
+                       slice_len, params, hist_off, hist_ids, extra_ids, stats, cands, cand_stride);
   else
-    hipLaunchKernelGGL(scan_kernel<false>, grid, dim3(kThreads), 0, stream, logits, row_stride, n,
-                       n_seg, params, hist_off, hist_ids, extra_ids, stats, cands, cand_stride);
+    hipLaunchKernelGGL(scan_kernel<false>, grid, dim3(kThreads), 0, stream, logits, zero, row_stride, n, n_seg,
+                       slice_len, params, hist_off, hist_ids, extra_ids, stats, cands, cand_stride);
   return hipGetLastError();
 }
 

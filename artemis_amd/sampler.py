@@ -85,6 +85,7 @@ def lib() -> C.CDLL:
                                 vp, vp, vp]
         L.as_argmax_rows.argtypes = [vp, vp, u64, u32, u32, vp, vp, u64, u32, u32]
         L.as_debug_exp.argtypes = [vp, vp, vp, u32]
+        L.as_debug_exp2f.argtypes = [vp, vp, vp, u32]
         L.as_profile.argtypes = [vp, C.c_int]
         L.as_profile_read.argtypes = [vp, C.POINTER(C.c_double), C.POINTER(C.c_double), C.POINTER(u32)]
         _lib = L
@@ -250,6 +251,14 @@ class Context:
     def debug_exp(self, x: torch.Tensor) -> torch.Tensor:
         y = torch.empty_like(x)
         self._ok(lib().as_debug_exp(self.h, x.data_ptr(), y.data_ptr(), x.numel()))
+        return y
+
+    def debug_exp2f(self, x: torch.Tensor) -> torch.Tensor:
+        """2^x by the GPU instruction behind the scan's sums (diagnostics)."""
+        assert x.is_cuda and x.dtype == torch.float32
+        y = torch.empty_like(x)
+        self._ok(lib().as_debug_exp2f(self.h, x.data_ptr(), y.data_ptr(), x.numel()))
+        torch.cuda.synchronize()
         return y
 
 

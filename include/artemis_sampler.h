@@ -136,6 +136,8 @@ int as_profile_read(as_ctx* ctx, double* scan_ms, double* finish_ms, uint32_t* c
 
 /* Diagnostics: y[i] = exp(x[i]) on the GPU with the sampler's f64 exp (device arrays). */
 int as_debug_exp(as_ctx* ctx, const double* x, double* y, uint32_t n);
+/* Diagnostics: y[i] = 2^x[i] by the GPU instruction the scan's error-bounded sums use. */
+int as_debug_exp2f(as_ctx* ctx, const float* x, float* y, uint32_t n);
 
 #ifdef __cplusplus
 }

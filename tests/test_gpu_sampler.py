@@ -111,6 +111,19 @@ def test_gpu_exp_is_the_hosts(ctx):
     assert same.all(), x[~same][:5]
 
 
+def test_gpu_exp2f_is_within_the_sums_bound(ctx):
+    # The scan's sums take 2 ulp per term for the hardware 2^x; it must stay within 1 over the
+    # arguments the sums give it (x <= 0 down to the f32 normal range).
+    rng = np.random.default_rng(12)
+    x = np.concatenate([-(rng.random(2_000_000) * 126.0), -(rng.random(500_000) * 2.0),
+                        np.array([0.0, -0.5, -1.0, -1e-30, -125.99, -126.0])]).astype(np.float32)
+    y = ctx.debug_exp2f(torch.from_numpy(x).cuda()).cpu().numpy().astype(np.float64)
+    exact = np.exp2(x.astype(np.float64))
+    ulp = np.spacing(exact.astype(np.float32)).astype(np.float64)
+    err = np.abs(y - exact) / ulp
+    assert err.max() <= 1.0, (err.max(), x[np.argmax(err)])
+
+
 GRID = []
 for temp in [0.0, 0.6, 1.0, 5.0, 1e-6]:
     for top_k in [0, 1, 2, 20, 300]:
