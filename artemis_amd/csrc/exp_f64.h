@@ -36,7 +36,11 @@ AS_HD inline double double_of(uint64_t u) { return __builtin_bit_cast(double, u)
 AS_HD inline double fused(double a, double b, double c) { return __builtin_fma(a, b, c); }
 
 // |x| >= 512 with a finite result: the scale's exponent is out of range, so it is rebuilt with an
-// offset and the result rescaled; below 2^-1022 the sum is rounded once before scaling.
+// offset and the result rescaled; below 2^-1022 the sum is rounded once before scaling. Out of line
+// on the device, so that a loop of exp_with does not evaluate it for every argument.
+#if defined(__HIP_DEVICE_COMPILE__)
+__attribute__((noinline))
+#endif
 AS_HD inline double exp_special(double tmp, uint64_t sbits, uint64_t ki) {
   if ((ki & 0x80000000ull) == 0) {
     sbits -= 1009ull << 52;
@@ -57,26 +61,14 @@ AS_HD inline double exp_special(double tmp, uint64_t sbits, uint64_t ki) {
   return 0x1p-1022 * y;
 }
 
-// `tab` is kTable or a copy of it (a kernel stages one in LDS).
-AS_HD inline double exp_with(const uint64_t* tab, double x) {
+// The reduction and polynomial shared by both entry points: tmp and the scale's bits.
+AS_HD inline double exp_reduced(const uint64_t* tab, double x, uint64_t* sbits_out, uint64_t* ki_out) {
   const double kInvLn2N = 0x1.71547652b82fep0 * 128.0;
   const double kNegLn2HiN = -0x1.62e42fefa0000p-8;
   const double kNegLn2LoN = -0x1.cf79abc9e3b3ap-47;
   const double kShift = 0x1.8p52;
   const double kC2 = 0x1.ffffffffffdbdp-2, kC3 = 0x1.555555555543cp-3;
   const double kC4 = 0x1.55555cf172b91p-5, kC5 = 0x1.1111167a4d017p-7;
-
-  uint32_t abstop = (uint32_t)(bits_of(x) >> 52) & 0x7ff;
-  // 0x3c9 is the exponent field of 2^-54, 0x408 of 512, 0x409 of 1024.
-  if (abstop - 0x3c9u >= 0x408u - 0x3c9u) {
-    if (abstop - 0x3c9u >= 0x80000000u) return 1.0 + x;  // |x| < 2^-54, and 0
-    if (abstop >= 0x409u) {
-      if (bits_of(x) == 0xfff0000000000000ull) return 0.0;  // -inf
-      if (abstop >= 0x7ffu) return 1.0 + x;                  // +inf, NaN
-      return (bits_of(x) >> 63) ? 0.0 : __builtin_inf();     // underflow, overflow
-    }
-    abstop = 0;  // 512 <= |x| < 1024: exp_special
-  }
   double kd = fused(kInvLn2N, x, kShift);
   uint64_t ki = bits_of(kd);
   kd -= kShift;
@@ -90,10 +82,40 @@ AS_HD inline double exp_with(const uint64_t* tab, double x) {
   double b = fused(r, kC5, kC4);
   double tmp = fused(r2, a, tail + r);
   tmp = fused(r2 * r2, b, tmp);
-  if (abstop == 0) return exp_special(tmp, sbits, ki);
-  double scale = double_of(sbits);
+  *sbits_out = sbits;
+  *ki_out = ki;
+  return tmp;
+}
+
+// exp_with for -512 < x < 512 only (where it takes no special case; for |x| < 2^-54 both give
+// 1 + x rounded): no branch, for loops over many arguments.
+AS_HD inline double exp_core(const uint64_t* tab, double x) {
+  uint64_t sbits, ki;
+  const double tmp = exp_reduced(tab, x, &sbits, &ki);
+  const double scale = double_of(sbits);
   return fused(scale, tmp, scale);
 }
+
+// `tab` is kTable or a copy of it (a kernel stages one in LDS).
+AS_HD inline double exp_with(const uint64_t* tab, double x) {
+  uint32_t abstop = (uint32_t)(bits_of(x) >> 52) & 0x7ff;
+  // 0x3c9 is the exponent field of 2^-54, 0x408 of 512, 0x409 of 1024.
+  if (abstop - 0x3c9u >= 0x408u - 0x3c9u) {
+    if (abstop - 0x3c9u >= 0x80000000u) return 1.0 + x;  // |x| < 2^-54, and 0
+    if (abstop >= 0x409u) {
+      if (bits_of(x) == 0xfff0000000000000ull) return 0.0;  // -inf
+      if (abstop >= 0x7ffu) return 1.0 + x;                  // +inf, NaN
+      return (bits_of(x) >> 63) ? 0.0 : __builtin_inf();     // underflow, overflow
+    }
+    abstop = 0;  // 512 <= |x| < 1024: exp_special
+  }
+  uint64_t sbits, ki;
+  const double tmp = exp_reduced(tab, x, &sbits, &ki);
+  if (abstop == 0) return exp_special(tmp, sbits, ki);
+  const double scale = double_of(sbits);
+  return fused(scale, tmp, scale);
+}
+
 
 AS_HD inline double exp(double x) { return exp_with(kTable, x); }
 

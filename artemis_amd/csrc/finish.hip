@@ -49,6 +49,8 @@ struct Shared {
   uint64_t bound_key;
   double u01, sum, x, eps;
 };
+// The workgroup's LDS, at file scope so that the out-of-line paths below address it as LDS.
+__shared__ Shared g_sh;
 
 // --- block helpers ------------------------------------------------------------------------------
 
@@ -111,7 +113,7 @@ __device__ __forceinline__ uint32_t history_bounds(const FinishArgs& a, const Ro
 // Thread 0's left-to-right f64 fold of term(i), i in [0, m), staged through LDS in tiles that all
 // threads fill. Returns the sum to every thread.
 template <class Term>
-__device__ double seq_fold(Shared& sh, uint32_t m, Term term) {
+__device__ __forceinline__ double seq_fold(Shared& sh, uint32_t m, Term term) {
   double* stage = sh.wd;
   double acc = 0.0;
   for (uint32_t t0 = 0; t0 < m; t0 += kStage) {
@@ -130,7 +132,7 @@ __device__ double seq_fold(Shared& sh, uint32_t m, Term term) {
 }
 
 // One stable pass of an LSD radix sort on 8 bits: (src_key, src_id) -> (dst_key, dst_id).
-__device__ void radix_pass(Shared& sh, uint32_t n, int shift, const uint32_t* src_key,
+__device__ __forceinline__ void radix_pass(Shared& sh, uint32_t n, int shift, const uint32_t* src_key,
                            const uint32_t* src_id, uint32_t* dst_key, uint32_t* dst_id) {
   uint32_t* wcnt = reinterpret_cast<uint32_t*>(sh.sk);  // [kWaves][256]
   const uint32_t tid = threadIdx.x, lane = tid & (kWave - 1), w = tid / kWave;
@@ -186,7 +188,8 @@ __device__ void radix_pass(Shared& sh, uint32_t n, int shift, const uint32_t* sr
 
 // The reference's algorithm in its own order: Sampler::sample's dispatch (sample.rs:136-149),
 // draw_full_sort (157-198) for top-k rows and draw_partial (208-293) otherwise.
-__device__ __noinline__ void exact_row(const FinishArgs& a, const RowParams& p, uint32_t row, Shared& sh) {
+__device__ __noinline__ void exact_row(const FinishArgs& a, const RowParams& p, uint32_t row) {
+  Shared& sh = g_sh;
   const uint32_t n = a.n, tid = threadIdx.x;
   uint32_t* S = a.scratch + (uint64_t)row * a.scratch_stride;
   uint32_t* cnt = S;
@@ -644,40 +647,52 @@ __device__ __forceinline__ uint32_t stream_draw(Shared& sh, const uint64_t* buf,
   return res;
 }
 
-// The deep path's passes over a row: 16 values per thread per step, four 16-byte loads in flight
-// (scalar loads for an unaligned row or the ragged end). f(i, v) runs for each value.
+// The deep path's passes over a row: 16 values per thread per step, with their history counts
+// (cnt, 0 when null), all loads of a step issued before any value is used (16-byte loads, scalar
+// ones for an unaligned row or the ragged end). f(i, v, c) runs for each value.
 template <class F>
-__device__ __forceinline__ void for_each_value(const float* x, uint32_t n, bool vec, F f) {
+__device__ __forceinline__ void for_each_value(const float* x, const uint32_t* cnt, uint32_t n, bool vec, F f) {
   typedef float f32x4 __attribute__((ext_vector_type(4)));
+  typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
   constexpr uint32_t kStep = 16 * kThreads;
   const uint32_t tid = threadIdx.x;
   for (uint32_t b0 = 0; b0 < n; b0 += kStep) {
     if (vec && b0 + kStep <= n) {
       f32x4 q[4];
+      u32x4 k[4];
 #pragma unroll
-      for (int j = 0; j < 4; ++j) q[j] = *reinterpret_cast<const f32x4*>(x + b0 + (j * kThreads + tid) * 4);
+      for (int j = 0; j < 4; ++j) {
+        const uint32_t e = b0 + (j * kThreads + tid) * 4;
+        q[j] = *reinterpret_cast<const f32x4*>(x + e);
+        k[j] = cnt ? *reinterpret_cast<const u32x4*>(cnt + e) : u32x4{0u, 0u, 0u, 0u};
+      }
 #pragma unroll
       for (int j = 0; j < 4; ++j)
 #pragma unroll
-        for (int c = 0; c < 4; ++c) f(b0 + (j * kThreads + tid) * 4 + c, q[j][c]);
+        for (int c = 0; c < 4; ++c) f(b0 + (j * kThreads + tid) * 4 + c, q[j][c], k[j][c]);
     } else {
       float q[16];
+      uint32_t k[16];
 #pragma unroll
       for (int j = 0; j < 16; ++j) {
         const uint32_t i = b0 + j * kThreads + tid;
         q[j] = (i < n) ? x[i] : 0.0f;
+        k[j] = (cnt && i < n) ? cnt[i] : 0u;
       }
 #pragma unroll
       for (int j = 0; j < 16; ++j) {
         const uint32_t i = b0 + j * kThreads + tid;
-        if (i < n) f(i, q[j]);
+        if (i < n) f(i, q[j], k[j]);
       }
     }
   }
 }
 
+__device__ __noinline__ float penalize_out(float x, uint32_t c, const RowParams& p) { return penalize(x, c, p); }
+
 // Returns true when it settled the row.
-__device__ __noinline__ bool deep_row(const FinishArgs& a, const RowParams& p, uint32_t row, Shared& sh) {
+__device__ __noinline__ bool deep_row(const FinishArgs& a, const RowParams& p, uint32_t row) {
+  Shared& sh = g_sh;
   const uint32_t n = a.n, tid = threadIdx.x, lane = tid & (kWave - 1);
   uint32_t* S = a.scratch + (uint64_t)row * a.scratch_stride;
   uint32_t* cnt = S;
@@ -702,20 +717,17 @@ __device__ __noinline__ bool deep_row(const FinishArgs& a, const RowParams& p, u
     }
     __syncthreads();
   }
-  auto pvalue = [&](uint32_t i, float v) -> float {
-    if (pen) {
-      const uint32_t c = cnt[i];
-      if (c) v = penalize(v, c, p);
-    }
-    return v;
-  };
+  // The counts start 16-byte aligned (the scratch stride is a multiple of 4 words). History values
+  // are few: their penalty runs out of line, so that the passes do not evaluate it for every value.
+  const uint32_t* pcnt = pen ? cnt : nullptr;
+  auto pvalue = [&](float v, uint32_t c) -> float { return __builtin_expect(c != 0, 0) ? penalize_out(v, c, p) : v; };
   const bool vec = a.vec && a.row_stride % 4 == 0;
 
   if (p.mode == kModeGreedy) {
     // greedy / greedy_penalized (sample.rs:9-17, 378-396) over the whole row.
     float gv = 0.0f;
     uint32_t gi = kNone;
-    for_each_value(x, n, vec, [&](uint32_t i, float v) { greedy_merge(gv, gi, pvalue(i, v), i); });
+    for_each_value(x, pcnt, n, vec, [&](uint32_t i, float v, uint32_t c) { greedy_merge(gv, gi, pvalue(v, c), i); });
     wave_greedy(gv, gi);
     if (lane == 0) {
       sh.wd[tid / kWave] = (double)gv;
@@ -753,69 +765,88 @@ __device__ __noinline__ bool deep_row(const FinishArgs& a, const RowParams& p, u
   auto w_temp = [&](double v) { return as_exp::exp_with(tab, __ddiv_rn(__dsub_rn(v, top), temp)); };
   auto w_one = [&](double v) { return as_exp::exp_with(tab, __dsub_rn(v, top)); };
 
-  // The row's total, when the cut or the draw needs it, is summed here in pass 1 from the host-exact
-  // exp of the reference's own f64 arguments: every term has the reference's bits, so the sum is
-  // within (n + this fold's depth) * 2^-53 of the reference's left fold (the slices' f32 sums are too
-  // loose for a cut this deep, where neighbouring cumulative weights differ by ~1e-5 of the total).
+  // The row's total, when the cut or the draw needs it: first the slices' certified sums (within
+  // about 1e-6 of the total); when a decision falls inside that bound (a cut this deep has
+  // neighbouring cumulative weights ~1e-5 of the total apart), exact_total() sums the host-exact exp
+  // of the reference's own f64 arguments, within (n + its fold's depth) * 2^-53 of the reference's
+  // left fold.
   const bool need_total = !topk && (p.top_p < 1.0f || unfiltered);
   double X = 0.0, eps = 0.0;
+  if (need_total) {
+    slices_total(a, sh, top, temp, unfiltered, &X, &eps);
+    if (!(X - eps > 0.0 && eps == eps)) return false;
+  }
+  bool exact = false;
 
   // Pass 1: a histogram of the keys by distance from the largest, with f32 weight sums.
   uint32_t s1 = 0;
   while ((mk >> s1) >= kDeepBins) ++s1;
+  // Counts (u32) and weights in 2^-32 units (u64: LDS integer atomics; float ones serialise).
   uint32_t* hc = reinterpret_cast<uint32_t*>(sh.wd);
-  float* hm = reinterpret_cast<float*>(sh.wd) + kDeepBins;
+  uint64_t* hm = reinterpret_cast<uint64_t*>(sh.wd) + kDeepBins / 2;
+  static_assert(kDeepBins * 12 <= sizeof(sh.wd), "histogram room");
   for (uint32_t b = tid; b < kDeepBins; b += kThreads) {
     hc[b] = 0;
-    hm[b] = 0.0f;
+    hm[b] = 0ull;
   }
   __syncthreads();
-  const bool masses = need_total;
   const float topf = key_value(mk), inv_t = 1.0f / p.temp;
-  double tsum = 0.0;
-  for_each_value(x, n, vec, [&](uint32_t i, float v0) {
-    const float v = pvalue(i, v0);
+  // One value into the histogram: its bin and (for the cut's bin) its weight, exp(d) <= 1 in 2^-32
+  // units rounded down.
+  auto count = [&](float v) {
     const uint32_t b = (mk - total_key(v)) >> s1;
     atomicAdd(&hc[b], 1u);
-    if (masses) {
-      atomicAdd(&hm[b], unfiltered ? __expf((v - topf) * inv_t) : __expf(v - topf));
-      const double d = __dsub_rn((double)v, top);
-      tsum = __dadd_rn(tsum, as_exp::exp_with(tab, unfiltered ? __ddiv_rn(d, temp) : d));
+    if (need_total) {
+      const float f = unfiltered ? __expf((v - topf) * inv_t) : __expf(v - topf);
+      atomicAdd(reinterpret_cast<unsigned long long*>(&hm[b]), (unsigned long long)(f * 0x1p32f));
     }
+  };
+  // The stream leaves history positions (count c != 0) out; each history id is then counted once,
+  // penalised, by the thread that sets its count's top bit first.
+  for_each_value(x, pcnt, n, vec, [&](uint32_t, float v, uint32_t c) {
+    if (__builtin_expect(c == 0, 1)) count(v);
   });
-  if (need_total) {
-    X = block_sum_f64<kWaves>(tsum, sh.red_d);
-    eps = kU * 1.02 * ((double)n + (double)(n / kThreads) + 32.0) * X;
-    if (!(X - eps > 0.0 && eps == eps)) return false;
+  if (pen) {
+    auto hist_one = [&](uint32_t id) {
+      if (id >= n) return;
+      const uint32_t old = atomicOr(&cnt[id], 0x80000000u);
+      if (!(old & 0x80000000u)) count(penalize(x[id], old, p));
+    };
+    for (uint32_t h = hb + tid; h < he; h += kThreads) hist_one(a.hist_ids[h]);
+    for (uint32_t h = tid; h < extra; h += kThreads) hist_one(a.extra_ids[h]);
   }
   __syncthreads();
-  if (tid == 0) {
-    uint32_t bc = kDeepBins - 1;
-    if (topk) {
-      uint32_t c = 0;
-      for (uint32_t b = 0; b < kDeepBins; ++b) {
-        c += hc[b];
-        if (c >= k) {
-          bc = b;
-          break;
-        }
-      }
-    } else {
-      const double target = unfiltered ? sh.u01 * (X + eps) * 1.05 : (p.top_p < 1.0f ? top_p * (X + eps) * 1.05 : 0.0);
-      if (masses) {
-        double c = 0.0;
-        for (uint32_t b = 0; b < kDeepBins; ++b) {
-          c += (double)hm[b];
-          if (c >= target) {
-            bc = b;
-            break;
-          }
-        }
-      }
-      if (has_floor) bc = min(bc, (mk - fk) >> s1);
+  {
+    // The cut's bin bc: the first whose running count reaches k (top-k), or whose running f32
+    // weight reaches the target with 5% to spare; four bins per thread, then block scans.
+    static_assert(kDeepBins == 4 * kThreads, "four bins per thread");
+    uint32_t c4[4], csum = 0;
+    double m4[4], msum = 0.0;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      c4[q] = hc[tid * 4 + q];
+      m4[q] = (double)hm[tid * 4 + q] * 0x1p-32;
+      csum += c4[q];
+      msum += m4[q];
     }
-    sh.keep = bc;
-    sh.pick = 0;
+    uint32_t call;
+    uint32_t cb = block_exclusive_scan_u32(csum, sh.red_u, &call);
+    double mb = block_exclusive_scan_f64(msum, sh.red_d);
+    const double target = unfiltered ? sh.u01 * (X + eps) * 1.05 : (p.top_p < 1.0f ? top_p * (X + eps) * 1.05 : 0.0);
+    uint32_t first = kDeepBins - 1;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      cb += c4[q];
+      mb += m4[q];
+      const bool hit = topk ? (cb >= k) : (need_total && mb >= target);
+      if (hit) first = min(first, tid * 4 + q);
+    }
+    uint32_t bc = block_min_u32<kWaves>(first, sh.red_u);
+    if (!topk && has_floor) bc = min(bc, (mk - fk) >> s1);
+    if (tid == 0) {
+      sh.keep = bc;
+      sh.pick = 0;
+    }
   }
   __syncthreads();
   const uint32_t bc = sh.keep;
@@ -827,17 +858,24 @@ __device__ __noinline__ bool deep_row(const FinishArgs& a, const RowParams& p, u
     const uint64_t below = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
     for (uint32_t b0 = 0; b0 < n; b0 += kStep) {
       float q[16];
-      uint32_t idx[16];
+      uint32_t idx[16], hc16[16];
       if (vec && b0 + kStep <= n) {
         typedef float f32x4 __attribute__((ext_vector_type(4)));
+        typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
         f32x4 t[4];
+        u32x4 k[4];
 #pragma unroll
-        for (int j = 0; j < 4; ++j) t[j] = *reinterpret_cast<const f32x4*>(x + b0 + (j * kThreads + tid) * 4);
+        for (int j = 0; j < 4; ++j) {
+          const uint32_t e = b0 + (j * kThreads + tid) * 4;
+          t[j] = *reinterpret_cast<const f32x4*>(x + e);
+          k[j] = pcnt ? *reinterpret_cast<const u32x4*>(pcnt + e) : u32x4{0u, 0u, 0u, 0u};
+        }
 #pragma unroll
         for (int j = 0; j < 4; ++j)
 #pragma unroll
           for (int c = 0; c < 4; ++c) {
             q[4 * j + c] = t[j][c];
+            hc16[4 * j + c] = k[j][c];
             idx[4 * j + c] = b0 + (j * kThreads + tid) * 4 + c;
           }
       } else {
@@ -845,6 +883,7 @@ __device__ __noinline__ bool deep_row(const FinishArgs& a, const RowParams& p, u
         for (int j = 0; j < 16; ++j) {
           idx[j] = b0 + j * kThreads + tid;
           q[j] = (idx[j] < n) ? x[idx[j]] : 0.0f;
+          hc16[j] = (pcnt && idx[j] < n) ? pcnt[idx[j]] : 0u;
         }
       }
       uint32_t keys[16];
@@ -852,8 +891,8 @@ __device__ __noinline__ bool deep_row(const FinishArgs& a, const RowParams& p, u
       uint32_t tot = 0;
 #pragma unroll
       for (int j = 0; j < 16; ++j) {
-        keys[j] = (idx[j] < n) ? total_key(pvalue(idx[j], q[j])) : 0u;
-        const bool take = idx[j] < n && ((mk - keys[j]) >> s1) <= bc;
+        keys[j] = (idx[j] < n) ? total_key(q[j]) : 0u;
+        const bool take = idx[j] < n && hc16[j] == 0 && ((mk - keys[j]) >> s1) <= bc;
         m[j] = __ballot(take);
         tot += (uint32_t)__popcll(m[j]);
       }
@@ -865,6 +904,18 @@ __device__ __noinline__ bool deep_row(const FinishArgs& a, const RowParams& p, u
         if ((m[j] >> lane) & 1ull) bufA[base + __popcll(m[j] & below)] = pack(keys[j], idx[j]);
         base += (uint32_t)__popcll(m[j]);
       }
+    }
+    if (pen) {
+      // Each history id once more, penalised, by the thread that clears its count's top bit.
+      auto hist_two = [&](uint32_t id) {
+        if (id >= n) return;
+        const uint32_t old = atomicAnd(&cnt[id], 0x7fffffffu);
+        if (!(old & 0x80000000u)) return;
+        const uint32_t key = total_key(penalize(x[id], old & 0x7fffffffu, p));
+        if (((mk - key) >> s1) <= bc) bufA[atomicAdd(&sh.pick, 1u)] = pack(key, id);
+      };
+      for (uint32_t h = hb + tid; h < he; h += kThreads) hist_two(a.hist_ids[h]);
+      for (uint32_t h = tid; h < extra; h += kThreads) hist_two(a.extra_ids[h]);
     }
   }
   __syncthreads();
@@ -922,6 +973,46 @@ __device__ __noinline__ bool deep_row(const FinishArgs& a, const RowParams& p, u
   }
   auto val_at = [&](uint32_t j) -> double { return (double)packed_value(bufA[j]); };
 
+  // The exact total: exp_core per value streamed (arguments at or below -512 give terms under
+  // 1e-222 of a total of at least 1, left out, far inside eps), then the history ids penalised (each
+  // claimed by setting its count's top bit, which pass 2 cleared). One loop per case, so that no
+  // division is evaluated where none is needed.
+  auto exact_total = [&]() {
+    const uint64_t* t = g_sh.tab;
+    double acc = 0.0;
+    if (unfiltered) {
+      for_each_value(x, pcnt, n, vec, [&](uint32_t, float v, uint32_t c) {
+        if (__builtin_expect(c == 0, 1)) {
+          const double d = __ddiv_rn(__dsub_rn((double)v, top), temp);
+          acc = __dadd_rn(acc, d > -512.0 ? as_exp::exp_core(t, d) : 0.0);
+        }
+      });
+    } else {
+      for_each_value(x, pcnt, n, vec, [&](uint32_t, float v, uint32_t c) {
+        if (__builtin_expect(c == 0, 1)) {
+          const double d = __dsub_rn((double)v, top);
+          acc = __dadd_rn(acc, d > -512.0 ? as_exp::exp_core(t, d) : 0.0);
+        }
+      });
+    }
+    if (pen) {
+      auto hist_three = [&](uint32_t id) {
+        if (id >= n) return;
+        const uint32_t old = atomicOr(&cnt[id], 0x80000000u);
+        if (old & 0x80000000u) return;
+        double d = __dsub_rn((double)penalize(x[id], old, p), top);
+        if (unfiltered) d = __ddiv_rn(d, temp);
+        acc = __dadd_rn(acc, as_exp::exp_with(t, d));
+      };
+      for (uint32_t h = hb + tid; h < he; h += kThreads) hist_three(a.hist_ids[h]);
+      for (uint32_t h = tid; h < extra; h += kThreads) hist_three(a.extra_ids[h]);
+    }
+    X = block_sum_f64<kWaves>(acc, sh.red_d);
+    eps = kU * 1.02 * ((double)n + (double)(n / kThreads) + 32.0) * X;
+    exact = true;
+    return X - eps > 0.0 && eps == eps;
+  };
+
   // The cut.
   uint32_t keep = kNone;
   if (topk) {
@@ -949,23 +1040,35 @@ __device__ __noinline__ bool deep_row(const FinishArgs& a, const RowParams& p, u
       im = block_min_u32<kWaves>(first, sh.red_u);
     }
     const bool im_exact = (im < D) || complete;
-    uint32_t jl = D, jh = D;
-    if (p.top_p < 1.0f) stream_cross(sh, bufA, D, w_one, X, eps, top_p, &jl, &jh);
-    if (im_exact && im <= jl) keep = im;
-    else if (jl < D && jl == jh) keep = jh + 1;
-    else if (jl == D && complete) keep = n;
-    else return false;
+    for (;;) {
+      uint32_t jl = D, jh = D;
+      if (p.top_p < 1.0f) stream_cross(sh, bufA, D, w_one, X, eps, top_p, &jl, &jh);
+      if (im_exact && im <= jl) keep = im;
+      else if (jl < D && jl == jh) keep = jh + 1;
+      else if (jl == D && complete) keep = n;
+      else if (!exact && p.top_p < 1.0f) {
+        if (!exact_total()) return false;
+        continue;
+      } else return false;
+      break;
+    }
   }
 
   // The draw.
   uint32_t pick;
   double tot;
   if (unfiltered) {
-    const uint32_t j = stream_draw(sh, bufA, D, w_temp, sh.u01 * (X - eps) * (1.0 - 3.0 * kU),
-                                   sh.u01 * (X + eps) * (1.0 + 3.0 * kU));
-    if (j != kNone && j < D) pick = j;
-    else if (j == D && complete) pick = n - 1;
-    else return false;
+    for (;;) {
+      const uint32_t j = stream_draw(sh, bufA, D, w_temp, sh.u01 * (X - eps) * (1.0 - 3.0 * kU),
+                                     sh.u01 * (X + eps) * (1.0 + 3.0 * kU));
+      if (j != kNone && j < D) pick = j;
+      else if (j == D && complete) pick = n - 1;
+      else if (!exact) {
+        if (!exact_total()) return false;
+        continue;
+      } else return false;
+      break;
+    }
     keep = n;
     tot = X;
   } else {
@@ -994,7 +1097,7 @@ __device__ __noinline__ bool deep_row(const FinishArgs& a, const RowParams& p, u
 // --- the kernel ---------------------------------------------------------------------------------
 
 __global__ __launch_bounds__(kThreads) void finish_kernel(const FinishArgs* __restrict__ ap) {
-  __shared__ Shared sh;
+  Shared& sh = g_sh;
   const FinishArgs& a = *ap;
   const uint32_t row = blockIdx.x, tid = threadIdx.x;
   const RowParams p = a.params[row];
@@ -1360,9 +1463,9 @@ __global__ __launch_bounds__(kThreads) void finish_kernel(const FinishArgs* __re
 
   if (sh.exact) {
     __syncthreads();
-    if (!deep_row(a, a.params[row], row, sh)) {
+    if (!deep_row(a, a.params[row], row)) {
       __syncthreads();
-      exact_row(a, a.params[row], row, sh);
+      exact_row(a, a.params[row], row);
     }
   }
 }
