@@ -50,7 +50,11 @@ struct RowParams {
   // slice of the row has published, and the largest key any slice has seen (min-p rows).
   uint32_t share_bound;
   uint32_t share_top;
+  // Top-k rows: wave i < kShareSlots of the row keeps here the key of its q-th best value so far,
+  // q = ceil(k / slots); once every slot is set, their minimum has at least k values at or above it.
+  uint32_t slot[16];
 };
+constexpr uint32_t kShareSlots = 16;
 
 // Per (row, slice) results of the scan.
 struct SegStats {

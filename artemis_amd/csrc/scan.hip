@@ -42,6 +42,9 @@ constexpr uint32_t kGroupStep = kWaves * kChunk;
 constexpr uint32_t kCapW = as_launch::kWaveCap;
 constexpr int kQ = kCapW / kWave;               // buffer entries per lane when a wave reads it whole
 constexpr uint32_t kRoom = 4 * kWave;           // the most one 16-byte group per lane appends
+// Rows without a top-k start from the 16th best of each wave's first chunk: shared over a row's
+// waves, about its 2,000th-3,000th value, near the depth their selects keep, so that few run.
+constexpr uint32_t kFirstRankPartial = 16;
 constexpr uint32_t kHash = as_launch::kHistSlots;
 constexpr int kHashPer = kHash / kThreads;
 constexpr int kHashShift = 32 - __builtin_ctz(kHash);  // the multiplicative hash's top bits
@@ -293,7 +296,8 @@ __device__ __noinline__ WaveState spill(WaveState ws, uint64_t* out, uint32_t ro
 // least C values of the chunk meet (with C above 128, the 128th); published to the row. Fewer valid
 // values leave it at 0. Out of line: it runs once a slice.
 __device__ __noinline__ WaveState first_tau(WaveState ws, f32x4 v0, f32x4 v1, f32x4 v2, f32x4 v3,
-                                            uint32_t masked, uint32_t e0, uint32_t C, uint32_t* share) {
+                                            uint32_t masked, uint32_t e0, uint32_t C, uint32_t* share,
+                                            uint32_t* slot, uint32_t q) {
   const f32x4 v[kU] = {v0, v1, v2, v3};
   uint64_t top[2] = {0ull, 0ull};
 #pragma unroll
@@ -315,7 +319,26 @@ __device__ __noinline__ WaveState first_tau(WaveState ws, f32x4 v0, f32x4 v1, f3
     raise_tau(ws, t);
     publish(share, (uint32_t)(t >> 32));
   }
+  if (slot) {
+    const uint64_t tq = wave_kth<2>(top, q, 0u, 0u);
+    if (tq != 0ull) publish(slot, (uint32_t)(tq >> 32));
+  }
   return ws;
+}
+
+// The q-th largest of the lanes' x (0 when fewer than q lanes hold a nonzero x): at most q rounds
+// of a wave maximum.
+__device__ __forceinline__ uint32_t wave_qth(uint32_t x, uint32_t q) {
+  uint32_t need = q;
+  for (uint32_t it = 0; it < q; ++it) {
+    const uint32_t m = wave_max_u32(x);
+    if (m == 0) return 0;
+    const uint32_t c = (uint32_t)__popcll(__ballot(x == m));
+    if (c >= need) return m;
+    need -= c;
+    if (x == m) x = 0;
+  }
+  return 0;
 }
 
 // The largest unmasked value of the wave's first chunk sets min-p's first floor. When two in five
@@ -350,7 +373,7 @@ __device__ __noinline__ WaveState first_floor(WaveState ws, f32x4 v0, f32x4 v1, 
     ws.spill = false;
     ws.C = as_launch::kPartialRank;
     ws.sel = select_at(ws.C);
-    ws = first_tau(ws, v0, v1, v2, v3, masked, e0, ws.C, share);
+    ws = first_tau(ws, v0, v1, v2, v3, masked, e0, kFirstRankPartial, share, nullptr, 0u);
   }
   return ws;
 }
@@ -359,11 +382,16 @@ struct Slice {
   const float* x;       // the row
   const float* zero;    // kChunk readable zeros, for the loads of a wave with no full chunk
   uint32_t* share;      // the row's shared words
+  uint32_t* slots;      // the row's slots (top-k rows), n_slots of them; mine (or null)
+  uint32_t* my_slot;
+  uint32_t n_slots;
+  uint32_t q;           // the rank each slot holds
   uint32_t b0, b1;      // the slice's values [b0, b1)
   uint32_t C;           // candidates per wave
   uint64_t* out;        // the slice's candidates in HBM
   uint32_t room;        // how many of them the stream may write
-  bool first;           // the first chunk sets tau
+  bool first;           // the first chunk sets tau, to its first_rank-th best
+  uint32_t first_rank;
   bool pen;             // history values are left out of the stream
   bool floor_on;        // min-p's floor applies to the candidates (a row without a top-k)
   float scale;          // log2(e), or log2(e) / T for sums of exp((l - m) / T)
@@ -483,7 +511,7 @@ __device__ __forceinline__ void chunk(Lane& ln, WaveState& ws, const Slice& sl,
   if (kFirst) {
     const uint32_t all = mask[0] | mask[1] << 4 | mask[2] << 8 | mask[3] << 12;
     if (sl.floor_on) ws = first_floor(ws, q[0], q[1], q[2], q[3], all, c0 + lane * 4, sl.ln_min_p, sl.share);
-    else if (sl.first) ws = first_tau(ws, q[0], q[1], q[2], q[3], all, c0 + lane * 4, ws.C, sl.share);
+    else if (sl.first) ws = first_tau(ws, q[0], q[1], q[2], q[3], all, c0 + lane * 4, sl.first_rank, sl.share, sl.my_slot, sl.q);
   }
   float m4[kU];
 #pragma unroll
@@ -559,10 +587,27 @@ __device__ __forceinline__ void load_at(f32x4 (&q)[kU], const Slice& sl, const W
   else load_chunk<kVec>(q, sl.zero, 0);
 }
 
-// The row's shared words as read: the published bound, and min-p's largest key.
-__device__ __forceinline__ void apply_shared(WaveState& ws, const Slice& sl, uint64_t w) {
+// Lane i < n_slots reads the row's slot i (others: all ones, so that the wave's minimum is the slots').
+__device__ __forceinline__ uint32_t read_slot(const Slice& sl) {
+  const uint32_t lane = threadIdx.x & (kWave - 1);
+  if (lane < sl.n_slots) return __hip_atomic_load(sl.slots + lane, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  return 0xFFFFFFFFu;
+}
+
+// The row's shared words as read: the published bound, the slots' minimum (top-k rows: once every
+// slot is set, at least k values of the row rank at or above it), and min-p's largest key.
+__device__ __forceinline__ void apply_shared(WaveState& ws, const Slice& sl, uint64_t w, uint32_t sv, uint32_t ln_amax) {
   const uint32_t b = __builtin_amdgcn_readfirstlane((uint32_t)w);
   raise_tau(ws, (uint64_t)b << 32);
+  if (sl.n_slots) {
+    raise_tau(ws, (uint64_t)wave_min_u32(sv) << 32);
+    // The wave's slot: the q-th largest of its lanes' largest appended keys (q distinct unmasked
+    // values of the wave rank at or above it).
+    if (sl.my_slot) {
+      const uint32_t t = wave_qth(ln_amax, sl.q);
+      if (t) publish(sl.my_slot, t);
+    }
+  }
   if (sl.floor_on) {
     const uint32_t top = __builtin_amdgcn_readfirstlane((uint32_t)(w >> 32));
     if (top > ws.top) {
@@ -584,9 +629,10 @@ __device__ __forceinline__ void stream(Lane& ln, WaveState& ws, const Slice& sl,
     chunk<kKind, false, true>(ln, ws, sl, qa, wk.c0);
     for (uint32_t i = 1; i < nfull; i += 2) {
       const uint64_t w = kShare ? read_shared(sl.share) : 0ull;
+      const uint32_t sv = read_slot(sl);
       load_at<kVec>(qa, sl, wk, i + 1);
       chunk<kKind, false, false>(ln, ws, sl, qb, wk.c0 + i * kGroupStep);
-      if (kShare) apply_shared(ws, sl, w);
+      if (kShare) apply_shared(ws, sl, w, sv, ln.amax);
       if (i + 1 >= nfull) break;
       load_at<kVec>(qb, sl, wk, i + 2);
       chunk<kKind, false, false>(ln, ws, sl, qa, wk.c0 + (i + 1) * kGroupStep);
@@ -633,6 +679,12 @@ __global__ __launch_bounds__(kThreads, 3) void scan_kernel(
   // A top-k row's tau must have k values at or above it; rows without a top-k take the best the
   // first chunk gives.
   sl.first = mode == kModeTopK ? sl.C <= 2u * kWave : true;
+  sl.first_rank = mode == kModeTopK ? sl.C : kFirstRankPartial;
+  // Top-k rows: the first min(waves of the row, kShareSlots) waves each own a slot.
+  sl.slots = params[row].slot;
+  sl.n_slots = (mode == kModeTopK && sl.first) ? min(n_seg * kWaves, kShareSlots) : 0u;
+  sl.q = sl.n_slots ? (p.top_k + sl.n_slots - 1) / sl.n_slots : 0u;
+  sl.my_slot = (seg * kWaves + w < sl.n_slots) ? sl.slots + seg * kWaves + w : nullptr;
 
   uint32_t hb = 0, he = 0;
   if (hist_ids) {
@@ -700,12 +752,11 @@ __global__ __launch_bounds__(kThreads, 3) void scan_kernel(
   __syncthreads();
 
   // The raw values of the slice's history ids, in flight during the stream.
-  uint32_t hidv[kHashPer];
   float hx[kHashPer];
 #pragma unroll
   for (int k = 0; k < kHashPer; ++k) {
-    hidv[k] = sl.pen ? sh.hid[tid + k * kThreads] : kEmpty;
-    hx[k] = (hidv[k] != kEmpty) ? sl.x[hidv[k]] : 0.0f;
+    const uint32_t id = sl.pen ? sh.hid[tid + k * kThreads] : kEmpty;
+    hx[k] = (id != kEmpty) ? sl.x[id] : 0.0f;
   }
 
   Lane ln;
@@ -747,10 +798,11 @@ __global__ __launch_bounds__(kThreads, 3) void scan_kernel(
   // The slice's history values, penalised.
   const bool sums = kind == kKindSumTop || kind == kKindSumTemp;
   uint64_t hpk[kHashPer];
-  uint32_t hkey_max = 0;
+  uint32_t hkey_max = 0, hidv[kHashPer];
 #pragma unroll
   for (int k = 0; k < kHashPer; ++k) {
     hpk[k] = 0;
+    hidv[k] = sl.pen ? sh.hid[tid + k * kThreads] : kEmpty;
     if (hidv[k] != kEmpty) {
       const float v = penalize(hx[k], sh.hcnt[tid + k * kThreads], p);
       const uint32_t key = total_key(v);
