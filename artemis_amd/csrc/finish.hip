@@ -778,9 +778,16 @@ __device__ __noinline__ bool deep_row(const FinishArgs& a, const RowParams& p, u
   }
   bool exact = false;
 
-  // Pass 1: a histogram of the keys by distance from the largest, with f32 weight sums.
-  uint32_t s1 = 0;
-  while ((mk >> s1) >= kDeepBins) ++s1;
+  // Pass 1: a histogram of the values by distance below the largest, kDeepBins bins over dspan
+  // (32, or 32 T for weights exp((l - top) / T): below it a value's weight is under e^-32 of the
+  // largest), the last bin holding everything further down; with f32 weight sums. The bin is
+  // monotone in the value, so every value ranking above the cut lies in a bin at or before its.
+  const float topf = key_value(mk), inv_t = 1.0f / p.temp;
+  const float bsc = (float)kDeepBins / (unfiltered ? 32.0f * p.temp : 32.0f);
+  auto bin_of = [&](float v) -> uint32_t {
+    const float t = (topf - v) * bsc;
+    return t < (float)(kDeepBins - 1) ? (uint32_t)t : kDeepBins - 1;
+  };
   // Counts (u32) and weights in 2^-32 units (u64: LDS integer atomics; float ones serialise).
   uint32_t* hc = reinterpret_cast<uint32_t*>(sh.wd);
   uint64_t* hm = reinterpret_cast<uint64_t*>(sh.wd) + kDeepBins / 2;
@@ -790,11 +797,10 @@ __device__ __noinline__ bool deep_row(const FinishArgs& a, const RowParams& p, u
     hm[b] = 0ull;
   }
   __syncthreads();
-  const float topf = key_value(mk), inv_t = 1.0f / p.temp;
   // One value into the histogram: its bin and (for the cut's bin) its weight, exp(d) <= 1 in 2^-32
   // units rounded down.
   auto count = [&](float v) {
-    const uint32_t b = (mk - total_key(v)) >> s1;
+    const uint32_t b = bin_of(v);
     atomicAdd(&hc[b], 1u);
     if (need_total) {
       const float f = unfiltered ? __expf((v - topf) * inv_t) : __expf(v - topf);
@@ -832,7 +838,7 @@ __device__ __noinline__ bool deep_row(const FinishArgs& a, const RowParams& p, u
     uint32_t call;
     uint32_t cb = block_exclusive_scan_u32(csum, sh.red_u, &call);
     double mb = block_exclusive_scan_f64(msum, sh.red_d);
-    const double target = unfiltered ? sh.u01 * (X + eps) * 1.05 : (p.top_p < 1.0f ? top_p * (X + eps) * 1.05 : 0.0);
+    const double target = unfiltered ? sh.u01 * (X + eps) * 1.005 : (p.top_p < 1.0f ? top_p * (X + eps) * 1.005 : 0.0);
     uint32_t first = kDeepBins - 1;
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
@@ -842,7 +848,7 @@ __device__ __noinline__ bool deep_row(const FinishArgs& a, const RowParams& p, u
       if (hit) first = min(first, tid * 4 + q);
     }
     uint32_t bc = block_min_u32<kWaves>(first, sh.red_u);
-    if (!topk && has_floor) bc = min(bc, (mk - fk) >> s1);
+    if (!topk && has_floor) bc = min(bc, bin_of(key_value(fk)));
     if (tid == 0) {
       sh.keep = bc;
       sh.pick = 0;
@@ -892,7 +898,7 @@ __device__ __noinline__ bool deep_row(const FinishArgs& a, const RowParams& p, u
 #pragma unroll
       for (int j = 0; j < 16; ++j) {
         keys[j] = (idx[j] < n) ? total_key(q[j]) : 0u;
-        const bool take = idx[j] < n && hc16[j] == 0 && ((mk - keys[j]) >> s1) <= bc;
+        const bool take = idx[j] < n && hc16[j] == 0 && bin_of(q[j]) <= bc;
         m[j] = __ballot(take);
         tot += (uint32_t)__popcll(m[j]);
       }
@@ -911,8 +917,8 @@ __device__ __noinline__ bool deep_row(const FinishArgs& a, const RowParams& p, u
         if (id >= n) return;
         const uint32_t old = atomicAnd(&cnt[id], 0x7fffffffu);
         if (!(old & 0x80000000u)) return;
-        const uint32_t key = total_key(penalize(x[id], old & 0x7fffffffu, p));
-        if (((mk - key) >> s1) <= bc) bufA[atomicAdd(&sh.pick, 1u)] = pack(key, id);
+        const float v = penalize(x[id], old & 0x7fffffffu, p);
+        if (bin_of(v) <= bc) bufA[atomicAdd(&sh.pick, 1u)] = pack(total_key(v), id);
       };
       for (uint32_t h = hb + tid; h < he; h += kThreads) hist_two(a.hist_ids[h]);
       for (uint32_t h = tid; h < extra; h += kThreads) hist_two(a.extra_ids[h]);
@@ -922,16 +928,21 @@ __device__ __noinline__ bool deep_row(const FinishArgs& a, const RowParams& p, u
   const uint32_t D = sh.pick;
   const bool complete = (D == n);
 
-  // Bucket sort of bufA[0..D) into rank order (through bufB).
+  // Bucket sort of bufA[0..D) into rank order (through bufB): kDeepBins value buckets over the range
+  // the collected values span (monotone in the value, so bucket order is rank order).
+  uint32_t kmin = 0xFFFFFFFFu;
+  for (uint32_t i = tid; i < D; i += kThreads) kmin = min(kmin, (uint32_t)(bufA[i] >> 32));
+  kmin = block_min_u32<kWaves>(kmin, sh.red_u);
+  const float span2 = topf - key_value(kmin);
+  const float bsc2 = span2 > 0.0f ? (float)(kDeepBins - 1) / span2 : 0.0f;
+  auto bin_p = [&](uint64_t x) {
+    const float t = (topf - packed_value(x)) * bsc2;
+    return t < (float)(kDeepBins - 1) ? (uint32_t)t : kDeepBins - 1;
+  };
   {
-    uint32_t kmin = 0xFFFFFFFFu;
-    for (uint32_t i = tid; i < D; i += kThreads) kmin = min(kmin, (uint32_t)(bufA[i] >> 32));
-    kmin = block_min_u32<kWaves>(kmin, sh.red_u);
-    uint32_t s2 = 0;
-    while (((mk - kmin) >> s2) >= kDeepBins) ++s2;
     for (uint32_t b = tid; b < kDeepBins; b += kThreads) hc[b] = 0;
     __syncthreads();
-    for (uint32_t i = tid; i < D; i += kThreads) atomicAdd(&hc[(mk - (uint32_t)(bufA[i] >> 32)) >> s2], 1u);
+    for (uint32_t i = tid; i < D; i += kThreads) atomicAdd(&hc[bin_p(bufA[i])], 1u);
     __syncthreads();
     // Exclusive scan of the 4096 counts: four per thread, then the block.
     uint32_t* bs = hc + kDeepBins;  // bucket starts (over hm's space)
@@ -955,14 +966,14 @@ __device__ __noinline__ bool deep_row(const FinishArgs& a, const RowParams& p, u
     // by subtraction as slots are taken).
     for (uint32_t i = tid; i < D; i += kThreads) {
       const uint64_t v = bufA[i];
-      const uint32_t b = (mk - (uint32_t)(v >> 32)) >> s2;
+      const uint32_t b = bin_p(v);
       const uint32_t slot = atomicSub(&hc[b], 1u) - 1u;
       bufB[bs[b] + slot] = v;
     }
     __syncthreads();
     for (uint32_t i = tid; i < D; i += kThreads) {
       const uint64_t v = bufB[i];
-      const uint32_t b = (mk - (uint32_t)(v >> 32)) >> s2;
+      const uint32_t b = bin_p(v);
       const uint32_t s0 = bs[b];
       const uint32_t e0 = (b + 1 < kDeepBins) ? bs[b + 1] : D;
       uint32_t r = 0;
