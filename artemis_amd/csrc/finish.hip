@@ -1,18 +1,23 @@
-// Pass 2, one workgroup per row: merges the segments' results and chooses the token.
+// Pass 2, one 1024-thread workgroup per row: merges the slices' results and chooses the token.
 //
-// Top-k rows (0 < k < n with k segment candidates each): the union of the segments' top k holds
-// the row's top k; a bitonic sort in LDS orders it by rank and one thread runs draw_full_sort's f64
-// tail (sample.rs:157-198) in the reference's own order, so every sum and comparison is bit-exact.
+// The scan leaves, per slice, its statistics (non-finite index, greedy pick, largest key, sums) and
+// the values ranking at or above its bound; R, the largest bound of a truncated slice (raised to
+// min-p's floor), makes every value of the row ranking >= R a candidate. The candidates >= R are
+// loaded into LDS and bucket-sorted by rank.
 //
-// Rows without a top-k (draw_partial, sample.rs:208-293): the union of the segments' best 256 is a
-// complete rank prefix down to the best of the truncated segments' last candidates. The min-p cut
-// is an exact comparison. The top-p cut and the unfiltered draw depend on a sum over the whole row
-// in index order; that sum comes from the segments' partial sums with a rigorous error bound that
-// covers the reference's own left-to-right rounding, and a decision is taken only when the bound
-// cannot change it. The kept set's draw is then exact. A row whose decision falls within the bound,
-// or whose cut lies past the complete prefix, runs the exact-order path below: a stable radix sort
-// of the whole row in HBM scratch and the reference's sequential folds, so its token is the
-// reference's in every case.
+// Top-k rows: when at least k candidates rank >= R they hold the row's k best, and one thread runs
+// draw_full_sort's f64 tail (sample.rs:157-198) in the reference's own order, so every sum and
+// comparison is bit-exact.
+//
+// Rows without a top-k (draw_partial, sample.rs:208-293): the sorted candidates are a complete rank
+// prefix down to R. The min-p cut is an exact comparison. The top-p cut and the unfiltered draw
+// depend on a sum over the whole row in index order; that sum comes from the slices' partial sums
+// with a rigorous error bound that covers the reference's own left-to-right rounding, and a
+// decision is taken only when the bound cannot change it. The kept set's draw is then exact.
+// A row whose cut or draw lies past the candidates takes the deep path (a histogram of the row,
+// then every value down to the deciding bin, sorted in HBM scratch); one whose decision a bound
+// still cannot settle takes the exact-order path: a stable radix sort of the whole row and the
+// reference's sequential folds, so its token is the reference's in every case.
 #include "sampler_device.h"
 #include "launch.h"
 #include "../../include/artemis_sampler.h"
@@ -551,10 +556,13 @@ __device__ __forceinline__ uint32_t decide_draw(Shared& sh, uint32_t m, const do
 // --- the deep path ------------------------------------------------------------------------------
 //
 // For a row whose cut or draw lies past the fast path's sorted candidates: one pass over the row
-// histograms its keys (with f32 weight sums per bin), which fixes the lowest bin that can hold the
-// cut (or the draw), with slack; a second pass collects every value down to that bin; a bucket
-// sort in HBM scratch puts them in rank order; and the same certified decisions as the fast path
-// run while streaming through them. When a bound still cannot decide, the exact-order path runs.
+// histograms its values into bins (fine near the row's largest value; each bin's count and its
+// weight in fixed point, added with integer LDS atomics), which fixes the lowest bin that can hold
+// the cut (or the draw), with a margin; a second pass collects every value down to that bin; a
+// bucket sort in HBM scratch puts them in rank order; and the same certified decisions as the fast
+// path run while streaming through them. The row's exact total in index order is computed only
+// when the slices' certified sums leave a decision open. When a bound still cannot decide, the
+// exact-order path runs.
 
 constexpr uint32_t kDeepBins = 4096;
 constexpr uint32_t kDeepBucketMax = 4096;
