@@ -50,9 +50,9 @@ struct Shared {
   uint32_t red_u[kWaves];
   double red_d[kWaves];
   // Row scalars.
-  uint32_t bad, gi, mk, total, trunc, keep, pick, done, exact, prefix, stats_bad, nsk;
+  uint32_t bad, gi, mk, total, trunc, keep, pick, done, exact, prefix, stats_bad, nsk, tail_over;
   uint64_t bound_key;
-  double u01, sum, x, eps;
+  double u01, sum, x, eps, x1, eps1, r_prefix, w_lo, w_hi;
 };
 // The workgroup's LDS, at file scope so that the out-of-line paths below address it as LDS.
 __shared__ Shared g_sh;
@@ -1113,6 +1113,181 @@ __device__ __noinline__ bool deep_row(const FinishArgs& a, const RowParams& p, u
   return true;
 }
 
+// --- the draw's unsorted tail --------------------------------------------------------------------
+//
+// Bounds [sh.w_lo, sh.w_hi] on W, the sum of exp((l - top) / T) over S: the row's values that rank below
+// R and are >= fl (min-p's floor as an f32, or -inf). One pass over the row; the history's ids are
+// marked in an LDS bitmap and counted in an LDS hash, left out of the stream and added penalised.
+// Each term comes from the hardware's exp2: for |t| <= 126 its error (the instruction's, and four
+// roundings of t of 2^-24 |t| each) is below 3e-5 relative, and below that terms are under 2^-126
+// each; terms add in f32 in runs of at most 16 (under 1e-6 relative), then in f64. Returns false when
+// the history does not fit the tables.
+constexpr uint32_t kTailHash = 1024;
+
+__device__ __noinline__ bool tail_sums(const FinishArgs& a, const RowParams& p, uint32_t row, uint64_t R,
+                                       float fl, float topf) {
+  Shared& sh = g_sh;
+  const uint32_t n = a.n, tid = threadIdx.x;
+  const float* x = a.logits + (uint64_t)row * a.row_stride;
+  uint32_t hb;
+  const uint32_t he = history_bounds(a, p, row, &hb);
+  const uint32_t extra = a.extra_ids ? p.extra : 0;
+  const bool pen = (p.flags & kFlagPenalties) && (he > hb || extra > 0);
+  // The bitmap over sh.wd, the hash over the sort's bucket tables (both free here).
+  uint32_t* bm = reinterpret_cast<uint32_t*>(sh.wd);
+  uint32_t* hid = sh.bcnt;
+  uint32_t* hcnt = sh.bstart;
+  static_assert(kTailHash <= sizeof(sh.bcnt) / 4 && kTailHash <= sizeof(sh.bstart) / 4, "hash room");
+  if (pen) {
+    const uint32_t words = (n + 31) / 32;
+    if (words > sizeof(sh.wd) / 4) return false;
+    for (uint32_t i = tid; i < words; i += kThreads) bm[i] = 0;
+    for (uint32_t i = tid; i < kTailHash; i += kThreads) {
+      hid[i] = kNone;
+      hcnt[i] = 0;
+    }
+    if (tid == 0) sh.tail_over = 0;
+    __syncthreads();
+    auto mark = [&](uint32_t id) {
+      if (id >= n) return;
+      atomicOr(&bm[id >> 5], 1u << (id & 31u));
+      uint32_t h = (id * 0x9E3779B1u) >> (32 - 10);
+      static_assert(kTailHash == 1u << 10, "the hash's top bits");
+      for (uint32_t probe = 0; probe < kTailHash; ++probe) {
+        const uint32_t prev = atomicCAS(&hid[h], kNone, id);
+        if (prev == kNone || prev == id) {
+          atomicAdd(&hcnt[h], 1u);
+          return;
+        }
+        h = (h + 1) & (kTailHash - 1);
+      }
+      sh.tail_over = 1;
+    };
+    for (uint32_t h = hb + tid; h < he; h += kThreads) mark(a.hist_ids[h]);
+    for (uint32_t h = tid; h < extra; h += kThreads) mark(a.extra_ids[h]);
+    __syncthreads();
+    if (sh.tail_over) return false;
+  }
+  // In S: v >= fl, and v ranks below R: v < R's value, or (rarely) equal to it and below in the
+  // packed order (which also orders -0 below +0).
+  const float rv = key_value((uint32_t)(R >> 32));
+  const float sw = (1.0f / p.temp) * 1.44269502f;
+  auto term = [&](float v, uint32_t id) -> float {
+    bool in = v >= fl && v < rv;
+    if (__builtin_expect(v == rv, 0)) in = v >= fl && pack(total_key(v), id) < R;
+    return in ? __builtin_amdgcn_exp2f((v - topf) * sw) : 0.0f;
+  };
+  double w = 0.0;
+  typedef float f32x4 __attribute__((ext_vector_type(4)));
+  auto masked = [&](uint32_t i) { return pen && ((bm[i >> 5] >> (i & 31u)) & 1u); };
+  if (a.vec && a.row_stride % 4 == 0) {
+    // 16-byte groups, kG per thread per batch, two batches in flight: batch b+1's loads are issued
+    // before batch b is summed.
+    constexpr uint32_t kG = 4, kS = kG * kThreads;
+    const uint32_t ng = n / 4;
+    const f32x4* xv = reinterpret_cast<const f32x4*>(x);
+    f32x4 qa[kG], qb[kG];
+    auto load = [&](f32x4 (&q)[kG], uint32_t g0) {
+#pragma unroll
+      for (uint32_t k = 0; k < kG; ++k) {
+        const uint32_t g = g0 + k * kThreads + tid;
+        q[k] = (g < ng) ? xv[g] : f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+      }
+    };
+    auto sum = [&](const f32x4 (&q)[kG], uint32_t g0) {
+      float acc = 0.0f;
+#pragma unroll
+      for (uint32_t k = 0; k < kG; ++k) {
+        const uint32_t g = g0 + k * kThreads + tid;
+        const uint32_t mask = (g >= ng) ? 15u : pen ? (bm[g >> 3] >> ((4 * g) & 31u)) & 15u : 0u;
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+          const float t = term(q[k][c], 4 * g + c);
+          acc += ((mask >> c) & 1u) ? 0.0f : t;
+        }
+      }
+      w += (double)acc;
+    };
+    load(qa, 0);
+    for (uint32_t g0 = 0; g0 < ng; g0 += 2 * kS) {
+      load(qb, g0 + kS);
+      sum(qa, g0);
+      load(qa, g0 + 2 * kS);
+      sum(qb, g0 + kS);
+    }
+    for (uint32_t i = 4 * ng + tid; i < n; i += kThreads)
+      if (!masked(i)) w += (double)term(x[i], i);
+  } else {
+    for (uint32_t i = tid; i < n; i += kThreads)
+      if (!masked(i)) w += (double)term(x[i], i);
+  }
+  if (pen)
+    for (uint32_t s = tid; s < kTailHash; s += kThreads)
+      if (hid[s] != kNone) w += (double)term(penalize(x[hid[s]], hcnt[s], p), hid[s]);
+  w = block_sum_f64<kWaves>(w, sh.red_d);
+  const double flush = (double)n * 0x1p-125;
+  if (tid == 0) {
+    sh.w_lo = fmax(0.0, w * (1.0 - 1e-4) - flush);
+    sh.w_hi = w * (1.0 + 1e-4) + flush;
+  }
+  __syncthreads();
+  return true;
+}
+
+// The draw when neither filter stops among the P sorted values, so that the kept set runs past
+// them (draw_partial, sample.rs:260-272). The draw is still settled when u falls among the sorted
+// values with the unsorted tail's weight bounded. First from the sorted values alone: each unsorted
+// weight is at most the last sorted one, and for T <= 1 with top-p's total known, w = e^(1/T) <=
+// e * e_last^(1/T - 1) with e = exp(l - top) <= e_last, so the tail is at most e_last^(1/T - 1)
+// times total1's unsorted part. When u falls within that bound of a cumulative weight, one pass
+// over the row bounds S's weight W (S: the values below R, and above the floor). The kept tail is
+// S's first values in rank order: its weight is at most W; all of W when only the floor cuts; and
+// for T <= 1 at least K / M of W, with K the kept tail's mass at T = 1 and M S's (the ratio of the
+// two weights, exp(l - top)^(1/T - 1), falls with the rank). K >= top-p's cumulative mass past the
+// sorted values, or K = M >= W when the floor cuts first. sh.x1 +- sh.eps1 is total1 and sh.r_prefix
+// the sorted values' mass at T = 1 (top-p rows); with_tail: [sh.w_lo, sh.w_hi] bounds W. Returns
+// the rank drawn (P: past every sorted value; kNone: undecided); sh.sum gets the sorted weight.
+__device__ __noinline__ uint32_t draw_past(const FinishArgs& a, const RowParams& p, uint32_t P, bool with_tail) {
+  Shared& sh = g_sh;
+  const double x1 = sh.x1, eps1 = sh.eps1, r_prefix = sh.r_prefix;
+  const uint32_t n = a.n, tid = threadIdx.x;
+  const uint64_t* tab = sh.tab;
+  const double top = (double)key_value(sh.mk), temp = (double)p.temp, top_p = (double)p.top_p;
+  auto val = [&](uint32_t i) -> double { return (double)packed_value(sh.sk[i]); };
+  const double g40 = gamma_n(40.0), gn = gamma_n((double)n);
+  double lo = 0.0, w_hi = __builtin_inf();
+  if (with_tail) {
+    const double w_lo = sh.w_lo;
+    w_hi = sh.w_hi;
+    if (!(p.top_p < 1.0f)) {
+      lo = w_lo;
+    } else if (p.temp <= 1.0f) {
+      const double m_hi = (x1 + eps1) - r_prefix * (1.0 - 2.0 * g40);
+      const double kp = top_p * (x1 - eps1) * (1.0 - 1e-9) - r_prefix * (1.0 + 1e-9);
+      const double k1 = fmin(kp, w_lo);
+      if (k1 > 0.0 && m_hi > 0.0) lo = k1 / m_hi * w_lo;
+    }
+  }
+  for (uint32_t i = tid; i < P; i += kThreads)
+    sh.wd[i] = as_exp::exp_with(tab, __ddiv_rn(__dsub_rn(val(i), top), temp));
+  __syncthreads();
+  double loc[8], off;
+  const double SP = prefix_scan(sh, P, loc, &off);
+  double tail = (double)(n - P) * sh.wd[P - 1] * (1.0 + 4.0 * kU);
+  if (p.top_p < 1.0f && p.temp <= 1.0f) {
+    const double e_last = as_exp::exp_with(tab, __dsub_rn(val(P - 1), top));
+    const double rest = (x1 + eps1) - r_prefix * (1.0 - 2.0 * g40);
+    const double t2 = pow(e_last, 1.0 / temp - 1.0) * (1.0 + 1e-9) * (rest > 0.0 ? rest : 0.0);
+    if (t2 < tail) tail = t2;
+  }
+  tail = fmin(tail, w_hi);
+  const double slo = (SP * (1.0 - g40 - 4.0 * kU) + lo) * (1.0 - gn);
+  const double shi = (SP * (1.0 + g40 + 4.0 * kU) + tail) * (1.0 + gn);
+  const uint32_t j = decide_draw(sh, P, loc, off, sh.u01 * slo * (1.0 - 3.0 * kU), sh.u01 * shi * (1.0 + 3.0 * kU));
+  if (tid == 0) sh.sum = SP;
+  return j;
+}
+
 // --- the kernel ---------------------------------------------------------------------------------
 
 __global__ __launch_bounds__(kThreads) void finish_kernel(const FinishArgs* __restrict__ ap) {
@@ -1349,33 +1524,21 @@ __global__ __launch_bounds__(kThreads) void finish_kernel(const FinishArgs* __re
       } else if (jl == P && complete) {
         keep = n;  // neither filter stops: every value
       } else if (jl == P && !im_exact && !a.kept_ids) {
-        // Neither filter stops among the P sorted values: the kept set runs past them. The draw is
-        // still settled when u falls among the sorted values with the unsorted tail's weight
-        // bounded: it is at most (n - P) times the last sorted weight.
-        for (uint32_t i = tid; i < P; i += kThreads) sh.wd[i] = w_temp(val(i));
-        __syncthreads();
-        double loc[8], off;
-        const double SP = prefix_scan(sh, P, loc, &off);
-        // Each unsorted weight is at most the last sorted one. For T <= 1 with top-p's total known,
-        // also w = e^(1/T) <= e * e_last^(1/T - 1) with e = exp(l - top) <= e_last, so the tail is
-        // at most e_last^(1/T - 1) times total1's unsorted part.
-        double tail = (double)(n - P) * sh.wd[P - 1] * (1.0 + 4.0 * kU);
-        if (p.top_p < 1.0f && p.temp <= 1.0f) {
-          const double e_last = w_one(val(P - 1));
-          const double rest = (x1 + eps1) - r_prefix * (1.0 - 2.0 * gamma_n(40.0));
-          const double t2 = pow(e_last, 1.0 / temp - 1.0) * (1.0 + 1e-9) * (rest > 0.0 ? rest : 0.0);
-          if (t2 < tail) tail = t2;
+        // Neither filter stops among the P sorted values: the kept set runs past them.
+        if (tid == 0) {
+          sh.x1 = x1;
+          sh.eps1 = eps1;
+          sh.r_prefix = r_prefix;
         }
-        const double g40 = gamma_n(40.0), gn = gamma_n((double)n);
-        const double slo = SP * (1.0 - g40 - 4.0 * kU) * (1.0 - gn);
-        const double shi = (SP * (1.0 + g40 + 4.0 * kU) + tail) * (1.0 + gn);
-        const uint32_t j = decide_draw(sh, P, loc, off, sh.u01 * slo * (1.0 - 3.0 * kU),
-                                       sh.u01 * shi * (1.0 + 3.0 * kU));
+        __syncthreads();
+        uint32_t j = draw_past(a, a.params[row], P, false);
+        if (j == kNone && tail_sums(a, a.params[row], row, R, has_floor ? floor_f32(floor) : -__builtin_inff(),
+                                    key_value(sh.mk))) {
+          status |= AS_ROW_TAIL_PASS;
+          j = draw_past(a, a.params[row], P, true);
+        }
         if (j != kNone && j < P) {
-          if (tid == 0) {
-            sh.pick = j;
-            sh.sum = SP;
-          }
+          if (tid == 0) sh.pick = j;  // sh.sum holds the sorted weight
           drawn = true;
           keep = P;  // a lower bound: the kept set's full size is not known
           status |= AS_ROW_KEPT_PARTIAL;

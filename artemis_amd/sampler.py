@@ -22,6 +22,9 @@ AS_OK = 0
 AS_ROW_OK = 0
 AS_ROW_NONFINITE = 1
 AS_ROW_EXACT_PATH = 0x100
+AS_ROW_KEPT_PARTIAL = 0x200
+AS_ROW_DEEP_PATH = 0x400
+AS_ROW_TAIL_PASS = 0x800
 NO_DRAFT = 0xFFFFFFFF
 
 

@@ -43,6 +43,9 @@ extern "C" {
 /* OR-ed into the status: the cut or the draw lay past the fast path's candidates and a second pass
  * over the row settled it (informational; the token is the reference's either way). */
 #define AS_ROW_DEEP_PATH 0x400u
+/* OR-ed into the status with AS_ROW_KEPT_PARTIAL: the draw needed one pass over the row to bound
+ * the weight of the kept values past the sorted ones (informational). */
+#define AS_ROW_TAIL_PASS 0x800u
 
 /* The draft id argmax_rows writes for a row with no finite value
  * (crates/kernels/src/dispatch.rs:61, NO_DRAFT). */

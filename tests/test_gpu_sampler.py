@@ -217,6 +217,35 @@ def test_config5_batch(ctx):
     assert (g["rng"] == rng).all()
 
 
+def test_draws_past_the_sorted_values_match_the_oracle(ctx):
+    # A row whose kept set runs far past the values the finish kernel sorts (top-p keeps ~16,500
+    # values, min-p's floor ~111,000), drawn under many seeds: some draws fall within the tail's
+    # first bound and take the pass that bounds the unsorted weight, others the deep path; every
+    # token and stream must be the oracle's. Also with only the floor cutting, and with T > 1.
+    from artemis_amd import AS_ROW_TAIL_PASS, workloads
+    w = workloads.config5()
+    r = 111
+    base = w.params[r]
+    row = np.ascontiguousarray(w.logits[r])
+    hist = w.histories[r]
+    params, seeds = [], []
+    for variant in [dict(), dict(top_p=1.0), dict(temp=1.3, top_p=0.9)]:
+        for s in range(48):
+            p = dict(temp=base.temp, top_k=0, top_p=base.top_p, min_p=base.min_p, presence=base.presence,
+                     frequency=base.frequency, repetition=base.repetition)
+            p.update(variant)
+            params.append(p)
+            seeds.append(9000 + len(seeds))
+    rows = len(params)
+    g = gpu_batch(ctx, row, params, seeds, [hist] * rows)
+    off, ids = csr([hist] * rows, rows)
+    want, rng = O.sample_rows(params, seeds, row, off, ids, threads=8, shared=True)
+    bad = np.nonzero(g["tokens"] != want)[0]
+    assert len(bad) == 0, [(int(i), params[i], int(g["tokens"][i]), int(want[i]), int(g["status"][i])) for i in bad[:5]]
+    assert (g["rng"] == rng).all()
+    assert (g["status"][:48] & AS_ROW_TAIL_PASS).any(), g["status"][:48]
+
+
 def test_whole_vocabulary_plants(ctx):
     # sample.rs:807-885's plants at the model's vocabulary: ties with the k-th best in later runs,
     # penalised ids in low runs, top values on run edges, signed zeros, all equal, spread highs.
