@@ -3,6 +3,7 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <chrono>
 #include <cmath>
 #include <cstdio>
 #include <cstring>
@@ -14,7 +15,9 @@
 #include "sampler_device.h"
 
 using as_dev::RowParams;
+using as_dev::RowShare;
 using as_dev::SegStats;
+using as_launch::kArgsSlot;
 
 struct as_ctx {
   int device = 0;
@@ -24,9 +27,11 @@ struct as_ctx {
   as_launch::FinishArgs* d_args = nullptr;  // the start of d_block
   void* d_block = nullptr;
   void* h_block[2] = {nullptr, nullptr};
-  hipEvent_t staged[2] = {nullptr, nullptr};
-  int next = 0;
+  uint64_t* h_done = nullptr;  // pinned: the last call whose scan has ended (the finish kernel writes it)
+  uint64_t calls = 0;
   SegStats* d_stats = nullptr;
+  RowShare* d_share = nullptr;
+  bool share_dirty = false;  // a scan ran without its finish (a failed launch): the context is unusable
   uint64_t* d_cands = nullptr;
   uint32_t* d_scratch = nullptr;
   uint64_t scratch_stride = 0;
@@ -134,8 +139,7 @@ RowParams make_row(const as_sampling& s, uint32_t n, const Plan& pl) {
 
 bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
 
-constexpr size_t kArgsSlot = 256;
-static_assert(sizeof(as_launch::FinishArgs) <= kArgsSlot, "FinishArgs slot");
+static_assert(sizeof(as_launch::FinishArgs) <= kArgsSlot && kArgsSlot % 16 == 0, "FinishArgs slot");
 
 // The next profiling event (created on first use), or null when profiling is off.
 hipEvent_t next_event(as_ctx* c) {
@@ -149,9 +153,11 @@ hipEvent_t next_event(as_ctx* c) {
   return c->ev[c->ev_used++];
 }
 
-// One call over n_rows rows: the finish kernel's arguments and the rows' parameter blocks go to the
-// device in one copy through a pinned staging buffer (waiting only if the same buffer's previous
-// copy has not finished), then the scan and finish kernels.
+// One call over n_rows rows: the finish kernel's arguments and the rows' parameter blocks are written
+// to one of two pinned host blocks (waiting only if the call that read that block two calls ago has
+// not finished); the scan reads them there and copies them to device memory for the finish kernel.
+// No copy is queued: a host-to-device copy of a few tens of KB goes through a DMA engine whose
+// hand-offs with the kernels cost more than the kernels' own reads of the block.
 int run_rows(as_ctx* c, const Plan& pl, const RowParams* rows, const float* logits, uint64_t row_stride,
              uint32_t n, uint32_t n_rows, const uint32_t* hist_off, const uint32_t* hist_ids,
              const uint32_t* extra_ids, uint64_t* rng, uint32_t* tokens, uint32_t* status,
@@ -164,6 +170,7 @@ int run_rows(as_ctx* c, const Plan& pl, const RowParams* rows, const float* logi
   a.n = n;
   a.n_seg = n_seg;
   a.params = c->d_params;
+  a.share = c->d_share;
   a.hist_off = hist_off;
   a.hist_ids = hist_ids;
   a.extra_ids = extra_ids;
@@ -180,16 +187,29 @@ int run_rows(as_ctx* c, const Plan& pl, const RowParams* rows, const float* logi
   a.vec = vec ? 1u : 0u;
   a.scratch = c->d_scratch;
   a.scratch_stride = c->scratch_stride;
+  a.done = c->h_done;
+  a.call = ++c->calls;
 
-  const int b = c->next;
-  c->next ^= 1;
-  AS_HIP(c, hipEventSynchronize(c->staged[b]));
+  if (c->share_dirty)
+    return fail(c, AS_ERR_HIP, "an earlier call launched its scan but not its finish kernel: the context's "
+                               "shared words are not clear; destroy it and create another");
+  // Block b was last read by the scan of call a.call - 2; the finish kernel after it wrote its number.
+  const int b = (int)(a.call & 1);
+  // Waits while the GPU works through the calls before it (the host runs at most two calls ahead);
+  // past 50 ms (a stream held up elsewhere) it waits for the stream instead.
+  if (a.call > 2 && __atomic_load_n(c->h_done, __ATOMIC_ACQUIRE) < a.call - 2) {
+    const auto t0 = std::chrono::steady_clock::now();
+    while (__atomic_load_n(c->h_done, __ATOMIC_ACQUIRE) < a.call - 2) {
+      if (std::chrono::steady_clock::now() - t0 > std::chrono::milliseconds(50)) {
+        AS_HIP(c, hipStreamSynchronize(c->stream));
+        break;
+      }
+    }
+  }
   char* h = static_cast<char*>(c->h_block[b]);
+  std::memset(h, 0, kArgsSlot);
   std::memcpy(h, &a, sizeof a);
   std::memcpy(h + kArgsSlot, rows, sizeof(RowParams) * n_rows);
-  AS_HIP(c, hipMemcpyAsync(c->d_block, h, kArgsSlot + sizeof(RowParams) * n_rows, hipMemcpyHostToDevice,
-                           c->stream));
-  AS_HIP(c, hipEventRecord(c->staged[b], c->stream));
 
   hipEvent_t e0 = nullptr, e1 = nullptr, e2 = nullptr;
   if (c->profile && c->ev_used + 3 <= 3 * 4096) {
@@ -198,11 +218,13 @@ int run_rows(as_ctx* c, const Plan& pl, const RowParams* rows, const float* logi
     e2 = next_event(c);
   }
   if (e0) AS_HIP(c, hipEventRecord(e0, c->stream));
+  c->share_dirty = true;
   AS_HIP(c, as_launch::scan(c->stream, vec, logits, c->d_zero, row_stride, n, n_rows, n_seg, pl.slice_len,
-                            c->d_params, hist_off, hist_ids, extra_ids, c->d_stats, c->d_cands,
+                            h, c->d_block, c->d_share, hist_off, hist_ids, extra_ids, c->d_stats, c->d_cands,
                             pl.stride));
   if (e1) AS_HIP(c, hipEventRecord(e1, c->stream));
   AS_HIP(c, as_launch::finish(c->stream, n_rows, c->d_args));
+  c->share_dirty = false;
   if (e2) AS_HIP(c, hipEventRecord(e2, c->stream));
   return AS_OK;
 }
@@ -256,15 +278,15 @@ int as_destroy(as_ctx* c) {
   if (c->stream) (void)hipStreamSynchronize(c->stream);
   (void)hipFree(c->d_block);
   (void)hipFree(c->d_stats);
+  (void)hipFree(c->d_share);
   (void)hipFree(c->d_cands);
   (void)hipFree(c->d_scratch);
   (void)hipFree(c->d_vstatus);
   (void)hipFree(c->d_zero);
   for (hipEvent_t e : c->ev) (void)hipEventDestroy(e);
-  for (int b = 0; b < 2; ++b) {
+  for (int b = 0; b < 2; ++b)
     if (c->h_block[b]) (void)hipHostFree(c->h_block[b]);
-    if (c->staged[b]) (void)hipEventDestroy(c->staged[b]);
-  }
+  if (c->h_done) (void)hipHostFree(c->h_done);
   delete c;
   return AS_OK;
 }
@@ -293,17 +315,18 @@ int as_create(int device, void* hip_stream, uint32_t max_rows, uint32_t max_voca
     c->d_params = reinterpret_cast<RowParams*>(static_cast<char*>(c->d_block) + kArgsSlot);
   }
   if (e == hipSuccess) e = hipMalloc(&c->d_stats, sizeof(SegStats) * (uint64_t)max_rows * max_seg);
+  if (e == hipSuccess) e = hipMalloc(&c->d_share, sizeof(RowShare) * max_rows);
+  if (e == hipSuccess) e = hipMemset(c->d_share, 0, sizeof(RowShare) * max_rows);
   if (e == hipSuccess)
     e = hipMalloc(&c->d_cands, sizeof(uint64_t) * (uint64_t)max_rows * as_launch::kCandCap);
   if (e == hipSuccess) e = hipMalloc(&c->d_scratch, sizeof(uint32_t) * (uint64_t)max_rows * c->scratch_stride);
   if (e == hipSuccess) e = hipMalloc(&c->d_vstatus, sizeof(uint32_t) * max_rows);
   if (e == hipSuccess) e = hipMalloc(&c->d_zero, sizeof(float) * 1024);
   if (e == hipSuccess) e = hipMemset(c->d_zero, 0, sizeof(float) * 1024);
-  for (int b = 0; b < 2 && e == hipSuccess; ++b) {
+  for (int b = 0; b < 2 && e == hipSuccess; ++b)
     e = hipHostMalloc(&c->h_block[b], kArgsSlot + sizeof(RowParams) * max_rows, hipHostMallocDefault);
-    if (e == hipSuccess) e = hipEventCreateWithFlags(&c->staged[b], hipEventDisableTiming);
-    if (e == hipSuccess) e = hipEventRecord(c->staged[b], c->stream);
-  }
+  if (e == hipSuccess) e = hipHostMalloc((void**)&c->h_done, 64, hipHostMallocCoherent);
+  if (e == hipSuccess) *c->h_done = 0;
   if (e != hipSuccess) {
     std::fprintf(stderr, "as_create: %s\n", hipGetErrorString(e));
     as_destroy(c);

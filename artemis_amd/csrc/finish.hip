@@ -1298,7 +1298,11 @@ __global__ __launch_bounds__(kThreads) void finish_kernel(const FinishArgs* __re
   const SegStats* gst = a.stats + (uint64_t)row * a.n_seg;
   const uint32_t n = a.n;
   if (tid < 256) sh.tab[tid] = as_exp::kTable[tid];
-  // The segments' results, all loads in flight at once.
+  // The row's shared words go back to zero for the next scan (this call's scan has ended), and the
+  // host learns that the scan no longer reads the call's parameter block.
+  if (tid < sizeof(RowShare) / 4) reinterpret_cast<uint32_t*>(a.share + row)[tid] = 0u;
+  if (row == 0 && tid == 0) __hip_atomic_store(a.done, a.call, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+  // The slices' results, all loads in flight at once.
   for (uint32_t s = tid; s < a.n_seg; s += kThreads) sh.seg[s] = gst[s];
   __syncthreads();
   const SegStats* st = sh.seg;

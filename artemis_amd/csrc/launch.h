@@ -33,12 +33,18 @@ constexpr uint32_t kHistReserve = 64;
 // Distinct history ids a slice can count (an LDS hash); more send the row to the exact path.
 constexpr uint32_t kHistSlots = 512;
 
+// The finish kernel's arguments and the rows' parameter blocks travel together, in one pinned host
+// block: FinishArgs in the first kArgsSlot bytes, then RowParams per row. The scan reads it where
+// the host wrote it and copies it to device memory for the finish kernel.
+constexpr uint32_t kArgsSlot = 256;
+
 struct FinishArgs {
   const float* logits;
   uint64_t row_stride;
   uint32_t n;
   uint32_t n_seg;
   const as_dev::RowParams* params;
+  as_dev::RowShare* share;
   const uint32_t* hist_off;
   const uint32_t* hist_ids;
   const uint32_t* extra_ids;
@@ -55,14 +61,17 @@ struct FinishArgs {
   uint32_t vec;             // the rows are 16-byte aligned (float4 loads)
   uint32_t* scratch;        // deep and exact paths: 5 x n u32 (+ alignment) per row
   uint64_t scratch_stride;  // u32 per row
+  uint64_t* done;           // pinned host word: the call number whose scan has ended (the host
+  uint64_t call;            //   reuses a parameter block once its call's scan is over)
 };
 
 // n_seg slices of slice_len values per row (the last one shorter).
 // zero: 1,024 readable floats (the loads of a wave with no full chunk of its slice read there).
+// block_in: the pinned host block (arguments, then n_rows RowParams); block_out: its device copy.
 hipError_t scan(hipStream_t stream, bool vec, const float* logits, const float* zero, uint64_t row_stride,
-                uint32_t n, uint32_t n_rows, uint32_t n_seg, uint32_t slice_len, as_dev::RowParams* params,
-                const uint32_t* hist_off, const uint32_t* hist_ids, const uint32_t* extra_ids,
-                as_dev::SegStats* stats, uint64_t* cands, uint32_t cand_stride);
+                uint32_t n, uint32_t n_rows, uint32_t n_seg, uint32_t slice_len, const void* block_in,
+                void* block_out, as_dev::RowShare* share, const uint32_t* hist_off, const uint32_t* hist_ids,
+                const uint32_t* extra_ids, as_dev::SegStats* stats, uint64_t* cands, uint32_t cand_stride);
 
 hipError_t finish(hipStream_t stream, uint32_t n_rows, const FinishArgs* a);
 

@@ -46,15 +46,20 @@ struct RowParams {
   uint32_t hist_len;
   uint32_t extra;       // ids of the extra list appended to the history (verify drafts)
   uint32_t cap;         // candidate slots per slice (slices x cap fit the finish LDS)
-  // Written by the scan during a call (uploaded as zero): the largest wave threshold's key any
-  // slice of the row has published, and the largest key any slice has seen (min-p rows).
-  uint32_t share_bound;
-  uint32_t share_top;
+  uint32_t pad_;
+};
+static_assert(sizeof(RowParams) % 16 == 0, "whole 16-byte words");
+
+// A row's words that its slices share during a scan, in device memory; zero before the scan (the
+// context clears them once, and the finish kernel clears its row's after each scan).
+constexpr uint32_t kShareSlots = 16;
+struct RowShare {
+  uint32_t bound;  // the largest wave threshold's key any slice of the row has published
+  uint32_t top;    // the largest key any slice has seen (min-p rows)
   // Top-k rows: wave i < kShareSlots of the row keeps here the key of its q-th best value so far,
   // q = ceil(k / slots); once every slot is set, their minimum has at least k values at or above it.
-  uint32_t slot[16];
+  uint32_t slot[kShareSlots];
 };
-constexpr uint32_t kShareSlots = 16;
 
 // Per (row, slice) results of the scan.
 struct SegStats {

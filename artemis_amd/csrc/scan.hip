@@ -78,6 +78,7 @@ struct Shared {
   uint32_t hist_out;
   uint32_t overflow;
   uint32_t out_n;  // candidates the waves have written to HBM during the stream
+  RowParams prm;   // the row's parameters, as read from the host block
 };
 // The workgroup's LDS, at file scope so that the out-of-line helpers below address it directly.
 __shared__ Shared g_sh;
@@ -93,8 +94,8 @@ __device__ __forceinline__ uint64_t wave_min_u64(uint64_t v) {
   return v;
 }
 
-// The row's shared words (RowParams::share_bound, share_top), at device scope: the slices of a row
-// run on different XCDs.
+// The row's shared words (RowShare::bound, top), at device scope: the slices of a row run on
+// different XCDs.
 __device__ __forceinline__ void publish(uint32_t* word, uint32_t key) {
   if (word && (threadIdx.x & (kWave - 1)) == 0)
     __hip_atomic_fetch_max(word, key, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -650,23 +651,78 @@ __device__ __forceinline__ void stream(Lane& ln, WaveState& ws, const Slice& sl,
 template <bool kVec>
 __global__ __launch_bounds__(kThreads, 3) void scan_kernel(
     const float* __restrict__ logits, const float* __restrict__ zero, uint64_t row_stride, uint32_t n,
-    uint32_t n_seg, uint32_t slice_len, RowParams* params,
-    const uint32_t* __restrict__ hist_off, const uint32_t* __restrict__ hist_ids,
+    uint32_t n_seg, uint32_t slice_len, const uint32_t* block_in, uint32_t* __restrict__ block_out,
+    RowShare* share, const uint32_t* __restrict__ hist_off, const uint32_t* __restrict__ hist_ids,
     const uint32_t* __restrict__ extra_ids, SegStats* __restrict__ stats, uint64_t* __restrict__ cands,
     uint32_t cand_stride) {
   Shared& sh = g_sh;
   const uint32_t row = blockIdx.y, seg = blockIdx.x, tid = threadIdx.x;
   const uint32_t lane = tid & (kWave - 1), w = tid / kWave;
-  const RowParams& p = params[row];
+
+  // The row's parameters, read where the host wrote them (pinned memory, read with system-scope
+  // loads so that no cache serves an earlier call's), into LDS; the row's first slice also copies
+  // them to device memory for the finish kernel, and the first workgroup copies its arguments.
+  constexpr uint32_t kArgWords = as_launch::kArgsSlot / 4, kRowWords = sizeof(RowParams) / 4;
+  static_assert(kRowWords <= kThreads && kArgWords <= kThreads, "one word per thread");
+  {
+    const uint32_t base = kArgWords + row * kRowWords;
+    if (tid < kRowWords) {
+      const uint32_t v = __hip_atomic_load(block_in + base + tid, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+      reinterpret_cast<uint32_t*>(&sh.prm)[tid] = v;
+      if (seg == 0) block_out[base + tid] = v;
+    }
+    if (seg == 0 && row == 0 && tid < kArgWords)
+      block_out[tid] = __hip_atomic_load(block_in + tid, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+  }
 
   Slice sl;
   sl.x = logits + (uint64_t)row * row_stride;
   sl.zero = zero;
-  sl.share = &params[row].share_bound;
+  sl.share = &share[row].bound;
   sl.b0 = seg * slice_len;
   sl.out = cands + ((uint64_t)row * n_seg + seg) * cand_stride;
   sl.room = cand_stride > as_launch::kHistReserve ? cand_stride - as_launch::kHistReserve : 0u;
   sl.b1 = min(sl.b0 + slice_len, n);
+  const uint32_t len = sl.b1 - sl.b0;
+
+  // In flight with the parameters: the first history ids (kHistRegs per thread; a CSR history is
+  // read before the parameters say whether penalties act), then the wave's first two chunks; the
+  // ids come back first and the LDS tables are built while the chunks arrive.
+  uint32_t hb = 0, he = 0;
+  if (hist_ids && hist_off) {
+    hb = hist_off[row];
+    he = hist_off[row + 1];
+  }
+  constexpr int kHistRegs = 8;
+  uint32_t hreg[kHistRegs];
+#pragma unroll
+  for (int k = 0; k < kHistRegs; ++k) {
+    const uint32_t h = hb + tid + k * kThreads;
+    hreg[k] = (h < he) ? hist_ids[h] : kEmpty;
+  }
+  Walk wk;
+  wk.c0 = sl.b0 + w * kChunk;
+  wk.nfull = (wk.c0 + kChunk <= sl.b1) ? (sl.b1 - wk.c0 - kChunk) / kGroupStep + 1 : 0;
+  f32x4 qa[kU], qb[kU];
+  load_at<kVec>(qa, sl, wk, 0);
+  load_at<kVec>(qb, sl, wk, 1);
+  if (tid == 0) {
+    sh.hist_out = 0;
+    sh.overflow = 0;
+    sh.out_n = 0;
+  }
+  __syncthreads();  // the parameters are in LDS
+
+  const RowParams& p = sh.prm;
+  if (hist_ids && !hist_off) {
+    hb = p.hist_begin;
+    he = p.hist_begin + p.hist_len;
+#pragma unroll
+    for (int k = 0; k < kHistRegs; ++k) {
+      const uint32_t h = hb + tid + k * kThreads;
+      hreg[k] = (h < he) ? hist_ids[h] : kEmpty;
+    }
+  }
   const uint32_t mode = p.mode, flags = p.flags;
   sl.floor_on = mode == kModePartial && p.min_p > 0.0f;
   sl.ln_min_p = p.ln_min_p;
@@ -681,46 +737,13 @@ __global__ __launch_bounds__(kThreads, 3) void scan_kernel(
   sl.first = mode == kModeTopK ? sl.C <= 2u * kWave : true;
   sl.first_rank = mode == kModeTopK ? sl.C : kFirstRankPartial;
   // Top-k rows: the first min(waves of the row, kShareSlots) waves each own a slot.
-  sl.slots = params[row].slot;
+  sl.slots = share[row].slot;
   sl.n_slots = (mode == kModeTopK && sl.first) ? min(n_seg * kWaves, kShareSlots) : 0u;
   sl.q = sl.n_slots ? (p.top_k + sl.n_slots - 1) / sl.n_slots : 0u;
   sl.my_slot = (seg * kWaves + w < sl.n_slots) ? sl.slots + seg * kWaves + w : nullptr;
-
-  uint32_t hb = 0, he = 0;
-  if (hist_ids) {
-    if (hist_off) {
-      hb = hist_off[row];
-      he = hist_off[row + 1];
-    } else {
-      hb = p.hist_begin;
-      he = p.hist_begin + p.hist_len;
-    }
-  }
   const uint32_t extra = extra_ids ? p.extra : 0;
   sl.pen = (flags & kFlagPenalties) && (he > hb || extra > 0);
-  const uint32_t len = sl.b1 - sl.b0;
 
-  // In flight together: the first history ids (kHistRegs per thread), then the wave's first two
-  // chunks; the ids come back first and the LDS tables are built while the chunks arrive.
-  constexpr int kHistRegs = 8;
-  uint32_t hreg[kHistRegs];
-#pragma unroll
-  for (int k = 0; k < kHistRegs; ++k) {
-    const uint32_t h = hb + tid + k * kThreads;
-    hreg[k] = (sl.pen && h < he) ? hist_ids[h] : kEmpty;
-  }
-  Walk wk;
-  wk.c0 = sl.b0 + w * kChunk;
-  wk.nfull = (wk.c0 + kChunk <= sl.b1) ? (sl.b1 - wk.c0 - kChunk) / kGroupStep + 1 : 0;
-  f32x4 qa[kU], qb[kU];
-  load_at<kVec>(qa, sl, wk, 0);
-  load_at<kVec>(qb, sl, wk, 1);
-
-  if (tid == 0) {
-    sh.hist_out = 0;
-    sh.overflow = 0;
-    sh.out_n = 0;
-  }
   if (sl.pen) {
     for (uint32_t i = tid; i < (len + 31) / 32; i += kThreads) sh.bitmap[i] = 0;
     for (uint32_t i = tid; i < kHash; i += kThreads) {
@@ -999,16 +1022,18 @@ __global__ __launch_bounds__(kThreads, 3) void scan_kernel(
 namespace as_launch {
 
 hipError_t scan(hipStream_t stream, bool vec, const float* logits, const float* zero, uint64_t row_stride,
-                uint32_t n, uint32_t n_rows, uint32_t n_seg, uint32_t slice_len, as_dev::RowParams* params,
-                const uint32_t* hist_off, const uint32_t* hist_ids, const uint32_t* extra_ids,
-                as_dev::SegStats* stats, uint64_t* cands, uint32_t cand_stride) {
+                uint32_t n, uint32_t n_rows, uint32_t n_seg, uint32_t slice_len, const void* block_in,
+                void* block_out, as_dev::RowShare* share, const uint32_t* hist_off, const uint32_t* hist_ids,
+                const uint32_t* extra_ids, as_dev::SegStats* stats, uint64_t* cands, uint32_t cand_stride) {
   dim3 grid(n_seg, n_rows);
+  const uint32_t* in = static_cast<const uint32_t*>(block_in);
+  uint32_t* out = static_cast<uint32_t*>(block_out);
   if (vec)
     hipLaunchKernelGGL(scan_kernel<true>, grid, dim3(kThreads), 0, stream, logits, zero, row_stride, n, n_seg,
-                       slice_len, params, hist_off, hist_ids, extra_ids, stats, cands, cand_stride);
+                       slice_len, in, out, share, hist_off, hist_ids, extra_ids, stats, cands, cand_stride);
   else
     hipLaunchKernelGGL(scan_kernel<false>, grid, dim3(kThreads), 0, stream, logits, zero, row_stride, n, n_seg,
-                       slice_len, params, hist_off, hist_ids, extra_ids, stats, cands, cand_stride);
+                       slice_len, in, out, share, hist_off, hist_ids, extra_ids, stats, cands, cand_stride);
   return hipGetLastError();
 }
 

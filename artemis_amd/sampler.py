@@ -129,6 +129,19 @@ def rng_state(seed: int) -> List[int]:
     return [int(x) for x in s]
 
 
+class PackedSampling:
+    """A batch's settings converted once to the C ABI's as_sampling array, for callers that sample the
+    same rows' settings step after step (the engine holds such an array; building it from Python
+    objects costs far more than the call)."""
+
+    def __init__(self, params: Sequence[Sampling]):
+        self.n = len(params)
+        self.arr = (_CSampling * self.n)(*[p._c() for p in params])
+
+    def __len__(self) -> int:
+        return self.n
+
+
 def _u64_as_i64(xs: Sequence[int]) -> List[int]:
     return [x - (1 << 64) if x >= (1 << 63) else x for x in xs]
 
@@ -175,21 +188,31 @@ class Context:
     def sync(self):
         self._ok(lib().as_sync(self.h))
 
-    def sample_batch(self, logits: torch.Tensor, params: Sequence[Sampling], rng: torch.Tensor,
+    def outputs(self, n_rows: int, kept_cap: int = 0, device=None):
+        """Output tensors for sample_batch's `out`: (tokens, status, kept_count, kept_ids, kept_probs)."""
+        dev = device if device is not None else torch.device("cuda", self.device)
+        return (torch.empty(n_rows, dtype=torch.int32, device=dev), torch.empty(n_rows, dtype=torch.int32, device=dev),
+                torch.empty(n_rows, dtype=torch.int32, device=dev),
+                torch.empty((n_rows, max(kept_cap, 1)), dtype=torch.int32, device=dev),
+                torch.empty((n_rows, max(kept_cap, 1)), dtype=torch.float64, device=dev))
+
+    def sample_batch(self, logits: torch.Tensor, params, rng: torch.Tensor,
                      hist_offsets: Optional[torch.Tensor] = None, hist_ids: Optional[torch.Tensor] = None,
-                     kept_cap: int = 0, row_stride: Optional[int] = None, n_vocab: Optional[int] = None):
-        """Sampler::sample on every row at once. Returns (tokens, status, kept_count, kept_ids,
-        kept_probs) device tensors; `rng` ([n, 4] int64) is advanced in place."""
+                     kept_cap: int = 0, row_stride: Optional[int] = None, n_vocab: Optional[int] = None,
+                     out=None):
+        """Sampler::sample on every row at once. `params`: a sequence of Sampling, or a
+        PackedSampling. Returns (tokens, status, kept_count, kept_ids, kept_probs) device tensors
+        (`out` when given, from outputs()); `rng` ([n, 4] int64) is advanced in place."""
         n_rows = len(params)
         assert logits.is_cuda and logits.dtype == torch.float32
         stride = row_stride if row_stride is not None else logits.stride(0)
         nv = n_vocab if n_vocab is not None else logits.shape[-1]
         dev = logits.device
-        tokens = torch.empty(n_rows, dtype=torch.int32, device=dev)
-        status = torch.empty(n_rows, dtype=torch.int32, device=dev)
-        kept_count = torch.empty(n_rows, dtype=torch.int32, device=dev)
-        kept_ids = torch.empty((n_rows, max(kept_cap, 1)), dtype=torch.int32, device=dev)
-        kept_probs = torch.empty((n_rows, max(kept_cap, 1)), dtype=torch.float64, device=dev)
+        if out is None:
+            out = self.outputs(n_rows, kept_cap, dev)
+        tokens, status, kept_count, kept_ids, kept_probs = out
+        assert tokens.numel() >= n_rows and status.numel() >= n_rows and kept_count.numel() >= n_rows
+        assert kept_ids.shape[-1] >= max(kept_cap, 1) and kept_probs.shape[-1] >= max(kept_cap, 1)
         assert rng.dtype == torch.int64 and rng.is_cuda and rng.shape[0] >= n_rows
         b = _CBatch()
         b.logits = logits.data_ptr()
@@ -209,7 +232,7 @@ class Context:
             b.kept_ids = kept_ids.data_ptr()
             b.kept_probs = kept_probs.data_ptr()
             b.kept_cap = kept_cap
-        arr = (_CSampling * n_rows)(*[p._c() for p in params])
+        arr = params.arr if isinstance(params, PackedSampling) else (_CSampling * n_rows)(*[p._c() for p in params])
         self._ok(lib().as_sample(self.h, C.byref(b), arr))
         return tokens, status, kept_count, kept_ids, kept_probs
 
