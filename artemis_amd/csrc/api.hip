@@ -31,6 +31,7 @@ struct as_ctx {
   uint64_t calls = 0;
   SegStats* d_stats = nullptr;
   RowShare* d_share = nullptr;
+  as_dev::RowTail* d_tail = nullptr;
   bool share_dirty = false;  // a scan ran without its finish (a failed launch): the context is unusable
   uint64_t* d_cands = nullptr;
   uint32_t* d_scratch = nullptr;
@@ -171,6 +172,7 @@ int run_rows(as_ctx* c, const Plan& pl, const RowParams* rows, const float* logi
   a.n_seg = n_seg;
   a.params = c->d_params;
   a.share = c->d_share;
+  a.tail = c->d_tail;
   a.hist_off = hist_off;
   a.hist_ids = hist_ids;
   a.extra_ids = extra_ids;
@@ -223,6 +225,7 @@ int run_rows(as_ctx* c, const Plan& pl, const RowParams* rows, const float* logi
                             h, c->d_block, c->d_share, hist_off, hist_ids, extra_ids, c->d_stats, c->d_cands,
                             pl.stride));
   if (e1) AS_HIP(c, hipEventRecord(e1, c->stream));
+  AS_HIP(c, as_launch::tail(c->stream, n_rows, n, c->d_args));
   AS_HIP(c, as_launch::finish(c->stream, n_rows, c->d_args));
   c->share_dirty = false;
   if (e2) AS_HIP(c, hipEventRecord(e2, c->stream));
@@ -279,6 +282,7 @@ int as_destroy(as_ctx* c) {
   (void)hipFree(c->d_block);
   (void)hipFree(c->d_stats);
   (void)hipFree(c->d_share);
+  (void)hipFree(c->d_tail);
   (void)hipFree(c->d_cands);
   (void)hipFree(c->d_scratch);
   (void)hipFree(c->d_vstatus);
@@ -317,6 +321,8 @@ int as_create(int device, void* hip_stream, uint32_t max_rows, uint32_t max_voca
   if (e == hipSuccess) e = hipMalloc(&c->d_stats, sizeof(SegStats) * (uint64_t)max_rows * max_seg);
   if (e == hipSuccess) e = hipMalloc(&c->d_share, sizeof(RowShare) * max_rows);
   if (e == hipSuccess) e = hipMemset(c->d_share, 0, sizeof(RowShare) * max_rows);
+  if (e == hipSuccess) e = hipMalloc(&c->d_tail, sizeof(as_dev::RowTail) * max_rows);
+  if (e == hipSuccess) e = hipMemset(c->d_tail, 0, sizeof(as_dev::RowTail) * max_rows);
   if (e == hipSuccess)
     e = hipMalloc(&c->d_cands, sizeof(uint64_t) * (uint64_t)max_rows * as_launch::kCandCap);
   if (e == hipSuccess) e = hipMalloc(&c->d_scratch, sizeof(uint32_t) * (uint64_t)max_rows * c->scratch_stride);

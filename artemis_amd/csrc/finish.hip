@@ -50,9 +50,10 @@ struct Shared {
   uint32_t red_u[kWaves];
   double red_d[kWaves];
   // Row scalars.
-  uint32_t bad, gi, mk, total, trunc, keep, pick, done, exact, prefix, stats_bad, nsk, tail_over;
+  uint32_t bad, gi, mk, total, trunc, keep, pick, done, exact, prefix, stats_bad, nsk, tail_over, have_tail, tail_count,
+      tail_listed;
   uint64_t bound_key;
-  double u01, sum, x, eps, x1, eps1, r_prefix, w_lo, w_hi;
+  double u01, sum, x, eps, x1, eps1, r_prefix, w_lo, w_hi, m_lo, m_hi;
 };
 // The workgroup's LDS, at file scope so that the out-of-line paths below address it as LDS.
 __shared__ Shared g_sh;
@@ -95,22 +96,6 @@ __device__ double block_exclusive_scan_f64(double x, double* wave_tot) {
   double excl_in_wave = __shfl_up(incl, 1, kWave);
   if (lane == 0) excl_in_wave = 0.0;
   return __dadd_rn(before, excl_in_wave);
-}
-
-__device__ __forceinline__ uint32_t history_bounds(const FinishArgs& a, const RowParams& p,
-                                                   uint32_t row, uint32_t* hb) {
-  uint32_t b = 0, e = 0;
-  if (a.hist_ids) {
-    if (a.hist_off) {
-      b = a.hist_off[row];
-      e = a.hist_off[row + 1];
-    } else {
-      b = p.hist_begin;
-      e = p.hist_begin + p.hist_len;
-    }
-  }
-  *hb = b;
-  return e;
 }
 
 // --- the exact-order path ---------------------------------------------------------------------
@@ -1116,7 +1101,8 @@ __device__ __noinline__ bool deep_row(const FinishArgs& a, const RowParams& p, u
 // --- the draw's unsorted tail --------------------------------------------------------------------
 //
 // Bounds [sh.w_lo, sh.w_hi] on W, the sum of exp((l - top) / T) over S: the row's values that rank below
-// R and are >= fl (min-p's floor as an f32, or -inf). One pass over the row; the history's ids are
+// R and are >= fl (min-p's floor as an f32, or -inf), and [sh.m_lo, sh.m_hi] on M, the sum of
+// exp(l - top) over S. One pass over the row; the history's ids are
 // marked in an LDS bitmap and counted in an LDS hash, left out of the stream and added penalised.
 // Each term comes from the hardware's exp2: for |t| <= 126 its error (the instruction's, and four
 // roundings of t of 2^-24 |t| each) is below 3e-5 relative, and below that terms are under 2^-126
@@ -1171,13 +1157,24 @@ __device__ __noinline__ bool tail_sums(const FinishArgs& a, const RowParams& p, 
   // In S: v >= fl, and v ranks below R: v < R's value, or (rarely) equal to it and below in the
   // packed order (which also orders -0 below +0).
   const float rv = key_value((uint32_t)(R >> 32));
-  const float sw = (1.0f / p.temp) * 1.44269502f;
-  auto term = [&](float v, uint32_t id) -> float {
+  const float s1 = 1.44269502f, sw = (1.0f / p.temp) * s1;
+  double w = 0.0, m = 0.0;
+  // v's terms into (tw, tm) when v is in S.
+  auto term = [&](float v, uint32_t id, float& tw, float& tm) {
     bool in = v >= fl && v < rv;
     if (__builtin_expect(v == rv, 0)) in = v >= fl && pack(total_key(v), id) < R;
-    return in ? __builtin_amdgcn_exp2f((v - topf) * sw) : 0.0f;
+    if (in) {
+      const float d = v - topf;
+      tw += __builtin_amdgcn_exp2f(d * sw);
+      tm += __builtin_amdgcn_exp2f(d * s1);
+    }
   };
-  double w = 0.0;
+  auto one = [&](float v, uint32_t id) {
+    float tw = 0.0f, tm = 0.0f;
+    term(v, id, tw, tm);
+    w += (double)tw;
+    m += (double)tm;
+  };
   typedef float f32x4 __attribute__((ext_vector_type(4)));
   auto masked = [&](uint32_t i) { return pen && ((bm[i >> 5] >> (i & 31u)) & 1u); };
   if (a.vec && a.row_stride % 4 == 0) {
@@ -1195,18 +1192,17 @@ __device__ __noinline__ bool tail_sums(const FinishArgs& a, const RowParams& p, 
       }
     };
     auto sum = [&](const f32x4 (&q)[kG], uint32_t g0) {
-      float acc = 0.0f;
+      float tw = 0.0f, tm = 0.0f;
 #pragma unroll
       for (uint32_t k = 0; k < kG; ++k) {
         const uint32_t g = g0 + k * kThreads + tid;
         const uint32_t mask = (g >= ng) ? 15u : pen ? (bm[g >> 3] >> ((4 * g) & 31u)) & 15u : 0u;
 #pragma unroll
-        for (int c = 0; c < 4; ++c) {
-          const float t = term(q[k][c], 4 * g + c);
-          acc += ((mask >> c) & 1u) ? 0.0f : t;
-        }
+        for (int c = 0; c < 4; ++c)
+          if (!((mask >> c) & 1u)) term(q[k][c], 4 * g + c, tw, tm);
       }
-      w += (double)acc;
+      w += (double)tw;
+      m += (double)tm;
     };
     load(qa, 0);
     for (uint32_t g0 = 0; g0 < ng; g0 += 2 * kS) {
@@ -1216,19 +1212,22 @@ __device__ __noinline__ bool tail_sums(const FinishArgs& a, const RowParams& p, 
       sum(qb, g0 + kS);
     }
     for (uint32_t i = 4 * ng + tid; i < n; i += kThreads)
-      if (!masked(i)) w += (double)term(x[i], i);
+      if (!masked(i)) one(x[i], i);
   } else {
     for (uint32_t i = tid; i < n; i += kThreads)
-      if (!masked(i)) w += (double)term(x[i], i);
+      if (!masked(i)) one(x[i], i);
   }
   if (pen)
     for (uint32_t s = tid; s < kTailHash; s += kThreads)
-      if (hid[s] != kNone) w += (double)term(penalize(x[hid[s]], hcnt[s], p), hid[s]);
+      if (hid[s] != kNone) one(penalize(x[hid[s]], hcnt[s], p), hid[s]);
   w = block_sum_f64<kWaves>(w, sh.red_d);
+  m = block_sum_f64<kWaves>(m, sh.red_d);
   const double flush = (double)n * 0x1p-125;
   if (tid == 0) {
     sh.w_lo = fmax(0.0, w * (1.0 - 1e-4) - flush);
     sh.w_hi = w * (1.0 + 1e-4) + flush;
+    sh.m_lo = fmax(0.0, m * (1.0 - 1e-4) - flush);
+    sh.m_hi = m * (1.0 + 1e-4) + flush;
   }
   __syncthreads();
   return true;
@@ -1244,9 +1243,10 @@ __device__ __noinline__ bool tail_sums(const FinishArgs& a, const RowParams& p, 
 // S's first values in rank order: its weight is at most W; all of W when only the floor cuts; and
 // for T <= 1 at least K / M of W, with K the kept tail's mass at T = 1 and M S's (the ratio of the
 // two weights, exp(l - top)^(1/T - 1), falls with the rank). K >= top-p's cumulative mass past the
-// sorted values, or K = M >= W when the floor cuts first. sh.x1 +- sh.eps1 is total1 and sh.r_prefix
-// the sorted values' mass at T = 1 (top-p rows); with_tail: [sh.w_lo, sh.w_hi] bounds W. Returns
-// the rank drawn (P: past every sorted value; kNone: undecided); sh.sum gets the sorted weight.
+// sorted values, or K = M when the floor cuts first. sh.x1 +- sh.eps1 is total1 and sh.r_prefix the
+// sorted values' mass at T = 1 (top-p rows); with_tail: [sh.w_lo, sh.w_hi] bounds W and [sh.m_lo,
+// sh.m_hi] bounds M. Returns the rank drawn (P: past every sorted value; kNone: undecided); sh.sum
+// gets the sorted weight.
 __device__ __noinline__ uint32_t draw_past(const FinishArgs& a, const RowParams& p, uint32_t P, bool with_tail) {
   Shared& sh = g_sh;
   const double x1 = sh.x1, eps1 = sh.eps1, r_prefix = sh.r_prefix;
@@ -1257,14 +1257,16 @@ __device__ __noinline__ uint32_t draw_past(const FinishArgs& a, const RowParams&
   const double g40 = gamma_n(40.0), gn = gamma_n((double)n);
   double lo = 0.0, w_hi = __builtin_inf();
   if (with_tail) {
-    const double w_lo = sh.w_lo;
+    const double w_lo = sh.w_lo, m_lo = sh.m_lo, m_hi = sh.m_hi;
     w_hi = sh.w_hi;
-    if (!(p.top_p < 1.0f)) {
+    // Top-p's target past the sorted values, at least kp: when S's whole mass is below it, the
+    // floor cuts first (or nothing but the floor cuts) and the kept tail is all of S.
+    const double kp = (p.top_p < 1.0f) ? top_p * (x1 - eps1) * (1.0 - 1e-9) - r_prefix * (1.0 + 1e-9)
+                                       : __builtin_inf();
+    if (m_hi < kp) {
       lo = w_lo;
     } else if (p.temp <= 1.0f) {
-      const double m_hi = (x1 + eps1) - r_prefix * (1.0 - 2.0 * g40);
-      const double kp = top_p * (x1 - eps1) * (1.0 - 1e-9) - r_prefix * (1.0 + 1e-9);
-      const double k1 = fmin(kp, w_lo);
+      const double k1 = fmin(kp, m_lo);
       if (k1 > 0.0 && m_hi > 0.0) lo = k1 / m_hi * w_lo;
     }
   }
@@ -1298,13 +1300,29 @@ __global__ __launch_bounds__(kThreads) void finish_kernel(const FinishArgs* __re
   const SegStats* gst = a.stats + (uint64_t)row * a.n_seg;
   const uint32_t n = a.n;
   if (tid < 256) sh.tab[tid] = as_exp::kTable[tid];
-  // The row's shared words go back to zero for the next scan (this call's scan has ended), and the
-  // host learns that the scan no longer reads the call's parameter block.
-  if (tid < sizeof(RowShare) / 4) reinterpret_cast<uint32_t*>(a.share + row)[tid] = 0u;
+  // The host learns that the scan no longer reads the call's parameter block.
   if (row == 0 && tid == 0) __hip_atomic_store(a.done, a.call, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+  // The tail kernel's sums for the row: whole when every part of a flagged row added its own (within
+  // 3e-5 relative per term; 1e-4 to spare, and terms under 2^-126 that may have flushed to 0).
+  if (tid == 0) {
+    const RowTail t = a.tail[row];
+    const uint32_t parts = (n + as_launch::kTailLen - 1) / as_launch::kTailLen;
+    sh.have_tail = (a.share[row].gave_up != 0u && t.parts == parts && t.failed == 0u) ? 1u : 0u;
+    const double flush = (double)n * 0x1p-125;
+    sh.w_lo = fmax(0.0, t.w * (1.0 - 1e-4) - flush);
+    sh.w_hi = t.w * (1.0 + 1e-4) + flush;
+    sh.m_lo = fmax(0.0, t.m * (1.0 - 1e-4) - flush);
+    sh.m_hi = t.m * (1.0 + 1e-4) + flush;
+    sh.tail_count = t.count;
+    sh.tail_listed = (t.lost == 0u && t.count <= kTailKeep) ? 1u : 0u;
+  }
   // The slices' results, all loads in flight at once.
   for (uint32_t s = tid; s < a.n_seg; s += kThreads) sh.seg[s] = gst[s];
   __syncthreads();
+  // The row's shared words and tail sums go back to zero for the next call (this call's scan and
+  // tail kernel have ended, and their words were read above).
+  if (tid < sizeof(RowShare) / 4) reinterpret_cast<uint32_t*>(a.share + row)[tid] = 0u;
+  if (tid >= 64 && tid < 64 + sizeof(RowTail) / 4) reinterpret_cast<uint32_t*>(a.tail + row)[tid - 64] = 0u;
   const SegStats* st = sh.seg;
 
   if (tid == 0) {
@@ -1527,6 +1545,21 @@ __global__ __launch_bounds__(kThreads) void finish_kernel(const FinishArgs* __re
         keep = jh + 1;  // top-p's cut, certainly, and min-p's comes later
       } else if (jl == P && complete) {
         keep = n;  // neither filter stops: every value
+      } else if (jl == P && !im_exact && sh.have_tail && sh.tail_listed && P + sh.tail_count <= (uint32_t)kCap &&
+                 sh.m_hi < (p.top_p < 1.0f ? top_p * (x1 - eps1) * (1.0 - 1e-9) - r_prefix * (1.0 + 1e-9)
+                                           : __builtin_inf())) {
+        // Neither filter stops among the sorted values, and S's whole mass is short of top-p's
+        // target past them, so the floor cuts first: the kept set is the sorted values and all of
+        // S, which the tail kernel listed. Sorted in with the candidates, they take the exact draw.
+        const uint64_t* list = reinterpret_cast<const uint64_t*>(a.scratch + (uint64_t)row * a.scratch_stride);
+        const uint32_t cnt = sh.tail_count;
+        for (uint32_t i = tid; i < cnt; i += kThreads) sh.sk[P + i] = list[i];
+        __syncthreads();
+        const uint32_t P2 = sort_candidates(sh, P + cnt, 0ull, sh.mk, kNone);
+        if (tid == 0) sh.prefix = P2;
+        keep = P2;
+        status |= AS_ROW_TAIL_PASS;
+        __syncthreads();
       } else if (jl == P && !im_exact && !a.kept_ids) {
         // Neither filter stops among the P sorted values: the kept set runs past them.
         if (tid == 0) {
@@ -1535,11 +1568,19 @@ __global__ __launch_bounds__(kThreads) void finish_kernel(const FinishArgs* __re
           sh.r_prefix = r_prefix;
         }
         __syncthreads();
-        uint32_t j = draw_past(a, a.params[row], P, false);
-        if (j == kNone && tail_sums(a, a.params[row], row, R, has_floor ? floor_f32(floor) : -__builtin_inff(),
-                                    key_value(sh.mk))) {
+        // The tail kernel's sums when it took the row; else the sorted values alone first, and one
+        // pass over the row when they cannot settle the draw.
+        uint32_t j;
+        if (sh.have_tail) {
           status |= AS_ROW_TAIL_PASS;
           j = draw_past(a, a.params[row], P, true);
+        } else {
+          j = draw_past(a, a.params[row], P, false);
+          if (j == kNone && tail_sums(a, a.params[row], row, R, has_floor ? floor_f32(floor) : -__builtin_inff(),
+                                      key_value(sh.mk))) {
+            status |= AS_ROW_TAIL_PASS;
+            j = draw_past(a, a.params[row], P, true);
+          }
         }
         if (j != kNone && j < P) {
           if (tid == 0) sh.pick = j;  // sh.sum holds the sorted weight

@@ -63,7 +63,30 @@ struct FinishArgs {
   uint64_t scratch_stride;  // u32 per row
   uint64_t* done;           // pinned host word: the call number whose scan has ended (the host
   uint64_t call;            //   reuses a parameter block once its call's scan is over)
+  as_dev::RowTail* tail;    // per row: the tail kernel's sums (min-p rows whose scan gave up)
 };
+
+// The row's history ids are hist_ids[*hb, return value), from the CSR offsets or the row's range.
+__device__ __forceinline__ uint32_t history_bounds(const FinishArgs& a, const as_dev::RowParams& p,
+                                                   uint32_t row, uint32_t* hb) {
+  uint32_t b = 0, e = 0;
+  if (a.hist_ids) {
+    if (a.hist_off) {
+      b = a.hist_off[row];
+      e = a.hist_off[row + 1];
+    } else {
+      b = p.hist_begin;
+      e = p.hist_begin + p.hist_len;
+    }
+  }
+  *hb = b;
+  return e;
+}
+
+// The tail kernel covers each of the first kTailRows flagged rows in parts of kTailLen values, one
+// 256-thread workgroup each (16 values per thread).
+constexpr uint32_t kTailLen = 4096;
+constexpr uint32_t kTailRows = 16;
 
 // n_seg slices of slice_len values per row (the last one shorter).
 // zero: 1,024 readable floats (the loads of a wave with no full chunk of its slice read there).
@@ -74,6 +97,10 @@ hipError_t scan(hipStream_t stream, bool vec, const float* logits, const float* 
                 const uint32_t* extra_ids, as_dev::SegStats* stats, uint64_t* cands, uint32_t cand_stride);
 
 hipError_t finish(hipStream_t stream, uint32_t n_rows, const FinishArgs* a);
+
+// Between the scan and the finish: the weights of S for min-p rows whose scan gave up keeping the
+// floor set whole (a no-op for the other rows).
+hipError_t tail(hipStream_t stream, uint32_t n_rows, uint32_t n, const FinishArgs* a);
 
 hipError_t accept(hipStream_t stream, const uint32_t* picks, const uint32_t* status,
                   const uint32_t* drafts, uint32_t k, const uint32_t* stop_ids, uint32_t n_stop,

@@ -59,7 +59,22 @@ struct RowShare {
   // Top-k rows: wave i < kShareSlots of the row keeps here the key of its q-th best value so far,
   // q = ceil(k / slots); once every slot is set, their minimum has at least k values at or above it.
   uint32_t slot[kShareSlots];
+  uint32_t gave_up;  // min-p rows: a slice's bound lay above its floor (not every value above it kept)
+  uint32_t pad_;
 };
+
+// A min-p row whose candidates do not hold its whole floor set: the weights of S, the row's values
+// that rank below the candidates' bound and lie at or above the floor, summed by the tail kernel
+// (sums of f32 terms from the hardware's exp2, each within 3e-5 relative; zero between calls).
+struct RowTail {
+  double w;        // sum of exp((l - top) / T) over S
+  double m;        // sum of exp(l - top) over S
+  uint32_t count;  // values in S; when at most kTailKeep, they are in the row's scratch (packed)
+  uint32_t parts;  // parts of the row summed (the sums cover S once every part has added)
+  uint32_t failed; // a part could not (more distinct history ids than its table holds)
+  uint32_t lost;   // a part held more of S than it could stage (the scratch list is incomplete)
+};
+constexpr uint32_t kTailKeep = 8192;
 
 // Per (row, slice) results of the scan.
 struct SegStats {

@@ -118,6 +118,22 @@ struct WaveState {
   bool spill;    // min-p rows keeping every value above the floor: a full buffer goes to HBM
 };
 
+// The state as scalars: it comes back from the out-of-line helpers in vector registers, and the
+// stream's tests and counts on it are cheaper on scalar ones.
+__device__ __forceinline__ WaveState uniform(WaveState ws) {
+  ws.cnt = __builtin_amdgcn_readfirstlane(ws.cnt);
+  ws.tau_f = __builtin_bit_cast(float, __builtin_amdgcn_readfirstlane(__builtin_bit_cast(uint32_t, ws.tau_f)));
+  // (readfirstlane returns a signed int: each half goes through uint32_t before it widens)
+  const uint32_t hi = (uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)(ws.tau >> 32));
+  const uint32_t lo = (uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)ws.tau);
+  ws.tau = ((uint64_t)hi << 32) | lo;
+  ws.top = __builtin_amdgcn_readfirstlane(ws.top);
+  ws.C = __builtin_amdgcn_readfirstlane(ws.C);
+  ws.sel = __builtin_amdgcn_readfirstlane(ws.sel);
+  ws.spill = __builtin_amdgcn_readfirstlane(ws.spill ? 1u : 0u) != 0u;
+  return ws;
+}
+
 // Selects run once the buffer holds twice C (at least C + 64), and whenever it might overflow.
 __device__ __forceinline__ uint32_t select_at(uint32_t C) { return min(max(2 * C, C + 64), kCapW - kRoom); }
 
@@ -225,9 +241,9 @@ __device__ __noinline__ WaveState wave_select(WaveState ws, uint32_t C, uint32_t
 }
 
 __device__ __forceinline__ void select_now(WaveState& ws, uint32_t C, uint32_t slack, uint32_t* share) {
-  if (ws.cnt <= 2 * kWave) ws = wave_select<2>(ws, C, slack, share);
-  else if (ws.cnt <= 6 * kWave) ws = wave_select<6>(ws, C, slack, share);
-  else ws = wave_select<kQ>(ws, C, slack, share);
+  if (ws.cnt <= 2 * kWave) ws = uniform(wave_select<2>(ws, C, slack, share));
+  else if (ws.cnt <= 6 * kWave) ws = uniform(wave_select<6>(ws, C, slack, share));
+  else ws = uniform(wave_select<kQ>(ws, C, slack, share));
   static_assert(kQ > 6, "three sizes");
 }
 
@@ -342,10 +358,10 @@ __device__ __forceinline__ uint32_t wave_qth(uint32_t x, uint32_t q) {
   return 0;
 }
 
-// The largest unmasked value of the wave's first chunk sets min-p's first floor. When two in five
-// of the chunk's values pass it (min_p so small that the floor bounds nothing), the wave keeps its
-// best kPartialRank like a row without min-p instead of every value above the floor (which still
-// applies). Out of line.
+// The largest unmasked value of the wave's first chunk sets min-p's first floor. When more than one
+// in a hundred of the chunk's values pass it (a floor set of thousands: appending each value above
+// it would cost more than keeping the best few hundred), the wave keeps its best kPartialRank like a
+// row without min-p instead of every value above the floor (which still applies). Out of line.
 __device__ __noinline__ WaveState first_floor(WaveState ws, f32x4 v0, f32x4 v1, f32x4 v2, f32x4 v3,
                                               uint32_t masked, uint32_t e0, double ln_min_p, uint32_t* share) {
   const f32x4 v[kU] = {v0, v1, v2, v3};
@@ -370,7 +386,7 @@ __device__ __noinline__ WaveState first_floor(WaveState ws, f32x4 v0, f32x4 v1, 
       n_v += (uint32_t)__popcll(__ballot(valid));
       n_f += (uint32_t)__popcll(__ballot(valid && v[j][c] >= ws.tau_f));
     }
-  if (5 * n_f > 2 * n_v && ws.C > as_launch::kPartialRank) {
+  if (100 * n_f > n_v && ws.C > as_launch::kPartialRank) {
     ws.spill = false;
     ws.C = as_launch::kPartialRank;
     ws.sel = select_at(ws.C);
@@ -429,22 +445,24 @@ struct Lane {
 };
 
 // Appends the values e0 .. e0+3 of one 16-byte group that reach tau's value and are not masked to
-// the wave's buffer, first making room when it might not take four more per lane.
+// the wave's buffer, first making room when it might not take four more per lane. A value's test is
+// one compare; the mask is looked at only when some lane passes it.
 __device__ __forceinline__ void append4(WaveState& ws, Lane& ln, const f32x4& v, uint32_t e0, uint32_t mask,
                                         const Slice& sl) {
   if (ws.cnt > kCapW - kRoom) {
-    if (ws.spill) ws = spill(ws, sl.out, sl.room, sl.share);
+    if (ws.spill) ws = uniform(spill(ws, sl.out, sl.room, sl.share));
     else select_now(ws, ws.C, ws.C / 4, sl.share);
   }
-  uint64_t* buf = g_sh.buf[threadIdx.x / kWave];
+  uint64_t* buf = g_sh.buf[__builtin_amdgcn_readfirstlane(threadIdx.x / kWave)];
+  const uint32_t nid = ~e0;  // e0 + c packs as nid - c
 #pragma unroll
   for (int c = 0; c < 4; ++c) {
+    if (__ballot(v[c] >= ws.tau_f) == 0ull) continue;
     const bool take = v[c] >= ws.tau_f && !((mask >> c) & 1u);
     const uint64_t m = __ballot(take);
-    if (m == 0ull) continue;
     if (take) {
       const uint32_t key = total_key(v[c]);
-      buf[ws.cnt + lanes_below(m)] = pack(key, e0 + c);
+      buf[ws.cnt + lanes_below(m)] = ((uint64_t)key << 32) | (nid - c);
       ln.amax = max(ln.amax, key);
     }
     ws.cnt += (uint32_t)__popcll(m);
@@ -511,8 +529,8 @@ __device__ __forceinline__ void chunk(Lane& ln, WaveState& ws, const Slice& sl,
 
   if (kFirst) {
     const uint32_t all = mask[0] | mask[1] << 4 | mask[2] << 8 | mask[3] << 12;
-    if (sl.floor_on) ws = first_floor(ws, q[0], q[1], q[2], q[3], all, c0 + lane * 4, sl.ln_min_p, sl.share);
-    else if (sl.first) ws = first_tau(ws, q[0], q[1], q[2], q[3], all, c0 + lane * 4, sl.first_rank, sl.share, sl.my_slot, sl.q);
+    if (sl.floor_on) ws = uniform(first_floor(ws, q[0], q[1], q[2], q[3], all, c0 + lane * 4, sl.ln_min_p, sl.share));
+    else if (sl.first) ws = uniform(first_tau(ws, q[0], q[1], q[2], q[3], all, c0 + lane * 4, sl.first_rank, sl.share, sl.my_slot, sl.q));
   }
   float m4[kU];
 #pragma unroll
@@ -875,7 +893,9 @@ __global__ __launch_bounds__(kThreads, 3) void scan_kernel(
     // One barrier for the slice's bound (the highest wave threshold and the row's shared one), its
     // largest key and its sums' reference.
     const uint64_t* wbuf = sh.buf[w];
-    const uint32_t shared_b = __builtin_amdgcn_readfirstlane((uint32_t)read_shared(sl.share));
+    const uint64_t shared = read_shared(sl.share);
+    const uint32_t shared_b = __builtin_amdgcn_readfirstlane((uint32_t)shared);
+    const uint32_t shared_top = __builtin_amdgcn_readfirstlane((uint32_t)(shared >> 32));
     const uint32_t kmax = wave_max_u32(max(hkey_max, ln.amax));
     const uint32_t rk = wave_max_u32(ln.ref > -__builtin_inff() ? total_key(ln.ref) : 0u);
     if (lane == 0) {
@@ -892,6 +912,11 @@ __global__ __launch_bounds__(kThreads, 3) void scan_kernel(
       rkey = max(rkey, sh.red_u[k]);
     }
     st.max_key = mk;
+    // A min-p row's slice whose bound lies above its floor (from the largest value it knows the row
+    // to hold) did not keep every value above the floor: the row is flagged for the tail kernel.
+    if (sl.floor_on && tid == 0 && bound > floor_tau(max(mk, shared_top), sl.ln_min_p))
+      __hip_atomic_fetch_max(&reinterpret_cast<RowShare*>(sl.share)->gave_up, 1u, __ATOMIC_RELAXED,
+                             __HIP_MEMORY_SCOPE_AGENT);
 
     // Candidates: those spilled during the stream that rank >= bound (compacted in place, a tile at a
     // time: every write lands before the tile being read), every buffered value >= bound, wave by

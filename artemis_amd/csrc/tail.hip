@@ -1,0 +1,232 @@
+// Between the scan and the finish kernel: for a min-p row without a top-k whose scan did not keep
+// every value above the floor (RowShare::gave_up; its floor set is thousands of values), the
+// weights of S, the values that rank below the finish kernel's bound R and lie at or above the
+// floor: W = sum of exp((l - top) / T) and M = sum of exp(l - top), and |S|; when S has at most
+// kTailKeep values they also go to the row's scratch (packed rank keys, in any order), so that the
+// finish kernel can sort the whole floor set. The finish kernel's
+// draw needs them when the kept set (sample.rs:230-272) runs past its sorted candidates: the kept
+// values past them are S's first in rank order (all of S when the floor cuts first). One 256-thread
+// workgroup per kTailLen values of a flagged row (the i-th flagged row, for i < kTailRows; a row past
+// them is left to the finish kernel), the parts' sums added with device atomics.
+#include "sampler_device.h"
+#include "launch.h"
+
+using namespace as_dev;
+using as_launch::FinishArgs;
+
+namespace {
+
+constexpr int kThreads = 256;
+constexpr int kWaves = kThreads / kWave;
+constexpr uint32_t kLen = as_launch::kTailLen;
+constexpr uint32_t kHash = 512;  // distinct history ids in a part
+constexpr uint32_t kStage = 2048;  // values of S a part stages in LDS before they go to scratch
+constexpr uint32_t kEmpty = 0xFFFFFFFFu;
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+static_assert(kLen % (16 * kThreads) == 0, "whole steps");
+
+struct Shared {
+  uint32_t bitmap[kLen / 32];
+  uint32_t hid[kHash];
+  uint32_t hcnt[kHash];
+  uint64_t stage[kStage];
+  double red[kWaves];
+  uint32_t red_u[kWaves];
+  uint32_t row;
+  uint32_t overflow;
+  uint32_t staged;
+  uint32_t base;
+};
+__shared__ Shared g_tsh;
+
+// The number of threads before this one (in the block) whose f is set, plus *base; *base then
+// grows by the block's count.
+__device__ __forceinline__ uint32_t block_exclusive_count(bool f, uint32_t* red, uint32_t* base) {
+  const uint64_t m = __ballot(f);
+  const uint32_t w = threadIdx.x / kWave;
+  const uint32_t in_wave = __builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0u));
+  __syncthreads();
+  if ((threadIdx.x & (kWave - 1)) == 0) red[w] = (uint32_t)__popcll(m);
+  __syncthreads();
+  uint32_t off = *base, all = 0;
+  for (int k = 0; k < kWaves; ++k) {
+    if (k < (int)w) off += red[k];
+    all += red[k];
+  }
+  *base += all;
+  return off + in_wave;
+}
+
+// Whether the finish kernel can need S for the row: a min-p row without a top-k that a slice flagged
+// (its bound lay above its floor), whose finish takes its fast path (no slice with unfinished statistics
+// or non-finite values), and whose candidates' bound R lies above the floor. Fills R, the row's
+// largest value and the floor (as an f32).
+__device__ bool needs_tail(const FinishArgs& a, uint32_t row, uint64_t* R_out, float* top_out, float* fl_out) {
+  if (a.share[row].gave_up == 0u) return false;
+  const RowParams& p = a.params[row];
+  if (p.mode != kModePartial || !(p.min_p > 0.0f)) return false;
+  uint32_t top = 0;
+  uint64_t R = 0;
+  for (uint32_t s = 0; s < a.n_seg; ++s) {
+    const SegStats& t = a.stats[(uint64_t)row * a.n_seg + s];
+    top = max(top, t.max_key);
+    if (t.truncated & 1u) R = max(R, t.bound);
+    if ((t.truncated & 2u) || t.nonfinite != kNone) return false;
+  }
+  const float topf = key_value(top);
+  const float fl = floor_f32(__dadd_rn((double)topf, p.ln_min_p));
+  if (((uint64_t)total_key(fl) << 32) >= R) return false;
+  *R_out = R;
+  *top_out = topf;
+  *fl_out = fl;
+  return true;
+}
+
+__global__ __launch_bounds__(kThreads) void tail_kernel(const FinishArgs* __restrict__ ap, uint32_t n_rows) {
+  Shared& sh = g_tsh;
+  const FinishArgs& a = *ap;
+  const uint32_t part = blockIdx.x, nth = blockIdx.y, tid = threadIdx.x;
+  // The nth flagged row, in row order, when it needs S.
+  if (tid == 0) sh.row = kNone;
+  uint32_t before = 0;
+  for (uint32_t r0 = 0; r0 < n_rows; r0 += kThreads) {
+    const uint32_t r = r0 + tid;
+    const bool f = r < n_rows && a.share[r].gave_up != 0u;
+    const uint32_t mine = block_exclusive_count(f, sh.red_u, &before);
+    if (f && mine == nth) sh.row = r;
+  }
+  __syncthreads();
+  const uint32_t row = sh.row;
+  if (row == kNone) return;
+  uint64_t R = 0;
+  float topf = 0.0f, fl = 0.0f;
+  if (!needs_tail(a, row, &R, &topf, &fl)) return;
+  const RowParams& p = a.params[row];
+  const uint32_t n = a.n, b0 = part * kLen, b1 = min(b0 + kLen, n), len = b1 - b0;
+  const float* x = a.logits + (uint64_t)row * a.row_stride;
+  // The part's values (16 per thread) in flight while the row's history is read.
+  const bool vec = a.vec && a.row_stride % 4 == 0 && len == kLen;
+  float v[16];
+  if (vec) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const f32x4 q = *reinterpret_cast<const f32x4*>(x + b0 + (j * kThreads + tid) * 4);
+#pragma unroll
+      for (int c = 0; c < 4; ++c) v[4 * j + c] = q[c];
+    }
+  } else {
+#pragma unroll
+    for (int k = 0; k < 16; ++k) {
+      const uint32_t off = k * kThreads + tid;
+      v[k] = off < len ? x[b0 + off] : 0.0f;
+    }
+  }
+
+  uint32_t hb;
+  const uint32_t he = as_launch::history_bounds(a, p, row, &hb);
+  const uint32_t extra = a.extra_ids ? p.extra : 0;
+  const bool pen = (p.flags & kFlagPenalties) && (he > hb || extra > 0);
+  if (pen) {
+    for (uint32_t i = tid; i < kLen / 32; i += kThreads) sh.bitmap[i] = 0;
+    for (uint32_t i = tid; i < kHash; i += kThreads) {
+      sh.hid[i] = kEmpty;
+      sh.hcnt[i] = 0;
+    }
+  }
+  if (tid == 0) {
+    sh.overflow = 0;
+    sh.staged = 0;
+  }
+  __syncthreads();
+  if (pen) {
+    auto mark = [&](uint32_t id) {
+      const uint32_t off = id - b0;
+      if (off >= len) return;
+      atomicOr(&sh.bitmap[off >> 5], 1u << (off & 31u));
+      uint32_t h = (id * 0x9E3779B1u) >> (32 - 9);
+      static_assert(kHash == 1u << 9, "the hash's top bits");
+      for (uint32_t probe = 0; probe < kHash; ++probe) {
+        const uint32_t prev = atomicCAS(&sh.hid[h], kEmpty, id);
+        if (prev == kEmpty || prev == id) {
+          atomicAdd(&sh.hcnt[h], 1u);
+          return;
+        }
+        h = (h + 1) & (kHash - 1);
+      }
+      sh.overflow = 1;
+    };
+    for (uint32_t h = hb + tid; h < he; h += kThreads) mark(a.hist_ids[h]);
+    for (uint32_t h = tid; h < extra; h += kThreads) mark(a.extra_ids[h]);
+    __syncthreads();
+  }
+  if (sh.overflow) {
+    if (tid == 0) __hip_atomic_fetch_or(&a.tail[row].failed, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    return;
+  }
+
+  // In S: v >= fl, and v ranks below R: v < R's value, or (rarely) equal to it and below in the
+  // packed order (which also orders -0 below +0).
+  const float rv = key_value((uint32_t)(R >> 32));
+  const float s1 = 1.44269502f, sw = (1.0f / p.temp) * s1;
+  float gw = 0.0f, gm = 0.0f;
+  uint32_t cnt = 0;
+  auto add = [&](float val, uint32_t id) {
+    bool in = val >= fl && val < rv;
+    if (__builtin_expect(val == rv, 0)) in = val >= fl && pack(total_key(val), id) < R;
+    if (in) {
+      const float d = val - topf;
+      gw += __builtin_amdgcn_exp2f(d * sw);
+      gm += __builtin_amdgcn_exp2f(d * s1);
+      ++cnt;
+      const uint32_t i = atomicAdd(&sh.staged, 1u);
+      if (i < kStage) sh.stage[i] = pack(total_key(val), id);
+    }
+  };
+#pragma unroll
+  for (int k = 0; k < 16; ++k) {
+    const uint32_t off = vec ? ((k / 4) * kThreads + tid) * 4 + (k % 4) : k * kThreads + tid;
+    if (off < len && !(pen && ((sh.bitmap[off >> 5] >> (off & 31u)) & 1u))) add(v[k], b0 + off);
+  }
+  double w = (double)gw, m = (double)gm;
+  if (pen) {
+    for (uint32_t s = tid; s < kHash; s += kThreads) {
+      const uint32_t id = sh.hid[s];
+      if (id == kEmpty) continue;
+      gw = 0.0f;
+      gm = 0.0f;
+      add(penalize(x[id], sh.hcnt[s], p), id);
+      w += (double)gw;
+      m += (double)gm;
+    }
+  }
+  w = block_sum_f64<kWaves>(w, sh.red);
+  m = block_sum_f64<kWaves>(m, sh.red);
+  cnt = block_sum_u32<kWaves>(cnt, sh.red_u);
+  RowTail& t = a.tail[row];
+  if (tid == 0) {
+    __hip_atomic_fetch_add(&t.w, w, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __hip_atomic_fetch_add(&t.m, m, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    sh.base = __hip_atomic_fetch_add(&t.count, cnt, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (cnt > kStage) __hip_atomic_fetch_or(&t.lost, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+  __syncthreads();
+  // The staged values to scratch, at the part's place in the row's list, when the list can hold them.
+  const uint32_t base = sh.base, staged = min(cnt, kStage);
+  uint64_t* list = reinterpret_cast<uint64_t*>(a.scratch + (uint64_t)row * a.scratch_stride);
+  if (base + staged <= kTailKeep)
+    for (uint32_t i = tid; i < staged; i += kThreads) list[base + i] = sh.stage[i];
+  __syncthreads();
+  if (tid == 0) __hip_atomic_fetch_add(&t.parts, 1u, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+}  // namespace
+
+namespace as_launch {
+
+hipError_t tail(hipStream_t stream, uint32_t n_rows, uint32_t n, const FinishArgs* a) {
+  hipLaunchKernelGGL(tail_kernel, dim3((n + kTailLen - 1) / kTailLen, min(n_rows, kTailRows)), dim3(kThreads), 0,
+                     stream, a, n_rows);
+  return hipGetLastError();
+}
+
+}  // namespace as_launch

@@ -246,6 +246,30 @@ def test_draws_past_the_sorted_values_match_the_oracle(ctx):
     assert (g["status"][:48] & AS_ROW_TAIL_PASS).any(), g["status"][:48]
 
 
+def test_large_floor_sets_match_the_oracle(ctx):
+    # min-p rows whose floor set holds thousands of values (config 5's rows 254 and 151: 4,302 and
+    # 3,365 values above the floor, top-p far deeper): the scan keeps a few thousand candidates and
+    # the tail kernel lists the rest of the floor set, which the finish kernel sorts in. Tokens,
+    # streams, kept counts and kept lists must be the oracle's, under many seeds.
+    from artemis_amd import AS_ROW_TAIL_PASS, workloads
+    w = workloads.config5()
+    params, seeds, rows, hists = [], [], [], []
+    for r in (254, 151):
+        b = w.params[r]
+        for s in range(32):
+            params.append(dict(temp=b.temp, top_k=0, top_p=b.top_p, min_p=b.min_p, presence=b.presence,
+                               frequency=b.frequency, repetition=b.repetition))
+            seeds.append(7000 + len(seeds))
+            rows.append(w.logits[r])
+            hists.append(w.histories[r])
+    rows = np.stack(rows)
+    g = gpu_batch(ctx, rows, params, seeds, hists, kept_cap=16)
+    want = oracle_rows(rows, params, seeds, hists, kept_cap=16)
+    check_rows(g, want, params, kept_cap=16, label="floor sets")
+    # The tail kernel takes the first 16 flagged rows of a call; the finish kernel settles the rest.
+    assert (g["status"][:16] & AS_ROW_TAIL_PASS).all(), g["status"]
+
+
 def test_whole_vocabulary_plants(ctx):
     # sample.rs:807-885's plants at the model's vocabulary: ties with the k-th best in later runs,
     # penalised ids in low runs, top values on run edges, signed zeros, all equal, spread highs.
