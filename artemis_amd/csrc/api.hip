@@ -38,6 +38,8 @@ struct as_ctx {
   uint64_t scratch_stride = 0;
   uint32_t* d_vstatus = nullptr;
   float* d_zero = nullptr;  // 1,024 zeros the scan's idle loads read
+  as_launch::RowOrder order{};  // the scan's row order for the current call
+  std::vector<std::pair<double, uint32_t>> order_cost;  // its sort keys (kept: no allocation per call)
   std::string err;
   // Profiling: events before the scan, between the kernels and after the finish, per call.
   bool profile = false;
@@ -140,6 +142,37 @@ RowParams make_row(const as_sampling& s, uint32_t n, const Plan& pl) {
 
 bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
 
+// The scan's expected cost of a row's slices, in rough units (a scheduling estimate only: it sets the
+// order in which rows are launched, never what they compute). Greedy rows only stream; top-k rows
+// append and select more as k grows; rows without a top-k keep more candidates and add sums, and
+// min-p's floor set (all of it is kept) grows quickly as min_p falls.
+double row_cost(const RowParams& r) {
+  switch (r.mode) {
+    case as_dev::kModeTopK:
+      return 1.0 + r.top_k / 50.0;
+    case as_dev::kModePartial: {
+      double c = 2.0;
+      if (r.min_p > 0.0f && r.min_p < 0.03f) c += 1.5;
+      if (r.min_p > 0.0f && r.min_p < 0.005f) c += 1.0;
+      return c;
+    }
+    default:
+      return 0.0;
+  }
+}
+
+// The costliest rows first (ties in row order), so that they get the older waves of their CU.
+void order_rows(const RowParams* rows, uint32_t n_rows, as_launch::RowOrder* o,
+                std::vector<std::pair<double, uint32_t>>& c) {
+  o->on = 0;
+  if (n_rows < 2 || n_rows > as_launch::kOrderMax) return;
+  c.resize(n_rows);
+  for (uint32_t r = 0; r < n_rows; ++r) c[r] = {-row_cost(rows[r]), r};
+  std::stable_sort(c.begin(), c.end());
+  for (uint32_t r = 0; r < n_rows; ++r) o->r[r] = (uint16_t)c[r].second;
+  o->on = 1;
+}
+
 static_assert(sizeof(as_launch::FinishArgs) <= kArgsSlot && kArgsSlot % 16 == 0, "FinishArgs slot");
 
 // The next profiling event (created on first use), or null when profiling is off.
@@ -221,9 +254,10 @@ int run_rows(as_ctx* c, const Plan& pl, const RowParams* rows, const float* logi
   }
   if (e0) AS_HIP(c, hipEventRecord(e0, c->stream));
   c->share_dirty = true;
+  order_rows(rows, n_rows, &c->order, c->order_cost);
   AS_HIP(c, as_launch::scan(c->stream, vec, logits, c->d_zero, row_stride, n, n_rows, n_seg, pl.slice_len,
                             h, c->d_block, c->d_share, hist_off, hist_ids, extra_ids, c->d_stats, c->d_cands,
-                            pl.stride));
+                            pl.stride, c->order));
   if (e1) AS_HIP(c, hipEventRecord(e1, c->stream));
   AS_HIP(c, as_launch::tail(c->stream, n_rows, n, c->d_args));
   AS_HIP(c, as_launch::finish(c->stream, n_rows, c->d_args));
@@ -309,6 +343,7 @@ int as_create(int device, void* hip_stream, uint32_t max_rows, uint32_t max_voca
   c->max_vocab = max_vocab;
   c->max_history = max_history;
   c->max_seg = max_seg;
+  c->order_cost.reserve(std::min(max_rows, as_launch::kOrderMax));
   // Per row: u32 counts [n], then (8-byte aligned) two u64 buffers [n] each for the deep and
   // exact-order paths; rounded to 4 words so every row's scratch starts 16-byte aligned.
   c->scratch_stride = (5ull * max_vocab + 2 + 3) & ~3ull;

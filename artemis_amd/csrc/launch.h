@@ -88,13 +88,25 @@ __device__ __forceinline__ uint32_t history_bounds(const FinishArgs& a, const as
 constexpr uint32_t kTailLen = 4096;
 constexpr uint32_t kTailRows = 16;
 
+// The order in which the scan's workgroups take rows: the workgroups of launch row y (grid y) scan
+// row r[y]. Workgroups launched earlier hold the older waves of their CU, which the hardware serves
+// first, so a slice's time grows with its launch position (about 10% from the first 256 workgroups to
+// the last); the host puts the rows it expects to cost most first. At most kOrderMax rows (a larger
+// call, or on = 0, takes the rows in order). Passed by value, in the kernel's arguments.
+constexpr uint32_t kOrderMax = 1024;
+struct RowOrder {
+  uint32_t on;
+  uint16_t r[kOrderMax];
+};
+
 // n_seg slices of slice_len values per row (the last one shorter).
 // zero: 1,024 readable floats (the loads of a wave with no full chunk of its slice read there).
 // block_in: the pinned host block (arguments, then n_rows RowParams); block_out: its device copy.
 hipError_t scan(hipStream_t stream, bool vec, const float* logits, const float* zero, uint64_t row_stride,
                 uint32_t n, uint32_t n_rows, uint32_t n_seg, uint32_t slice_len, const void* block_in,
                 void* block_out, as_dev::RowShare* share, const uint32_t* hist_off, const uint32_t* hist_ids,
-                const uint32_t* extra_ids, as_dev::SegStats* stats, uint64_t* cands, uint32_t cand_stride);
+                const uint32_t* extra_ids, as_dev::SegStats* stats, uint64_t* cands, uint32_t cand_stride,
+                const RowOrder& order);
 
 hipError_t finish(hipStream_t stream, uint32_t n_rows, const FinishArgs* a);
 

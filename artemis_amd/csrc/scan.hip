@@ -15,7 +15,7 @@
 //     above its threshold tau; values are tested four at a time by their maximum. tau rises when the
 //     buffer holds a few times C values (C = top_k, or a fixed depth for rows without a top-k) to the
 //     C-th best it holds, and the wave publishes that key to the row's shared word with a
-//     device-wide atomic max. Every wave of the row reads the word once per two chunks and raises its
+//     device-wide atomic max. Every wave of the row reads the word once per kShareEvery chunks and raises its
 //     own tau to it: for a top-k row a wave holding k values at or above a key proves that no value
 //     below it is among the row's k best (sample.rs:157-166), so all slices filter with the best
 //     bound any of them has found. Rows with min-p also share the largest value seen, and no wave
@@ -45,6 +45,11 @@ constexpr uint32_t kRoom = 4 * kWave;           // the most one 16-byte group pe
 // Rows without a top-k start from the 16th best of each wave's first chunk: shared over a row's
 // waves, about its 2,000th-3,000th value, near the depth their selects keep, so that few run.
 constexpr uint32_t kFirstRankPartial = 16;
+// Waves read the row's shared words once per kShareEvery chunks (an even number): the read is an
+// agent-scope load, slower than the stream's own, and loads complete in order, so each read delays
+// the chunk loaded after it (measured: every two chunks cost ~7 us per top-k slice over every eight).
+constexpr uint32_t kShareEvery = 8;
+static_assert(kShareEvery % 2 == 0, "reads fall on the loop's odd chunks");
 constexpr uint32_t kHash = as_launch::kHistSlots;
 constexpr int kHashPer = kHash / kThreads;
 constexpr int kHashShift = 32 - __builtin_ctz(kHash);  // the multiplicative hash's top bits
@@ -311,8 +316,9 @@ __device__ __noinline__ WaveState spill(WaveState ws, uint64_t* out, uint32_t ro
 // The starting threshold from the wave's first chunk (16 values per lane, those with a bit set in
 // `masked` left out): the lane's two best by rank, then the wave's C-th best of those 128, which at
 // least C values of the chunk meet (with C above 128, the 128th); published to the row. Fewer valid
-// values leave it at 0. Out of line: it runs once a slice.
-__device__ __noinline__ WaveState first_tau(WaveState ws, f32x4 v0, f32x4 v1, f32x4 v2, f32x4 v3,
+// values leave it at 0. Inline, as first_floor: it runs while the wave's next chunk is in flight,
+// and an out-of-line call begins by waiting for every load the wave has issued.
+__device__ __forceinline__ WaveState first_tau(WaveState ws, f32x4 v0, f32x4 v1, f32x4 v2, f32x4 v3,
                                             uint32_t masked, uint32_t e0, uint32_t C, uint32_t* share,
                                             uint32_t* slot, uint32_t q) {
   const f32x4 v[kU] = {v0, v1, v2, v3};
@@ -361,8 +367,8 @@ __device__ __forceinline__ uint32_t wave_qth(uint32_t x, uint32_t q) {
 // The largest unmasked value of the wave's first chunk sets min-p's first floor. When more than one
 // in a hundred of the chunk's values pass it (a floor set of thousands: appending each value above
 // it would cost more than keeping the best few hundred), the wave keeps its best kPartialRank like a
-// row without min-p instead of every value above the floor (which still applies). Out of line.
-__device__ __noinline__ WaveState first_floor(WaveState ws, f32x4 v0, f32x4 v1, f32x4 v2, f32x4 v3,
+// row without min-p instead of every value above the floor (which still applies).
+__device__ __forceinline__ WaveState first_floor(WaveState ws, f32x4 v0, f32x4 v1, f32x4 v2, f32x4 v3,
                                               uint32_t masked, uint32_t e0, double ln_min_p, uint32_t* share) {
   const f32x4 v[kU] = {v0, v1, v2, v3};
   uint32_t k = 0;
@@ -637,8 +643,8 @@ __device__ __forceinline__ void apply_shared(WaveState& ws, const Slice& sl, uin
 }
 
 // The walk: qa and qb hold chunks 0 and 1 (as loaded); chunk i+1 is in flight while chunk i is
-// worked on, and the row's shared words are read once per two chunks; then the partial chunk at the
-// slice's end.
+// worked on, and the row's shared words are read once per kShareEvery chunks; then the partial chunk
+// at the slice's end.
 template <int kKind, bool kVec>
 __device__ __forceinline__ void stream(Lane& ln, WaveState& ws, const Slice& sl,
                                        const Walk& wk, f32x4 (&qa)[kU], f32x4 (&qb)[kU]) {
@@ -647,11 +653,12 @@ __device__ __forceinline__ void stream(Lane& ln, WaveState& ws, const Slice& sl,
   if (nfull > 0) {
     chunk<kKind, false, true>(ln, ws, sl, qa, wk.c0);
     for (uint32_t i = 1; i < nfull; i += 2) {
-      const uint64_t w = kShare ? read_shared(sl.share) : 0ull;
-      const uint32_t sv = read_slot(sl);
+      const bool now = kShare && (i % kShareEvery) == 1;
+      const uint64_t w = now ? read_shared(sl.share) : 0ull;
+      const uint32_t sv = now ? read_slot(sl) : 0xFFFFFFFFu;
       load_at<kVec>(qa, sl, wk, i + 1);
       chunk<kKind, false, false>(ln, ws, sl, qb, wk.c0 + i * kGroupStep);
-      if (kShare) apply_shared(ws, sl, w, sv, ln.amax);
+      if (now) apply_shared(ws, sl, w, sv, ln.amax);
       if (i + 1 >= nfull) break;
       load_at<kVec>(qb, sl, wk, i + 2);
       chunk<kKind, false, false>(ln, ws, sl, qa, wk.c0 + (i + 1) * kGroupStep);
@@ -672,9 +679,9 @@ __global__ __launch_bounds__(kThreads, 3) void scan_kernel(
     uint32_t n_seg, uint32_t slice_len, const uint32_t* block_in, uint32_t* __restrict__ block_out,
     RowShare* share, const uint32_t* __restrict__ hist_off, const uint32_t* __restrict__ hist_ids,
     const uint32_t* __restrict__ extra_ids, SegStats* __restrict__ stats, uint64_t* __restrict__ cands,
-    uint32_t cand_stride) {
+    uint32_t cand_stride, as_launch::RowOrder order) {
   Shared& sh = g_sh;
-  const uint32_t row = blockIdx.y, seg = blockIdx.x, tid = threadIdx.x;
+  const uint32_t row = order.on ? (uint32_t)order.r[blockIdx.y] : blockIdx.y, seg = blockIdx.x, tid = threadIdx.x;
   const uint32_t lane = tid & (kWave - 1), w = tid / kWave;
 
   // The row's parameters, read where the host wrote them (pinned memory, read with system-scope
@@ -1049,16 +1056,17 @@ namespace as_launch {
 hipError_t scan(hipStream_t stream, bool vec, const float* logits, const float* zero, uint64_t row_stride,
                 uint32_t n, uint32_t n_rows, uint32_t n_seg, uint32_t slice_len, const void* block_in,
                 void* block_out, as_dev::RowShare* share, const uint32_t* hist_off, const uint32_t* hist_ids,
-                const uint32_t* extra_ids, as_dev::SegStats* stats, uint64_t* cands, uint32_t cand_stride) {
+                const uint32_t* extra_ids, as_dev::SegStats* stats, uint64_t* cands, uint32_t cand_stride,
+                const RowOrder& order) {
   dim3 grid(n_seg, n_rows);
   const uint32_t* in = static_cast<const uint32_t*>(block_in);
   uint32_t* out = static_cast<uint32_t*>(block_out);
   if (vec)
     hipLaunchKernelGGL(scan_kernel<true>, grid, dim3(kThreads), 0, stream, logits, zero, row_stride, n, n_seg,
-                       slice_len, in, out, share, hist_off, hist_ids, extra_ids, stats, cands, cand_stride);
+                       slice_len, in, out, share, hist_off, hist_ids, extra_ids, stats, cands, cand_stride, order);
   else
     hipLaunchKernelGGL(scan_kernel<false>, grid, dim3(kThreads), 0, stream, logits, zero, row_stride, n, n_seg,
-                       slice_len, in, out, share, hist_off, hist_ids, extra_ids, stats, cands, cand_stride);
+                       slice_len, in, out, share, hist_off, hist_ids, extra_ids, stats, cands, cand_stride, order);
   return hipGetLastError();
 }
 
