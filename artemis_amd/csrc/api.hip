@@ -32,6 +32,7 @@ struct as_ctx {
   SegStats* d_stats = nullptr;
   RowShare* d_share = nullptr;
   as_dev::RowTail* d_tail = nullptr;
+  as_dev::TailBins* d_tail_bins = nullptr;
   bool share_dirty = false;  // a scan ran without its finish (a failed launch): the context is unusable
   uint64_t* d_cands = nullptr;
   uint32_t* d_scratch = nullptr;
@@ -206,6 +207,7 @@ int run_rows(as_ctx* c, const Plan& pl, const RowParams* rows, const float* logi
   a.params = c->d_params;
   a.share = c->d_share;
   a.tail = c->d_tail;
+  a.tail_bins = c->d_tail_bins;
   a.hist_off = hist_off;
   a.hist_ids = hist_ids;
   a.extra_ids = extra_ids;
@@ -317,6 +319,7 @@ int as_destroy(as_ctx* c) {
   (void)hipFree(c->d_stats);
   (void)hipFree(c->d_share);
   (void)hipFree(c->d_tail);
+  (void)hipFree(c->d_tail_bins);
   (void)hipFree(c->d_cands);
   (void)hipFree(c->d_scratch);
   (void)hipFree(c->d_vstatus);
@@ -358,6 +361,8 @@ int as_create(int device, void* hip_stream, uint32_t max_rows, uint32_t max_voca
   if (e == hipSuccess) e = hipMemset(c->d_share, 0, sizeof(RowShare) * max_rows);
   if (e == hipSuccess) e = hipMalloc(&c->d_tail, sizeof(as_dev::RowTail) * max_rows);
   if (e == hipSuccess) e = hipMemset(c->d_tail, 0, sizeof(as_dev::RowTail) * max_rows);
+  if (e == hipSuccess) e = hipMalloc(&c->d_tail_bins, sizeof(as_dev::TailBins) * max_rows);
+  if (e == hipSuccess) e = hipMemset(c->d_tail_bins, 0, sizeof(as_dev::TailBins) * max_rows);
   if (e == hipSuccess)
     e = hipMalloc(&c->d_cands, sizeof(uint64_t) * (uint64_t)max_rows * as_launch::kCandCap);
   if (e == hipSuccess) e = hipMalloc(&c->d_scratch, sizeof(uint32_t) * (uint64_t)max_rows * c->scratch_stride);

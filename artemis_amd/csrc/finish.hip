@@ -51,7 +51,7 @@ struct Shared {
   double red_d[kWaves];
   // Row scalars.
   uint32_t bad, gi, mk, total, trunc, keep, pick, done, exact, prefix, stats_bad, nsk, tail_over, have_tail, tail_count,
-      tail_listed;
+      tail_listed, tail_parts;
   uint64_t bound_key;
   double u01, sum, x, eps, x1, eps1, r_prefix, w_lo, w_hi, m_lo, m_hi;
 };
@@ -1245,9 +1245,13 @@ __device__ __noinline__ bool tail_sums(const FinishArgs& a, const RowParams& p, 
 // two weights, exp(l - top)^(1/T - 1), falls with the rank). K >= top-p's cumulative mass past the
 // sorted values, or K = M when the floor cuts first. sh.x1 +- sh.eps1 is total1 and sh.r_prefix the
 // sorted values' mass at T = 1 (top-p rows); with_tail: [sh.w_lo, sh.w_hi] bounds W and [sh.m_lo,
-// sh.m_hi] bounds M. Returns the rank drawn (P: past every sorted value; kNone: undecided); sh.sum
-// gets the sorted weight.
-__device__ __noinline__ uint32_t draw_past(const FinishArgs& a, const RowParams& p, uint32_t P, bool with_tail) {
+// sh.m_hi] bounds M. With bins (the tail kernel's histogram of S, TailBins), the cut is placed
+// within S by the bins' cumulative mass at T = 1: every bin whose cumulative mass stays below top-p's
+// least target is kept whole, and no bin past the first whose cumulative mass reaches its largest
+// target is kept at all, which bounds the kept tail's weight by sums of whole bins. Returns the rank
+// drawn (P: past every sorted value; kNone: undecided); sh.sum gets the sorted weight.
+__device__ __noinline__ uint32_t draw_past(const FinishArgs& a, const RowParams& p, uint32_t row, uint32_t P,
+                                           bool with_tail, bool bins) {
   Shared& sh = g_sh;
   const double x1 = sh.x1, eps1 = sh.eps1, r_prefix = sh.r_prefix;
   const uint32_t n = a.n, tid = threadIdx.x;
@@ -1268,6 +1272,31 @@ __device__ __noinline__ uint32_t draw_past(const FinishArgs& a, const RowParams&
     } else if (p.temp <= 1.0f) {
       const double k1 = fmin(kp, m_lo);
       if (k1 > 0.0 && m_hi > 0.0) lo = k1 / m_hi * w_lo;
+    }
+    if (bins && p.top_p < 1.0f) {
+      // Top-p's target past the sorted values lies in [kp, kq]. Each bin's sums are within 1e-4
+      // relative (as RowTail's) plus its flushed terms; their prefix sums add at most gamma(256).
+      const double kq = top_p * (x1 + eps1) * (1.0 + 1e-9) - r_prefix * (1.0 - 1e-9);
+      const double fl_b = (double)n * 0x1p-125, slack = 1e-4 + gamma_n(300.0);
+      const as_dev::TailBins& tb = a.tail_bins[row];
+      double bm = 0.0, bw = 0.0;
+      if (tid < as_dev::kTailBins) {
+        bm = tb.m[tid];
+        bw = tb.w[tid];
+      }
+      const double mlo = fmax(0.0, bm * (1.0 - slack) - fl_b), mhi = bm * (1.0 + slack) + fl_b;
+      const double wlo = fmax(0.0, bw * (1.0 - slack) - fl_b), whi = bw * (1.0 + slack) + fl_b;
+      const double cm_hi = __dadd_rn(block_exclusive_scan_f64(mhi, sh.red_d), mhi);
+      const double cm_lo = __dadd_rn(block_exclusive_scan_f64(mlo, sh.red_d), mlo);
+      const bool valid = tid < as_dev::kTailBins;
+      // b_min: the first bin whose cumulative mass can reach kp (the bins before it are kept whole);
+      // b_max: the first whose cumulative mass surely reaches kq (no later bin is kept).
+      const uint32_t b_min = block_min_u32<kWaves>(valid && cm_hi >= kp ? tid : kNone, sh.red_u);
+      const uint32_t b_max = block_min_u32<kWaves>(valid && cm_lo >= kq ? tid : kNone, sh.red_u);
+      const double before = block_sum_f64<kWaves>(valid && tid < b_min ? wlo : 0.0, sh.red_d);
+      const double upto = block_sum_f64<kWaves>(valid && tid <= b_max ? whi : 0.0, sh.red_d);
+      lo = fmax(lo, before * (1.0 - gamma_n(300.0)));
+      if (b_max != kNone) w_hi = fmin(w_hi, upto * (1.0 + gamma_n(300.0)));
     }
   }
   for (uint32_t i = tid; i < P; i += kThreads)
@@ -1292,9 +1321,8 @@ __device__ __noinline__ uint32_t draw_past(const FinishArgs& a, const RowParams&
 
 // --- the kernel ---------------------------------------------------------------------------------
 
-__global__ __launch_bounds__(kThreads) void finish_kernel(const FinishArgs* __restrict__ ap) {
+__device__ __forceinline__ void finish_row(const FinishArgs& a) {
   Shared& sh = g_sh;
-  const FinishArgs& a = *ap;
   const uint32_t row = blockIdx.x, tid = threadIdx.x;
   const RowParams p = a.params[row];
   const SegStats* gst = a.stats + (uint64_t)row * a.n_seg;
@@ -1315,6 +1343,7 @@ __global__ __launch_bounds__(kThreads) void finish_kernel(const FinishArgs* __re
     sh.m_hi = t.m * (1.0 + 1e-4) + flush;
     sh.tail_count = t.count;
     sh.tail_listed = (t.lost == 0u && t.count <= kTailKeep) ? 1u : 0u;
+    sh.tail_parts = t.parts;
   }
   // The slices' results, all loads in flight at once.
   for (uint32_t s = tid; s < a.n_seg; s += kThreads) sh.seg[s] = gst[s];
@@ -1573,13 +1602,13 @@ __global__ __launch_bounds__(kThreads) void finish_kernel(const FinishArgs* __re
         uint32_t j;
         if (sh.have_tail) {
           status |= AS_ROW_TAIL_PASS;
-          j = draw_past(a, a.params[row], P, true);
+          j = draw_past(a, a.params[row], row, P, true, true);
         } else {
-          j = draw_past(a, a.params[row], P, false);
+          j = draw_past(a, a.params[row], row, P, false, false);
           if (j == kNone && tail_sums(a, a.params[row], row, R, has_floor ? floor_f32(floor) : -__builtin_inff(),
                                       key_value(sh.mk))) {
             status |= AS_ROW_TAIL_PASS;
-            j = draw_past(a, a.params[row], P, true);
+            j = draw_past(a, a.params[row], row, P, true, false);
           }
         }
         if (j != kNone && j < P) {
@@ -1694,6 +1723,18 @@ __global__ __launch_bounds__(kThreads) void finish_kernel(const FinishArgs* __re
       __syncthreads();
       exact_row(a, a.params[row], row);
     }
+  }
+}
+
+__global__ __launch_bounds__(kThreads) void finish_kernel(const FinishArgs* __restrict__ ap) {
+  const FinishArgs& a = *ap;
+  finish_row(a);
+  // The row's tail histogram goes back to zero for the next call once this row is done with it
+  // (every path above has ended, in every thread).
+  __syncthreads();
+  if (g_sh.tail_parts != 0u && threadIdx.x < as_dev::kTailBins) {
+    a.tail_bins[blockIdx.x].m[threadIdx.x] = 0.0;
+    a.tail_bins[blockIdx.x].w[threadIdx.x] = 0.0;
   }
 }
 

@@ -64,6 +64,7 @@ struct FinishArgs {
   uint64_t* done;           // pinned host word: the call number whose scan has ended (the host
   uint64_t call;            //   reuses a parameter block once its call's scan is over)
   as_dev::RowTail* tail;    // per row: the tail kernel's sums (min-p rows whose scan gave up)
+  as_dev::TailBins* tail_bins;  // per row: the tail kernel's histogram of S
 };
 
 // The row's history ids are hist_ids[*hb, return value), from the CSR offsets or the row's range.

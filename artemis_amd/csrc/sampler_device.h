@@ -75,6 +75,15 @@ struct RowTail {
   uint32_t lost;   // a part held more of S than it could stage (the scratch list is incomplete)
 };
 constexpr uint32_t kTailKeep = 8192;
+// The tail kernel's histogram of S by value: bin b holds the values v with
+// floor(min(rv - v) * kTailBins / (rv - fl), kTailBins - 1) = b (rv: the value of the candidates' bound,
+// fl: the floor), so that every value of bin b ranks above every value of bin b + 1; per bin the
+// sums of exp(l - top) (m) and exp((l - top) / T) (w), each term as in RowTail. Zero between calls.
+constexpr uint32_t kTailBins = 256;
+struct TailBins {
+  double m[kTailBins];
+  double w[kTailBins];
+};
 
 // Per (row, slice) results of the scan.
 struct SegStats {

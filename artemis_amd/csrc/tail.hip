@@ -3,7 +3,8 @@
 // weights of S, the values that rank below the finish kernel's bound R and lie at or above the
 // floor: W = sum of exp((l - top) / T) and M = sum of exp(l - top), and |S|; when S has at most
 // kTailKeep values they also go to the row's scratch (packed rank keys, in any order), so that the
-// finish kernel can sort the whole floor set. The finish kernel's
+// finish kernel can sort the whole floor set; and S's histogram by value (TailBins), which places
+// top-p's cut within one bin. The finish kernel's
 // draw needs them when the kept set (sample.rs:230-272) runs past its sorted candidates: the kept
 // values past them are S's first in rank order (all of S when the floor cuts first). One 256-thread
 // workgroup per kTailLen values of a flagged row (the i-th flagged row, for i < kTailRows; a row past
@@ -25,7 +26,11 @@ constexpr uint32_t kEmpty = 0xFFFFFFFFu;
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 static_assert(kLen % (16 * kThreads) == 0, "whole steps");
 
+constexpr uint32_t kBins = as_dev::kTailBins;
+
 struct Shared {
+  double bin_m[kBins];  // the part's histogram of S (TailBins)
+  double bin_w[kBins];
   uint32_t bitmap[kLen / 32];
   uint32_t hid[kHash];
   uint32_t hcnt[kHash];
@@ -137,6 +142,10 @@ __global__ __launch_bounds__(kThreads) void tail_kernel(const FinishArgs* __rest
     sh.overflow = 0;
     sh.staged = 0;
   }
+  for (uint32_t b = tid; b < kBins; b += kThreads) {
+    sh.bin_m[b] = 0.0;
+    sh.bin_w[b] = 0.0;
+  }
   __syncthreads();
   if (pen) {
     auto mark = [&](uint32_t id) {
@@ -168,6 +177,9 @@ __global__ __launch_bounds__(kThreads) void tail_kernel(const FinishArgs* __rest
   // packed order (which also orders -0 below +0).
   const float rv = key_value((uint32_t)(R >> 32));
   const float s1 = 1.44269502f, sw = (1.0f / p.temp) * s1;
+  // The histogram's scale: (rv - v) * bscale is monotone in v, so bins follow the rank order.
+  const float span = rv - fl;
+  const float bscale = (span > 0.0f && span < __builtin_inff()) ? (float)kBins / span : 0.0f;
   float gw = 0.0f, gm = 0.0f;
   uint32_t cnt = 0;
   auto add = [&](float val, uint32_t id) {
@@ -175,8 +187,12 @@ __global__ __launch_bounds__(kThreads) void tail_kernel(const FinishArgs* __rest
     if (__builtin_expect(val == rv, 0)) in = val >= fl && pack(total_key(val), id) < R;
     if (in) {
       const float d = val - topf;
-      gw += __builtin_amdgcn_exp2f(d * sw);
-      gm += __builtin_amdgcn_exp2f(d * s1);
+      const float tw = __builtin_amdgcn_exp2f(d * sw), tm = __builtin_amdgcn_exp2f(d * s1);
+      gw += tw;
+      gm += tm;
+      const uint32_t b = (uint32_t)fminf((rv - val) * bscale, (float)(kBins - 1));
+      atomicAdd(&sh.bin_w[b], (double)tw);
+      atomicAdd(&sh.bin_m[b], (double)tm);
       ++cnt;
       const uint32_t i = atomicAdd(&sh.staged, 1u);
       if (i < kStage) sh.stage[i] = pack(total_key(val), id);
@@ -203,6 +219,12 @@ __global__ __launch_bounds__(kThreads) void tail_kernel(const FinishArgs* __rest
   m = block_sum_f64<kWaves>(m, sh.red);
   cnt = block_sum_u32<kWaves>(cnt, sh.red_u);
   RowTail& t = a.tail[row];
+  // The part's bins into the row's (block_sum_f64 above ended with a barrier: the LDS bins are whole).
+  as_dev::TailBins& tb = a.tail_bins[row];
+  for (uint32_t b = tid; b < kBins; b += kThreads) {
+    if (sh.bin_w[b] != 0.0) __hip_atomic_fetch_add(&tb.w[b], sh.bin_w[b], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (sh.bin_m[b] != 0.0) __hip_atomic_fetch_add(&tb.m[b], sh.bin_m[b], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
   if (tid == 0) {
     __hip_atomic_fetch_add(&t.w, w, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     __hip_atomic_fetch_add(&t.m, m, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);

@@ -246,6 +246,47 @@ def test_draws_past_the_sorted_values_match_the_oracle(ctx):
     assert (g["status"][:48] & AS_ROW_TAIL_PASS).any(), g["status"][:48]
 
 
+def test_tail_histogram_draws_match_the_oracle(ctx):
+    # The tail kernel takes the first 16 flagged rows of a call and, with S's sums, bins S by value;
+    # the finish kernel places top-p's cut within one bin and draws past the sorted values from
+    # those bounds. Config 5's row 111 (top-p keeps ~16,500 values, min-p's floor ~111,000) under
+    # many seeds, 16 rows a call so that every row takes that path (and with T > 1, where the bins
+    # alone bound the kept tail from below): tokens and streams must be the oracle's.
+    from artemis_amd import AS_ROW_DEEP_PATH, AS_ROW_KEPT_PARTIAL, AS_ROW_TAIL_PASS, workloads
+    w = workloads.config5()
+    r = 111
+    base = w.params[r]
+    row = np.ascontiguousarray(w.logits[r])
+    hist = w.histories[r]
+    seen, deep = {}, {}
+    for variant, batches in [(dict(), 8), (dict(temp=1.3), 2)]:
+        key = tuple(sorted(variant.items()))
+        seen[key] = deep[key] = 0
+        for b in range(batches):
+            params, seeds = [], []
+            for s in range(16):
+                p = dict(temp=base.temp, top_k=0, top_p=base.top_p, min_p=base.min_p, presence=base.presence,
+                         frequency=base.frequency, repetition=base.repetition)
+                p.update(variant)
+                params.append(p)
+                seeds.append(20000 + 16 * (b + 10 * len(variant)) + s)
+            g = gpu_batch(ctx, row, params, seeds, [hist] * 16)
+            off, ids = csr([hist] * 16, 16)
+            want, rng = O.sample_rows(params, seeds, row, off, ids, threads=8, shared=True)
+            bad = np.nonzero(g["tokens"] != want)[0]
+            assert len(bad) == 0, [(int(i), params[i], int(g["tokens"][i]), int(want[i]), int(g["status"][i]))
+                                   for i in bad[:5]]
+            assert (g["rng"] == rng).all()
+            st = g["status"]
+            seen[key] += int(((st & AS_ROW_TAIL_PASS) != 0).sum())
+            deep[key] += int(((st & AS_ROW_DEEP_PATH) != 0).sum())
+    # At the row's own T (0.36) every draw took the tail kernel's sums and bins, and the bins
+    # settle nearly all of them (the first bound alone left about 1 in 20 to the deep path). At
+    # T = 1.3 the draw usually lands past the sorted values, which only the deep path can take.
+    assert seen[()] == 128, seen
+    assert deep[()] <= 3, deep
+
+
 def test_large_floor_sets_match_the_oracle(ctx):
     # min-p rows whose floor set holds thousands of values (config 5's rows 254 and 151: 4,302 and
     # 3,365 values above the floor, top-p far deeper): the scan keeps a few thousand candidates and
