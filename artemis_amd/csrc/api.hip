@@ -33,6 +33,7 @@ struct as_ctx {
   RowShare* d_share = nullptr;
   as_dev::RowTail* d_tail = nullptr;
   as_dev::TailBins* d_tail_bins = nullptr;
+  as_dev::TailList* d_tail_list = nullptr;
   bool share_dirty = false;  // a scan ran without its finish (a failed launch): the context is unusable
   uint64_t* d_cands = nullptr;
   uint32_t* d_scratch = nullptr;
@@ -208,6 +209,7 @@ int run_rows(as_ctx* c, const Plan& pl, const RowParams* rows, const float* logi
   a.share = c->d_share;
   a.tail = c->d_tail;
   a.tail_bins = c->d_tail_bins;
+  a.tail_list = c->d_tail_list;
   a.hist_off = hist_off;
   a.hist_ids = hist_ids;
   a.extra_ids = extra_ids;
@@ -259,9 +261,9 @@ int run_rows(as_ctx* c, const Plan& pl, const RowParams* rows, const float* logi
   order_rows(rows, n_rows, &c->order, c->order_cost);
   AS_HIP(c, as_launch::scan(c->stream, vec, logits, c->d_zero, row_stride, n, n_rows, n_seg, pl.slice_len,
                             h, c->d_block, c->d_share, hist_off, hist_ids, extra_ids, c->d_stats, c->d_cands,
-                            pl.stride, c->order));
+                            pl.stride, c->d_tail_list, c->order));
   if (e1) AS_HIP(c, hipEventRecord(e1, c->stream));
-  AS_HIP(c, as_launch::tail(c->stream, n_rows, n, c->d_args));
+  AS_HIP(c, as_launch::tail(c->stream, n_rows, n, a));
   AS_HIP(c, as_launch::finish(c->stream, n_rows, c->d_args));
   c->share_dirty = false;
   if (e2) AS_HIP(c, hipEventRecord(e2, c->stream));
@@ -320,6 +322,7 @@ int as_destroy(as_ctx* c) {
   (void)hipFree(c->d_share);
   (void)hipFree(c->d_tail);
   (void)hipFree(c->d_tail_bins);
+  (void)hipFree(c->d_tail_list);
   (void)hipFree(c->d_cands);
   (void)hipFree(c->d_scratch);
   (void)hipFree(c->d_vstatus);
@@ -363,6 +366,8 @@ int as_create(int device, void* hip_stream, uint32_t max_rows, uint32_t max_voca
   if (e == hipSuccess) e = hipMemset(c->d_tail, 0, sizeof(as_dev::RowTail) * max_rows);
   if (e == hipSuccess) e = hipMalloc(&c->d_tail_bins, sizeof(as_dev::TailBins) * max_rows);
   if (e == hipSuccess) e = hipMemset(c->d_tail_bins, 0, sizeof(as_dev::TailBins) * max_rows);
+  if (e == hipSuccess) e = hipMalloc(&c->d_tail_list, sizeof(as_dev::TailList));
+  if (e == hipSuccess) e = hipMemset(c->d_tail_list, 0, sizeof(as_dev::TailList));
   if (e == hipSuccess)
     e = hipMalloc(&c->d_cands, sizeof(uint64_t) * (uint64_t)max_rows * as_launch::kCandCap);
   if (e == hipSuccess) e = hipMalloc(&c->d_scratch, sizeof(uint32_t) * (uint64_t)max_rows * c->scratch_stride);

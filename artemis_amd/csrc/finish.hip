@@ -1328,8 +1328,12 @@ __device__ __forceinline__ void finish_row(const FinishArgs& a) {
   const SegStats* gst = a.stats + (uint64_t)row * a.n_seg;
   const uint32_t n = a.n;
   if (tid < 256) sh.tab[tid] = as_exp::kTable[tid];
-  // The host learns that the scan no longer reads the call's parameter block.
-  if (row == 0 && tid == 0) __hip_atomic_store(a.done, a.call, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+  // The host learns that the scan no longer reads the call's parameter block; the tail kernel's
+  // list empties for the next call's scan (this call's tail kernel has ended).
+  if (row == 0 && tid == 0) {
+    __hip_atomic_store(a.done, a.call, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+    a.tail_list->count = 0u;
+  }
   // The tail kernel's sums for the row: whole when every part of a flagged row added its own (within
   // 3e-5 relative per term; 1e-4 to spare, and terms under 2^-126 that may have flushed to 0).
   if (tid == 0) {

@@ -65,6 +65,7 @@ struct FinishArgs {
   uint64_t call;            //   reuses a parameter block once its call's scan is over)
   as_dev::RowTail* tail;    // per row: the tail kernel's sums (min-p rows whose scan gave up)
   as_dev::TailBins* tail_bins;  // per row: the tail kernel's histogram of S
+  as_dev::TailList* tail_list;  // the rows the scan flagged for the tail kernel
 };
 
 // The row's history ids are hist_ids[*hb, return value), from the CSR offsets or the row's range.
@@ -84,10 +85,11 @@ __device__ __forceinline__ uint32_t history_bounds(const FinishArgs& a, const as
   return e;
 }
 
-// The tail kernel covers each of the first kTailRows flagged rows in parts of kTailLen values, one
-// 256-thread workgroup each (16 values per thread).
+// The tail kernel covers each of the first kTailRows flagged rows in parts of kTailLen values (16
+// values per thread of a 256-thread workgroup); at most kTailGroups workgroups take the parts in turn.
 constexpr uint32_t kTailLen = 4096;
-constexpr uint32_t kTailRows = 16;
+constexpr uint32_t kTailRows = as_dev::kTailListMax;
+constexpr uint32_t kTailGroups = 256;
 
 // The order in which the scan's workgroups take rows: the workgroups of launch row y (grid y) scan
 // row r[y]. Workgroups launched earlier hold the older waves of their CU, which the hardware serves
@@ -107,13 +109,13 @@ hipError_t scan(hipStream_t stream, bool vec, const float* logits, const float* 
                 uint32_t n, uint32_t n_rows, uint32_t n_seg, uint32_t slice_len, const void* block_in,
                 void* block_out, as_dev::RowShare* share, const uint32_t* hist_off, const uint32_t* hist_ids,
                 const uint32_t* extra_ids, as_dev::SegStats* stats, uint64_t* cands, uint32_t cand_stride,
-                const RowOrder& order);
+                as_dev::TailList* tail_list, const RowOrder& order);
 
 hipError_t finish(hipStream_t stream, uint32_t n_rows, const FinishArgs* a);
 
 // Between the scan and the finish: the weights of S for min-p rows whose scan gave up keeping the
 // floor set whole (a no-op for the other rows).
-hipError_t tail(hipStream_t stream, uint32_t n_rows, uint32_t n, const FinishArgs* a);
+hipError_t tail(hipStream_t stream, uint32_t n_rows, uint32_t n, const FinishArgs& a);
 
 hipError_t accept(hipStream_t stream, const uint32_t* picks, const uint32_t* status,
                   const uint32_t* drafts, uint32_t k, const uint32_t* stop_ids, uint32_t n_stop,

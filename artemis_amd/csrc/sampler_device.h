@@ -85,6 +85,14 @@ struct TailBins {
   double w[kTailBins];
 };
 
+// The rows a call's scan flagged for the tail kernel (RowShare::gave_up), in the order the scan
+// flagged them: the first kTailListMax of them. The finish kernel clears the count after each call.
+constexpr uint32_t kTailListMax = 16;
+struct TailList {
+  uint32_t count;  // rows flagged (may exceed kTailListMax)
+  uint32_t rows[kTailListMax];
+};
+
 // Per (row, slice) results of the scan.
 struct SegStats {
   uint32_t nonfinite;   // first index holding NaN/inf in the raw logits, or kNone

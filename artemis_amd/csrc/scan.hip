@@ -679,7 +679,7 @@ __global__ __launch_bounds__(kThreads, 3) void scan_kernel(
     uint32_t n_seg, uint32_t slice_len, const uint32_t* block_in, uint32_t* __restrict__ block_out,
     RowShare* share, const uint32_t* __restrict__ hist_off, const uint32_t* __restrict__ hist_ids,
     const uint32_t* __restrict__ extra_ids, SegStats* __restrict__ stats, uint64_t* __restrict__ cands,
-    uint32_t cand_stride, as_launch::RowOrder order) {
+    uint32_t cand_stride, TailList* tail_list, as_launch::RowOrder order) {
   Shared& sh = g_sh;
   const uint32_t row = order.on ? (uint32_t)order.r[blockIdx.y] : blockIdx.y, seg = blockIdx.x, tid = threadIdx.x;
   const uint32_t lane = tid & (kWave - 1), w = tid / kWave;
@@ -921,9 +921,15 @@ __global__ __launch_bounds__(kThreads, 3) void scan_kernel(
     st.max_key = mk;
     // A min-p row's slice whose bound lies above its floor (from the largest value it knows the row
     // to hold) did not keep every value above the floor: the row is flagged for the tail kernel.
-    if (sl.floor_on && tid == 0 && bound > floor_tau(max(mk, shared_top), sl.ln_min_p))
-      __hip_atomic_fetch_max(&reinterpret_cast<RowShare*>(sl.share)->gave_up, 1u, __ATOMIC_RELAXED,
-                             __HIP_MEMORY_SCOPE_AGENT);
+    // The first slice to flag the row lists it for the tail kernel.
+    if (sl.floor_on && tid == 0 && bound > floor_tau(max(mk, shared_top), sl.ln_min_p)) {
+      const uint32_t was = __hip_atomic_fetch_max(&reinterpret_cast<RowShare*>(sl.share)->gave_up, 1u,
+                                                  __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      if (was == 0u) {
+        const uint32_t i = __hip_atomic_fetch_add(&tail_list->count, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (i < kTailListMax) tail_list->rows[i] = row;
+      }
+    }
 
     // Candidates: those spilled during the stream that rank >= bound (compacted in place, a tile at a
     // time: every write lands before the tile being read), every buffered value >= bound, wave by
@@ -1057,16 +1063,16 @@ hipError_t scan(hipStream_t stream, bool vec, const float* logits, const float* 
                 uint32_t n, uint32_t n_rows, uint32_t n_seg, uint32_t slice_len, const void* block_in,
                 void* block_out, as_dev::RowShare* share, const uint32_t* hist_off, const uint32_t* hist_ids,
                 const uint32_t* extra_ids, as_dev::SegStats* stats, uint64_t* cands, uint32_t cand_stride,
-                const RowOrder& order) {
+                as_dev::TailList* tail_list, const RowOrder& order) {
   dim3 grid(n_seg, n_rows);
   const uint32_t* in = static_cast<const uint32_t*>(block_in);
   uint32_t* out = static_cast<uint32_t*>(block_out);
   if (vec)
     hipLaunchKernelGGL(scan_kernel<true>, grid, dim3(kThreads), 0, stream, logits, zero, row_stride, n, n_seg,
-                       slice_len, in, out, share, hist_off, hist_ids, extra_ids, stats, cands, cand_stride, order);
+                       slice_len, in, out, share, hist_off, hist_ids, extra_ids, stats, cands, cand_stride, tail_list, order);
   else
     hipLaunchKernelGGL(scan_kernel<false>, grid, dim3(kThreads), 0, stream, logits, zero, row_stride, n, n_seg,
-                       slice_len, in, out, share, hist_off, hist_ids, extra_ids, stats, cands, cand_stride, order);
+                       slice_len, in, out, share, hist_off, hist_ids, extra_ids, stats, cands, cand_stride, tail_list, order);
   return hipGetLastError();
 }
 

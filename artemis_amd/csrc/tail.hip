@@ -6,9 +6,10 @@
 // finish kernel can sort the whole floor set; and S's histogram by value (TailBins), which places
 // top-p's cut within one bin. The finish kernel's
 // draw needs them when the kept set (sample.rs:230-272) runs past its sorted candidates: the kept
-// values past them are S's first in rank order (all of S when the floor cuts first). One 256-thread
-// workgroup per kTailLen values of a flagged row (the i-th flagged row, for i < kTailRows; a row past
-// them is left to the finish kernel), the parts' sums added with device atomics.
+// values past them are S's first in rank order (all of S when the floor cuts first). The scan lists
+// the rows it flags (TailList: the first kTailRows; a row past them is left to the finish kernel);
+// each row is covered in parts of kTailLen values, which up to kTailGroups 256-thread workgroups
+// take in turn, and the parts' sums add with device atomics.
 #include "sampler_device.h"
 #include "launch.h"
 
@@ -31,36 +32,18 @@ constexpr uint32_t kBins = as_dev::kTailBins;
 struct Shared {
   double bin_m[kBins];  // the part's histogram of S (TailBins)
   double bin_w[kBins];
+  float vals[kLen];     // the part's raw values (the history's are read here)
   uint32_t bitmap[kLen / 32];
   uint32_t hid[kHash];
   uint32_t hcnt[kHash];
   uint64_t stage[kStage];
   double red[kWaves];
   uint32_t red_u[kWaves];
-  uint32_t row;
   uint32_t overflow;
   uint32_t staged;
   uint32_t base;
 };
 __shared__ Shared g_tsh;
-
-// The number of threads before this one (in the block) whose f is set, plus *base; *base then
-// grows by the block's count.
-__device__ __forceinline__ uint32_t block_exclusive_count(bool f, uint32_t* red, uint32_t* base) {
-  const uint64_t m = __ballot(f);
-  const uint32_t w = threadIdx.x / kWave;
-  const uint32_t in_wave = __builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0u));
-  __syncthreads();
-  if ((threadIdx.x & (kWave - 1)) == 0) red[w] = (uint32_t)__popcll(m);
-  __syncthreads();
-  uint32_t off = *base, all = 0;
-  for (int k = 0; k < kWaves; ++k) {
-    if (k < (int)w) off += red[k];
-    all += red[k];
-  }
-  *base += all;
-  return off + in_wave;
-}
 
 // Whether the finish kernel can need S for the row: a min-p row without a top-k that a slice flagged
 // (its bound lay above its floor), whose finish takes its fast path (no slice with unfinished statistics
@@ -87,29 +70,15 @@ __device__ bool needs_tail(const FinishArgs& a, uint32_t row, uint64_t* R_out, f
   return true;
 }
 
-__global__ __launch_bounds__(kThreads) void tail_kernel(const FinishArgs* __restrict__ ap, uint32_t n_rows) {
+// One part of one flagged row: its share of S's sums, bins and list. Every load that needs only the
+// row is issued at once (the part's values, the history's bounds, the row's parameters and slice
+// statistics), then the history's ids; the history's raw values are read from the part's values,
+// staged in LDS.
+__device__ __forceinline__ void tail_part(const FinishArgs& a, uint32_t row, uint32_t part) {
   Shared& sh = g_tsh;
-  const FinishArgs& a = *ap;
-  const uint32_t part = blockIdx.x, nth = blockIdx.y, tid = threadIdx.x;
-  // The nth flagged row, in row order, when it needs S.
-  if (tid == 0) sh.row = kNone;
-  uint32_t before = 0;
-  for (uint32_t r0 = 0; r0 < n_rows; r0 += kThreads) {
-    const uint32_t r = r0 + tid;
-    const bool f = r < n_rows && a.share[r].gave_up != 0u;
-    const uint32_t mine = block_exclusive_count(f, sh.red_u, &before);
-    if (f && mine == nth) sh.row = r;
-  }
-  __syncthreads();
-  const uint32_t row = sh.row;
-  if (row == kNone) return;
-  uint64_t R = 0;
-  float topf = 0.0f, fl = 0.0f;
-  if (!needs_tail(a, row, &R, &topf, &fl)) return;
-  const RowParams& p = a.params[row];
+  const uint32_t tid = threadIdx.x;
   const uint32_t n = a.n, b0 = part * kLen, b1 = min(b0 + kLen, n), len = b1 - b0;
   const float* x = a.logits + (uint64_t)row * a.row_stride;
-  // The part's values (16 per thread) in flight while the row's history is read.
   const bool vec = a.vec && a.row_stride % 4 == 0 && len == kLen;
   float v[16];
   if (vec) {
@@ -126,11 +95,27 @@ __global__ __launch_bounds__(kThreads) void tail_kernel(const FinishArgs* __rest
       v[k] = off < len ? x[b0 + off] : 0.0f;
     }
   }
-
+  const RowParams& p = a.params[row];
   uint32_t hb;
   const uint32_t he = as_launch::history_bounds(a, p, row, &hb);
+  uint64_t R = 0;
+  float topf = 0.0f, fl = 0.0f;
+  if (!needs_tail(a, row, &R, &topf, &fl)) return;
   const uint32_t extra = a.extra_ids ? p.extra : 0;
   const bool pen = (p.flags & kFlagPenalties) && (he > hb || extra > 0);
+  constexpr int kHistRegs = 8;
+  uint32_t hreg[kHistRegs];
+#pragma unroll
+  for (int k = 0; k < kHistRegs; ++k) {
+    const uint32_t h = hb + tid + k * kThreads;
+    hreg[k] = (pen && h < he) ? a.hist_ids[h] : kEmpty;
+  }
+  // The part's values into LDS (position off = value b0 + off).
+#pragma unroll
+  for (int k = 0; k < 16; ++k) {
+    const uint32_t off = vec ? ((k / 4) * kThreads + tid) * 4 + (k % 4) : k * kThreads + tid;
+    if (off < kLen) sh.vals[off] = v[k];
+  }
   if (pen) {
     for (uint32_t i = tid; i < kLen / 32; i += kThreads) sh.bitmap[i] = 0;
     for (uint32_t i = tid; i < kHash; i += kThreads) {
@@ -164,7 +149,10 @@ __global__ __launch_bounds__(kThreads) void tail_kernel(const FinishArgs* __rest
       }
       sh.overflow = 1;
     };
-    for (uint32_t h = hb + tid; h < he; h += kThreads) mark(a.hist_ids[h]);
+#pragma unroll
+    for (int k = 0; k < kHistRegs; ++k)
+      if (hreg[k] != kEmpty) mark(hreg[k]);
+    for (uint32_t h = hb + tid + kHistRegs * kThreads; h < he; h += kThreads) mark(a.hist_ids[h]);
     for (uint32_t h = tid; h < extra; h += kThreads) mark(a.extra_ids[h]);
     __syncthreads();
   }
@@ -210,7 +198,7 @@ __global__ __launch_bounds__(kThreads) void tail_kernel(const FinishArgs* __rest
       if (id == kEmpty) continue;
       gw = 0.0f;
       gm = 0.0f;
-      add(penalize(x[id], sh.hcnt[s], p), id);
+      add(penalize(sh.vals[id - b0], sh.hcnt[s], p), id);
       w += (double)gw;
       m += (double)gm;
     }
@@ -241,13 +229,27 @@ __global__ __launch_bounds__(kThreads) void tail_kernel(const FinishArgs* __rest
   if (tid == 0) __hip_atomic_fetch_add(&t.parts, 1u, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
 }
 
+// The workgroups take the (flagged row, part) items in turn. The arguments come by value: the rows
+// to cover are known after one load (the scan's list).
+__global__ __launch_bounds__(kThreads) void tail_kernel(const FinishArgs a) {
+  const uint32_t parts = (a.n + kLen - 1) / kLen;
+  for (uint32_t item = blockIdx.x; item < as_launch::kTailRows * parts; item += gridDim.x) {
+    // The list's count and this item's entry, loaded together (an entry past the count is unused).
+    const uint32_t r = a.tail_list->rows[item / parts];
+    const uint32_t flagged = min(a.tail_list->count, as_launch::kTailRows);
+    if (item >= flagged * parts) break;
+    __syncthreads();  // the previous item's tables are no longer read
+    tail_part(a, r, item % parts);
+  }
+}
+
 }  // namespace
 
 namespace as_launch {
 
-hipError_t tail(hipStream_t stream, uint32_t n_rows, uint32_t n, const FinishArgs* a) {
-  hipLaunchKernelGGL(tail_kernel, dim3((n + kTailLen - 1) / kTailLen, min(n_rows, kTailRows)), dim3(kThreads), 0,
-                     stream, a, n_rows);
+hipError_t tail(hipStream_t stream, uint32_t n_rows, uint32_t n, const FinishArgs& a) {
+  const uint32_t items = min(n_rows, kTailRows) * ((n + kTailLen - 1) / kTailLen);
+  hipLaunchKernelGGL(tail_kernel, dim3(min(items, kTailGroups)), dim3(kThreads), 0, stream, a);
   return hipGetLastError();
 }
 

@@ -307,8 +307,9 @@ def test_large_floor_sets_match_the_oracle(ctx):
     g = gpu_batch(ctx, rows, params, seeds, hists, kept_cap=16)
     want = oracle_rows(rows, params, seeds, hists, kept_cap=16)
     check_rows(g, want, params, kept_cap=16, label="floor sets")
-    # The tail kernel takes the first 16 flagged rows of a call; the finish kernel settles the rest.
-    assert (g["status"][:16] & AS_ROW_TAIL_PASS).all(), g["status"]
+    # The tail kernel takes the first 16 rows the scan flags (in the order it flags them); the finish
+    # kernel settles the rest.
+    assert ((g["status"] & AS_ROW_TAIL_PASS) != 0).sum() >= 16, g["status"]
 
 
 def test_whole_vocabulary_plants(ctx):
