@@ -170,9 +170,14 @@ __device__ __forceinline__ void tail_part(const FinishArgs& a, uint32_t row, uin
   const float bscale = (span > 0.0f && span < __builtin_inff()) ? (float)kBins / span : 0.0f;
   float gw = 0.0f, gm = 0.0f;
   uint32_t cnt = 0;
-  auto add = [&](float val, uint32_t id) {
+  auto in_s = [&](float val, uint32_t id) {
     bool in = val >= fl && val < rv;
     if (__builtin_expect(val == rv, 0)) in = val >= fl && pack(total_key(val), id) < R;
+    return in;
+  };
+  // Called by every lane of the wave at once: the values in S add their terms and bins, and are
+  // staged with one LDS atomic per wave.
+  auto add = [&](bool in, float val, uint32_t id) {
     if (in) {
       const float d = val - topf;
       const float tw = __builtin_amdgcn_exp2f(d * sw), tm = __builtin_amdgcn_exp2f(d * s1);
@@ -182,23 +187,32 @@ __device__ __forceinline__ void tail_part(const FinishArgs& a, uint32_t row, uin
       atomicAdd(&sh.bin_w[b], (double)tw);
       atomicAdd(&sh.bin_m[b], (double)tm);
       ++cnt;
-      const uint32_t i = atomicAdd(&sh.staged, 1u);
-      if (i < kStage) sh.stage[i] = pack(total_key(val), id);
+    }
+    const uint64_t mk = __ballot(in);
+    if (mk) {
+      uint32_t base = 0;
+      if ((tid & (kWave - 1)) == 0) base = atomicAdd(&sh.staged, (uint32_t)__popcll(mk));
+      base = __builtin_amdgcn_readfirstlane(base);
+      const uint32_t i = base + __builtin_amdgcn_mbcnt_hi((uint32_t)(mk >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)mk, 0u));
+      if (in && i < kStage) sh.stage[i] = pack(total_key(val), id);
     }
   };
 #pragma unroll
   for (int k = 0; k < 16; ++k) {
     const uint32_t off = vec ? ((k / 4) * kThreads + tid) * 4 + (k % 4) : k * kThreads + tid;
-    if (off < len && !(pen && ((sh.bitmap[off >> 5] >> (off & 31u)) & 1u))) add(v[k], b0 + off);
+    const bool valid = off < len && !(pen && ((sh.bitmap[off >> 5] >> (off & 31u)) & 1u));
+    add(valid && in_s(v[k], b0 + off), v[k], b0 + off);
   }
   double w = (double)gw, m = (double)gm;
   if (pen) {
+    static_assert(kHash % kThreads == 0, "every thread takes the same number of slots");
     for (uint32_t s = tid; s < kHash; s += kThreads) {
       const uint32_t id = sh.hid[s];
-      if (id == kEmpty) continue;
+      const bool has = id != kEmpty;
+      const float val = has ? penalize(sh.vals[id - b0], sh.hcnt[s], p) : 0.0f;
       gw = 0.0f;
       gm = 0.0f;
-      add(penalize(sh.vals[id - b0], sh.hcnt[s], p), id);
+      add(has && in_s(val, id), val, id);
       w += (double)gw;
       m += (double)gm;
     }
