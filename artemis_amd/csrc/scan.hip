@@ -682,7 +682,9 @@ __global__ __launch_bounds__(kThreads, 3) void scan_kernel(
     uint32_t cand_stride, TailList* tail_list, as_launch::RowOrder order) {
   Shared& sh = g_sh;
   const uint32_t row = order.on ? (uint32_t)order.r[blockIdx.y] : blockIdx.y, seg = blockIdx.x, tid = threadIdx.x;
-  const uint32_t lane = tid & (kWave - 1), w = tid / kWave;
+  // The wave's index as a scalar: the walk's bounds and addresses derive from it, and the compiler
+  // keeps the stream's loop control in scalar registers only when it knows them uniform.
+  const uint32_t lane = tid & (kWave - 1), w = __builtin_amdgcn_readfirstlane(tid / kWave);
 
   // The row's parameters, read where the host wrote them (pinned memory, read with system-scope
   // loads so that no cache serves an earlier call's), into LDS; the row's first slice also copies
@@ -736,7 +738,15 @@ __global__ __launch_bounds__(kThreads, 3) void scan_kernel(
     sh.overflow = 0;
     sh.out_n = 0;
   }
-  __syncthreads();  // the parameters are in LDS
+  // The history tables start empty (cleared while the parameters are on their way).
+  if (hist_ids || extra_ids) {
+    for (uint32_t i = tid; i < (len + 31) / 32; i += kThreads) sh.bitmap[i] = 0;
+    for (uint32_t i = tid; i < kHash; i += kThreads) {
+      sh.hid[i] = kEmpty;
+      sh.hcnt[i] = 0;
+    }
+  }
+  __syncthreads();  // the parameters are in LDS, the tables clear
 
   const RowParams& p = sh.prm;
   if (hist_ids && !hist_off) {
@@ -770,12 +780,6 @@ __global__ __launch_bounds__(kThreads, 3) void scan_kernel(
   sl.pen = (flags & kFlagPenalties) && (he > hb || extra > 0);
 
   if (sl.pen) {
-    for (uint32_t i = tid; i < (len + 31) / 32; i += kThreads) sh.bitmap[i] = 0;
-    for (uint32_t i = tid; i < kHash; i += kThreads) {
-      sh.hid[i] = kEmpty;
-      sh.hcnt[i] = 0;
-    }
-    __syncthreads();
     auto mark = [&](uint32_t id) {
       const uint32_t off = id - sl.b0;
       if (off >= len) return;
