@@ -1481,7 +1481,34 @@ __device__ __forceinline__ void finish_row(const FinishArgs& a) {
     }
     const uint32_t total = min(sh.nsk, (uint32_t)kCap);
     const bool too_many = sh.nsk > (uint32_t)kCap;  // more candidates >= R than the finish holds
-    const uint32_t P = sort_candidates(sh, total, R, sh.mk, p.mode == kModeTopK ? p.top_k : kNone);
+    // A row whose floor set the tail kernel listed (S: every value below R and at or above the floor),
+    // and whose whole floor set's mass at T = 1 is short of top-p's target: top-p never stops inside it
+    // and min-p's floor cuts first (sample.rs:237-251), so the kept set is the candidates and all of S,
+    // sorted once, together. The candidates' mass needs no order: a parallel sum of positive terms,
+    // within gamma(40) of exact, and the margins below are far wider.
+    bool floor_set = false;
+    if (p.mode == kModePartial && has_floor && !floor_cut && !too_many && sh.have_tail && sh.tail_listed &&
+        total + sh.tail_count <= (uint32_t)kCap) {
+      bool cuts_first = true;
+      if (p.top_p < 1.0f) {
+        double X, eps;
+        slices_total(a, sh, top, temp, false, &X, &eps);
+        double mc = 0.0;
+        for (uint32_t i = tid; i < total; i += kThreads) mc += w_one(val(i));
+        mc = block_sum_f64<kWaves>(mc, sh.red_d);
+        cuts_first = (X - eps > 0.0) && (eps == eps) &&
+                     sh.m_hi < top_p * (X - eps) * (1.0 - 1e-9) - mc * (1.0 + 1e-9);
+      }
+      if (cuts_first) {
+        const uint64_t* list = reinterpret_cast<const uint64_t*>(a.scratch + (uint64_t)row * a.scratch_stride);
+        const uint32_t cnt = sh.tail_count;
+        for (uint32_t i = tid; i < cnt; i += kThreads) sh.sk[total + i] = list[i];
+        __syncthreads();
+        floor_set = true;
+      }
+    }
+    const uint32_t P = floor_set ? sort_candidates(sh, total + sh.tail_count, 0ull, sh.mk, kNone)
+                                 : sort_candidates(sh, total, R, sh.mk, p.mode == kModeTopK ? p.top_k : kNone);
     if (tid == 0) sh.prefix = P;
     const bool complete = (P == n);  // every value of the row is sorted
     // A top-k row's k best are among the sorted values only when at least k rank at or above R.
@@ -1492,7 +1519,10 @@ __device__ __forceinline__ void finish_row(const FinishArgs& a) {
     bool drawn = false;
     double r_prefix = 0.0;  // the top-p scan's sum of exp(l - top) over the P sorted values
     double x1 = 0.0, eps1 = 0.0;  // total1 and its bound
-    if (short_topk || too_many) {
+    if (floor_set) {
+      keep = P;  // every value at or above the floor
+      status |= AS_ROW_TAIL_PASS;
+    } else if (short_topk || too_many) {
       keep = kNone;
     } else if (p.mode == kModeTopK) {
       // draw_full_sort over the k best (sample.rs:157-183).
