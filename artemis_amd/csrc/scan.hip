@@ -935,36 +935,11 @@ __global__ __launch_bounds__(kThreads, 3) void scan_kernel(
       }
     }
 
-    // Candidates: those spilled during the stream that rank >= bound (compacted in place, a tile at a
-    // time: every write lands before the tile being read), every buffered value >= bound, wave by
-    // wave, then the history values >= bound. When they would not fit the slice's slots, each wave
-    // first keeps only its share.
-    uint32_t spilled = sh.out_n;
-    if (spilled) {
-      __syncthreads();
-      if (tid == 0) sh.out_n = 0;
-      __syncthreads();
-      for (uint32_t t0 = 0; t0 < spilled; t0 += 4 * kThreads) {
-        uint64_t e[4];
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-          const uint32_t i = t0 + tid + q * kThreads;
-          e[q] = (i < spilled) ? sl.out[i] : 0ull;
-        }
-        __syncthreads();
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-          const bool keep = e[q] != 0ull && e[q] >= bound;
-          const uint64_t m = __ballot(keep);
-          uint32_t base = 0;
-          if (lane == 0 && m) base = atomicAdd(&sh.out_n, (uint32_t)__popcll(m));
-          base = __builtin_amdgcn_readfirstlane(base);
-          if (keep) sl.out[base + lanes_below(m)] = e[q];
-        }
-      }
-      __syncthreads();
-      spilled = sh.out_n;
-    }
+    // Candidates: those spilled during the stream (left where they are: some may rank below the bound,
+    // and the finish kernel drops every candidate below the row's bound as it loads them), every
+    // buffered value >= bound, wave by wave, then the history values >= bound. When they would not fit
+    // the slice's slots, each wave first keeps only its share.
+    const uint32_t spilled = sh.out_n;
     uint32_t all = 0, hall = 0;
     for (int pass = 0; pass < 2; ++pass) {
       uint32_t mine = 0;
