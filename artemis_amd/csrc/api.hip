@@ -40,6 +40,7 @@ struct as_ctx {
   uint64_t scratch_stride = 0;
   uint32_t* d_vstatus = nullptr;
   float* d_zero = nullptr;  // 1,024 zeros the scan's idle loads read
+  as_launch::LpPart* d_lp = nullptr;  // log-probabilities: per row, its parts' sums and lists
   as_launch::RowOrder order{};  // the scan's row order for the current call
   std::vector<std::pair<double, uint32_t>> order_cost;  // its sort keys (kept: no allocation per call)
   std::string err;
@@ -327,6 +328,7 @@ int as_destroy(as_ctx* c) {
   (void)hipFree(c->d_scratch);
   (void)hipFree(c->d_vstatus);
   (void)hipFree(c->d_zero);
+  (void)hipFree(c->d_lp);
   for (hipEvent_t e : c->ev) (void)hipEventDestroy(e);
   for (int b = 0; b < 2; ++b)
     if (c->h_block[b]) (void)hipHostFree(c->h_block[b]);
@@ -372,6 +374,8 @@ int as_create(int device, void* hip_stream, uint32_t max_rows, uint32_t max_voca
     e = hipMalloc(&c->d_cands, sizeof(uint64_t) * (uint64_t)max_rows * as_launch::kCandCap);
   if (e == hipSuccess) e = hipMalloc(&c->d_scratch, sizeof(uint32_t) * (uint64_t)max_rows * c->scratch_stride);
   if (e == hipSuccess) e = hipMalloc(&c->d_vstatus, sizeof(uint32_t) * max_rows);
+  if (e == hipSuccess)
+    e = hipMalloc(&c->d_lp, sizeof(as_launch::LpPart) * (uint64_t)max_rows * as_launch::lp_parts(max_vocab));
   if (e == hipSuccess) e = hipMalloc(&c->d_zero, sizeof(float) * 1024);
   if (e == hipSuccess) e = hipMemset(c->d_zero, 0, sizeof(float) * 1024);
   for (int b = 0; b < 2 && e == hipSuccess; ++b)
@@ -511,6 +515,26 @@ int as_debug_exp(as_ctx* c, const double* x, double* y, uint32_t n) {
   if (!x || !y) return fail(c, AS_ERR_INVALID, "as_debug_exp: no arrays");
   AS_HIP(c, hipSetDevice(c->device));
   AS_HIP(c, as_launch::debug_exp(c->stream, x, y, n));
+  return AS_OK;
+}
+
+int as_logprobs(as_ctx* c, const float* logits, uint64_t row_stride, uint32_t n_vocab, uint32_t n_rows,
+                const uint32_t* tokens, uint32_t top, float* logprob, uint32_t* top_ids, float* top_logprobs,
+                uint32_t* status) {
+  if (!c) return AS_ERR_INVALID;
+  if (!logits || !tokens || !logprob || n_vocab == 0 || n_rows == 0)
+    return fail(c, AS_ERR_INVALID, "as_logprobs: null array or zero size");
+  if (top > 0 && (!top_ids || !top_logprobs))
+    return fail(c, AS_ERR_INVALID, "as_logprobs: top > 0 needs top_ids and top_logprobs");
+  if (row_stride != 0 && row_stride < n_vocab)
+    return fail(c, AS_ERR_INVALID, "as_logprobs: row_stride below n_vocab");
+  if (n_rows > c->max_rows || n_vocab > c->max_vocab)
+    return fail(c, AS_ERR_CAPACITY, "as_logprobs: more rows or a wider vocabulary than the context holds");
+  if (as_launch::lp_parts(n_vocab) * as_launch::kLpTop > as_launch::kLpMerge)
+    return fail(c, AS_ERR_CAPACITY, "as_logprobs: vocabulary wider than the merge holds");
+  const bool vec = aligned16(logits) && (row_stride % 4 == 0);
+  AS_HIP(c, as_launch::logprobs(c->stream, vec, logits, row_stride, n_vocab, n_rows, c->d_lp, tokens, top, logprob,
+                                top_ids, top_logprobs, status));
   return AS_OK;
 }
 

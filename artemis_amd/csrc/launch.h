@@ -117,6 +117,23 @@ hipError_t finish(hipStream_t stream, uint32_t n_rows, const FinishArgs* a);
 // floor set whole (a no-op for the other rows).
 hipError_t tail(hipStream_t stream, uint32_t n_rows, uint32_t n, const FinishArgs& a);
 
+// Log-probabilities (logprobs.hip): rows in parts of kLpPart values, each part's 20 best and sums.
+constexpr uint32_t kLpPart = 8192;
+constexpr uint32_t kLpTop = 20;     // logprobs.rs:7, MAX_TOP
+constexpr uint32_t kLpMerge = 2048; // the parts' lists a row merges: lp_parts(n) * kLpTop at most
+__host__ __device__ constexpr uint32_t lp_parts(uint32_t n) { return (n + kLpPart - 1) / kLpPart; }
+struct LpPart {
+  double sum;         // sum of exp(x - max) over the part
+  float max;          // the part's largest value
+  uint32_t n_top;     // entries in top
+  uint32_t overflow;  // ties past the part's list: the row takes its best by full passes
+  uint32_t pad_;
+  uint64_t top[kLpTop];  // the part's best, packed (rank key of the logit with -0 as +0, ~id), in order
+};
+hipError_t logprobs(hipStream_t stream, bool vec, const float* logits, uint64_t row_stride, uint32_t n,
+                    uint32_t n_rows, LpPart* parts, const uint32_t* tokens, uint32_t top, float* logprob,
+                    uint32_t* top_ids, float* top_lps, uint32_t* status);
+
 hipError_t accept(hipStream_t stream, const uint32_t* picks, const uint32_t* status,
                   const uint32_t* drafts, uint32_t k, const uint32_t* stop_ids, uint32_t n_stop,
                   uint64_t* rng_state, uint32_t draws_per_row, uint32_t* result);

@@ -26,6 +26,9 @@ AS_ROW_KEPT_PARTIAL = 0x200
 AS_ROW_DEEP_PATH = 0x400
 AS_ROW_TAIL_PASS = 0x800
 NO_DRAFT = 0xFFFFFFFF
+AS_LP_OK = 0
+AS_LP_INEXACT = 1
+LP_MAX_TOP = 20  # logprobs.rs:7
 
 
 class SamplerError(RuntimeError):
@@ -89,6 +92,7 @@ def lib() -> C.CDLL:
         L.as_argmax_rows.argtypes = [vp, vp, u64, u32, u32, vp, vp, u64, u32, u32]
         L.as_debug_exp.argtypes = [vp, vp, vp, u32]
         L.as_debug_exp2f.argtypes = [vp, vp, vp, u32]
+        L.as_logprobs.argtypes = [vp, vp, u64, u32, u32, vp, u32, vp, vp, vp, vp]
         L.as_profile.argtypes = [vp, C.c_int]
         L.as_profile_read.argtypes = [vp, C.POINTER(C.c_double), C.POINTER(C.c_double), C.POINTER(u32)]
         _lib = L
@@ -264,6 +268,29 @@ class Context:
         self._ok(lib().as_argmax_rows(self.h, logits.data_ptr(), logits.stride(0), nv, logits.shape[0],
                                       ids.data_ptr(), rows_out.data_ptr(), embd, row_bytes, slot))
 
+    def logprobs(self, logits: torch.Tensor, tokens: torch.Tensor, top: int, row_stride: Optional[int] = None,
+                 n_vocab: Optional[int] = None):
+        """logprobs (logprobs.rs:12-38) on every row: (logprob [n] f32, top_ids [n, top] int32,
+        top_logprobs [n, top] f32, status [n] int32) device tensors; the first min(top, 20, n_vocab)
+        columns of each row are written. `tokens`: [n] int32 on the device."""
+        if logits.dim() == 1:
+            logits = logits.view(1, -1)
+        assert logits.is_cuda and logits.dtype == torch.float32
+        assert tokens.is_cuda and tokens.dtype == torch.int32
+        rows = tokens.numel()
+        stride = row_stride if row_stride is not None else (logits.stride(0) if logits.shape[0] > 1 else logits.shape[1])
+        nv = n_vocab if n_vocab is not None else logits.shape[1]
+        dev = logits.device
+        lp = torch.empty(rows, dtype=torch.float32, device=dev)
+        cols = max(top, 1)
+        ids = torch.full((rows, cols), -1, dtype=torch.int32, device=dev)
+        lps = torch.full((rows, cols), float("nan"), dtype=torch.float32, device=dev)
+        st = torch.empty(rows, dtype=torch.int32, device=dev)
+        self._ok(lib().as_logprobs(self.h, logits.data_ptr(), stride, nv, rows, tokens.data_ptr(), top,
+                                   lp.data_ptr(), ids.data_ptr() if top else None,
+                                   lps.data_ptr() if top else None, st.data_ptr()))
+        return lp, ids, lps, st
+
     def profile(self, enable: bool):
         """Start (or stop) recording HIP events around each call's scan and finish kernels."""
         self._ok(lib().as_profile(self.h, 1 if enable else 0))
@@ -333,6 +360,18 @@ class Sampler:
             raise SamplerError(f"non-finite logit at {int(_[0].item())}")
         self.history.append(t)
         return t
+
+
+def logprobs(logits: torch.Tensor, token: int, top: int):
+    """logprobs (logprobs.rs:12-38) of one finite row on the GPU: (token's log-probability,
+    [(id, log-probability)] for the min(top, 20, n) highest logits, by logit descending then id)."""
+    row = logits.reshape(1, -1)
+    ctx = _context_for(row.shape[1], row.device.index or 0)
+    tok = torch.tensor([token], dtype=torch.int32, device=row.device)
+    lp, ids, lps, _ = ctx.logprobs(row, tok, top)
+    n = min(top, LP_MAX_TOP, row.shape[1])
+    ids_h, lps_h = ids.cpu().numpy()[0], lps.cpu().numpy()[0]
+    return float(lp.item()), [(int(ids_h[i]), float(lps_h[i])) for i in range(n)]
 
 
 def greedy(logits: torch.Tensor) -> int:

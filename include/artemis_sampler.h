@@ -130,6 +130,21 @@ int as_argmax_rows(as_ctx* ctx, const float* logits, uint64_t row_stride, uint32
                    uint32_t n_rows, uint32_t* ids, uint64_t* rows_out, uint64_t embd,
                    uint32_t row_bytes, uint32_t slot);
 
+/* Log-probabilities of the model's own distribution (crates/engine/src/logprobs.rs:12-38), which the
+ * generation loop asks for per sampled token when a request wants them (turn.rs:361-364): for each of
+ * n_rows rows of raw logits (before penalties, temperature and filters; the rows must be finite),
+ * logprob[r] = ln softmax(row)[tokens[r]] in f32, and the `top` highest-logit ids with theirs (top
+ * clamped to 20 and to n_vocab; 0: none), sorted by logit descending, -0 and +0 tied, ties to the
+ * lower id (logprobs.rs:40-48). tokens: device [n_rows]; out: logprob [n_rows], top_ids and
+ * top_logprobs [n_rows][top] (the first min(top, 20, n_vocab) of each row written; may be NULL when
+ * top is 0), status [n_rows] or NULL: AS_LP_OK, or AS_LP_INEXACT when the bound on the sum's distance
+ * to the reference's left-to-right sum could move a value's rounding to f32 (the value is then within
+ * one f32 ulp of the reference's), or a token is out of range (its logprob is NaN). */
+#define AS_LP_OK 0u
+#define AS_LP_INEXACT 1u
+int as_logprobs(as_ctx* ctx, const float* logits, uint64_t row_stride, uint32_t n_vocab, uint32_t n_rows,
+                const uint32_t* tokens, uint32_t top, float* logprob, uint32_t* top_ids, float* top_logprobs,
+                uint32_t* status);
 /* Profiling: while enabled, each as_sample / as_verify records HIP events on the context's stream
  * around its scan and finish kernels (no counterpart in the reference, which samples on the CPU;
  * for benchmarks). as_profile_read waits for the stream and returns the summed kernel times of the

@@ -1,0 +1,150 @@
+"""Log-probabilities on the GPU (crates/engine/src/logprobs.rs:12-38) against the oracle, which
+restates the same function (oracle/sampler_oracle.cc, oc_logprobs). Top ids must be bit-exact. Values
+must be bit-exact on rows whose status is AS_LP_OK; on a row marked AS_LP_INEXACT (the bound on the
+parallel sum's distance to the reference's left-to-right sum could move a rounding to f32) each value
+must be within one f32 ulp of the oracle's (a log-probability error of at most 2^-23 relative, far
+inside the 1e-5 relative the probabilities must meet)."""
+import numpy as np
+import pytest
+
+import oracle_lib as O
+
+pytestmark = pytest.mark.gpu
+
+torch = pytest.importorskip("torch")
+
+VOCAB = 248_320
+
+
+@pytest.fixture(scope="module")
+def ctx():
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU")
+    from artemis_amd import Context
+    c = Context(max_rows=64, max_vocab=VOCAB)
+    yield c
+    c.close()
+
+
+def run(ctx, rows, tokens, top, row_stride=None, n_vocab=None):
+    dev = torch.device("cuda:0")
+    lg = torch.from_numpy(np.ascontiguousarray(rows, np.float32)).to(dev)
+    if lg.dim() == 1:
+        lg = lg.view(1, -1)
+    tok = torch.from_numpy(np.asarray(tokens, np.int32)).to(dev)
+    lp, ids, lps, st = ctx.logprobs(lg, tok, top, row_stride=row_stride, n_vocab=n_vocab)
+    torch.cuda.synchronize()
+    return lp.cpu().numpy(), ids.cpu().numpy(), lps.cpu().numpy(), st.cpu().numpy()
+
+
+def same_or_one_ulp(got, want, exact):
+    got, want = np.float32(got), np.float32(want)
+    if exact:
+        return got.tobytes() == want.tobytes()
+    return abs(float(got) - float(want)) <= float(np.spacing(np.abs(want)))
+
+
+def check(ctx, rows, tokens, top, label=""):
+    from artemis_amd import AS_LP_INEXACT
+    rows = np.atleast_2d(np.asarray(rows, np.float32))
+    lp, ids, lps, st = run(ctx, rows, tokens, top)
+    inexact = 0
+    for r in range(rows.shape[0]):
+        want_lp, want_top = O.logprobs(rows[r], int(tokens[r]), top)
+        exact = st[r] & AS_LP_INEXACT == 0
+        inexact += 0 if exact else 1
+        assert same_or_one_ulp(lp[r], want_lp, exact), (label, r, lp[r], want_lp, st[r])
+        n = len(want_top)
+        assert n == min(top, 20, rows.shape[1])
+        assert ids[r][:n].tolist() == [i for i, _ in want_top], (label, r, ids[r][:n].tolist(), want_top)
+        for j in range(n):
+            assert same_or_one_ulp(lps[r][j], want_top[j][1], exact), (label, r, j, lps[r][j], want_top[j])
+    return lp, ids, lps, st, inexact
+
+
+# ---- logprobs.rs:54-108, the reference's own tests ------------------------------------------------
+
+def test_logprobs_are_a_log_softmax_of_the_raw_logits(ctx):
+    l = np.array([1.0, 3.0, 2.0, 3.0], np.float32)
+    lp, ids, lps, st, _ = check(ctx, l, [2], 3)
+    lse = np.log(np.exp(1.0) + 2 * np.exp(3.0) + np.exp(2.0))
+    assert abs(float(lp[0]) - (2.0 - lse)) < 1e-6
+    assert ids[0][:3].tolist() == [1, 3, 2]  # a tie goes to the lower id
+    assert abs(float(lps[0][0]) - (3.0 - lse)) < 1e-6
+
+
+def test_logprobs_take_at_most_twenty_and_none_when_asked_for_none(ctx):
+    l = np.array([i % 37 for i in range(100)], np.float32)
+    _, ids, _, _, _ = check(ctx, l, [5], 25)
+    full = sorted(range(100), key=lambda i: (-l[i], i))
+    assert ids[0][:20].tolist() == full[:20]
+    lp, ids0, _, _, _ = check(ctx, l, [5], 0)
+    check(ctx, np.array([0.5, 0.25], np.float32), [0], 20)
+
+
+def test_tied_logits_across_the_cut_off_keep_the_lower_ids(ctx):
+    l = np.array([2.0, 5.0, 9.0, 5.0, 5.0, 9.0, 5.0, 1.0, 5.0], np.float32)
+    assert check(ctx, l, [0], 4)[1][0][:4].tolist() == [2, 5, 1, 3]
+    assert check(ctx, l, [0], 3)[1][0][:3].tolist() == [2, 5, 1]
+
+
+def test_negative_and_positive_zero_tie_to_the_lower_id(ctx):
+    l = np.array([-1.0, -0.0, 0.0, -0.0, 0.0], np.float32)
+    assert check(ctx, l, [0], 4)[1][0][:4].tolist() == [1, 2, 3, 4]
+
+
+def test_huge_logits_dont_overflow(ctx):
+    l = np.array([1e30, 1e30 - 1.0, -1e30], np.float32)
+    lp, _, lps, _, _ = check(ctx, l, [0], 2)
+    assert np.isfinite(lp[0]) and np.isfinite(lps[0][:2]).all()
+
+
+# ---- the model's width ---------------------------------------------------------------------------
+
+def test_config5_rows_match_the_oracle(ctx):
+    # Config 5's rows at the model's width, each at a token from its own sampled distribution's range
+    # (a top id, a middle one and the row's minimum).
+    from artemis_amd import workloads
+    w = workloads.config5(rows=16)
+    rows = w.logits
+    tokens = []
+    for r in range(rows.shape[0]):
+        order = np.argsort(-rows[r], kind="stable")
+        tokens.append(int(order[[0, 1000, -1][r % 3]]))
+    _, _, _, _, inexact = check(ctx, rows, tokens, 20, "config5")
+    assert inexact <= 2, inexact
+
+
+def test_ragged_widths_and_tops(ctx):
+    gen = np.random.default_rng(11)
+    for n in [1, 2, 5, 63, 8191, 8192, 8193, 20000, 100003]:
+        rows = (gen.standard_normal((3, n)) * 2.5).astype(np.float32)
+        tokens = gen.integers(0, n, size=3)
+        for top in [0, 1, 5, 20, 25]:
+            check(ctx, rows, tokens, top, f"n={n} top={top}")
+
+
+def test_heavy_ties(ctx):
+    # Ties across the parts' lists: every value equal (a part's list overflows and the row takes its
+    # best by full passes), and 3,000 copies of the maximum spread over the row.
+    n = 30000
+    same = np.full(n, 1.5, np.float32)
+    spread = (np.random.default_rng(5).standard_normal(n) * 2.0).astype(np.float32)
+    spread[np.random.default_rng(6).choice(n, 3000, replace=False)] = 9.0
+    check(ctx, np.stack([same, spread]), [7, 11], 20, "ties")
+
+
+def test_strided_and_shared_rows(ctx):
+    # A padded row stride, and stride 0 (every row reads the same row).
+    gen = np.random.default_rng(3)
+    n, stride = 10000, 10240
+    buf = (gen.standard_normal((2, stride)) * 2.5).astype(np.float32)
+    lp, ids, lps, st = run(ctx, buf, [4, 9], 20, row_stride=stride, n_vocab=n)
+    for r in range(2):
+        want_lp, want_top = O.logprobs(buf[r, :n], [4, 9][r], 20)
+        assert ids[r][:20].tolist() == [i for i, _ in want_top]
+        assert same_or_one_ulp(lp[r], want_lp, st[r] == 0)
+    lp, ids, lps, st = run(ctx, buf[0], [1, 2, 3], 20, row_stride=0, n_vocab=n)
+    want_top = O.logprobs(buf[0, :n], 1, 20)[1]
+    for r in range(3):
+        assert ids[r][:20].tolist() == [i for i, _ in want_top]
