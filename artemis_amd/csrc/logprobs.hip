@@ -5,8 +5,8 @@
 //
 // Two kernels over the rows in HBM:
 //   - lp_part_kernel: one 256-thread workgroup per kLpPart values of a row. Its largest value m_p,
-//     S_p = sum of exp(x - m_p) in f64 (the host libm's exp, as_exp::exp_with, each term as the
-//     reference computes it), and its 20 best by the reference's order: a threshold T from the
+//     S_p = sum of exp(x - m_p) in f64 (each term within 3 ulps of the reference's exp, from a
+//     table-free polynomial: exp_neg), and its 20 best by the reference's order: a threshold T from the
 //     waves (each wave's 20th best lane maximum: at least 20 values of the part rank at or above
 //     the largest of them) collects the few values at or above it into LDS, which a rank count sorts.
 //   - lp_row_kernel: one workgroup per row. M = max m_p; total = sum of S_p * exp(m_p - M);
@@ -14,8 +14,8 @@
 //     output is (x - lse) rounded to f32 (logprobs.rs:18, 34).
 //
 // The reference sums exp(x - M) left to right over the row; this sum is parallel, with a bound on
-// the distance between the two: gamma(n + 64) relative (both orders' rounding, the rescale of each
-// part and the f32 maximum's exactness), plus the logarithm's own ulp. An output is exact when that
+// the distance between the two: gamma(n + 64) relative (both orders' rounding, at most 4 ulps per
+// term between the two exps, and the rescale of each part), plus the logarithm's own ulp. An output is exact when that
 // bound cannot change its rounding to f32; otherwise the row's status says AS_LP_INEXACT and the
 // value is within one f32 ulp of the reference's.
 #include "sampler_device.h"
@@ -56,8 +56,36 @@ __device__ __forceinline__ uint64_t wave_qth_u64(uint64_t x, uint32_t q) {
 
 __device__ __forceinline__ double gamma_n(double n) { return n * kU / (1.0 - n * kU); }
 
+// exp(d) for d <= 0 without a table (the table's gathers from LDS conflict across lanes): d = k ln2 + r
+// with |r| <= ln2/2 (ln2 split in two, the product by k exact in the high part), then e^r by its Taylor
+// series to degree 12 (truncation below 2e-16 relative) in Horner form, and 2^k by the exponent
+// field. Within a few ulps of exp(d), which the sum's bound allows per term; d below -700 gives 0
+// (such a term is under 2^-1000 of the row's largest, which is 1).
+__device__ __forceinline__ double exp_neg(double d) {
+  const double kLog2e = 1.4426950408889634;
+  const double kLn2Hi = 6.93147180369123816490e-01, kLn2Lo = 1.90821492927058770002e-10;
+  const double dc = fmax(d, -708.0);  // 2^k stays a normal number; below -700 the result is 0 anyway
+  const double k = __builtin_rint(dc * kLog2e);
+  const double r = __builtin_fma(-k, kLn2Lo, __builtin_fma(-k, kLn2Hi, dc));
+  double p = 1.0 / 479001600.0;  // 1/12!
+  p = __builtin_fma(p, r, 1.0 / 39916800.0);
+  p = __builtin_fma(p, r, 1.0 / 3628800.0);
+  p = __builtin_fma(p, r, 1.0 / 362880.0);
+  p = __builtin_fma(p, r, 1.0 / 40320.0);
+  p = __builtin_fma(p, r, 1.0 / 5040.0);
+  p = __builtin_fma(p, r, 1.0 / 720.0);
+  p = __builtin_fma(p, r, 1.0 / 120.0);
+  p = __builtin_fma(p, r, 1.0 / 24.0);
+  p = __builtin_fma(p, r, 1.0 / 6.0);
+  p = __builtin_fma(p, r, 0.5);
+  p = __builtin_fma(p, r, 1.0);
+  p = __builtin_fma(p, r, 1.0);
+  const int64_t ki = (int64_t)k;
+  const double scale = __builtin_bit_cast(double, (uint64_t)(ki + 1023) << 52);
+  return d < -700.0 ? 0.0 : p * scale;
+}
+
 struct PartShared {
-  uint64_t tab[256];
   uint64_t list[kList];
   uint32_t n_list;
   uint32_t red_u[kWaves];
@@ -73,7 +101,6 @@ __global__ __launch_bounds__(kThreads) void lp_part_kernel(const float* __restri
   const uint32_t lane = tid & (kWave - 1), w = tid / kWave;
   const float* x = logits + (uint64_t)row * row_stride;
   const uint32_t b0 = part * kPart, b1 = min(b0 + kPart, n);
-  sh.tab[tid] = as_exp::kTable[tid];
   if (tid == 0) sh.n_list = 0;
 
   // Value q of this thread is at b0 + off(q): 16-byte groups when the row allows them.
@@ -101,7 +128,7 @@ __global__ __launch_bounds__(kThreads) void lp_part_kernel(const float* __restri
     kmax = max(kmax, total_key(v[q]));
     best = max(best, lp_key(v[q], b0 + off(q)));
   }
-  kmax = block_max_u32<kWaves>(kmax, sh.red_u);  // its barriers also publish sh.tab
+  kmax = block_max_u32<kWaves>(kmax, sh.red_u);
   const float m = key_value(kmax);
   const double md = (double)m;
 
@@ -109,7 +136,7 @@ __global__ __launch_bounds__(kThreads) void lp_part_kernel(const float* __restri
   double s = 0.0;
 #pragma unroll
   for (uint32_t q = 0; q < kPer; ++q)
-    if (b0 + off(q) < b1) s += as_exp::exp_with(sh.tab, (double)v[q] - md);
+    if (b0 + off(q) < b1) s += exp_neg((double)v[q] - md);
   s = block_sum_f64<kWaves>(s, sh.red_d);
 
   // The threshold: each wave's kTop-th best lane maximum, the largest of them.
@@ -152,7 +179,6 @@ struct RowShared {
   uint64_t tab[256];
   uint64_t merged[kMerge];
   uint64_t top[kTop];
-  uint32_t n_merged;
   uint32_t overflow;
   uint32_t inexact;
   uint32_t red_u[kWaves];
@@ -181,7 +207,6 @@ __global__ __launch_bounds__(kThreads) void lp_row_kernel(const float* __restric
   const LpPart* pp = parts + (uint64_t)row * n_parts;
   sh.tab[tid] = as_exp::kTable[tid];
   if (tid == 0) {
-    sh.n_merged = 0;
     sh.overflow = 0;
     sh.inexact = 0;
   }
@@ -196,8 +221,8 @@ __global__ __launch_bounds__(kThreads) void lp_row_kernel(const float* __restric
     const LpPart& q = pp[p];
     t += q.sum * as_exp::exp_with(sh.tab, (double)q.max - M);
     if (q.overflow) sh.overflow = 1;
-    const uint32_t base = atomicAdd(&sh.n_merged, q.n_top);
-    for (uint32_t i = 0; i < q.n_top; ++i) sh.merged[base + i] = q.top[i];
+    // Part p's list at merged[p * kTop ...), padded with zeros (below every key).
+    for (uint32_t i = 0; i < kTop; ++i) sh.merged[p * kTop + i] = i < q.n_top ? q.top[i] : 0ull;
   }
   const double total = block_sum_f64<kWaves>(t, sh.red_d);
   const double lnt = log(total);
@@ -209,12 +234,25 @@ __global__ __launch_bounds__(kThreads) void lp_row_kernel(const float* __restric
   const uint32_t nt = min(min(top, kTop), n);
   if (nt > 0) {
     if (!sh.overflow) {
-      // The merged lists hold the row's nt best: each part's list holds its own best kTop.
-      const uint32_t nm = sh.n_merged;
-      for (uint32_t i = tid; i < nm; i += kThreads) {
-        const uint64_t key = sh.merged[i];
+      // The parts' lists hold the row's nt best (each part's list holds its own best kTop). An
+      // entry's rank is the count of larger keys, found in each part's descending list by bisection;
+      // only an entry at place i < nt of its own list can rank below nt.
+      const uint32_t nm = n_parts * kTop;
+      for (uint32_t e = tid; e < nm; e += kThreads) {
+        const uint32_t i = e % kTop;
+        const uint64_t key = sh.merged[e];
+        if (i >= nt || key == 0ull) continue;
         uint32_t r = 0;
-        for (uint32_t j = 0; j < nm; ++j) r += sh.merged[j] > key ? 1u : 0u;
+        for (uint32_t p = 0; p < n_parts; ++p) {
+          const uint64_t* l = sh.merged + p * kTop;
+          uint32_t lo = 0, hi = kTop;  // l[0..lo) > key >= l[hi..kTop)
+          while (lo < hi) {
+            const uint32_t mid = (lo + hi) / 2;
+            if (l[mid] > key) lo = mid + 1;
+            else hi = mid;
+          }
+          r += lo;
+        }
         if (r < nt) sh.top[r] = key;
       }
     } else {

@@ -126,6 +126,47 @@ def gpu_batch1(reps=200):
     return out
 
 
+def gpu_logprobs(reps=50):
+    """as_logprobs (logprobs.rs:12-38) at top 20: kernel time per call for config 5's 256 rows
+    (HIP events on the library's stream, inputs rotated over three copies) and the wall time of one
+    row per call."""
+    import torch
+
+    from artemis_amd import Context, workloads
+
+    w = workloads.config5()
+    dev = torch.device("cuda:0")
+    rows, n = w.logits.shape
+    host = torch.from_numpy(w.logits)
+    sets = [host.to(dev) for _ in range(3)]
+    tokens = torch.arange(rows, dtype=torch.int32, device=dev) * 7
+    ctx = Context(max_rows=rows, max_vocab=n)
+    for i in range(5):
+        ctx.logprobs(sets[i % 3], tokens, 20)
+    torch.cuda.synchronize()
+    stream = torch.cuda.current_stream()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(stream)
+    for i in range(reps):
+        ctx.logprobs(sets[i % 3], tokens, 20)
+    e1.record(stream)
+    torch.cuda.synchronize()
+    batch_us = e0.elapsed_time(e1) / reps * 1e3
+    one = sets[0][:1]
+    tok1 = tokens[:1]
+    times = []
+    for i in range(reps):
+        t0 = time.perf_counter()
+        lp, *_ = ctx.logprobs(one, tok1, 20)
+        lp.cpu()
+        times.append(time.perf_counter() - t0)
+    ctx.close()
+    alg = 4 * rows * n
+    return dict(batch256_us=round(batch_us, 2), rows_per_s=round(rows / (batch_us * 1e-6), 1),
+                hbm_frac=round(alg / (batch_us * 1e-6) / (HBM_PEAK_GBS * 1e9), 4),
+                batch1_us_median=round(float(np.median(times)) * 1e6, 2))
+
+
 def cpu_baseline(budget_s=12.0):
     """The CPU oracle (the C++ restatement of the reference sampler) on this host: one row per call
     on one core, over a bounded sample of configuration 5's rows; and the 256 rows over all cores."""
@@ -193,6 +234,8 @@ def main():
     g = gpu_config5(a.steps, a.warmup)
     log("bench: batch-1 latency")
     b1 = gpu_batch1()
+    log("bench: log-probabilities")
+    lpb = gpu_logprobs()
     ms_per_step = g["wall"] / a.steps * 1e3
     rows_per_s = g["rows"] / (ms_per_step / 1e3)
     achieved = g["alg_bytes"] / (g["scan_ms"] / 1e3) / 1e9
@@ -235,6 +278,7 @@ def main():
         "kernels_us": {"scan": round(g["scan_ms"] * 1e3, 2), "finish": round(g["finish_ms"] * 1e3, 2)},
         "exact_path_rows": g["exact_rows"],
         "batch1": b1,
+        "logprobs_top20": lpb,
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,
                      "kernel": "scan_kernel", "bytes_per_launch": g["alg_bytes"]},
