@@ -5,17 +5,18 @@
 //
 // Two kernels over the rows in HBM:
 //   - lp_part_kernel: one 256-thread workgroup per kLpPart values of a row. Its largest value m_p,
-//     S_p = sum of exp(x - m_p) in f64 (each term within 3 ulps of the reference's exp, from a
-//     table-free polynomial: exp_neg), and its 20 best by the reference's order: a threshold T from the
-//     waves (each wave's 20th best lane maximum: at least 20 values of the part rank at or above
-//     the largest of them) collects the few values at or above it into LDS, which a rank count sorts.
+//     S_p = sum of exp(x - m_p) in f64 (each term within kExpRel of the reference's exp, from a
+//     table-free polynomial: exp_neg), and its 20 best by the reference's order: each wave's 5th best
+//     lane maximum, the smallest of the four, is a threshold with at least 20 values of the part at
+//     or above it; the few values there go into LDS, where a rank count sorts them.
 //   - lp_row_kernel: one workgroup per row. M = max m_p; total = sum of S_p * exp(m_p - M);
-//     lse = M + ln(total) (logprobs.rs:14-16); the parts' lists merge into the row's `top` best; each
-//     output is (x - lse) rounded to f32 (logprobs.rs:18, 34).
+//     lse = M + ln(total) (logprobs.rs:14-16); the parts' entries at or above the largest of the
+//     parts' nt-th entries hold the row's nt best, and a rank count orders them; each output is
+//     (x - lse) rounded to f32 (logprobs.rs:18, 34).
 //
 // The reference sums exp(x - M) left to right over the row; this sum is parallel, with a bound on
-// the distance between the two: gamma(n + 64) relative (both orders' rounding, at most 4 ulps per
-// term between the two exps, and the rescale of each part), plus the logarithm's own ulp. An output is exact when that
+// the distance between the two: gamma(n + 64) relative (both orders' rounding and the rescale of
+// each part), kExpRel for the terms' exp, plus the logarithm's own ulp. An output is exact when that
 // bound cannot change its rounding to f32; otherwise the row's status says AS_LP_INEXACT and the
 // value is within one f32 ulp of the reference's.
 #include "sampler_device.h"
@@ -56,34 +57,49 @@ __device__ __forceinline__ uint64_t wave_qth_u64(uint64_t x, uint32_t q) {
 
 __device__ __forceinline__ double gamma_n(double n) { return n * kU / (1.0 - n * kU); }
 
-// exp(d) for d <= 0 without a table (the table's gathers from LDS conflict across lanes): d = k ln2 + r
-// with |r| <= ln2/2 (ln2 split in two, the product by k exact in the high part), then e^r by its Taylor
-// series to degree 12 (truncation below 2e-16 relative) in Horner form, and 2^k by the exponent
-// field. Within a few ulps of exp(d), which the sum's bound allows per term; d below -700 gives 0
-// (such a term is under 2^-1000 of the row's largest, which is 1).
-__device__ __forceinline__ double exp_neg(double d) {
-  const double kLog2e = 1.4426950408889634;
-  const double kLn2Hi = 6.93147180369123816490e-01, kLn2Lo = 1.90821492927058770002e-10;
-  const double dc = fmax(d, -708.0);  // 2^k stays a normal number; below -700 the result is 0 anyway
-  const double k = __builtin_rint(dc * kLog2e);
-  const double r = __builtin_fma(-k, kLn2Lo, __builtin_fma(-k, kLn2Hi, dc));
-  double p = 1.0 / 479001600.0;  // 1/12!
-  p = __builtin_fma(p, r, 1.0 / 39916800.0);
-  p = __builtin_fma(p, r, 1.0 / 3628800.0);
-  p = __builtin_fma(p, r, 1.0 / 362880.0);
-  p = __builtin_fma(p, r, 1.0 / 40320.0);
-  p = __builtin_fma(p, r, 1.0 / 5040.0);
-  p = __builtin_fma(p, r, 1.0 / 720.0);
-  p = __builtin_fma(p, r, 1.0 / 120.0);
-  p = __builtin_fma(p, r, 1.0 / 24.0);
-  p = __builtin_fma(p, r, 1.0 / 6.0);
-  p = __builtin_fma(p, r, 0.5);
-  p = __builtin_fma(p, r, 1.0);
-  p = __builtin_fma(p, r, 1.0);
-  const int64_t ki = (int64_t)k;
-  const double scale = __builtin_bit_cast(double, (uint64_t)(ki + 1023) << 52);
-  return d < -700.0 ? 0.0 : p * scale;
-}
+// Relative error of exp_neg against exp, per term: the polynomial's truncation (3.07e-13 for |f| <= 1/2),
+// the rounding of t = d * log2(e) (at most |t| <= 1022 times 2^-53, times ln 2) and of the Horner steps.
+constexpr double kExpRel = 5.0e-13;
+
+// exp(d) for d <= 0 without a table (a table's gathers from LDS conflict across lanes): e^d = 2^t,
+// t = d log2(e) = k + f with k = rint(t) and |f| <= 1/2 (f = t - k exactly), 2^f by its Taylor
+// series in f to degree 10 (coefficients ln(2)^i / i!), 2^k by ldexp (ExpPoly::exp_neg). Within kExpRel
+// of exp(d); the parallel sum it feeds is bounded at gamma(n) ~ 2.7e-11 relative anyway, so a few
+// ulps more per term change nothing. Below d = -708 the argument is clamped (such a term is under
+// 2^-1021 of the row's largest, which is 1).
+//
+// The coefficients of 2^f, highest degree first. Read from constant memory once per thread, they stay
+// in scalar registers, which each fused multiply-add takes as an operand (as immediates, each step
+// would first rebuild its coefficient in two vector moves).
+__constant__ double kExp2Poly[11] = {
+    7.054911620801123e-09,  1.01780860092397e-07,  1.321548679014431e-06, 1.5252733804059841e-05,
+    0.0001540353039338161,  0.0013333558146428443, 0.009618129107628477,  0.05550410866482158,
+    0.24022650695910072,    0.6931471805599453,    1.0};
+
+struct ExpPoly {
+  double c[11];
+  __device__ __forceinline__ void load() {
+#pragma unroll
+    for (int i = 0; i < 11; ++i) c[i] = kExp2Poly[i];
+  }
+  __device__ __forceinline__ double exp_neg(double d) const {
+    const double t = fmax(d, -708.0) * 1.4426950408889634;
+    const double k = __builtin_rint(t);
+    const double f = t - k;
+    double p = c[0];
+#pragma unroll
+    for (int i = 1; i < 11; ++i) p = __builtin_fma(p, f, c[i]);
+    return __builtin_amdgcn_ldexp(p, (int32_t)k);
+  }
+};
+
+// The value part of lp_key.
+__device__ __forceinline__ uint32_t lp_vkey(float x) { return total_key(x == 0.0f ? 0.0f : x); }
+
+// Each wave's kLaneQ-th best lane maximum; the smallest of them has kWaves * kLaneQ values of the part
+// at or above it.
+constexpr uint32_t kLaneQ = (kTop + kWaves - 1) / kWaves;
+static_assert(kLaneQ * kWaves >= kTop, "the waves' thresholds cover the part's best kTop");
 
 struct PartShared {
   uint64_t list[kList];
@@ -93,71 +109,78 @@ struct PartShared {
   uint64_t red_k[kWaves];
 };
 
-__global__ __launch_bounds__(kThreads) void lp_part_kernel(const float* __restrict__ logits, uint64_t row_stride,
-                                                           uint32_t n, uint32_t vec, LpPart* __restrict__ parts,
-                                                           uint32_t n_parts) {
-  __shared__ PartShared sh;
-  const uint32_t part = blockIdx.x, row = blockIdx.y, tid = threadIdx.x;
-  const uint32_t lane = tid & (kWave - 1), w = tid / kWave;
-  const float* x = logits + (uint64_t)row * row_stride;
-  const uint32_t b0 = part * kPart, b1 = min(b0 + kPart, n);
-  if (tid == 0) sh.n_list = 0;
-
-  // Value q of this thread is at b0 + off(q): 16-byte groups when the row allows them.
-  const bool v4 = vec && b1 - b0 == kPart;
-  auto off = [&](uint32_t q) { return v4 ? ((q / 4) * kThreads + tid) * 4 + (q % 4) : q * kThreads + tid; };
+// One part, b0 .. b1 of row x. kV4: the part is whole and 16-byte aligned, each thread's values in
+// 16-byte groups.
+template <bool kV4>
+__device__ __forceinline__ void lp_part(PartShared& sh, const float* __restrict__ x, uint32_t b0, uint32_t b1,
+                                        LpPart& out) {
+  const uint32_t tid = threadIdx.x, lane = tid & (kWave - 1), w = tid / kWave;
+  auto off = [&](uint32_t q) { return kV4 ? ((q / 4) * kThreads + tid) * 4 + (q % 4) : q * kThreads + tid; };
+  auto valid = [&](uint32_t q) { return kV4 || b0 + off(q) < b1; };
   float v[kPer];
-  if (v4) {
+  if (kV4) {
 #pragma unroll
     for (uint32_t g = 0; g < kPer / 4; ++g) {
-      const f32x4 t = *reinterpret_cast<const f32x4*>(x + b0 + (g * kThreads + tid) * 4);
+      const f32x4 t = __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(x + b0 + (g * kThreads + tid) * 4));
 #pragma unroll
       for (int c = 0; c < 4; ++c) v[4 * g + c] = t[c];
     }
   } else {
 #pragma unroll
-    for (uint32_t q = 0; q < kPer; ++q) v[q] = (b0 + off(q) < b1) ? x[b0 + off(q)] : 0.0f;
+    for (uint32_t q = 0; q < kPer; ++q) v[q] = valid(q) ? x[b0 + off(q)] : 0.0f;
   }
 
-  // The part's largest value (by rank key: the largest of finite values).
-  uint32_t kmax = 0;
-  uint64_t best = 0;
+  // The thread's best by the reference's order: its values come in index order, so the first of
+  // equal values holds the lower id. On finite values IEEE `>` is the key order with -0 and +0 tied.
+  // A thread holds values when its first one is in the part.
+  float bv = v[0];
+  uint32_t bq = 0;
 #pragma unroll
-  for (uint32_t q = 0; q < kPer; ++q) {
-    if (b0 + off(q) >= b1) continue;
-    kmax = max(kmax, total_key(v[q]));
-    best = max(best, lp_key(v[q], b0 + off(q)));
+  for (uint32_t q = 1; q < kPer; ++q) {
+    if (valid(q) && v[q] > bv) {
+      bv = v[q];
+      bq = q;
+    }
   }
-  kmax = block_max_u32<kWaves>(kmax, sh.red_u);
+  const bool has = valid(0);
+  const uint32_t bk = has ? lp_vkey(bv) : 0u;
+  const uint64_t best = has ? pack(bk, b0 + off(bq)) : 0ull;
+
+  // The part's largest value (-0 and +0 alike: both give the same differences).
+  const uint32_t kmax = block_max_u32<kWaves>(bk, sh.red_u);
   const float m = key_value(kmax);
   const double md = (double)m;
 
-  // S_p, each term the reference's exp(f64(x) - m).
+  // S_p, each term within kExpRel of the reference's exp(f64(x) - m).
+  ExpPoly ep;
+  ep.load();
   double s = 0.0;
 #pragma unroll
   for (uint32_t q = 0; q < kPer; ++q)
-    if (b0 + off(q) < b1) s += exp_neg((double)v[q] - md);
-  s = block_sum_f64<kWaves>(s, sh.red_d);
+    if (valid(q)) s += ep.exp_neg((double)v[q] - md);
 
-  // The threshold: each wave's kTop-th best lane maximum, the largest of them.
-  const uint64_t tw = wave_qth_u64(best, kTop);
+  // The threshold: the smallest of the waves' kLaneQ-th best lane maxima (0 when a wave holds fewer).
+  const uint64_t tw = wave_qth_u64(best, kLaneQ);
   if (lane == 0) sh.red_k[w] = tw;
-  __syncthreads();
+  if (tid == 0) sh.n_list = 0;
+  s = block_sum_f64<kWaves>(s, sh.red_d);  // its barriers publish red_k and n_list
   uint64_t T = sh.red_k[0];
-  for (int k = 1; k < kWaves; ++k) T = max(T, sh.red_k[k]);
+  for (int k = 1; k < kWaves; ++k) T = min(T, sh.red_k[k]);
+  // The threshold's value (minus infinity for T = 0): only values at or above it can pass.
+  const float t_val = T ? key_value((uint32_t)(T >> 32)) : -__builtin_inff();
   // Every value at or above it, into the list.
 #pragma unroll
   for (uint32_t q = 0; q < kPer; ++q) {
-    if (b0 + off(q) >= b1) continue;
-    const uint64_t key = lp_key(v[q], b0 + off(q));
-    if (key >= T) {
-      const uint32_t i = atomicAdd(&sh.n_list, 1u);
-      if (i < kList) sh.list[i] = key;
+    if (valid(q) && v[q] >= t_val) {
+      const uint64_t key = pack(lp_vkey(v[q]), b0 + off(q));
+      if (key >= T) {
+        const uint32_t i = atomicAdd(&sh.n_list, 1u);
+        if (i < kList) sh.list[i] = key;
+      }
     }
   }
   __syncthreads();
   const uint32_t n_list = sh.n_list;
-  LpPart& out = parts[(uint64_t)row * n_parts + part];
   // The list's kTop best, in order: each entry's place is the number of entries above it.
   if (n_list <= kList) {
     for (uint32_t i = tid; i < n_list; i += kThreads) {
@@ -175,10 +198,23 @@ __global__ __launch_bounds__(kThreads) void lp_part_kernel(const float* __restri
   }
 }
 
+__global__ __launch_bounds__(kThreads) void lp_part_kernel(const float* __restrict__ logits, uint64_t row_stride,
+                                                           uint32_t n, uint32_t vec, LpPart* __restrict__ parts,
+                                                           uint32_t n_parts) {
+  __shared__ PartShared sh;
+  const uint32_t part = blockIdx.x, row = blockIdx.y;
+  const float* x = logits + (uint64_t)row * row_stride;
+  const uint32_t b0 = part * kPart, b1 = min(b0 + kPart, n);
+  LpPart& out = parts[(uint64_t)row * n_parts + part];
+  if (vec && b1 - b0 == kPart) lp_part<true>(sh, x, b0, b1, out);
+  else lp_part<false>(sh, x, b0, b1, out);
+}
+
 struct RowShared {
   uint64_t tab[256];
   uint64_t merged[kMerge];
   uint64_t top[kTop];
+  uint32_t n_merged;
   uint32_t overflow;
   uint32_t inexact;
   uint32_t red_u[kWaves];
@@ -207,6 +243,7 @@ __global__ __launch_bounds__(kThreads) void lp_row_kernel(const float* __restric
   const LpPart* pp = parts + (uint64_t)row * n_parts;
   sh.tab[tid] = as_exp::kTable[tid];
   if (tid == 0) {
+    sh.n_merged = 0;
     sh.overflow = 0;
     sh.inexact = 0;
   }
@@ -215,49 +252,53 @@ __global__ __launch_bounds__(kThreads) void lp_row_kernel(const float* __restric
   for (uint32_t p = tid; p < n_parts; p += kThreads) kmax = max(kmax, total_key(pp[p].max));
   kmax = block_max_u32<kWaves>(kmax, sh.red_u);
   const double M = (double)key_value(kmax);
-  // total = sum of S_p * exp(m_p - M); the parts' lists into one.
+  // total = sum of S_p * exp(m_p - M).
+  const uint32_t nt = min(min(top, kTop), n);
   double t = 0.0;
+  uint64_t cut = 0;
   for (uint32_t p = tid; p < n_parts; p += kThreads) {
     const LpPart& q = pp[p];
     t += q.sum * as_exp::exp_with(sh.tab, (double)q.max - M);
     if (q.overflow) sh.overflow = 1;
-    // Part p's list at merged[p * kTop ...), padded with zeros (below every key).
-    for (uint32_t i = 0; i < kTop; ++i) sh.merged[p * kTop + i] = i < q.n_top ? q.top[i] : 0ull;
+    // A part listing nt entries has nt values at or above its nt-th: no value below the largest
+    // such entry is among the row's nt best.
+    if (nt > 0 && q.n_top >= nt) cut = max(cut, q.top[nt - 1]);
   }
   const double total = block_sum_f64<kWaves>(t, sh.red_d);
+  cut = wave_max_u64(cut);
+  if ((tid & (kWave - 1)) == 0) sh.red_k[tid / kWave] = cut;
+  __syncthreads();
+  for (int k = 0; k < kWaves; ++k) cut = max(cut, sh.red_k[k]);
   const double lnt = log(total);
   const double lse = M + lnt;
   // The distance to the reference's lse: both sums' roundings (n terms each, the parts' rescales),
-  // the logarithm's ulp and the final addition.
-  const double e = gamma_n((double)n + 64.0) + 4.0 * kU * fabs(lnt) + 2.0 * kU * fabs(lse);
+  // each term's exp, the logarithm's ulp and the final addition.
+  const double e = gamma_n((double)n + 64.0) + kExpRel + 4.0 * kU * fabs(lnt) + 2.0 * kU * fabs(lse);
 
-  const uint32_t nt = min(min(top, kTop), n);
   if (nt > 0) {
     if (!sh.overflow) {
-      // The parts' lists hold the row's nt best (each part's list holds its own best kTop). An
-      // entry's rank is the count of larger keys, found in each part's descending list by bisection;
-      // only an entry at place i < nt of its own list can rank below nt.
+      // The parts' entries at or above the cut hold the row's nt best (each part's list holds its
+      // own best kTop); an entry's place among them is the count of larger ones.
       const uint32_t nm = n_parts * kTop;
-      for (uint32_t e = tid; e < nm; e += kThreads) {
-        const uint32_t i = e % kTop;
-        const uint64_t key = sh.merged[e];
-        if (i >= nt || key == 0ull) continue;
-        uint32_t r = 0;
-        for (uint32_t p = 0; p < n_parts; ++p) {
-          const uint64_t* l = sh.merged + p * kTop;
-          uint32_t lo = 0, hi = kTop;  // l[0..lo) > key >= l[hi..kTop)
-          while (lo < hi) {
-            const uint32_t mid = (lo + hi) / 2;
-            if (l[mid] > key) lo = mid + 1;
-            else hi = mid;
-          }
-          r += lo;
+      for (uint32_t i = tid; i < nm; i += kThreads) {
+        const LpPart& q = pp[i / kTop];
+        if (i % kTop < q.n_top) {
+          const uint64_t key = q.top[i % kTop];
+          if (key >= cut) sh.merged[atomicAdd(&sh.n_merged, 1u)] = key;
         }
+      }
+      __syncthreads();
+      const uint32_t nc = sh.n_merged;
+      for (uint32_t i = tid; i < nc; i += kThreads) {
+        const uint64_t key = sh.merged[i];
+        uint32_t r = 0;
+        for (uint32_t j = 0; j < nc; ++j) r += sh.merged[j] > key ? 1u : 0u;
         if (r < nt) sh.top[r] = key;
       }
     } else {
       // Heavy ties overflowed a part's list: the row's best, one full pass each (the largest key
       // below the one before).
+      __syncthreads();  // every thread has read the cut from red_k
       uint64_t prev = ~0ull;
       for (uint32_t r = 0; r < nt; ++r) {
         uint64_t b = 0;
