@@ -481,6 +481,23 @@ int as_argmax_rows(as_ctx* c, const float* logits, uint64_t row_stride, uint32_t
   return AS_OK;
 }
 
+uint64_t as_row_bytes(uint32_t wtype, uint64_t n) {
+  static const uint32_t per[6] = {1, 1, 32, 256, 256, 256}, bytes[6] = {4, 2, 34, 144, 176, 210};
+  if (wtype > AS_WTYPE_Q6_K || n % per[wtype] != 0) return 0;
+  return n / per[wtype] * bytes[wtype];
+}
+
+int as_embed_rows(as_ctx* c, const uint64_t* rows, uint32_t wtype, uint32_t n, float* y, uint32_t n_tokens) {
+  if (!c) return AS_ERR_INVALID;
+  if (n_tokens == 0 || n == 0) return AS_OK;
+  if (!rows || !y) return fail(c, AS_ERR_INVALID, "as_embed_rows: null rows or y");
+  if (as_row_bytes(wtype, n) == 0)
+    return fail(c, AS_ERR_INVALID, "as_embed_rows: unknown weight type, or n is not a whole number of its blocks");
+  AS_HIP(c, hipSetDevice(c->device));
+  AS_HIP(c, as_launch::embed_rows(c->stream, rows, wtype, n, y, n_tokens));
+  return AS_OK;
+}
+
 int as_profile(as_ctx* c, int enable) {
   if (!c) return AS_ERR_INVALID;
   c->profile = enable != 0;

@@ -138,6 +138,10 @@ hipError_t accept(hipStream_t stream, const uint32_t* picks, const uint32_t* sta
                   const uint32_t* drafts, uint32_t k, const uint32_t* stop_ids, uint32_t n_stop,
                   uint64_t* rng_state, uint32_t draws_per_row, uint32_t* result);
 
+// embed.hip: y[t] = the row at rows[t] dequantized (wtype an AS_WTYPE_*, n whole blocks).
+hipError_t embed_rows(hipStream_t stream, const uint64_t* rows, uint32_t wtype, uint32_t n, float* y,
+                      uint32_t n_tokens);
+
 hipError_t argmax_rows(hipStream_t stream, bool vec, const float* logits, uint64_t row_stride,
                        uint32_t n, uint32_t n_rows, uint32_t* ids, uint64_t* rows_out,
                        uint64_t embd, uint32_t row_bytes, uint32_t slot);

@@ -66,6 +66,18 @@ class _CBatch(C.Structure):
     ]
 
 
+# Weight types of embedding rows, by the reference's codes (kernels/src/lib.rs:438-447).
+WTYPE = {"F32": 0, "BF16": 1, "Q8_0": 2, "Q4_K": 3, "Q5_K": 4, "Q6_K": 5}
+
+
+def row_bytes(wtype: int, n: int) -> int:
+    """WType::row_bytes (quant.rs:66-74); raises for an unknown type or a partial block."""
+    b = lib().as_row_bytes(wtype, n)
+    if b == 0 and n != 0:
+        raise SamplerError(f"weight type {wtype} has no rows of {n} values (unknown type, or not whole blocks)")
+    return b
+
+
 _lib = None
 
 
@@ -90,6 +102,9 @@ def lib() -> C.CDLL:
         L.as_verify.argtypes = [vp, vp, u64, u32, vp, u32, vp, u32, vp, u32, C.POINTER(_CSampling),
                                 vp, vp, vp]
         L.as_argmax_rows.argtypes = [vp, vp, u64, u32, u32, vp, vp, u64, u32, u32]
+        L.as_row_bytes.argtypes = [u32, u64]
+        L.as_row_bytes.restype = u64
+        L.as_embed_rows.argtypes = [vp, vp, u32, u32, vp, u32]
         L.as_debug_exp.argtypes = [vp, vp, vp, u32]
         L.as_debug_exp2f.argtypes = [vp, vp, vp, u32]
         L.as_logprobs.argtypes = [vp, vp, u64, u32, u32, vp, u32, vp, vp, vp, vp]
@@ -267,6 +282,18 @@ class Context:
         nv = n if n is not None else logits.shape[1]
         self._ok(lib().as_argmax_rows(self.h, logits.data_ptr(), logits.stride(0), nv, logits.shape[0],
                                       ids.data_ptr(), rows_out.data_ptr(), embd, row_bytes, slot))
+
+    def embed_rows(self, rows: torch.Tensor, wtype: int, n: int, y: Optional[torch.Tensor] = None) -> torch.Tensor:
+        """embed_rows (dispatch.rs:97-120): y[t] = the embedding row at device address rows[t]
+        dequantized (quant.rs:77-252). `rows`: [tokens] int64 on the device, as argmax_rows writes
+        them; `wtype`: one of WTYPE's codes; returns y ([tokens, n] f32 on the device)."""
+        assert rows.is_cuda and rows.dtype == torch.int64 and rows.is_contiguous()
+        t = rows.numel()
+        if y is None:
+            y = torch.empty((t, n), dtype=torch.float32, device=rows.device)
+        assert y.is_cuda and y.dtype == torch.float32 and y.is_contiguous() and y.numel() >= t * n
+        self._ok(lib().as_embed_rows(self.h, rows.data_ptr(), wtype, n, y.data_ptr(), t))
+        return y
 
     def logprobs(self, logits: torch.Tensor, tokens: torch.Tensor, top: int, row_stride: Optional[int] = None,
                  n_vocab: Optional[int] = None):

@@ -130,6 +130,29 @@ int as_argmax_rows(as_ctx* ctx, const float* logits, uint64_t row_stride, uint32
                    uint32_t n_rows, uint32_t* ids, uint64_t* rows_out, uint64_t embd,
                    uint32_t row_bytes, uint32_t slot);
 
+/* Weight types of embedding rows, by the reference's codes (crates/kernels/src/lib.rs:438-447,
+ * shaders/quant.glsl:2-8): ggml's block layouts (crates/qwen36/src/quant.rs:60-74). */
+#define AS_WTYPE_F32 0u
+#define AS_WTYPE_BF16 1u
+#define AS_WTYPE_Q8_0 2u
+#define AS_WTYPE_Q4_K 3u
+#define AS_WTYPE_Q5_K 4u
+#define AS_WTYPE_Q6_K 5u
+
+/* WType::row_bytes (crates/qwen36/src/quant.rs:66-74): bytes in a row of n values of type wtype;
+ * 0 for an unknown type or an n that is not a whole number of the type's blocks (the reference
+ * panics there). A host-only function. */
+uint64_t as_row_bytes(uint32_t wtype, uint64_t n);
+
+/* embed_rows (crates/kernels/src/dispatch.rs:97-120, shaders/embed_rows.comp): y[t][0..n) = the
+ * embedding row at address rows[t] dequantized as dequant_row does (quant.rs:77-252), bit for
+ * bit, for t < n_tokens. rows is a device array of n_tokens u64 addresses (argmax_rows writes
+ * them); each must be 2-byte aligned and readable by the GPU (an HBM table, or pinned host memory)
+ * and hold as_row_bytes(wtype, n) bytes. y: [n_tokens][n] f32 on the device. Stream-ordered.
+ * AS_ERR_INVALID for a bad type, an n that is not whole blocks, or null pointers. */
+int as_embed_rows(as_ctx* ctx, const uint64_t* rows, uint32_t wtype, uint32_t n, float* y,
+                  uint32_t n_tokens);
+
 /* Log-probabilities of the model's own distribution (crates/engine/src/logprobs.rs:12-38), which the
  * generation loop asks for per sampled token when a request wants them (turn.rs:361-364): for each of
  * n_rows rows of raw logits (before penalties, temperature and filters; the rows must be finite),

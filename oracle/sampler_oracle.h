@@ -112,6 +112,13 @@ void oc_sample_rows(const oc_params* params, const uint64_t* seeds, const float*
                     const uint32_t* hist_ids, unsigned threads, uint32_t* tokens,
                     uint64_t* rng_out);
 
+// crates/qwen36/src/quant.rs:60-252 (quant_oracle.cc): weight types by the reference's codes
+// (0 F32, 1 BF16, 2 Q8_0, 3 Q4_K, 4 Q5_K, 5 Q6_K). oc_row_bytes is 0 for an unknown type or a
+// row that is not whole blocks; oc_dequant_row returns 1 for those (and writes nothing).
+uint64_t oc_row_bytes(uint32_t wtype, uint64_t n);
+int oc_dequant_row(uint32_t wtype, const uint8_t* row, uint64_t n, float* out);
+float oc_half_to_float(uint16_t h);
+
 #ifdef __cplusplus
 }
 #endif

@@ -101,6 +101,12 @@ def lib():
         L.oc_exp_array.argtypes = [f64p, f64p, C.c_size_t]
         L.oc_sample_rows.argtypes = [C.POINTER(Params), u64p, f32p, C.c_size_t, C.c_size_t,
                                      C.c_size_t, u32p, u32p, C.c_uint, u32p, u64p]
+        L.oc_row_bytes.argtypes = [C.c_uint32, C.c_uint64]
+        L.oc_row_bytes.restype = C.c_uint64
+        L.oc_dequant_row.argtypes = [C.c_uint32, C.c_void_p, C.c_uint64, f32p]
+        L.oc_dequant_row.restype = C.c_int
+        L.oc_half_to_float.argtypes = [C.c_uint16]
+        L.oc_half_to_float.restype = C.c_float
         _lib = L
     return _lib
 
@@ -285,3 +291,21 @@ def sample_rows(rows_params, seeds, logits, hist_off=None, hist_ids=None, thread
     lib().oc_sample_rows(P, s.ctypes.data_as(u64p), logits.ctypes.data_as(f32p), 0 if shared else n, n,
                          rows, hop, hip, threads, toks.ctypes.data_as(u32p), rng.ctypes.data_as(u64p))
     return toks, rng
+
+
+# Weight types by the reference's codes (quant.glsl:2-8).
+WTYPES = {"F32": 0, "BF16": 1, "Q8_0": 2, "Q4_K": 3, "Q5_K": 4, "Q6_K": 5}
+
+
+def row_bytes(wtype: int, n: int) -> int:
+    return lib().oc_row_bytes(wtype, n)
+
+
+def dequant_row(wtype: int, row, n: int):
+    """quant.rs:77-104 on one row's bytes: n f32 values."""
+    raw = np.ascontiguousarray(np.frombuffer(bytes(row), dtype=np.uint8))
+    out = np.zeros(n, np.float32)
+    rc = lib().oc_dequant_row(wtype, raw.ctypes.data, n, out.ctypes.data_as(f32p))
+    if rc != 0:
+        raise ValueError("not a whole-block row")
+    return out

@@ -23,7 +23,7 @@ def L():
 
 def declared():
     text = open(HEADER).read()
-    return sorted(set(re.findall(r"^\s*(?:int|void|const char\*)\s+(as_\w+)\(", text, re.M)))
+    return sorted(set(re.findall(r"^\s*(?:int|void|uint64_t|const char\*)\s+(as_\w+)\(", text, re.M)))
 
 
 def test_the_library_exports_every_declared_entry_point(L):
@@ -73,3 +73,14 @@ def test_calls_without_a_context_fail_cleanly(L):
     assert L.as_sample(None, None, None) != 0
     assert L.as_sync(None) != 0
     assert L.as_destroy(None) != 0
+
+
+def test_row_bytes_matches_the_oracle(L):
+    from artemis_amd import WTYPE, row_bytes
+    for name, code in WTYPE.items():
+        for n in (0, 1, 2, 32, 100, 256, 512, 2048, 2080, 248320):
+            assert L.as_row_bytes(code, n) == oracle_lib.row_bytes(code, n), (name, n)
+    assert L.as_row_bytes(6, 256) == 0
+    assert row_bytes(WTYPE["Q6_K"], 2048) == 8 * 210
+    with pytest.raises(Exception):
+        row_bytes(WTYPE["Q4_K"], 100)
