@@ -12,7 +12,7 @@ import sys
 HERE = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(HERE, "csrc")
 LIB = os.path.join(HERE, "libartemis_sampler.so")
-SOURCES = ["api.hip", "scan.hip", "tail.hip", "finish.hip", "misc.hip", "logprobs.hip", "embed.hip"]
+SOURCES = ["api.hip", "scan.hip", "tail.hip", "finish.hip", "misc.hip", "logprobs.hip", "embed.hip", "matvec.hip"]
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 
 FLAGS = [

@@ -41,6 +41,7 @@ struct as_ctx {
   uint32_t* d_vstatus = nullptr;
   float* d_zero = nullptr;  // 1,024 zeros the scan's idle loads read
   as_launch::LpPart* d_lp = nullptr;  // log-probabilities: per row, its parts' sums and lists
+  uint64_t* d_mv_partials = nullptr;  // head_argmax: each matvec workgroup's best key
   as_launch::RowOrder order{};  // the scan's row order for the current call
   std::vector<std::pair<double, uint32_t>> order_cost;  // its sort keys (kept: no allocation per call)
   std::string err;
@@ -329,6 +330,7 @@ int as_destroy(as_ctx* c) {
   (void)hipFree(c->d_vstatus);
   (void)hipFree(c->d_zero);
   (void)hipFree(c->d_lp);
+  (void)hipFree(c->d_mv_partials);
   for (hipEvent_t e : c->ev) (void)hipEventDestroy(e);
   for (int b = 0; b < 2; ++b)
     if (c->h_block[b]) (void)hipHostFree(c->h_block[b]);
@@ -374,6 +376,7 @@ int as_create(int device, void* hip_stream, uint32_t max_rows, uint32_t max_voca
     e = hipMalloc(&c->d_cands, sizeof(uint64_t) * (uint64_t)max_rows * as_launch::kCandCap);
   if (e == hipSuccess) e = hipMalloc(&c->d_scratch, sizeof(uint32_t) * (uint64_t)max_rows * c->scratch_stride);
   if (e == hipSuccess) e = hipMalloc(&c->d_vstatus, sizeof(uint32_t) * max_rows);
+  if (e == hipSuccess) e = hipMalloc(&c->d_mv_partials, sizeof(uint64_t) * as_launch::kMatvecGroups);
   if (e == hipSuccess)
     e = hipMalloc(&c->d_lp, sizeof(as_launch::LpPart) * (uint64_t)max_rows * as_launch::lp_parts(max_vocab));
   if (e == hipSuccess) e = hipMalloc(&c->d_zero, sizeof(float) * 1024);
@@ -495,6 +498,50 @@ int as_embed_rows(as_ctx* c, const uint64_t* rows, uint32_t wtype, uint32_t n, f
     return fail(c, AS_ERR_INVALID, "as_embed_rows: unknown weight type, or n is not a whole number of its blocks");
   AS_HIP(c, hipSetDevice(c->device));
   AS_HIP(c, as_launch::embed_rows(c->stream, rows, wtype, n, y, n_tokens));
+  return AS_OK;
+}
+
+// The shape and alignment checks as_matvec and as_head_argmax share.
+int check_matvec(as_ctx* c, const char* who, const void* w, uint32_t wtype, uint32_t k, const float* x) {
+  char msg[160];
+  if (!w || !x) {
+    std::snprintf(msg, sizeof msg, "%s: null weights or input", who);
+    return fail(c, AS_ERR_INVALID, msg);
+  }
+  if (as_row_bytes(wtype, k) == 0 || k % 32 != 0 || k > as_launch::kMatvecMaxK) {
+    std::snprintf(msg, sizeof msg, "%s: unknown weight type, or k is not whole 32-value units and blocks of it "
+                  "(at most %u)", who, as_launch::kMatvecMaxK);
+    return fail(c, AS_ERR_INVALID, msg);
+  }
+  const uintptr_t align = wtype <= AS_WTYPE_BF16 ? 4 : 2;
+  if ((uintptr_t)w % align != 0 || (uintptr_t)x % 4 != 0) {
+    std::snprintf(msg, sizeof msg, "%s: weights must be %u-byte aligned and x 4-byte aligned", who, (unsigned)align);
+    return fail(c, AS_ERR_INVALID, msg);
+  }
+  return AS_OK;
+}
+
+int as_matvec(as_ctx* c, const void* w, uint32_t wtype, uint32_t rows, uint32_t k, const float* x, float* y) {
+  if (!c) return AS_ERR_INVALID;
+  if (rows == 0) return AS_OK;
+  int rc = check_matvec(c, "as_matvec", w, wtype, k, x);
+  if (rc != AS_OK) return rc;
+  if (!y) return fail(c, AS_ERR_INVALID, "as_matvec: null y");
+  AS_HIP(c, hipSetDevice(c->device));
+  AS_HIP(c, as_launch::matvec(c->stream, w, wtype, as_row_bytes(wtype, k), rows, k, x, y));
+  return AS_OK;
+}
+
+int as_head_argmax(as_ctx* c, const void* w, uint32_t wtype, uint32_t rows, uint32_t k, const float* x,
+                   float* logits, uint32_t* ids, uint64_t* rows_out, uint64_t embd, uint32_t embd_row_bytes,
+                   uint32_t slot) {
+  if (!c) return AS_ERR_INVALID;
+  int rc = check_matvec(c, "as_head_argmax", w, wtype, k, x);
+  if (rc != AS_OK) return rc;
+  if (rows == 0 || !ids || !rows_out) return fail(c, AS_ERR_INVALID, "as_head_argmax: no rows, or null ids/rows_out");
+  AS_HIP(c, hipSetDevice(c->device));
+  AS_HIP(c, as_launch::head_argmax(c->stream, w, wtype, as_row_bytes(wtype, k), rows, k, x, logits,
+                                   c->d_mv_partials, ids, rows_out, embd, embd_row_bytes, slot));
   return AS_OK;
 }
 

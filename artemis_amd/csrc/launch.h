@@ -138,6 +138,16 @@ hipError_t accept(hipStream_t stream, const uint32_t* picks, const uint32_t* sta
                   const uint32_t* drafts, uint32_t k, const uint32_t* stop_ids, uint32_t n_stop,
                   uint64_t* rng_state, uint32_t draws_per_row, uint32_t* result);
 
+// matvec.hip: y = W x (the reference's matvec, bit for bit), and the same with argmax_rows fused
+// (partials: kMatvecGroups u64 of scratch). k at most kMatvecMaxK (x is staged in LDS).
+constexpr uint32_t kMatvecGroups = 2048;
+constexpr uint32_t kMatvecMaxK = 8192;
+hipError_t matvec(hipStream_t stream, const void* w, uint32_t wtype, uint64_t row_bytes, uint32_t rows, uint32_t k,
+                  const float* x, float* y);
+hipError_t head_argmax(hipStream_t stream, const void* w, uint32_t wtype, uint64_t row_bytes, uint32_t rows,
+                       uint32_t k, const float* x, float* y, uint64_t* partials, uint32_t* ids, uint64_t* rows_out,
+                       uint64_t embd, uint32_t embd_row_bytes, uint32_t slot);
+
 // embed.hip: y[t] = the row at rows[t] dequantized (wtype an AS_WTYPE_*, n whole blocks).
 hipError_t embed_rows(hipStream_t stream, const uint64_t* rows, uint32_t wtype, uint32_t n, float* y,
                       uint32_t n_tokens);

@@ -1,0 +1,247 @@
+// The output head's matvec, with the greedy draft step fused into it.
+//
+// matvec (crates/kernels/shaders/matvec.glsl, matvec_{type}.comp; dispatch Kernels::matvec):
+// y = W x for `rows` rows of k values of a weight type (quant.glsl's six), each output as the
+// reference computes it, bit for bit: lane l of a 32-lane row group sums the row's 32-value units
+// l, l + 32, ... in order from 0 (quant.glsl's lane_sum; each unit_dot adds its rounded products in
+// order), and the 32 partials meet in the tree p[i] += p[i + s] for s = 16, 8, 4, 2, 1
+// (tree32.glsl; twin/mod.rs:15-25). The library is built without contraction, so every product is
+// rounded before its add, as the reference's `precise` arithmetic is.
+//
+// On CDNA4 a wave of 64 lanes holds two row groups (a 32-lane xor shuffle stays inside its half),
+// so a 256-thread workgroup computes 8 rows at a time and walks row groups grid-stride. x is staged
+// once per workgroup in LDS, unit u at xs[33 u ..] (the pad of one float puts the 32 lanes' reads of
+// 32 different units in 32 different banks). Weights are read once, straight from HBM: 2-byte loads
+// for the quantized types (Q8_0 and Q6_K blocks, 34 and 210 bytes, are only 2-byte aligned), 4-byte
+// loads for F32 and BF16.
+//
+// head_argmax: the same rows with argmax_rows' epilogue (crates/kernels/shaders/argmax_rows.comp):
+// the largest finite output, ties to the lower index (-0 and +0 tie), computed as the outputs are
+// produced: each workgroup keeps its best as one u64 key, and a one-workgroup kernel takes the
+// largest key and writes ids[slot] and rows_out[slot] = embd + id * row_bytes (AS_NO_DRAFT and row
+// 0's address when no output is finite). The logits need not be written or read again.
+#include "sampler_device.h"
+#include "launch.h"
+#include "../../include/artemis_sampler.h"
+
+using namespace as_dev;
+
+namespace {
+
+constexpr uint32_t kThreads = 256;
+constexpr uint32_t kRowsPerGroup = kThreads / 32;  // 8 rows of 32 lanes
+constexpr uint32_t kFinalThreads = 1024;
+
+__device__ __forceinline__ float half_u16(uint32_t h) { return (float)__builtin_bit_cast(_Float16, (uint16_t)h); }
+__device__ __forceinline__ uint32_t byte_of(const uint32_t (&h)[16], uint32_t l) {
+  return (h[l >> 1] >> (8 * (l & 1))) & 0xFFu;
+}
+
+// quant.glsl unit_dot (twin/matvec.rs:21-84) for unit u of the row; x: the unit's 32 inputs in LDS.
+template <uint32_t kType>
+__device__ __forceinline__ float unit_dot(const uint8_t* __restrict__ row, uint32_t u, const float* x) {
+  if constexpr (kType == AS_WTYPE_F32) {
+    const uint32_t* w = reinterpret_cast<const uint32_t*>(row + 128u * u);
+    uint32_t wv[32];
+#pragma unroll
+    for (int i = 0; i < 32; ++i) wv[i] = w[i];
+    float s = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 32; ++i) s = s + __uint_as_float(wv[i]) * x[i];
+    return s;
+  } else if constexpr (kType == AS_WTYPE_BF16) {
+    const uint32_t* w = reinterpret_cast<const uint32_t*>(row + 64u * u);
+    uint32_t wv[16];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) wv[i] = w[i];
+    float s = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      s = s + __uint_as_float(wv[i] << 16) * x[2 * i];
+      s = s + __uint_as_float(wv[i] & 0xFFFF0000u) * x[2 * i + 1];
+    }
+    return s;
+  } else if constexpr (kType == AS_WTYPE_Q8_0) {
+    const uint16_t* b = reinterpret_cast<const uint16_t*>(row + 34u * u);
+    uint32_t q[16];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) q[i] = b[1 + i];
+    const float d = half_u16(b[0]);
+    float s = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 32; ++i) s = s + (float)(int8_t)byte_of(q, i) * x[i];
+    return d * s;
+  } else if constexpr (kType == AS_WTYPE_Q4_K || kType == AS_WTYPE_Q5_K) {
+    constexpr bool kQ5 = kType == AS_WTYPE_Q5_K;
+    const uint8_t* blk = row + (kQ5 ? 176u : 144u) * (u / 8);
+    const uint16_t* b = reinterpret_cast<const uint16_t*>(blk);
+    const uint32_t j = u % 8, c = j / 2, sh = 4 * (j % 2);
+    uint32_t hd[8], qs[16], qh[16];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) hd[i] = b[i];  // d, dmin, 12 bytes of scales and mins
+#pragma unroll
+    for (int i = 0; i < 16; ++i) qs[i] = b[(kQ5 ? 24 : 8) + 16 * c + i];
+    if constexpr (kQ5) {
+#pragma unroll
+      for (int i = 0; i < 16; ++i) qh[i] = b[8 + i];
+    }
+    // ggml's get_scale_min_k4 over the 12 bytes at offset 4 (quant.glsl scale_min_k4).
+    auto sb = [&](uint32_t i) { return (hd[2 + (i >> 1)] >> (8 * (i & 1))) & 0xFFu; };
+    uint32_t sc, mn;
+    if (j < 4) {
+      sc = sb(j) & 63u;
+      mn = sb(j + 4) & 63u;
+    } else {
+      sc = (sb(j + 4) & 0xFu) | ((sb(j - 4) >> 6) << 4);
+      mn = (sb(j + 4) >> 4) | ((sb(j) >> 6) << 4);
+    }
+    float sq = 0.0f, sx = 0.0f;
+#pragma unroll
+    for (int l = 0; l < 32; ++l) {
+      uint32_t q = (byte_of(qs, l) >> sh) & 0xFu;
+      if (kQ5 && ((byte_of(qh, l) >> j) & 1u)) q += 16u;
+      sq = sq + (float)q * x[l];
+      sx = sx + x[l];
+    }
+    const float a = (half_u16(hd[0]) * (float)sc) * sq;
+    const float m = (half_u16(hd[1]) * (float)mn) * sx;
+    return a - m;
+  } else {
+    // Q6_K: unit j of a block is half n = j / 4, quarter m = j % 4.
+    const uint16_t* b = reinterpret_cast<const uint16_t*>(row + 210u * (u / 8));
+    const uint32_t j = u % 8, n = j / 4, m = j % 4;
+    uint32_t ql[16], qh[16];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) ql[i] = b[32 * n + 16 * (m & 1) + i];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) qh[i] = b[64 + 16 * n + i];
+    const uint32_t scs = b[96 + 4 * n + m], dh = b[104];
+    const uint32_t shl = 4 * (m >> 1), shh = 2 * m;
+    float sa = 0.0f, sbs = 0.0f;
+#pragma unroll
+    for (int l = 0; l < 32; ++l) {
+      const uint32_t v6 = ((byte_of(ql, l) >> shl) & 0xFu) | (((byte_of(qh, l) >> shh) & 3u) << 4);
+      const float prod = (float)((int)v6 - 32) * x[l];
+      if (l < 16) sa = sa + prod;
+      else sbs = sbs + prod;
+    }
+    const float sca = (float)(int8_t)(scs & 0xFFu), scb = (float)(int8_t)(scs >> 8);
+    const float pa = sca * sa, pb = scb * sbs;
+    return half_u16(dh) * (pa + pb);
+  }
+}
+
+// argmax_rows' order as one u64: finite values by value (-0 as +0), then the lower index; 0 for a
+// non-finite value (below every finite key).
+__device__ __forceinline__ uint64_t draft_key(float v, uint32_t i) {
+  return is_finite_bits(v) ? pack(total_key(v == 0.0f ? 0.0f : v), i) : 0ull;
+}
+
+template <uint32_t kType, bool kArgmax>
+__global__ __launch_bounds__(kThreads) void matvec_kernel(const uint8_t* __restrict__ w, uint64_t row_bytes,
+                                                          uint32_t rows, uint32_t k, const float* __restrict__ x,
+                                                          float* __restrict__ y, uint64_t* __restrict__ partials) {
+  extern __shared__ float xs[];  // k / 32 units of 33 floats
+  __shared__ uint64_t red[kThreads / kWave];
+  const uint32_t tid = threadIdx.x, units = k / 32;
+  for (uint32_t i = tid; i < k; i += kThreads) xs[(i / 32) * 33 + (i % 32)] = x[i];
+  __syncthreads();
+  const uint32_t lane = tid & 31, slot = tid / 32;
+  const uint32_t n_groups = (rows + kRowsPerGroup - 1) / kRowsPerGroup;
+  uint64_t best = 0;
+  for (uint32_t g = blockIdx.x; g < n_groups; g += gridDim.x) {
+    const uint32_t row = g * kRowsPerGroup + slot;
+    float acc = 0.0f;
+    if (row < rows) {
+      const uint8_t* wr = w + (uint64_t)row * row_bytes;
+      for (uint32_t u = lane; u < units; u += 32) acc = acc + unit_dot<kType>(wr, u, xs + u * 33);
+    }
+    // tree32.glsl: lanes past a short row's units hold +0.0.
+    acc = acc + __shfl_xor(acc, 16, 32);
+    acc = acc + __shfl_xor(acc, 8, 32);
+    acc = acc + __shfl_xor(acc, 4, 32);
+    acc = acc + __shfl_xor(acc, 2, 32);
+    acc = acc + __shfl_xor(acc, 1, 32);
+    if (lane == 0 && row < rows) {
+      if (y) y[row] = acc;
+      if (kArgmax) best = max(best, draft_key(acc, row));
+    }
+  }
+  if constexpr (kArgmax) {
+    best = wave_max_u64(best);
+    if ((tid & (kWave - 1)) == 0) red[tid / kWave] = best;
+    __syncthreads();
+    if (tid == 0) {
+      for (uint32_t i = 1; i < kThreads / kWave; ++i) best = max(best, red[i]);
+      partials[blockIdx.x] = best;
+    }
+  }
+}
+
+__global__ __launch_bounds__(kFinalThreads) void draft_final_kernel(const uint64_t* __restrict__ partials,
+                                                                    uint32_t n_partials, uint32_t* __restrict__ ids,
+                                                                    uint64_t* __restrict__ rows_out, uint64_t embd,
+                                                                    uint32_t row_bytes, uint32_t slot) {
+  __shared__ uint64_t red[kFinalThreads / kWave];
+  uint64_t best = 0;
+  for (uint32_t i = threadIdx.x; i < n_partials; i += kFinalThreads) best = max(best, partials[i]);
+  best = wave_max_u64(best);
+  if ((threadIdx.x & (kWave - 1)) == 0) red[threadIdx.x / kWave] = best;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    for (uint32_t i = 1; i < kFinalThreads / kWave; ++i) best = max(best, red[i]);
+    const uint32_t id = best ? packed_id(best) : AS_NO_DRAFT;
+    ids[slot] = id;
+    rows_out[slot] = embd + (uint64_t)(best ? id : 0u) * (uint64_t)row_bytes;
+  }
+}
+
+template <bool kArgmax>
+hipError_t launch(hipStream_t stream, const void* w, uint32_t wtype, uint64_t row_bytes, uint32_t rows, uint32_t k,
+                  const float* x, float* y, uint64_t* partials, uint32_t groups) {
+  const size_t lds = (size_t)(k / 32) * 33 * sizeof(float);
+  const uint8_t* wb = static_cast<const uint8_t*>(w);
+  const dim3 grid(groups), block(kThreads);
+  switch (wtype) {
+#define AS_MV(T)                                                                                                    \
+  case T:                                                                                                           \
+    hipLaunchKernelGGL((matvec_kernel<T, kArgmax>), grid, block, lds, stream, wb, row_bytes, rows, k, x, y, partials); \
+    break;
+    AS_MV(AS_WTYPE_F32)
+    AS_MV(AS_WTYPE_BF16)
+    AS_MV(AS_WTYPE_Q8_0)
+    AS_MV(AS_WTYPE_Q4_K)
+    AS_MV(AS_WTYPE_Q5_K)
+    AS_MV(AS_WTYPE_Q6_K)
+#undef AS_MV
+    default: return hipErrorInvalidValue;
+  }
+  return hipGetLastError();
+}
+
+}  // namespace
+
+namespace as_launch {
+
+uint32_t matvec_groups(uint32_t rows) {
+  const uint32_t n_groups = (rows + kRowsPerGroup - 1) / kRowsPerGroup;
+  return n_groups < kMatvecGroups ? n_groups : kMatvecGroups;
+}
+
+hipError_t matvec(hipStream_t stream, const void* w, uint32_t wtype, uint64_t row_bytes, uint32_t rows, uint32_t k,
+                  const float* x, float* y) {
+  return launch<false>(stream, w, wtype, row_bytes, rows, k, x, y, nullptr, matvec_groups(rows));
+}
+
+hipError_t head_argmax(hipStream_t stream, const void* w, uint32_t wtype, uint64_t row_bytes, uint32_t rows,
+                       uint32_t k, const float* x, float* y, uint64_t* partials, uint32_t* ids, uint64_t* rows_out,
+                       uint64_t embd, uint32_t embd_row_bytes, uint32_t slot) {
+  const uint32_t groups = matvec_groups(rows);
+  hipError_t e = launch<true>(stream, w, wtype, row_bytes, rows, k, x, y, partials, groups);
+  if (e != hipSuccess) return e;
+  hipLaunchKernelGGL(draft_final_kernel, dim3(1), dim3(kFinalThreads), 0, stream, partials, groups, ids, rows_out,
+                     embd, embd_row_bytes, slot);
+  return hipGetLastError();
+}
+
+}  // namespace as_launch

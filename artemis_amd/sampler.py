@@ -105,6 +105,8 @@ def lib() -> C.CDLL:
         L.as_row_bytes.argtypes = [u32, u64]
         L.as_row_bytes.restype = u64
         L.as_embed_rows.argtypes = [vp, vp, u32, u32, vp, u32]
+        L.as_matvec.argtypes = [vp, vp, u32, u32, u32, vp, vp]
+        L.as_head_argmax.argtypes = [vp, vp, u32, u32, u32, vp, vp, vp, vp, u64, u32, u32]
         L.as_debug_exp.argtypes = [vp, vp, vp, u32]
         L.as_debug_exp2f.argtypes = [vp, vp, vp, u32]
         L.as_logprobs.argtypes = [vp, vp, u64, u32, u32, vp, u32, vp, vp, vp, vp]
@@ -294,6 +296,35 @@ class Context:
         assert y.is_cuda and y.dtype == torch.float32 and y.is_contiguous() and y.numel() >= t * n
         self._ok(lib().as_embed_rows(self.h, rows.data_ptr(), wtype, n, y.data_ptr(), t))
         return y
+
+    def matvec(self, w: torch.Tensor, wtype: int, rows: int, k: int, x: torch.Tensor,
+               y: Optional[torch.Tensor] = None) -> torch.Tensor:
+        """matvec (dispatch.rs Kernels::matvec): y = W x, bit for bit the reference's. `w`: the rows'
+        bytes on the device (row r at r * row_bytes(wtype, k)); `x`: [k] f32; returns y ([rows] f32)."""
+        assert w.is_cuda and x.is_cuda and x.dtype == torch.float32 and x.is_contiguous() and x.numel() == k
+        assert w.numel() * w.element_size() >= rows * row_bytes(wtype, k)
+        if y is None:
+            y = torch.empty(rows, dtype=torch.float32, device=x.device)
+        assert y.is_cuda and y.dtype == torch.float32 and y.numel() >= rows
+        self._ok(lib().as_matvec(self.h, w.data_ptr(), wtype, rows, k, x.data_ptr(), y.data_ptr()))
+        return y
+
+    def head_argmax(self, w: torch.Tensor, wtype: int, rows: int, k: int, x: torch.Tensor, ids: torch.Tensor,
+                    rows_out: torch.Tensor, embd: int, embd_row_bytes: int, slot: int = 0,
+                    logits: Optional[torch.Tensor] = None) -> None:
+        """The head's matvec with argmax_rows fused: ids[slot] and rows_out[slot] as argmax_rows
+        (dispatch.rs:121-153) would write them from the head's logits; `logits` (optional) gets
+        the logits too."""
+        assert w.is_cuda and x.is_cuda and x.dtype == torch.float32 and x.is_contiguous() and x.numel() == k
+        assert w.numel() * w.element_size() >= rows * row_bytes(wtype, k)
+        assert ids.is_cuda and ids.dtype == torch.int32 and ids.numel() > slot
+        assert rows_out.is_cuda and rows_out.dtype == torch.int64 and rows_out.numel() > slot
+        lp = 0
+        if logits is not None:
+            assert logits.is_cuda and logits.dtype == torch.float32 and logits.numel() >= rows
+            lp = logits.data_ptr()
+        self._ok(lib().as_head_argmax(self.h, w.data_ptr(), wtype, rows, k, x.data_ptr(), lp, ids.data_ptr(),
+                                      rows_out.data_ptr(), embd, embd_row_bytes, slot))
 
     def logprobs(self, logits: torch.Tensor, tokens: torch.Tensor, top: int, row_stride: Optional[int] = None,
                  n_vocab: Optional[int] = None):

@@ -153,6 +153,24 @@ uint64_t as_row_bytes(uint32_t wtype, uint64_t n);
 int as_embed_rows(as_ctx* ctx, const uint64_t* rows, uint32_t wtype, uint32_t n, float* y,
                   uint32_t n_tokens);
 
+/* matvec (crates/kernels/src/dispatch.rs Kernels::matvec, shaders/matvec.glsl): y = W x for `rows`
+ * rows of k values of type wtype (row r at w + r * as_row_bytes(wtype, k)), each output bit for
+ * bit as the reference's kernel and its twin (crates/kernels/src/twin/matvec.rs:86-131) give it.
+ * k: a multiple of 32 and of the type's block, at most 8192. w: 4-byte aligned for F32 and BF16,
+ * 2-byte aligned for the quantized types; x: [k] f32, y: [rows] f32, device memory. */
+int as_matvec(as_ctx* ctx, const void* w, uint32_t wtype, uint32_t rows, uint32_t k, const float* x,
+              float* y);
+
+/* The output head with the greedy draft step fused (decode.rs:850 runs the head's matvec, then
+ * mtp.rs's argmax_rows reads its logits): as_matvec of the head into `logits` (may be null: the
+ * logits are then never written), and, as the outputs are produced, argmax_rows' result:
+ * ids[slot] = the largest finite output's row (ties to the lower row, -0 and +0 tied) or
+ * AS_NO_DRAFT, rows_out[slot] = embd + id * embd_row_bytes (id 0 for AS_NO_DRAFT), for embed_rows.
+ * Stream-ordered; calls on one context must not overlap (they share its scratch). */
+int as_head_argmax(as_ctx* ctx, const void* w, uint32_t wtype, uint32_t rows, uint32_t k,
+                   const float* x, float* logits, uint32_t* ids, uint64_t* rows_out, uint64_t embd,
+                   uint32_t embd_row_bytes, uint32_t slot);
+
 /* Log-probabilities of the model's own distribution (crates/engine/src/logprobs.rs:12-38), which the
  * generation loop asks for per sampled token when a request wants them (turn.rs:361-364): for each of
  * n_rows rows of raw logits (before penalties, temperature and filters; the rows must be finite),

@@ -1,16 +1,23 @@
-// CPU oracle for embedding-row dequantization: TEST INFRASTRUCTURE ONLY.
+// CPU oracle for weight rows: dequantization and the matvec twin. TEST INFRASTRUCTURE ONLY.
 //
 // A C++ restatement of crates/qwen36/src/quant.rs (WType::block / row_bytes at 60-74,
 // dequant_row at 77-104, q8_0_block 161-167, scale_min_k4 170-179, q4k_block 182-206,
 // q5k_block 209-228, q6k_block 231-252): ggml's block layouts for the six weight types the
 // reference accepts, dequantized in the same f32 operations and order (products rounded before
 // the subtraction; the build keeps every product unfused). Only tests/ load it, as the checker
-// for the GPU's embed_rows.
+// for the GPU's embed_rows, matvec and head_argmax.
+//
+// oc_matvec restates the twin of the matvec kernels (crates/kernels/src/twin/matvec.rs:21-131,
+// twin/mod.rs:15-25), which the reference's GPU matvec equals bit for bit
+// (crates/kernels/tests/gpu_kernels.rs:112-140).
 //
 // Pinned by (tests/test_oracle_quant.py): the reference's gguf-py rows of each type
 // (crates/qwen36/tests/fixtures, checked at the reference's own 1e-6 tolerance and counted bit
 // for bit), its hand-built blocks (quant.rs:266-409), numpy's own f16 conversion for every f16
-// bit pattern, and row_bytes' table (quant.rs:270-277).
+// bit pattern, and row_bytes' table (quant.rs:270-277). oc_matvec: integer-valued rows and inputs
+// whose every sum is exact (so any order gives the exact dot product, which numpy computes), the f64
+// dot product of the dequantized row within the f32 sums' error bound, and lane partials whose
+// tree order is visible in the result.
 #include "sampler_oracle.h"
 
 #include <cmath>
@@ -100,9 +107,112 @@ void q6k_block(const uint8_t* b, float* out) {
   }
 }
 
+// crates/kernels/src/twin/matvec.rs:21-84 (unit_dot): sum of w * x over 32-value unit u of a row,
+// in the twin's f32 operations (each product rounded, then added, in order from 0).
+float unit_dot(uint32_t t, const uint8_t* row, uint64_t u, const float* xs) {
+  const float* x = xs + 32 * u;
+  switch (t) {
+    case 0: {
+      const uint8_t* w = row + 128 * u;
+      float s = 0.0f;
+      for (int i = 0; i < 32; ++i) {
+        float v;
+        std::memcpy(&v, w + 4 * i, 4);
+        const float p = v * x[i];
+        s = s + p;
+      }
+      return s;
+    }
+    case 1: {
+      const uint8_t* w = row + 64 * u;
+      float s = 0.0f;
+      for (int i = 0; i < 32; ++i) {
+        const uint32_t bits = (uint32_t)(w[2 * i] | (w[2 * i + 1] << 8)) << 16;
+        float v;
+        std::memcpy(&v, &bits, 4);
+        const float p = v * x[i];
+        s = s + p;
+      }
+      return s;
+    }
+    case 2: {
+      const uint8_t* b = row + 34 * u;
+      float s = 0.0f;
+      for (int i = 0; i < 32; ++i) {
+        const float p = (float)(int8_t)b[2 + i] * x[i];
+        s = s + p;
+      }
+      return half_at(b, 0) * s;
+    }
+    case 3:
+    case 4: {
+      const bool q5 = t == 4;
+      const uint32_t bsz = q5 ? 176 : 144;
+      const uint8_t* b = row + bsz * (u / 8);
+      const uint32_t j = (uint32_t)(u % 8), c = j / 2, sh = 4 * (j % 2);
+      uint8_t sc, mn;
+      scale_min_k4(j, b + 4, &sc, &mn);
+      const uint8_t* qs = b + (q5 ? 48 : 16) + 32 * c;
+      float sq = 0.0f, sx = 0.0f;
+      for (int l = 0; l < 32; ++l) {
+        uint32_t q = (qs[l] >> sh) & 0xF;
+        if (q5 && ((b[16 + l] >> j) & 1)) q += 16;
+        const float p = (float)q * x[l];
+        sq = sq + p;
+        sx = sx + x[l];
+      }
+      const float a = (half_at(b, 0) * (float)sc) * sq;
+      const float m = (half_at(b, 2) * (float)mn) * sx;
+      return a - m;
+    }
+    default: {
+      const uint8_t* b = row + 210 * (u / 8);
+      const uint32_t j = (uint32_t)(u % 8), n = j / 4, m = j % 4;
+      const uint8_t *ql = b + 64 * n + 32 * (m & 1), *qh = b + 128 + 32 * n;
+      const uint32_t shl = 4 * (m >> 1), shh = 2 * m;
+      float sa = 0.0f, sb = 0.0f;
+      for (int l = 0; l < 32; ++l) {
+        const uint32_t lo = (ql[l] >> shl) & 0xF, hi = (qh[l] >> shh) & 3;
+        const float p = (float)((int)(lo | (hi << 4)) - 32) * x[l];
+        if (l < 16) sa = sa + p;
+        else sb = sb + p;
+      }
+      const float sca = (float)(int8_t)b[192 + 8 * n + 2 * m], scb = (float)(int8_t)b[192 + 8 * n + 2 * m + 1];
+      const float pa = sca * sa, pb = scb * sb;
+      return half_at(b, 208) * (pa + pb);
+    }
+  }
+}
+
+// twin/mod.rs:15-25 (tree): p[i] += p[i + s] for s = n/2, n/4, ..., 1; the result is p[0].
+float tree(float* p, int n) {
+  for (int s = n / 2; s > 0; s /= 2)
+    for (int i = 0; i < s; ++i) p[i] = p[i] + p[i + s];
+  return p[0];
+}
+
 }  // namespace
 
 extern "C" {
+
+// twin/matvec.rs:86-97 (row_dot) and 126-131 (matvec): lane l of 32 sums units l, l + 32, ... in
+// order from 0, then the 32 partials meet in the tree.
+int oc_matvec(uint32_t wtype, const uint8_t* w, uint64_t rows, uint64_t k, const float* x, float* y) {
+  const uint64_t rb = oc_row_bytes(wtype, k);
+  if (k % 32 != 0 || (rb == 0 && k != 0)) return 1;
+  const uint64_t units = k / 32;
+  for (uint64_t r = 0; r < rows; ++r) {
+    float p[32];
+    for (uint64_t lane = 0; lane < 32; ++lane) {
+      float s = 0.0f;
+      for (uint64_t u = lane; u < units; u += 32) s = s + unit_dot(wtype, w + r * rb, u, x);
+      p[lane] = s;
+    }
+    y[r] = tree(p, 32);
+  }
+  return 0;
+}
+
 
 uint64_t oc_row_bytes(uint32_t wtype, uint64_t n) {
   if (wtype > 5 || n % kPer[wtype] != 0) return 0;

@@ -118,6 +118,9 @@ void oc_sample_rows(const oc_params* params, const uint64_t* seeds, const float*
 uint64_t oc_row_bytes(uint32_t wtype, uint64_t n);
 int oc_dequant_row(uint32_t wtype, const uint8_t* row, uint64_t n, float* out);
 float oc_half_to_float(uint16_t h);
+// twin/matvec.rs:126-131: y = W x for `rows` rows of k values (k a multiple of 32, whole blocks),
+// each output as a 32-lane row of the reference's matvec kernel sums it. 1 for a bad shape.
+int oc_matvec(uint32_t wtype, const uint8_t* w, uint64_t rows, uint64_t k, const float* x, float* y);
 
 #ifdef __cplusplus
 }

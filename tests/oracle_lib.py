@@ -107,6 +107,8 @@ def lib():
         L.oc_dequant_row.restype = C.c_int
         L.oc_half_to_float.argtypes = [C.c_uint16]
         L.oc_half_to_float.restype = C.c_float
+        L.oc_matvec.argtypes = [C.c_uint32, C.c_void_p, C.c_uint64, C.c_uint64, f32p, f32p]
+        L.oc_matvec.restype = C.c_int
         _lib = L
     return _lib
 
@@ -309,3 +311,14 @@ def dequant_row(wtype: int, row, n: int):
     if rc != 0:
         raise ValueError("not a whole-block row")
     return out
+
+
+def matvec(wtype: int, w, rows: int, k: int, x):
+    """twin/matvec.rs:126-131: y = W x, each output as the reference's 32-lane matvec row sums it."""
+    raw = np.ascontiguousarray(np.frombuffer(bytes(w), dtype=np.uint8))
+    assert raw.size == rows * row_bytes(wtype, k)
+    xa, xp = _f32(x)
+    y = np.zeros(rows, np.float32)
+    if lib().oc_matvec(wtype, raw.ctypes.data, rows, k, xp, y.ctypes.data_as(f32p)) != 0:
+        raise ValueError("bad matvec shape")
+    return y

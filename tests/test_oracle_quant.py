@@ -164,3 +164,88 @@ def test_random_blocks_match_a_vectorised_decoding(name):
         got = O.dequant_row(O.WTYPES[name], t[r].tobytes(), n)
         want = _np_dequant(name, t[r].tobytes(), n)
         assert np.array_equal(got.view(np.uint32), want.view(np.uint32)), (name, r)
+
+
+# The matvec twin (oc_matvec, restating crates/kernels/src/twin/matvec.rs:21-131).
+
+def integer_table(rng, name, rows, k):
+    """Rows whose dequantized weights are small integers (scales 1, mins 0 or small), so that every
+    partial sum with integer inputs is exact in f32 whatever the order."""
+    t = random_table(rng, name, rows, k)
+    one = np.float16(1.0).tobytes()
+    if name == "F32":
+        t[:] = rng.integers(-8, 9, size=(rows, k)).astype("<f4").view(np.uint8).reshape(rows, -1)
+    elif name == "BF16":
+        v = rng.integers(-8, 9, size=(rows, k)).astype(np.float32).view(np.uint32) >> 16
+        t[:] = v.astype("<u2").view(np.uint8).reshape(rows, -1)
+    elif name == "Q8_0":
+        blk = t.reshape(rows, -1, 34)
+        blk[:, :, 0:2] = np.frombuffer(one, np.uint8)
+    elif name in ("Q4_K", "Q5_K"):
+        blk = t.reshape(rows, -1, 144 if name == "Q4_K" else 176)
+        blk[:, :, 0:2] = np.frombuffer(one, np.uint8)
+        blk[:, :, 2:4] = np.frombuffer(one, np.uint8)
+        blk[:, :, 4:16] &= 0x03  # scales and mins 0..3 (the high bits cleared)
+    else:
+        blk = t.reshape(rows, -1, 210)
+        blk[:, :, 208:210] = np.frombuffer(one, np.uint8)
+        blk[:, :, 192:208] = rng.integers(-3, 4, size=blk[:, :, 192:208].shape).astype(np.int8).view(np.uint8)
+    return t
+
+
+@pytest.mark.parametrize("name", list(FIXTURES))
+def test_matvec_is_the_exact_dot_product_on_integer_rows(name):
+    rng = np.random.default_rng(5)
+    rows, k = 6, 2048
+    code = O.WTYPES[name]
+    t = integer_table(rng, name, rows, k)
+    x = rng.integers(-4, 5, size=k).astype(np.float32)
+    y = O.matvec(code, t.tobytes(), rows, k, x)
+    for r in range(rows):
+        w = O.dequant_row(code, t[r].tobytes(), k).astype(np.float64)
+        assert np.all(w == np.round(w)), name
+        assert y[r] == float(np.dot(w, x.astype(np.float64))), (name, r)
+
+
+@pytest.mark.parametrize("name", list(FIXTURES))
+def test_matvec_within_the_f32_bound_of_the_f64_dot(name):
+    rng = np.random.default_rng(6)
+    rows, k = 8, 2048
+    code = O.WTYPES[name]
+    t = random_table(rng, name, rows, k)
+    x = rng.uniform(-1, 1, size=k).astype(np.float32)
+    y = O.matvec(code, t.tobytes(), rows, k, x)
+    for r in range(rows):
+        w = O.dequant_row(code, t[r].tobytes(), k).astype(np.float64)
+        exact = float(np.dot(w, x.astype(np.float64)))
+        # Each output is at most k additions and a few scalings deep; the dequantized weights of the
+        # quantized types differ from dequant_row's only by the order of the scale products.
+        bound = (k + 64) * 2.0 ** -24 * float(np.sum(np.abs(w * x))) + 1e-30
+        assert abs(float(y[r]) - exact) <= bound, (name, r, float(y[r]), exact, bound)
+
+
+def test_matvec_adds_the_lanes_in_the_twins_tree():
+    # F32 rows of k = 1024: lane l's partial is row[32 l] * x[32 l]. Partials 2^24 at lane 0 and 1 at
+    # lanes 1 and 17: the tree (twin/mod.rs:15-25) adds lane 17 into lane 1 first (2, exact), then
+    # 2^24 + 2; lanes added one by one would round 2^24 + 1 down twice, to 2^24.
+    k = 1024
+    w = np.zeros(k, np.float32)
+    w[0], w[32], w[32 * 17] = 2.0 ** 24, 1.0, 1.0
+    x = np.zeros(k, np.float32)
+    x[::32] = 1.0
+    y = O.matvec(O.WTYPES["F32"], w.tobytes(), 1, k, x)
+    p = (w * x).reshape(32, 32).sum(axis=1).astype(np.float32)
+    s = 16
+    while s:
+        p[:s] = (p[:s] + p[s:2 * s]).astype(np.float32)
+        s //= 2
+    assert p[0] == 2.0 ** 24 + 2 and y[0] == p[0]
+    seq = np.float32(0)
+    for v in (w * x).reshape(32, 32).sum(axis=1).astype(np.float32):
+        seq = np.float32(seq + v)
+    assert seq != y[0]
+
+
+def test_matvec_refuses_partial_units():
+    with pytest.raises(ValueError):
+        O.matvec(O.WTYPES["F32"], bytes(4 * 40), 1, 40, np.zeros(40, np.float32))
