@@ -140,7 +140,7 @@ hipError_t accept(hipStream_t stream, const uint32_t* picks, const uint32_t* sta
 
 // matvec.hip: y = W x (the reference's matvec, bit for bit), and the same with argmax_rows fused
 // (partials: kMatvecGroups u64 of scratch). k at most kMatvecMaxK (x is staged in LDS).
-constexpr uint32_t kMatvecGroups = 2048;
+constexpr uint32_t kMatvecGroups = 4096;  // the most workgroups a launch uses
 constexpr uint32_t kMatvecMaxK = 8192;
 hipError_t matvec(hipStream_t stream, const void* w, uint32_t wtype, uint64_t row_bytes, uint32_t rows, uint32_t k,
                   const float* x, float* y);

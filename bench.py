@@ -167,6 +167,58 @@ def gpu_logprobs(reps=50):
                 batch1_us_median=round(float(np.median(times)) * 1e6, 2))
 
 
+def gpu_head(reps=30):
+    """The output head (248,320 Q6_K rows of 2,048, decode.rs:850) as as_matvec (logits written) and
+    as as_head_argmax (argmax_rows fused, no logits), then embed_rows of the draft: HIP events on the
+    library's stream; weights 417 MB (past the 256 MB Infinity Cache, so every call reads HBM)."""
+    import torch
+
+    from artemis_amd import Context, WTYPE, row_bytes
+
+    rows, k, q6 = 248_320, 2048, WTYPE["Q6_K"]
+    rb = row_bytes(q6, k)
+    dev = torch.device("cuda:0")
+    g = torch.Generator(device=dev)
+    g.manual_seed(5)
+    w = torch.randint(0, 256, (rows, rb), dtype=torch.uint8, device=dev, generator=g)
+    blocks = w.view(rows * (k // 256), 210)
+    blocks[:, 208] = 0x00  # every block's f16 d = 2^-8: finite outputs
+    blocks[:, 209] = 0x1C
+    x = (torch.rand(k, device=dev, generator=g) * 2 - 1).contiguous()
+    y = torch.empty(rows, dtype=torch.float32, device=dev)
+    ids = torch.zeros(1, dtype=torch.int32, device=dev)
+    addr = torch.zeros(1, dtype=torch.int64, device=dev)
+    emb = w  # the embedding table: the head's own rows (tied), so every draft id has its row
+    ctx = Context(max_rows=16, max_vocab=4096)
+    stream = torch.cuda.current_stream()
+
+    def timed(fn):
+        for _ in range(3):
+            fn()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        for _ in range(reps):
+            fn()
+        e1.record(stream)
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) / reps * 1e3
+
+    mv_us = timed(lambda: ctx.matvec(w, q6, rows, k, x, y))
+    ha_us = timed(lambda: ctx.head_argmax(w, q6, rows, k, x, ids, addr, emb.data_ptr(), rb))
+    def draft_step():
+        ctx.head_argmax(w, q6, rows, k, x, ids, addr, emb.data_ptr(), rb)
+        ctx.embed_rows(addr, q6, k)
+
+    chain_us = timed(draft_step)
+    ctx.close()
+    wbytes = rows * rb
+    return dict(weights_bytes=wbytes,
+                matvec_us=round(mv_us, 2), matvec_hbm_frac=round((wbytes + 4 * rows) / (mv_us * 1e-6) / (HBM_PEAK_GBS * 1e9), 4),
+                head_argmax_us=round(ha_us, 2), head_argmax_hbm_frac=round(wbytes / (ha_us * 1e-6) / (HBM_PEAK_GBS * 1e9), 4),
+                head_argmax_embed_us=round(chain_us, 2))
+
+
 def cpu_baseline(budget_s=12.0):
     """The CPU oracle (the C++ restatement of the reference sampler) on this host: one row per call
     on one core, over a bounded sample of configuration 5's rows; and the 256 rows over all cores."""
@@ -236,6 +288,8 @@ def main():
     b1 = gpu_batch1()
     log("bench: log-probabilities")
     lpb = gpu_logprobs()
+    log("bench: output head")
+    head = gpu_head()
     ms_per_step = g["wall"] / a.steps * 1e3
     rows_per_s = g["rows"] / (ms_per_step / 1e3)
     achieved = g["alg_bytes"] / (g["scan_ms"] / 1e3) / 1e9
@@ -279,6 +333,7 @@ def main():
         "exact_path_rows": g["exact_rows"],
         "batch1": b1,
         "logprobs_top20": lpb,
+        "head_q6k_248320x2048": head,
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,
                      "kernel": "scan_kernel", "bytes_per_launch": g["alg_bytes"]},
