@@ -6,9 +6,10 @@
 // Two kernels over the rows in HBM:
 //   - lp_part_kernel: one 256-thread workgroup per kLpPart values of a row. Its largest value m_p,
 //     S_p = sum of exp(x - m_p) in f64 (each term within kExpRel of the reference's exp, from a
-//     table-free polynomial: exp_neg), and its 20 best by the reference's order: each wave's 5th best
-//     lane maximum, the smallest of the four, is a threshold with at least 20 values of the part at
-//     or above it; the few values there go into LDS, where a rank count sorts them.
+//     table-free polynomial: exp_neg), and its 20 best by the reference's order: each wave's 5th
+//     largest lane maximum (by value), the smallest of the four, is a threshold with at least 20
+//     values of the part at or above it; the few values there go into LDS, where a rank count of
+//     their (value, id) keys sorts them.
 //   - lp_row_kernel: one workgroup per row. M = max m_p; total = sum of S_p * exp(m_p - M);
 //     lse = M + ln(total) (logprobs.rs:14-16); the parts' entries at or above the largest of the
 //     parts' nt-th entries hold the row's nt best, and a rank count orders them; each output is
@@ -43,12 +44,12 @@ static_assert(kPer % 4 == 0, "whole 16-byte groups per thread");
 // then the lower id.
 __device__ __forceinline__ uint64_t lp_key(float x, uint32_t id) { return pack(total_key(x == 0.0f ? 0.0f : x), id); }
 
-// The q-th largest of the lanes' keys (distinct; 0 for an empty lane), or 0 when fewer than q
-// lanes hold one.
-__device__ __forceinline__ uint64_t wave_qth_u64(uint64_t x, uint32_t q) {
-  uint64_t m = 0;
+// A key m such that at least q lanes hold a key at or above it (the q-th largest distinct key, or
+// lower when lanes tie), or 0 when fewer than q lanes hold one (0: an empty lane).
+__device__ __forceinline__ uint32_t wave_qth_u32(uint32_t x, uint32_t q) {
+  uint32_t m = 0;
   for (uint32_t it = 0; it < q; ++it) {
-    m = wave_max_u64(x);
+    m = wave_max_u32(x);
     if (m == 0) return 0;
     if (x == m) x = 0;
   }
@@ -104,9 +105,9 @@ static_assert(kLaneQ * kWaves >= kTop, "the waves' thresholds cover the part's b
 struct PartShared {
   uint64_t list[kList];
   uint32_t n_list;
+  uint32_t red_t[kWaves];
   uint32_t red_u[kWaves];
   double red_d[kWaves];
-  uint64_t red_k[kWaves];
 };
 
 // One part, b0 .. b1 of row x. kV4: the part is whole and 16-byte aligned, each thread's values in
@@ -130,21 +131,14 @@ __device__ __forceinline__ void lp_part(PartShared& sh, const float* __restrict_
     for (uint32_t q = 0; q < kPer; ++q) v[q] = valid(q) ? x[b0 + off(q)] : 0.0f;
   }
 
-  // The thread's best by the reference's order: its values come in index order, so the first of
-  // equal values holds the lower id. On finite values IEEE `>` is the key order with -0 and +0 tied.
-  // A thread holds values when its first one is in the part.
+  // The thread's largest value (rows are finite; -0 and +0 have one key). A thread holds values when
+  // its first one is in the part.
   float bv = v[0];
-  uint32_t bq = 0;
 #pragma unroll
-  for (uint32_t q = 1; q < kPer; ++q) {
-    if (valid(q) && v[q] > bv) {
-      bv = v[q];
-      bq = q;
-    }
-  }
+  for (uint32_t q = 1; q < kPer; ++q)
+    if (valid(q)) bv = fmaxf(bv, v[q]);
   const bool has = valid(0);
   const uint32_t bk = has ? lp_vkey(bv) : 0u;
-  const uint64_t best = has ? pack(bk, b0 + off(bq)) : 0ull;
 
   // The part's largest value (-0 and +0 alike: both give the same differences).
   const uint32_t kmax = block_max_u32<kWaves>(bk, sh.red_u);
@@ -159,24 +153,22 @@ __device__ __forceinline__ void lp_part(PartShared& sh, const float* __restrict_
   for (uint32_t q = 0; q < kPer; ++q)
     if (valid(q)) s += ep.exp_neg((double)v[q] - md);
 
-  // The threshold: the smallest of the waves' kLaneQ-th best lane maxima (0 when a wave holds fewer).
-  const uint64_t tw = wave_qth_u64(best, kLaneQ);
-  if (lane == 0) sh.red_k[w] = tw;
+  // The threshold: the smallest of the waves' kLaneQ-th largest lane maxima (0 when a wave holds
+  // fewer). Each wave has kLaneQ lanes whose maximum is at or above it, so at least kTop values of the
+  // part are, and every value among the part's kTop best is.
+  const uint32_t tw = wave_qth_u32(bk, kLaneQ);
+  if (lane == 0) sh.red_t[w] = tw;
   if (tid == 0) sh.n_list = 0;
-  s = block_sum_f64<kWaves>(s, sh.red_d);  // its barriers publish red_k and n_list
-  uint64_t T = sh.red_k[0];
-  for (int k = 1; k < kWaves; ++k) T = min(T, sh.red_k[k]);
-  // The threshold's value (minus infinity for T = 0): only values at or above it can pass.
-  const float t_val = T ? key_value((uint32_t)(T >> 32)) : -__builtin_inff();
-  // Every value at or above it, into the list.
+  s = block_sum_f64<kWaves>(s, sh.red_d);  // its barriers publish red_t and n_list
+  uint32_t T = sh.red_t[0];
+  for (int k = 1; k < kWaves; ++k) T = min(T, sh.red_t[k]);
+  // Every value at or above the threshold's value (all of them for T = 0), into the list.
+  const float t_val = T ? key_value(T) : -__builtin_inff();
 #pragma unroll
   for (uint32_t q = 0; q < kPer; ++q) {
     if (valid(q) && v[q] >= t_val) {
-      const uint64_t key = pack(lp_vkey(v[q]), b0 + off(q));
-      if (key >= T) {
-        const uint32_t i = atomicAdd(&sh.n_list, 1u);
-        if (i < kList) sh.list[i] = key;
-      }
+      const uint32_t i = atomicAdd(&sh.n_list, 1u);
+      if (i < kList) sh.list[i] = pack(lp_vkey(v[q]), b0 + off(q));
     }
   }
   __syncthreads();
