@@ -44,6 +44,7 @@ struct as_ctx {
   uint64_t* d_mv_partials = nullptr;  // head_argmax: each matvec workgroup's best key
   as_launch::RowOrder order{};  // the scan's row order for the current call
   std::vector<std::pair<double, uint32_t>> order_cost;  // its sort keys (kept: no allocation per call)
+  std::vector<RowParams> rows;  // the call's parameter blocks as built on the host (max_rows, kept)
   std::string err;
   // Profiling: events before the scan, between the kernels and after the finish, per call.
   bool profile = false;
@@ -230,6 +231,7 @@ int run_rows(as_ctx* c, const Plan& pl, const RowParams* rows, const float* logi
   a.scratch_stride = c->scratch_stride;
   a.done = c->h_done;
   a.call = ++c->calls;
+  a.max_history = c->max_history;
 
   if (c->share_dirty)
     return fail(c, AS_ERR_HIP, "an earlier call launched its scan but not its finish kernel: the context's "
@@ -265,7 +267,12 @@ int run_rows(as_ctx* c, const Plan& pl, const RowParams* rows, const float* logi
                             h, c->d_block, c->d_share, hist_off, hist_ids, extra_ids, c->d_stats, c->d_cands,
                             pl.stride, c->d_tail_list, c->order));
   if (e1) AS_HIP(c, hipEventRecord(e1, c->stream));
-  AS_HIP(c, as_launch::tail(c->stream, n_rows, n, a));
+  // The tail kernel serves only rows without a top-k that have min-p's floor (the scan flags no
+  // other row for it): a call with none skips its launch.
+  bool floor_rows = false;
+  for (uint32_t r = 0; r < n_rows && !floor_rows; ++r)
+    floor_rows = rows[r].mode == as_dev::kModePartial && rows[r].min_p > 0.0f;
+  if (floor_rows) AS_HIP(c, as_launch::tail(c->stream, n_rows, n, a));
   AS_HIP(c, as_launch::finish(c->stream, n_rows, c->d_args));
   c->share_dirty = false;
   if (e2) AS_HIP(c, hipEventRecord(e2, c->stream));
@@ -354,6 +361,7 @@ int as_create(int device, void* hip_stream, uint32_t max_rows, uint32_t max_voca
   c->max_history = max_history;
   c->max_seg = max_seg;
   c->order_cost.reserve(std::min(max_rows, as_launch::kOrderMax));
+  c->rows.resize(max_rows);
   // Per row: u32 counts [n], then (8-byte aligned) two u64 buffers [n] each for the deep and
   // exact-order paths; rounded to 4 words so every row's scratch starts 16-byte aligned.
   c->scratch_stride = (5ull * max_vocab + 2 + 3) & ~3ull;
@@ -422,7 +430,7 @@ int as_sample(as_ctx* c, const as_batch* b, const as_sampling* params) {
     c_max = std::max(c_max, wanted_cand(params[r], b->n_vocab));
   }
   const Plan pl = plan_slices(b->n_vocab, b->n_rows, c_max);
-  std::vector<RowParams> h(b->n_rows);
+  RowParams* h = c->rows.data();
   for (uint32_t r = 0; r < b->n_rows; ++r) {
     h[r] = make_row(params[r], b->n_vocab, pl);
     h[r].rng_index = r;
@@ -430,7 +438,7 @@ int as_sample(as_ctx* c, const as_batch* b, const as_sampling* params) {
     h[r].flags |= as_dev::kFlagRngWrite;
   }
   AS_HIP(c, hipSetDevice(c->device));
-  return run_rows(c, pl, h.data(), b->logits, b->row_stride, b->n_vocab, b->n_rows, b->hist_offsets,
+  return run_rows(c, pl, h, b->logits, b->row_stride, b->n_vocab, b->n_rows, b->hist_offsets,
                   b->hist_ids, nullptr, b->rng_state, b->tokens, b->status, b->kept_count,
                   b->kept_ids, b->kept_probs, b->kept_cap);
 }
@@ -446,13 +454,15 @@ int as_verify(as_ctx* c, const float* rows, uint64_t row_stride, uint32_t n_voca
     return fail(c, AS_ERR_INVALID, "as_verify: a list with a length has no pointer");
   if (n_vocab == 0 || row_stride < n_vocab)
     return fail(c, AS_ERR_INVALID, "as_verify: n_vocab must be at least 1 and at most row_stride");
-  if (k + 1 > c->max_rows || n_vocab > c->max_vocab)
+  if ((uint64_t)k + 1 > c->max_rows || n_vocab > c->max_vocab)
     return fail(c, AS_ERR_CAPACITY, "as_verify: more rows or a larger vocabulary than the context holds");
+  if ((uint64_t)hist_len + k > c->max_history)
+    return fail(c, AS_ERR_CAPACITY, "as_verify: the history and the drafts hold more ids than the context's max_history");
   char msg[160];
   if (as_check(params, msg, sizeof msg) != AS_OK) return fail(c, AS_ERR_PARAMS, msg);
   const Plan pl = plan_slices(n_vocab, k + 1, wanted_cand(*params, n_vocab));
   const bool draws = params->temp > 0.0f;
-  std::vector<RowParams> h(k + 1);
+  RowParams* h = c->rows.data();
   for (uint32_t i = 0; i <= k; ++i) {
     h[i] = make_row(*params, n_vocab, pl);
     h[i].rng_index = 0;
@@ -462,7 +472,7 @@ int as_verify(as_ctx* c, const float* rows, uint64_t row_stride, uint32_t n_voca
     h[i].extra = i;  // the drafts before row i were emitted when row i is sampled
   }
   AS_HIP(c, hipSetDevice(c->device));
-  int rc = run_rows(c, pl, h.data(), rows, row_stride, n_vocab, k + 1, nullptr, hist_len ? history : nullptr,
+  int rc = run_rows(c, pl, h, rows, row_stride, n_vocab, k + 1, nullptr, hist_len ? history : nullptr,
                     k ? drafts : nullptr, rng_state, picks, c->d_vstatus, nullptr, nullptr, nullptr, 0);
   if (rc != AS_OK) return rc;
   AS_HIP(c, as_launch::accept(c->stream, picks, c->d_vstatus, drafts, k, stop_ids, n_stop, rng_state,
@@ -597,6 +607,7 @@ int as_logprobs(as_ctx* c, const float* logits, uint64_t row_stride, uint32_t n_
   if (as_launch::lp_parts(n_vocab) * as_launch::kLpTop > as_launch::kLpMerge)
     return fail(c, AS_ERR_CAPACITY, "as_logprobs: vocabulary wider than the merge holds");
   const bool vec = aligned16(logits) && (row_stride % 4 == 0);
+  AS_HIP(c, hipSetDevice(c->device));
   AS_HIP(c, as_launch::logprobs(c->stream, vec, logits, row_stride, n_vocab, n_rows, c->d_lp, tokens, top, logprob,
                                 top_ids, top_logprobs, status));
   return AS_OK;

@@ -50,6 +50,7 @@ struct Shared {
   uint32_t red_u[kWaves];
   double red_d[kWaves];
   // Row scalars.
+  uint32_t hist_over;
   uint32_t bad, gi, mk, total, trunc, keep, pick, done, exact, prefix, stats_bad, nsk, tail_over, have_tail, tail_count,
       tail_listed, tail_parts;
   uint64_t bound_key;
@@ -1386,7 +1387,10 @@ __device__ __forceinline__ void finish_row(const FinishArgs& a) {
     sh.stats_bad = long_hist;
     sh.nsk = 0;
     sh.u01 = 0.0;
-    if (bad == kNone && p.mode != kModeGreedy) {
+    uint32_t hb = 0;
+    const uint32_t he = as_launch::history_bounds(a, p, row, &hb);
+    sh.hist_over = (he - hb > a.max_history) ? he - hb : 0u;
+    if (bad == kNone && p.mode != kModeGreedy && !sh.hist_over) {
       // One unit() per sampled row (sample.rs:189, 264, 276), after the row's skipped draws.
       uint64_t s4[4];
       uint64_t* src = a.rng_state + 4ull * p.rng_index;
@@ -1399,6 +1403,14 @@ __device__ __forceinline__ void finish_row(const FinishArgs& a) {
   }
   __syncthreads();
 
+  if (sh.hist_over) {
+    if (tid == 0) {
+      a.tokens[row] = kNone;
+      a.status[row] = AS_ROW_HISTORY;
+      if (a.kept_count) a.kept_count[row] = sh.hist_over;
+    }
+    return;
+  }
   if (sh.bad != kNone) {
     if (tid == 0) {
       a.tokens[row] = kNone;

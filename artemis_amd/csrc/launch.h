@@ -66,6 +66,7 @@ struct FinishArgs {
   as_dev::RowTail* tail;    // per row: the tail kernel's sums (min-p rows whose scan gave up)
   as_dev::TailBins* tail_bins;  // per row: the tail kernel's histogram of S
   as_dev::TailList* tail_list;  // the rows the scan flagged for the tail kernel
+  uint32_t max_history;     // a row with more history ids than this is refused (AS_ROW_HISTORY)
 };
 
 // The row's history ids are hist_ids[*hb, return value), from the CSR offsets or the row's range.

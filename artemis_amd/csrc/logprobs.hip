@@ -18,8 +18,9 @@
 // The reference sums exp(x - M) left to right over the row; this sum is parallel, with a bound on
 // the distance between the two: gamma(n + 64) relative (both orders' rounding and the rescale of
 // each part), kExpRel for the terms' exp, plus the logarithm's own ulp. An output is exact when that
-// bound cannot change its rounding to f32; otherwise the row's status says AS_LP_INEXACT and the
-// value is within one f32 ulp of the reference's.
+// bound cannot change its rounding to f32; otherwise the row's status says AS_LP_INEXACT, and the
+// value is within the bound plus one f32 ulp of the reference's, absolute (near lp = 0 that is many
+// ulps: the reference's left-to-right sum drops the terms under half an ulp of its running total).
 #include "sampler_device.h"
 #include "launch.h"
 #include "../../include/artemis_sampler.h"

@@ -21,6 +21,7 @@ LIB_PATH = os.path.join(HERE, "libartemis_sampler.so")
 AS_OK = 0
 AS_ROW_OK = 0
 AS_ROW_NONFINITE = 1
+AS_ROW_HISTORY = 2
 AS_ROW_EXACT_PATH = 0x100
 AS_ROW_KEPT_PARTIAL = 0x200
 AS_ROW_DEEP_PATH = 0x400

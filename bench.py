@@ -4,8 +4,10 @@ top-p + min-p chain) on one MI355X.
 
 A step is one as_sample call over the 256-row batch, inputs already in HBM. Three copies of the
 batch rotate between steps so no step finds its rows in the 256 MB Infinity Cache. The JSON line
-also carries batch-1 latency (configs 2 and 3, one row per call), the scan kernel's roofline from
-HIP events on the library's stream, and the CPU oracle timed on this host.
+also carries batch-1 latency (configs 1-4: greedy, stochastic, penalised, and as_verify over 6 rows),
+the roofline of the whole chain (every kernel of one as_sample call, HIP events on the library's
+stream) with the scan kernel's share beside it, and the CPU oracle timed on this host per
+configuration, with and without the reference's device-to-host copy of each row.
 
     python bench.py [--gpus 1] [--steps K] [--warmup W]
 """
@@ -22,7 +24,7 @@ sys.path.insert(0, ROOT)
 
 HBM_PEAK_GBS = 8000.0  # MI355X HBM3E, 8 TB/s
 CAL_FLOATS = 64 << 20  # the calibration copy: 256 MiB read, 256 MiB written
-TRAFFIC_FILE = os.path.join(ROOT, "profiles", "scan_kernel_config5_traffic.json")
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "sampler_chain_config5_traffic.json")
 
 
 def log(msg):
@@ -60,10 +62,11 @@ def gpu_config5(steps, warmup, copies=3):
     for i in range(warmup):
         ctx.sample_batch(sets[i % copies], packed, rng, d_off, d_ids, out=out)
     torch.cuda.synchronize()
-    # The exact-order path rate on this batch (informational).
+    # The rare paths' rates on this batch (informational).
     tok, st, *_ = ctx.sample_batch(sets[0], packed, rng, d_off, d_ids, out=out)
     status = st.cpu().numpy()
     exact_rows = int(((status & 0x100) != 0).sum())
+    deep_rows = int(((status & 0x400) != 0).sum())
 
     torch.cuda.synchronize()
     t0 = time.perf_counter()
@@ -76,19 +79,21 @@ def gpu_config5(steps, warmup, copies=3):
     ctx.profile(True)
     for i in range(steps):
         ctx.sample_batch(sets[i % copies], packed, rng, d_off, d_ids, out=out)
-    scan_ms, finish_ms, calls = ctx.profile_read()
+    scan_ms, rest_ms, calls = ctx.profile_read()
     ctx.profile(False)
     log(f"bench: {steps} steps in {wall * 1e3:.2f} ms; scan {scan_ms / calls * 1e3:.1f} us, "
-        f"finish {finish_ms / calls * 1e3:.1f} us per call; exact-path rows {exact_rows}")
+        f"after the scan {rest_ms / calls * 1e3:.1f} us per call; exact-path rows {exact_rows}, deep {deep_rows}")
     hist_bytes = 4 * len(ids)
     alg_bytes = 4 * rows * n + hist_bytes
     ctx.close()
-    return dict(rows=rows, n=n, wall=wall, scan_ms=scan_ms / calls, finish_ms=finish_ms / calls,
-                alg_bytes=alg_bytes, exact_rows=exact_rows, digest=w.digest(), history=len(ids) // rows)
+    return dict(rows=rows, n=n, wall=wall, scan_ms=scan_ms / calls, rest_ms=rest_ms / calls,
+                alg_bytes=alg_bytes, exact_rows=exact_rows, deep_rows=deep_rows, digest=w.digest(),
+                history=len(ids) // rows)
 
 
 def gpu_batch1(reps=200):
-    """One row per call, synchronised each time: µs per row at batch 1 (configs 2 and 3)."""
+    """One call per row (configs 1-3) or per verify step (config 4, 6 rows), synchronised each
+    time: wall µs per call (median and best) and the kernels' µs per call (HIP events)."""
     import torch
 
     from artemis_amd import Context, PackedSampling, Sampling, states_tensor, workloads
@@ -96,6 +101,7 @@ def gpu_batch1(reps=200):
     dev = torch.device("cuda:0")
     out = {}
     for name, w, s in [
+        ("config1", workloads.config1(), Sampling(0.0, 0, 1.0, 0.0)),
         ("config2", workloads.config2(draws=1), Sampling(0.6, 20, 0.95, 0.0)),
         ("config3", workloads.config3(draws=1), Sampling(0.7, 40, 0.9, 0.05, 0.5, 0.3, 1.05)),
     ]:
@@ -118,11 +124,41 @@ def gpu_batch1(reps=200):
         ctx.profile(True)
         for _ in range(reps):
             ctx.sample_batch(lg, packed, rng, d_off, d_ids, out=res)
-        scan_ms, finish_ms, calls = ctx.profile_read()
+        scan_ms, rest_ms, calls = ctx.profile_read()
         ctx.close()
         t = np.array(times) * 1e6
         out[name] = dict(us_per_row_median=round(float(np.median(t)), 2), us_per_row_best=round(float(t.min()), 2),
-                         kernel_us=round((scan_ms + finish_ms) / calls * 1e3, 2))
+                         kernel_us=round((scan_ms + rest_ms) / calls * 1e3, 2))
+    # Config 4: as_verify over k + 1 = 6 rows (5 drafts), T 0.6, top-p 0.95, the same stream state
+    # each call.
+    w = workloads.config4()
+    rows = torch.from_numpy(w.logits).to(dev)
+    drafts = torch.from_numpy(w.drafts.astype(np.int32)).to(dev)
+    ctx = Context(max_rows=8, max_vocab=rows.shape[1])
+    s = Sampling(0.6, 0, 0.95, 0.0)
+    st0 = states_tensor([1234], dev)
+    rng = st0.clone()
+    for _ in range(10):
+        rng.copy_(st0)
+        ctx.verify(rows, drafts, s, rng)
+    torch.cuda.synchronize()
+    times = []
+    for _ in range(reps):
+        rng.copy_(st0)
+        t0 = time.perf_counter()
+        _, result = ctx.verify(rows, drafts, s, rng)
+        res = result.cpu()
+        times.append(time.perf_counter() - t0)
+    ctx.profile(True)
+    for _ in range(reps):
+        rng.copy_(st0)
+        ctx.verify(rows, drafts, s, rng)
+    scan_ms, rest_ms, calls = ctx.profile_read()
+    ctx.close()
+    t = np.array(times) * 1e6
+    out["config4"] = dict(rows=int(rows.shape[0]), read=int(res[0]), accepted=int(res[1]),
+                          us_per_call_median=round(float(np.median(t)), 2), us_per_call_best=round(float(t.min()), 2),
+                          kernel_us=round((scan_ms + rest_ms) / calls * 1e3, 2))
     return out
 
 
@@ -206,6 +242,7 @@ def gpu_head(reps=30):
 
     mv_us = timed(lambda: ctx.matvec(w, q6, rows, k, x, y))
     ha_us = timed(lambda: ctx.head_argmax(w, q6, rows, k, x, ids, addr, emb.data_ptr(), rb))
+
     def draft_step():
         ctx.head_argmax(w, q6, rows, k, x, ids, addr, emb.data_ptr(), rb)
         ctx.embed_rows(addr, q6, k)
@@ -219,51 +256,84 @@ def gpu_head(reps=30):
                 head_argmax_embed_us=round(chain_us, 2))
 
 
-def cpu_baseline(budget_s=12.0):
-    """The CPU oracle (the C++ restatement of the reference sampler) on this host: one row per call
-    on one core, over a bounded sample of configuration 5's rows; and the 256 rows over all cores."""
+def cpu_baseline(reps=100):
+    """The CPU oracle (the C++ restatement of the reference sampler, -O3) on this host, per
+    configuration, one row (config 4: one verify step) per call on one core: the engine's per-row
+    work (the non-finite check and Sampler::sample; config 4 the verify loop) timed in C, median and
+    best of `reps` calls after a warm-up, alone and with the device-to-host copy of each row read
+    that the reference pays first (decode.rs:438, verify.rs:345), timed here from a GPU buffer into
+    pinned host memory. Config 5 cycles through its 256 rows. Also config 5's 256 rows over all
+    cores, one row per task."""
+    import torch
+
     sys.path.insert(0, os.path.join(ROOT, "tests"))
     import oracle_lib as O
 
     from artemis_amd import workloads
 
+    def settings(p):
+        return dict(temp=p.temp, top_k=p.top_k, top_p=p.top_p, min_p=p.min_p, presence=p.presence,
+                    frequency=p.frequency, repetition=p.repetition)
+
+    def stats(ns, copy_us):
+        c = np.array(ns) / 1e3
+        t = c + np.array(copy_us)
+        return dict(median_us=round(float(np.median(c)), 2), best_us=round(float(c.min()), 2),
+                    mean_us=round(float(c.mean()), 2),
+                    median_with_d2h_us=round(float(np.median(t)), 2), best_with_d2h_us=round(float(t.min()), 2))
+
+    dev = torch.device("cuda:0")
+    per = {}
+    for name, w in [("config1", workloads.config1()), ("config2", workloads.config2(draws=reps + 5)),
+                    ("config3", workloads.config3(draws=reps + 5)), ("config5", workloads.config5())]:
+        gpu_rows = torch.from_numpy(w.logits).to(dev)
+        host = torch.empty(w.logits.shape[1], dtype=torch.float32, pin_memory=True)
+        hview = host.numpy()
+        ns, copy = [], []
+        for i in range(reps + 5):
+            r = i % len(w.params)
+            smp = O.Sampler(w.seeds[r], **settings(w.params[r]))
+            if w.histories and len(w.histories[r]):
+                smp.add_history(w.histories[r])
+            torch.cuda.synchronize()
+            t0 = time.perf_counter()
+            host.copy_(gpu_rows[i % w.logits.shape[0]])
+            torch.cuda.synchronize()
+            cu = (time.perf_counter() - t0) * 1e6
+            _, t = smp.sample_timed(hview)
+            if i >= 5:
+                ns.append(t)
+                copy.append(cu)
+        per[name] = stats(ns, copy)
+        del gpu_rows
+    # Config 4: the verify loop over 6 rows (it stops at the first pick that differs from its draft).
+    w = workloads.config4()
+    gpu_rows = torch.from_numpy(w.logits).to(dev)
+    host = torch.empty(w.logits.shape, dtype=torch.float32, pin_memory=True)
+    ns, copy = [], []
+    picks = []
+    for i in range(reps + 2):
+        smp = O.Sampler(w.seeds[0], temp=0.6, top_k=0, top_p=0.95, min_p=0.0)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        host.copy_(gpu_rows)
+        torch.cuda.synchronize()
+        cu = (time.perf_counter() - t0) * 1e6
+        picks, t = smp.verify_timed(host.numpy(), list(w.drafts))
+        if i >= 2:
+            ns.append(t)
+            copy.append(cu)
+    per["config4"] = stats(ns, copy)
+    per["config4"]["rows_read"] = len(picks)
+    # Config 5's batch over all cores.
     w = workloads.config5()
-    params = [dict(temp=p.temp, top_k=p.top_k, top_p=p.top_p, min_p=p.min_p, presence=p.presence,
-                   frequency=p.frequency, repetition=p.repetition) for p in w.params]
     off, ids = w.hist_csr()
-    # One core: rows in order until the budget is spent (at least 32 rows).
-    done, t0 = 0, time.perf_counter()
-    chunk = 16
-    while done < w.logits.shape[0] and (time.perf_counter() - t0 < budget_s / 2 or done < 32):
-        sl = slice(done, done + chunk)
-        sub_off = off[done:done + chunk + 1] - off[done]
-        O.sample_rows(params[sl], w.seeds[sl], w.logits[sl], sub_off, ids[off[done]:off[min(done + chunk, len(params))]], threads=1)
-        done += chunk
-    one = time.perf_counter() - t0
+    params = [settings(p) for p in w.params]
     threads = min(os.cpu_count() or 1, 16)
     t1 = time.perf_counter()
     O.sample_rows(params, w.seeds, w.logits, off, ids, threads=threads)
     many = time.perf_counter() - t1
-    return dict(one_core_rows_per_s=done / one, rows_sampled=done, all_cores_rows_per_s=w.logits.shape[0] / many,
-                threads=threads)
-
-
-def d2h_row_us(reps=50):
-    """The reference copies each 993,280-byte row to the host before sampling (decode.rs:438)."""
-    import torch
-
-    from artemis_amd import workloads
-
-    x = torch.empty(workloads.VOCAB, dtype=torch.float32, device="cuda")
-    h = torch.empty(workloads.VOCAB, dtype=torch.float32, pin_memory=True)
-    for _ in range(5):
-        h.copy_(x)
-    torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    for _ in range(reps):
-        h.copy_(x)
-        torch.cuda.synchronize()
-    return (time.perf_counter() - t0) / reps * 1e6
+    return dict(per_config=per, all_cores_rows_per_s=w.logits.shape[0] / many, threads=threads)
 
 
 def main():
@@ -272,6 +342,7 @@ def main():
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--only-config5", action="store_true", help="only the config-5 steps (for profiling)")
     a = ap.parse_args()
     if a.gpus != 1:
         print(f"bench.py measures one GPU: the sampler's rows are independent and this build has no "
@@ -284,32 +355,36 @@ def main():
         sys.exit(2)
 
     g = gpu_config5(a.steps, a.warmup)
-    log("bench: batch-1 latency")
-    b1 = gpu_batch1()
-    log("bench: log-probabilities")
-    lpb = gpu_logprobs()
-    log("bench: output head")
-    head = gpu_head()
+    b1 = lpb = head = None
+    if not a.only_config5:
+        log("bench: batch-1 latency")
+        b1 = gpu_batch1()
+        log("bench: log-probabilities")
+        lpb = gpu_logprobs()
+        log("bench: output head")
+        head = gpu_head()
     ms_per_step = g["wall"] / a.steps * 1e3
     rows_per_s = g["rows"] / (ms_per_step / 1e3)
-    achieved = g["alg_bytes"] / (g["scan_ms"] / 1e3) / 1e9
+    chain_ms = g["scan_ms"] + g["rest_ms"]
+    achieved = g["alg_bytes"] / (chain_ms / 1e3) / 1e9
+    scan_achieved = g["alg_bytes"] / (g["scan_ms"] / 1e3) / 1e9
     traffic = None
     if os.path.exists(TRAFFIC_FILE):
-        # HBM bytes per scan launch from the committed rocprofv3 --pmc passes over this same command.
+        # HBM bytes per call of the chain from the committed rocprofv3 --pmc passes over this command.
         with open(TRAFFIC_FILE) as f:
-            traffic = json.load(f).get("scan_kernel_bytes_per_launch")
+            traffic = json.load(f).get("chain_bytes_per_call")
     cpu = None
-    if not a.no_cpu:
+    if not a.no_cpu and not a.only_config5:
         log("bench: CPU baseline")
         c = cpu_baseline()
-        d2h = d2h_row_us()
-        cpu = {"value": round(c["one_core_rows_per_s"], 2), "unit": "rows/s", "cores": 1, "kind": "port",
-               "sample": f"the oracle (C++ restatement of sample.rs, -O2) on the first {c['rows_sampled']} "
-                         f"config-5 rows, one fresh sampler and one draw per row, one core",
+        c5 = c["per_config"]["config5"]
+        cpu = {"value": round(1e6 / c5["mean_us"], 2), "unit": "rows/s", "cores": 1, "kind": "port",
+               "sample": "the oracle (C++ restatement of sample.rs, -O3): 100 config-5 rows in turn, one fresh "
+                         "sampler with the row's history and one draw each, the non-finite check and the "
+                         "sample timed, one core",
+               "per_config_us": c["per_config"],
                "all_cores": {"value": round(c["all_cores_rows_per_s"], 2), "cores": c["threads"],
-                             "sample": "all 256 config-5 rows, one row per task"},
-               "d2h_copy_us_per_row": round(d2h, 2),
-               "one_core_with_d2h_rows_per_s": round(1.0 / (1.0 / c["one_core_rows_per_s"] + d2h * 1e-6), 2)}
+                             "sample": "all 256 config-5 rows, one row per task"}}
     out = {
         "metric": "sampled rows/s (248,320-vocab f32, 256-row batch, full penalty+top-k+top-p+min-p chain)",
         "value": round(rows_per_s, 1),
@@ -329,14 +404,18 @@ def main():
                    "rows": g["rows"], "vocab": g["n"], "history": g["history"], "input_digest": g["digest"],
                    "parallelism": "single GPU"},
         "us_per_row": round(ms_per_step * 1e3 / g["rows"], 4),
-        "kernels_us": {"scan": round(g["scan_ms"] * 1e3, 2), "finish": round(g["finish_ms"] * 1e3, 2)},
+        "kernels_us": {"chain": round(chain_ms * 1e3, 2), "scan": round(g["scan_ms"] * 1e3, 2),
+                       "after_scan": round(g["rest_ms"] * 1e3, 2)},
         "exact_path_rows": g["exact_rows"],
+        "deep_path_rows": g["deep_rows"],
         "batch1": b1,
         "logprobs_top20": lpb,
         "head_q6k_248320x2048": head,
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,
-                     "kernel": "scan_kernel", "bytes_per_launch": g["alg_bytes"]},
+                     "kernel": "the as_sample chain: every kernel of one call (scan, tail, finish)",
+                     "bytes_per_launch": g["alg_bytes"],
+                     "scan_only": {"achieved": round(scan_achieved, 1), "frac": round(scan_achieved / HBM_PEAK_GBS, 4)}},
         "cpu_baseline": cpu,
     }
     print(json.dumps(out), flush=True)

@@ -6,8 +6,11 @@
  * the logits where the output head wrote them, in HBM.
  *
  * Conventions: device pointers are plain `void*`-compatible addresses on the context's device;
- * host pointers are marked `host`. Every launch is ordered on the context's stream and nothing
- * blocks the host except as_sync(). Calls return AS_OK or an AS_ERR_* code, and never throw;
+ * host pointers are marked `host`. Every launch is ordered on the context's stream. Nothing blocks
+ * the host except as_sync() and one bounded wait: as_sample and as_verify stage their rows'
+ * parameters in one of two pinned host blocks, so a call made while the call two before it has not
+ * started its kernels waits for it (a spin of at most 50 ms, then a wait for the stream).
+ * Calls return AS_OK or an AS_ERR_* code, and never throw;
  * as_last_error() gives a one-line message. A context is thread-compatible: one per engine thread
  * (the reference samples on its single worker thread, crates/engine/src/worker.rs:1-5).
  */
@@ -32,6 +35,9 @@ extern "C" {
 #define AS_ROW_NONFINITE 1u /* the row holds a NaN or an infinity: no token, the RNG is not advanced;
                                kept_count holds the first such index (Error::NonFinite,
                                crates/engine/src/decode.rs:439-444) */
+/* The row's history holds more ids than the context's max_history: no token, the RNG is not
+ * advanced; kept_count holds the row's history length. */
+#define AS_ROW_HISTORY 2u
 /* OR-ed into the status: the row was settled by the exact-order path (the reference's own
  * summation order), because a fast-path decision fell within its rounding bound or its cut lay
  * deeper than the fast path's candidates. Informational; the token is the same either way. */
@@ -73,7 +79,10 @@ typedef struct {
 typedef struct as_ctx as_ctx;
 
 /* Context: device ordinal, the HIP stream to order work on (NULL = the null stream), and the
- * largest batch, vocabulary and per-row history it must take. The context owns all scratch. */
+ * largest batch, vocabulary and per-row history it must take. The context owns all scratch.
+ * max_history: the most history ids one row may carry. as_verify refuses a longer history (with its
+ * drafts) with AS_ERR_CAPACITY; as_sample's offsets live on the device, so a longer row there is
+ * refused on the device with status AS_ROW_HISTORY. */
 int as_create(int device, void* hip_stream, uint32_t max_rows, uint32_t max_vocab,
               uint32_t max_history, as_ctx** out);
 int as_destroy(as_ctx* ctx);
@@ -178,9 +187,13 @@ int as_head_argmax(as_ctx* ctx, const void* w, uint32_t wtype, uint32_t rows, ui
  * clamped to 20 and to n_vocab; 0: none), sorted by logit descending, -0 and +0 tied, ties to the
  * lower id (logprobs.rs:40-48). tokens: device [n_rows]; out: logprob [n_rows], top_ids and
  * top_logprobs [n_rows][top] (the first min(top, 20, n_vocab) of each row written; may be NULL when
- * top is 0), status [n_rows] or NULL: AS_LP_OK, or AS_LP_INEXACT when the bound on the sum's distance
- * to the reference's left-to-right sum could move a value's rounding to f32 (the value is then within
- * one f32 ulp of the reference's), or a token is out of range (its logprob is NaN). */
+ * top is 0), status [n_rows] or NULL: AS_LP_OK (every value the reference's bits), or AS_LP_INEXACT
+ * when the bound e on the parallel sum's distance to the reference's left-to-right sum could move a
+ * value's rounding to f32, or a token is out of range (its logprob is NaN). The bound is absolute:
+ * |lse - lse_ref| <= e = gamma(n + 64) + 5e-13 + 2^-51 |ln total| + 2^-52 |lse| (gamma(m) =
+ * m 2^-53 / (1 - m 2^-53); about 2.8e-11 at the model's vocabulary), so an inexact value is within
+ * e + one f32 ulp of the reference's, and its exp within about e relative. Near lp = 0 (a
+ * near-certain token) that can be many f32 ulps. */
 #define AS_LP_OK 0u
 #define AS_LP_INEXACT 1u
 int as_logprobs(as_ctx* ctx, const float* logits, uint64_t row_stride, uint32_t n_vocab, uint32_t n_rows,

@@ -11,6 +11,7 @@
 #include <cmath>
 #include <cstdio>
 #include <cstring>
+#include <ctime>
 #include <map>
 #include <vector>
 
@@ -414,7 +415,22 @@ uint64_t oc_rng_below(uint64_t state[4], uint64_t n) { return rng_below(state, n
 uint32_t oc_greedy(const float* logits, size_t n) { return greedy(logits, n); }
 
 // sample.rs:22-34 (the block pass only decides whether the scan runs; the answer is the scan's).
+// sample.rs:22-34: a fold over 1,024-value blocks with no early exit inside a block (it
+// vectorizes), stopping at the first block that holds a non-finite value; only then the scan for it.
 int64_t oc_first_non_finite(const float* logits, size_t n) {
+  bool all_finite = true;
+  for (size_t b = 0; b < n && all_finite; b += 1024) {
+    const size_t e = std::min(n, b + 1024);
+    // is_finite as an exponent test on the bits, which the compiler vectorizes.
+    uint32_t ok = 1;
+    for (size_t i = b; i < e; ++i) {
+      uint32_t bits;
+      std::memcpy(&bits, logits + i, 4);
+      ok &= (uint32_t)((bits & 0x7F800000u) != 0x7F800000u);
+    }
+    all_finite = ok != 0;
+  }
+  if (all_finite) return -1;
   for (size_t i = 0; i < n; ++i)
     if (!std::isfinite(logits[i])) return (int64_t)i;
   return -1;
@@ -521,6 +537,39 @@ size_t oc_verify(oc_sampler* s, const float* rows, size_t n, const uint32_t* dra
   }
   *accepted = (uint32_t)(read - 1);
   return read;
+}
+
+// The CPU baseline's timers: the engine's per-row work, the non-finite check before the sampler
+// (decode.rs:437-447, sample.rs:22-34) and Sampler::sample (sample.rs:122-153), or the verify loop
+// over k+1 rows (spec/step.rs:340-385, each row checked first as verify.rs:345-348 does), timed on
+// the calling thread with CLOCK_MONOTONIC. The sampler (its RNG and history set) is built by the
+// caller beforehand, as the engine's Sampler already holds them. Returns nanoseconds.
+static double now_ns() {
+  timespec t;
+  clock_gettime(CLOCK_MONOTONIC, &t);
+  return (double)t.tv_sec * 1e9 + (double)t.tv_nsec;
+}
+
+double oc_sampler_sample_timed(oc_sampler* s, const float* logits, size_t n, uint32_t* token) {
+  const double t0 = now_ns();
+  const int64_t bad = oc_first_non_finite(logits, n);
+  *token = bad >= 0 ? 0xFFFFFFFFu : sample(*s, logits, n);
+  return now_ns() - t0;
+}
+
+double oc_verify_timed(oc_sampler* s, const float* rows, size_t n, const uint32_t* drafts, size_t k,
+                       uint32_t* picks, uint32_t* read) {
+  const double t0 = now_ns();
+  size_t r = 0;
+  for (size_t i = 0; i <= k; ++i) {
+    if (oc_first_non_finite(rows + i * n, n) >= 0) break;
+    const uint32_t y = sample(*s, rows + i * n, n);
+    picks[i] = y;
+    r = i + 1;
+    if (i < k && drafts[i] != y) break;
+  }
+  *read = (uint32_t)r;
+  return now_ns() - t0;
 }
 
 // logprobs.rs:12-48.

@@ -94,6 +94,11 @@ size_t oc_verify(oc_sampler* s, const float* rows, size_t n, const uint32_t* dra
                  uint32_t* stopped);
 
 // logprobs.rs:12-38: returns the token's log-probability; writes min(top, 20, n) (id, logprob).
+// The CPU baseline's timers (nanoseconds on the calling thread): the non-finite check and one
+// sample; or the verify loop over k+1 rows ([k+1][n]), each row checked first.
+double oc_sampler_sample_timed(oc_sampler* s, const float* logits, size_t n, uint32_t* token);
+double oc_verify_timed(oc_sampler* s, const float* rows, size_t n, const uint32_t* drafts, size_t k,
+                       uint32_t* picks, uint32_t* read);
 float oc_logprobs(const float* logits, size_t n, uint32_t token, uint32_t top, uint32_t* ids,
                   float* lps, size_t* n_top);
 

@@ -91,6 +91,10 @@ def lib():
         L.oc_verify.argtypes = [C.c_void_p, f32p, C.c_size_t, u32p, C.c_size_t, u32p, C.c_size_t,
                                 u32p, u32p, u32p]
         L.oc_verify.restype = C.c_size_t
+        L.oc_sampler_sample_timed.argtypes = [C.c_void_p, f32p, C.c_size_t, u32p]
+        L.oc_sampler_sample_timed.restype = C.c_double
+        L.oc_verify_timed.argtypes = [C.c_void_p, f32p, C.c_size_t, u32p, C.c_size_t, u32p, u32p]
+        L.oc_verify_timed.restype = C.c_double
         L.oc_logprobs.argtypes = [f32p, C.c_size_t, C.c_uint32, C.c_uint32, u32p, f32p,
                                   C.POINTER(C.c_size_t)]
         L.oc_logprobs.restype = C.c_float
@@ -195,6 +199,24 @@ class Sampler:
     def sample(self, logits) -> int:
         a, p = _f32(logits)
         return lib().oc_sampler_sample(self.h, p, len(a))
+
+    def sample_timed(self, logits):
+        """(token, ns): the non-finite check and one sample, timed in C."""
+        a, p = _f32(logits)
+        t = C.c_uint32()
+        ns = lib().oc_sampler_sample_timed(self.h, p, len(a), C.byref(t))
+        return t.value, ns
+
+    def verify_timed(self, rows, drafts):
+        """(picks, ns): the verify loop over k+1 rows, each checked first, timed in C."""
+        r = np.ascontiguousarray(rows, dtype=np.float32)
+        k = len(drafts)
+        d, dp = _u32(drafts if k else [0])
+        picks = np.zeros(k + 1, np.uint32)
+        read = C.c_uint32()
+        ns = lib().oc_verify_timed(self.h, r.ctypes.data_as(f32p), r.shape[1], dp, k,
+                                   picks.ctypes.data_as(u32p), C.byref(read))
+        return picks[: read.value].tolist(), ns
 
     def last_kept(self, cap=1 << 20):
         n = lib().oc_sampler_last_kept(self.h, None, None, 0)

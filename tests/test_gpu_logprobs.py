@@ -1,9 +1,11 @@
 """Log-probabilities on the GPU (crates/engine/src/logprobs.rs:12-38) against the oracle, which
 restates the same function (oracle/sampler_oracle.cc, oc_logprobs). Top ids must be bit-exact. Values
-must be bit-exact on rows whose status is AS_LP_OK; on a row marked AS_LP_INEXACT (the bound on the
+must be bit-exact on rows whose status is AS_LP_OK. On a row marked AS_LP_INEXACT (the bound on the
 parallel sum's distance to the reference's left-to-right sum could move a rounding to f32) each value
-must be within one f32 ulp of the oracle's (a log-probability error of at most 2^-23 relative, far
-inside the 1e-5 relative the probabilities must meet)."""
+must be within the library's absolute bound of the oracle's: |lp - lp_ref| <= e + one f32 ulp, with
+e = gamma(n + 64) + 5e-13 + 2^-51 |ln total| + 2^-52 |lse| (include/artemis_sampler.h), so exp(lp) is
+within about 3e-11 relative of the reference's probability, far inside the 1e-5 the probabilities
+must meet. Near-certain tokens (lp close to 0) are where that is many f32 ulps."""
 import numpy as np
 import pytest
 
@@ -37,11 +39,23 @@ def run(ctx, rows, tokens, top, row_stride=None, n_vocab=None):
     return lp.cpu().numpy(), ids.cpu().numpy(), lps.cpu().numpy(), st.cpu().numpy()
 
 
-def same_or_one_ulp(got, want, exact):
+U = 2.0 ** -53
+
+
+def lse_bound(row, lse):
+    """The library's bound e on |lse - lse_ref| for a row (include/artemis_sampler.h)."""
+    n = len(row)
+    g = (n + 64) * U / (1 - (n + 64) * U)
+    ln_total = lse - float(np.max(row))
+    return g + 5e-13 + 4 * U * abs(ln_total) + 2 * U * abs(lse)
+
+
+def same_or_within(got, want, exact, e):
     got, want = np.float32(got), np.float32(want)
     if exact:
         return got.tobytes() == want.tobytes()
-    return abs(float(got) - float(want)) <= float(np.spacing(np.abs(want)))
+    slack = e + 4 * U * abs(float(want)) + float(np.spacing(np.abs(want)))
+    return abs(float(got) - float(want)) <= slack
 
 
 def check(ctx, rows, tokens, top, label=""):
@@ -53,12 +67,13 @@ def check(ctx, rows, tokens, top, label=""):
         want_lp, want_top = O.logprobs(rows[r], int(tokens[r]), top)
         exact = st[r] & AS_LP_INEXACT == 0
         inexact += 0 if exact else 1
-        assert same_or_one_ulp(lp[r], want_lp, exact), (label, r, lp[r], want_lp, st[r])
+        e = lse_bound(rows[r], float(rows[r][int(tokens[r])]) - float(want_lp))
+        assert same_or_within(lp[r], want_lp, exact, e), (label, r, lp[r], want_lp, st[r])
         n = len(want_top)
         assert n == min(top, 20, rows.shape[1])
         assert ids[r][:n].tolist() == [i for i, _ in want_top], (label, r, ids[r][:n].tolist(), want_top)
         for j in range(n):
-            assert same_or_one_ulp(lps[r][j], want_top[j][1], exact), (label, r, j, lps[r][j], want_top[j])
+            assert same_or_within(lps[r][j], want_top[j][1], exact, e), (label, r, j, lps[r][j], want_top[j])
     return lp, ids, lps, st, inexact
 
 
@@ -143,8 +158,24 @@ def test_strided_and_shared_rows(ctx):
     for r in range(2):
         want_lp, want_top = O.logprobs(buf[r, :n], [4, 9][r], 20)
         assert ids[r][:20].tolist() == [i for i, _ in want_top]
-        assert same_or_one_ulp(lp[r], want_lp, st[r] == 0)
+        e = lse_bound(buf[r, :n], float(buf[r, [4, 9][r]]) - float(want_lp))
+        assert same_or_within(lp[r], want_lp, st[r] == 0, e)
     lp, ids, lps, st = run(ctx, buf[0], [1, 2, 3], 20, row_stride=0, n_vocab=n)
     want_top = O.logprobs(buf[0, :n], 1, 20)[1]
     for r in range(3):
         assert ids[r][:20].tolist() == [i for i, _ in want_top]
+
+
+def test_near_certain_tokens_at_the_models_width(ctx):
+    # One logit 30-40 above an N(0, 3) row: the reference's left-to-right sum loses every term under
+    # half an ulp of 1.0 that comes after the peak, the parallel sum keeps them; the values differ by
+    # many f32 ulps near lp = 0 and stay within the absolute bound.
+    gen = np.random.default_rng(31)
+    rows = (gen.standard_normal((6, VOCAB)) * 3.0).astype(np.float32)
+    peaks = [0, 1000, 124_160, 200_000, VOCAB - 2, 77]
+    for r, (p, lift) in enumerate(zip(peaks, [30.0, 32.0, 34.0, 36.0, 38.0, 40.0])):
+        rows[r, p] = np.float32(rows[r].max() + lift)
+    tokens = np.array(peaks, np.int32)
+    lp, ids, lps, st, inexact = check(ctx, rows, tokens, 20, "peaked")
+    assert (ids[:, 0] == np.array(peaks)).all()
+    assert (lp <= 0).all() and (lp > -1e-6).all()
