@@ -21,6 +21,9 @@
 // bound cannot change its rounding to f32; otherwise the row's status says AS_LP_INEXACT, and the
 // value is within the bound plus one f32 ulp of the reference's, absolute (near lp = 0 that is many
 // ulps: the reference's left-to-right sum drops the terms under half an ulp of its running total).
+#include <cstdio>
+#include <mutex>
+
 #include "sampler_device.h"
 #include "launch.h"
 #include "../../include/artemis_sampler.h"
@@ -350,3 +353,81 @@ hipError_t logprobs(hipStream_t stream, bool vec, const float* logits, uint64_t 
 }
 
 }  // namespace as_launch
+
+// ---- as_logprobs_static: the same two kernels with no allocation ---------------------------------
+//
+// The parts' results live in `scratch`, a file-scope device array each GPU holds once, for the life
+// of the process. On the host the array's name is only a stand-in for the device symbol: its device
+// address comes from hipGetSymbolAddress, once per device, and only that address is ever handed to a
+// kernel. Every call on a GPU shares the array, so calls that overlap on one GPU race; each call's
+// part kernel writes every field its row kernel reads, so nothing needs clearing between calls.
+
+namespace {
+
+constexpr uint32_t kStaticParts = 2048;  // 66 rows of the model's 248,320 values (31 parts each)
+static __device__ __align__(256) as_launch::LpPart scratch[kStaticParts];
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+as_launch::LpPart* g_scratch[kMaxDevices] = {};
+
+// The device address of `scratch` on the current device (looked up on a device's first call).
+hipError_t static_scratch(int dev, as_launch::LpPart** out) {
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch[dev]) {
+    void* p = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess) return e;
+    if (!p) return hipErrorInvalidSymbol;
+    g_scratch[dev] = static_cast<as_launch::LpPart*>(p);
+  }
+  *out = g_scratch[dev];
+  return hipSuccess;
+}
+
+int static_fail(char* err, size_t cap, int code, const char* msg) {
+  if (err && cap) std::snprintf(err, cap, "%s", msg);
+  return code;
+}
+
+}  // namespace
+
+extern "C" int as_logprobs_static(void* hip_stream, const float* logits, uint64_t row_stride, uint32_t n_vocab,
+                                  uint32_t n_rows, const uint32_t* tokens, uint32_t top, float* logprob,
+                                  uint32_t* top_ids, float* top_logprobs, uint32_t* status, char* err,
+                                  size_t err_cap) {
+  if (err && err_cap) err[0] = 0;
+  if (!logits || !tokens || !logprob || n_vocab == 0 || n_rows == 0)
+    return static_fail(err, err_cap, AS_ERR_INVALID, "as_logprobs_static: null array or zero size");
+  if (top > 0 && (!top_ids || !top_logprobs))
+    return static_fail(err, err_cap, AS_ERR_INVALID, "as_logprobs_static: top > 0 needs top_ids and top_logprobs");
+  if (row_stride != 0 && row_stride < n_vocab)
+    return static_fail(err, err_cap, AS_ERR_INVALID, "as_logprobs_static: row_stride below n_vocab");
+  const uint32_t parts = as_launch::lp_parts(n_vocab);
+  if (parts * as_launch::kLpTop > as_launch::kLpMerge)
+    return static_fail(err, err_cap, AS_ERR_CAPACITY, "as_logprobs_static: vocabulary wider than the merge holds");
+  if ((uint64_t)n_rows * parts > kStaticParts) {
+    char msg[200];
+    std::snprintf(msg, sizeof msg,
+                  "as_logprobs_static: %u rows of %u values need %llu parts; the static scratch holds %u "
+                  "(n_rows x ceil(n_vocab / %u) <= %u)",
+                  n_rows, n_vocab, (unsigned long long)n_rows * parts, kStaticParts, as_launch::kLpPart, kStaticParts);
+    return static_fail(err, err_cap, AS_ERR_CAPACITY, msg);
+  }
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e == hipSuccess && (dev < 0 || dev >= kMaxDevices)) e = hipErrorInvalidDevice;
+  as_launch::LpPart* parts_buf = nullptr;
+  if (e == hipSuccess) e = static_scratch(dev, &parts_buf);
+  if (e == hipSuccess) {
+    const bool vec = ((uintptr_t)logits & 15u) == 0 && row_stride % 4 == 0;
+    e = as_launch::logprobs((hipStream_t)hip_stream, vec, logits, row_stride, n_vocab, n_rows, parts_buf, tokens,
+                            top, logprob, top_ids, top_logprobs, status);
+  }
+  if (e != hipSuccess) {
+    char msg[200];
+    std::snprintf(msg, sizeof msg, "as_logprobs_static: %s", hipGetErrorString(e));
+    return static_fail(err, err_cap, AS_ERR_HIP, msg);
+  }
+  return AS_OK;
+}

@@ -111,6 +111,7 @@ def lib() -> C.CDLL:
         L.as_debug_exp.argtypes = [vp, vp, vp, u32]
         L.as_debug_exp2f.argtypes = [vp, vp, vp, u32]
         L.as_logprobs.argtypes = [vp, vp, u64, u32, u32, vp, u32, vp, vp, vp, vp]
+        L.as_logprobs_static.argtypes = [vp, vp, u64, u32, u32, vp, u32, vp, vp, vp, vp, C.c_char_p, C.c_size_t]
         L.as_profile.argtypes = [vp, C.c_int]
         L.as_profile_read.argtypes = [vp, C.POINTER(C.c_double), C.POINTER(C.c_double), C.POINTER(u32)]
         _lib = L

@@ -199,6 +199,20 @@ int as_head_argmax(as_ctx* ctx, const void* w, uint32_t wtype, uint32_t rows, ui
 int as_logprobs(as_ctx* ctx, const float* logits, uint64_t row_stride, uint32_t n_vocab, uint32_t n_rows,
                 const uint32_t* tokens, uint32_t top, float* logprob, uint32_t* top_ids, float* top_logprobs,
                 uint32_t* status);
+/* as_logprobs with no allocation and no context. No counterpart in the reference: it is for
+ * callers that cannot allocate device memory (code under HIP graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc). It runs as_logprobs' kernels, with the same arguments and
+ * results, on hip_stream (NULL = the null stream) on the current device. Their scratch is a static
+ * device array each GPU holds for the life of the process (2,048 parts of 8,192 values, 368 KiB):
+ * n_rows x ceil(n_vocab / 8192) must be at most 2,048 (66 rows at 248,320), else AS_ERR_CAPACITY.
+ * Every call on one GPU shares that array: calls that overlap on one GPU (other streams, other host
+ * threads) race and must be ordered by the caller. Nothing is allocated and nothing is freed; the
+ * device's first call looks the array's address up. err (host, may be NULL) gets a one-line message
+ * on failure. */
+int as_logprobs_static(void* hip_stream, const float* logits, uint64_t row_stride, uint32_t n_vocab,
+                       uint32_t n_rows, const uint32_t* tokens, uint32_t top, float* logprob,
+                       uint32_t* top_ids, float* top_logprobs, uint32_t* status, char* err,
+                       size_t err_cap);
 /* Profiling: while enabled, each as_sample / as_verify records HIP events on the context's stream
  * around its scan and finish kernels (no counterpart in the reference, which samples on the CPU;
  * for benchmarks). as_profile_read waits for the stream and returns the summed kernel times of the
