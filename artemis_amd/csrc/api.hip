@@ -35,6 +35,8 @@ struct as_ctx {
   as_dev::TailBins* d_tail_bins = nullptr;
   as_dev::TailList* d_tail_list = nullptr;
   bool share_dirty = false;  // a scan ran without its finish (a failed launch): the context is unusable
+  int force_path = 0;        // as_debug_path: 0 automatic, 1 the sliced scan, 2 the row kernel
+  uint32_t* d_fused_count = nullptr;  // the row kernel's count of ended workgroups
   uint64_t* d_cands = nullptr;
   uint32_t* d_scratch = nullptr;
   uint64_t scratch_stride = 0;
@@ -88,6 +90,7 @@ uint32_t wanted_cand(const as_sampling& s, uint32_t n) {
 // kernel's candidate room allows for the largest per-wave count, and slices of at most kSliceMax.
 struct Plan {
   uint32_t n_seg, slice_len, stride, limit;
+  bool row_kernel;  // one workgroup scans and finishes each row (fused.hip)
 };
 Plan plan_slices(uint32_t n, uint32_t n_rows, uint32_t c_max) {
   const uint32_t s_min = (n + as_launch::kSliceMax - 1) / as_launch::kSliceMax;
@@ -103,7 +106,27 @@ Plan plan_slices(uint32_t n, uint32_t n_rows, uint32_t c_max) {
   p.n_seg = (n + len - 1) / len;
   p.stride = as_launch::kCandCap / p.n_seg;
   p.limit = p.stride > as_launch::kHistReserve ? (p.stride - as_launch::kHistReserve) / 4 : 0;
+  p.row_kernel = false;
   return p;
+}
+
+// The row kernel's plan: one slice per row with all of the row's candidate slots.
+Plan plan_row_kernel(uint32_t n) {
+  Plan p;
+  p.n_seg = 1;
+  p.slice_len = n;
+  p.stride = as_launch::kCandCap;
+  p.limit = (as_launch::kCandCap - as_launch::kHistReserve) / 4;
+  p.row_kernel = true;
+  return p;
+}
+
+// Which kernels a call takes: the row kernel for batches that occupy the GPU with one workgroup per
+// row (and rows its LDS bitmap covers), the sliced scan otherwise; `force` (as_debug_path) overrides.
+Plan choose_plan(int force, uint32_t n, uint32_t n_rows, uint32_t c_max) {
+  const bool fits = n <= as_launch::kRowMaxVocab;
+  const bool row = force == 2 ? fits : force == 1 ? false : (fits && n_rows >= as_launch::kRowMinRows);
+  return row ? plan_row_kernel(n) : plan_slices(n, n_rows, c_max);
 }
 
 // The row's mode and parameter block (Sampler::sample's dispatch, sample.rs:129-150).
@@ -232,6 +255,8 @@ int run_rows(as_ctx* c, const Plan& pl, const RowParams* rows, const float* logi
   a.done = c->h_done;
   a.call = ++c->calls;
   a.max_history = c->max_history;
+  a.fused = pl.row_kernel ? 1u : 0u;
+  a.fused_count = c->d_fused_count;
 
   if (c->share_dirty)
     return fail(c, AS_ERR_HIP, "an earlier call launched its scan but not its finish kernel: the context's "
@@ -262,6 +287,15 @@ int run_rows(as_ctx* c, const Plan& pl, const RowParams* rows, const float* logi
   }
   if (e0) AS_HIP(c, hipEventRecord(e0, c->stream));
   c->share_dirty = true;
+  if (pl.row_kernel) {
+    AS_HIP(c, as_launch::sample_rows(c->stream, vec, logits, c->d_zero, row_stride, n, n_rows, h, c->d_block,
+                                     c->d_share, hist_off, hist_ids, extra_ids, c->d_stats, c->d_cands, pl.stride,
+                                     a));
+    c->share_dirty = false;
+    if (e1) AS_HIP(c, hipEventRecord(e1, c->stream));
+    if (e2) AS_HIP(c, hipEventRecord(e2, c->stream));
+    return AS_OK;
+  }
   order_rows(rows, n_rows, &c->order, c->order_cost);
   AS_HIP(c, as_launch::scan(c->stream, vec, logits, c->d_zero, row_stride, n, n_rows, n_seg, pl.slice_len,
                             h, c->d_block, c->d_share, hist_off, hist_ids, extra_ids, c->d_stats, c->d_cands,
@@ -338,6 +372,7 @@ int as_destroy(as_ctx* c) {
   (void)hipFree(c->d_zero);
   (void)hipFree(c->d_lp);
   (void)hipFree(c->d_mv_partials);
+  (void)hipFree(c->d_fused_count);
   for (hipEvent_t e : c->ev) (void)hipEventDestroy(e);
   for (int b = 0; b < 2; ++b)
     if (c->h_block[b]) (void)hipHostFree(c->h_block[b]);
@@ -387,6 +422,8 @@ int as_create(int device, void* hip_stream, uint32_t max_rows, uint32_t max_voca
   if (e == hipSuccess) e = hipMalloc(&c->d_mv_partials, sizeof(uint64_t) * as_launch::kMatvecGroups);
   if (e == hipSuccess)
     e = hipMalloc(&c->d_lp, sizeof(as_launch::LpPart) * (uint64_t)max_rows * as_launch::lp_parts(max_vocab));
+  if (e == hipSuccess) e = hipMalloc(&c->d_fused_count, sizeof(uint32_t));
+  if (e == hipSuccess) e = hipMemset(c->d_fused_count, 0, sizeof(uint32_t));
   if (e == hipSuccess) e = hipMalloc(&c->d_zero, sizeof(float) * 1024);
   if (e == hipSuccess) e = hipMemset(c->d_zero, 0, sizeof(float) * 1024);
   for (int b = 0; b < 2 && e == hipSuccess; ++b)
@@ -429,7 +466,7 @@ int as_sample(as_ctx* c, const as_batch* b, const as_sampling* params) {
       return fail(c, AS_ERR_PARAMS, "row " + std::to_string(r) + ": " + msg);
     c_max = std::max(c_max, wanted_cand(params[r], b->n_vocab));
   }
-  const Plan pl = plan_slices(b->n_vocab, b->n_rows, c_max);
+  const Plan pl = choose_plan(c->force_path, b->n_vocab, b->n_rows, c_max);
   RowParams* h = c->rows.data();
   for (uint32_t r = 0; r < b->n_rows; ++r) {
     h[r] = make_row(params[r], b->n_vocab, pl);
@@ -460,7 +497,7 @@ int as_verify(as_ctx* c, const float* rows, uint64_t row_stride, uint32_t n_voca
     return fail(c, AS_ERR_CAPACITY, "as_verify: the history and the drafts hold more ids than the context's max_history");
   char msg[160];
   if (as_check(params, msg, sizeof msg) != AS_OK) return fail(c, AS_ERR_PARAMS, msg);
-  const Plan pl = plan_slices(n_vocab, k + 1, wanted_cand(*params, n_vocab));
+  const Plan pl = choose_plan(c->force_path, n_vocab, k + 1, wanted_cand(*params, n_vocab));
   const bool draws = params->temp > 0.0f;
   RowParams* h = c->rows.data();
   for (uint32_t i = 0; i <= k; ++i) {
@@ -610,6 +647,12 @@ int as_logprobs(as_ctx* c, const float* logits, uint64_t row_stride, uint32_t n_
   AS_HIP(c, hipSetDevice(c->device));
   AS_HIP(c, as_launch::logprobs(c->stream, vec, logits, row_stride, n_vocab, n_rows, c->d_lp, tokens, top, logprob,
                                 top_ids, top_logprobs, status));
+  return AS_OK;
+}
+
+int as_debug_path(as_ctx* c, int path) {
+  if (!c || path < 0 || path > 2) return AS_ERR_INVALID;
+  c->force_path = path;
   return AS_OK;
 }
 

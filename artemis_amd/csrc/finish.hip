@@ -22,1763 +22,23 @@
 #include "launch.h"
 #include "../../include/artemis_sampler.h"
 
+#define AS_FIN_NS as_fin_sliced
+#define AS_FIN_THREADS 1024
+#define AS_FIN_MAX_SEG 256
+#include "finish_body.h"
+
 using namespace as_dev;
 using as_launch::FinishArgs;
 
 namespace {
 
-constexpr int kThreads = 1024;
-constexpr int kWaves = kThreads / kWave;
-constexpr int kCap = as_launch::kFinishCap;
-constexpr int kMaxSeg = 256;
-constexpr int kStage = 4096;
-constexpr double kU = 1.1102230246251565e-16;  // 2^-53, the unit roundoff
-
-__device__ __forceinline__ double gamma_n(double n) { return n * kU / (1.0 - n * kU); }
-
-struct Shared {
-  uint64_t sk[kCap];  // candidates (exact path: per-wave digit counts)
-  double wd[kCap];    // weights and prefix sums (exact path: staging for sequential folds)
-  uint64_t tab[256];
-  uint32_t hist[256];
-  uint32_t base[256];
-  uint32_t tot[256];
-  uint32_t seg_off[kMaxSeg + 1];
-  SegStats seg[kMaxSeg];
-  uint32_t bcnt[1024];
-  uint32_t bstart[1024];
-  uint32_t red_u[kWaves];
-  double red_d[kWaves];
-  // Row scalars.
-  uint32_t hist_over;
-  uint32_t bad, gi, mk, total, trunc, keep, pick, done, exact, prefix, stats_bad, nsk, tail_over, have_tail, tail_count,
-      tail_listed, tail_parts;
-  uint64_t bound_key;
-  double u01, sum, x, eps, x1, eps1, r_prefix, w_lo, w_hi, m_lo, m_hi;
-};
-// The workgroup's LDS, at file scope so that the out-of-line paths below address it as LDS.
-__shared__ Shared g_sh;
-
-// --- block helpers ------------------------------------------------------------------------------
-
-__device__ void bitonic_desc(uint64_t* s, uint32_t n) {
-  for (uint32_t k = 2; k <= n; k <<= 1) {
-    for (uint32_t j = k >> 1; j > 0; j >>= 1) {
-      for (uint32_t i = threadIdx.x; i < n; i += kThreads) {
-        const uint32_t ixj = i ^ j;
-        if (ixj > i) {
-          const uint64_t x = s[i], y = s[ixj];
-          const bool desc = (i & k) == 0;
-          if (desc ? (x < y) : (x > y)) {
-            s[i] = y;
-            s[ixj] = x;
-          }
-        }
-      }
-      __syncthreads();
-    }
-  }
-}
-
-// Exclusive prefix sum of one f64 per thread over the block.
-__device__ double block_exclusive_scan_f64(double x, double* wave_tot) {
-  const int lane = threadIdx.x & (kWave - 1), w = threadIdx.x / kWave;
-  double incl = x;
-  for (int o = 1; o < kWave; o <<= 1) {
-    const double y = __shfl_up(incl, o, kWave);
-    if (lane >= o) incl = __dadd_rn(incl, y);
-  }
-  __syncthreads();
-  if (lane == kWave - 1) wave_tot[w] = incl;
-  __syncthreads();
-  double before = 0.0;
-  for (int k = 0; k < w; ++k) before = __dadd_rn(before, wave_tot[k]);
-  // incl - x is not exact; recompute the exclusive value from the wave's shifted inclusive scan.
-  double excl_in_wave = __shfl_up(incl, 1, kWave);
-  if (lane == 0) excl_in_wave = 0.0;
-  return __dadd_rn(before, excl_in_wave);
-}
-
-// --- the exact-order path ---------------------------------------------------------------------
-
-// Thread 0's left-to-right f64 fold of term(i), i in [0, m), staged through LDS in tiles that all
-// threads fill. Returns the sum to every thread.
-template <class Term>
-__device__ __forceinline__ double seq_fold(Shared& sh, uint32_t m, Term term) {
-  double* stage = sh.wd;
-  double acc = 0.0;
-  for (uint32_t t0 = 0; t0 < m; t0 += kStage) {
-    const uint32_t c = min((uint32_t)kStage, m - t0);
-    for (uint32_t i = threadIdx.x; i < c; i += kThreads) stage[i] = term(t0 + i);
-    __syncthreads();
-    if (threadIdx.x == 0)
-      for (uint32_t i = 0; i < c; ++i) acc = __dadd_rn(acc, stage[i]);
-    __syncthreads();
-  }
-  if (threadIdx.x == 0) sh.sum = acc;
-  __syncthreads();
-  const double r = sh.sum;
-  __syncthreads();
-  return r;
-}
-
-// One stable pass of an LSD radix sort on 8 bits: (src_key, src_id) -> (dst_key, dst_id).
-__device__ __forceinline__ void radix_pass(Shared& sh, uint32_t n, int shift, const uint32_t* src_key,
-                           const uint32_t* src_id, uint32_t* dst_key, uint32_t* dst_id) {
-  uint32_t* wcnt = reinterpret_cast<uint32_t*>(sh.sk);  // [kWaves][256]
-  const uint32_t tid = threadIdx.x, lane = tid & (kWave - 1), w = tid / kWave;
-  if (tid < 256) sh.hist[tid] = 0;
-  __syncthreads();
-  for (uint32_t i = tid; i < n; i += kThreads) atomicAdd(&sh.hist[(src_key[i] >> shift) & 255u], 1u);
-  __syncthreads();
-  if (tid == 0) {
-    uint32_t run = 0;
-    for (int d = 0; d < 256; ++d) {
-      sh.base[d] = run;
-      run += sh.hist[d];
-    }
-  }
-  for (uint32_t i = tid; i < kWaves * 256; i += kThreads) wcnt[i] = 0;
-  __syncthreads();
-  const uint64_t below = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
-  for (uint32_t t0 = 0; t0 < n; t0 += kThreads) {
-    const uint32_t i = t0 + tid;
-    const bool valid = i < n;
-    const uint32_t k = valid ? src_key[i] : 0u, id = valid ? src_id[i] : 0u;
-    const uint32_t d = (k >> shift) & 255u;
-    uint64_t peers = __ballot(valid);
-#pragma unroll
-    for (int b = 0; b < 8; ++b) {
-      const uint64_t bb = __ballot(valid && ((d >> b) & 1u));
-      peers &= ((d >> b) & 1u) ? bb : ~bb;
-    }
-    const uint32_t rank = __popcll(peers & below), count = __popcll(peers);
-    if (valid && rank == count - 1) wcnt[w * 256 + d] = count;
-    __syncthreads();
-    if (tid < 256) {
-      uint32_t run = 0;
-      for (int ww = 0; ww < kWaves; ++ww) {
-        const uint32_t c = wcnt[ww * 256 + tid];
-        wcnt[ww * 256 + tid] = run;
-        run += c;
-      }
-      sh.tot[tid] = run;
-    }
-    __syncthreads();
-    if (valid) {
-      const uint32_t pos = sh.base[d] + wcnt[w * 256 + d] + rank;
-      dst_key[pos] = k;
-      dst_id[pos] = id;
-    }
-    __syncthreads();
-    if (tid < 256) sh.base[tid] += sh.tot[tid];
-    for (uint32_t j = tid; j < kWaves * 256; j += kThreads) wcnt[j] = 0;
-    __syncthreads();
-  }
-}
-
-// The reference's algorithm in its own order: Sampler::sample's dispatch (sample.rs:136-149),
-// draw_full_sort (157-198) for top-k rows and draw_partial (208-293) otherwise.
-__device__ __noinline__ void exact_row(const FinishArgs& a, const RowParams& p, uint32_t row) {
-  Shared& sh = g_sh;
-  const uint32_t n = a.n, tid = threadIdx.x;
-  uint32_t* S = a.scratch + (uint64_t)row * a.scratch_stride;
-  uint32_t* cnt = S;
-  uint32_t* keyA = S + n;
-  uint32_t* idA = S + 2 * (uint64_t)n;
-  uint32_t* keyB = S + 3 * (uint64_t)n;
-  uint32_t* idB = S + 4 * (uint64_t)n;
-  const float* x = a.logits + (uint64_t)row * a.row_stride;
-
-  uint32_t hb;
-  const uint32_t he = history_bounds(a, p, row, &hb);
-  const uint32_t extra = a.extra_ids ? p.extra : 0;
-  const bool pen = (p.flags & kFlagPenalties) && (he > hb || extra > 0);
-  if (pen) {
-    for (uint32_t i = tid; i < n; i += kThreads) cnt[i] = 0;
-    __syncthreads();
-    for (uint32_t h = hb + tid; h < he; h += kThreads) {
-      const uint32_t id = a.hist_ids[h];
-      if (id < n) atomicAdd(&cnt[id], 1u);
-    }
-    for (uint32_t h = tid; h < extra; h += kThreads) {
-      const uint32_t id = a.extra_ids[h];
-      if (id < n) atomicAdd(&cnt[id], 1u);
-    }
-    __syncthreads();
-  }
-  auto value = [&](uint32_t i) -> float {
-    float v = x[i];
-    if (pen) {
-      const uint32_t c = cnt[i];
-      if (c) v = penalize(v, c, p);
-    }
-    return v;
-  };
-  for (uint32_t i = tid; i < n; i += kThreads) {
-    keyA[i] = ~total_key(value(i));
-    idA[i] = i;
-  }
-  __syncthreads();
-  radix_pass(sh, n, 0, keyA, idA, keyB, idB);
-  radix_pass(sh, n, 8, keyB, idB, keyA, idA);
-  radix_pass(sh, n, 16, keyA, idA, keyB, idB);
-  radix_pass(sh, n, 24, keyB, idB, keyA, idA);
-  // Rank j: id idA[j], value key_value(~keyA[j]).
-  auto rv = [&](uint32_t j) -> double { return (double)key_value(~keyA[j]); };
-  const double top = rv(0);
-  const double temp = (double)p.temp;
-  const bool has_floor = p.min_p > 0.0f;
-  const double floor = __dadd_rn(top, p.ln_min_p);
-  const double top_p = (double)p.top_p;
-  const uint64_t* tab = sh.tab;
-  auto w_temp = [&](double v) { return as_exp::exp_with(tab, __ddiv_rn(__dsub_rn(v, top), temp)); };
-  auto w_one = [&](double v) { return as_exp::exp_with(tab, __dsub_rn(v, top)); };
-
-  uint32_t keep = 0;
-  bool unfiltered = false;
-  if (p.mode == kModeExactTopK || p.mode == kModeTopK) {
-    const uint32_t k = p.top_k;
-    keep = k;
-    if (p.top_p < 1.0f) {
-      const double total = seq_fold(sh, k, [&](uint32_t j) { return w_one(rv(j)); });
-      // The cumulative walk, thread 0 over staged weights.
-      if (tid == 0) sh.done = 0;
-      for (uint32_t t0 = 0; t0 < k; t0 += kStage) {
-        const uint32_t c = min((uint32_t)kStage, k - t0);
-        for (uint32_t i = tid; i < c; i += kThreads) sh.wd[i] = w_one(rv(t0 + i));
-        __syncthreads();
-        if (tid == 0) {
-          double cum = sh.sum;  // carried between tiles
-          if (t0 == 0) cum = 0.0;
-          for (uint32_t i = 0; i < c; ++i) {
-            cum = __dadd_rn(cum, __ddiv_rn(sh.wd[i], total));
-            if (cum >= top_p) {
-              sh.keep = t0 + i + 1;
-              sh.done = 1;
-              break;
-            }
-          }
-          sh.sum = cum;
-        }
-        __syncthreads();
-        if (sh.done) break;
-      }
-      if (sh.done) keep = sh.keep;
-      __syncthreads();
-    }
-    if (has_floor) {
-      uint32_t first = keep;
-      for (uint32_t j = tid; j < keep; j += kThreads)
-        if (!(rv(j) >= floor)) first = min(first, j);
-      keep = block_min_u32<kWaves>(first, sh.red_u);
-    }
-  } else if (p.top_p < 1.0f || has_floor) {
-    double total1 = 0.0;
-    if (p.top_p < 1.0f) total1 = seq_fold(sh, n, [&](uint32_t i) { return w_one((double)value(i)); });
-    keep = n;
-    if (tid == 0) {
-      sh.done = 0;
-      sh.sum = 0.0;
-    }
-    __syncthreads();
-    for (uint32_t t0 = 0; t0 < n; t0 += kStage) {
-      const uint32_t c = min((uint32_t)kStage, n - t0);
-      for (uint32_t i = tid; i < c; i += kThreads) {
-        const double v = rv(t0 + i);
-        // -1 marks the first token min-p drops (tested before top-p, sample.rs:237-251).
-        sh.wd[i] = (has_floor && v < floor) ? -1.0 : (p.top_p < 1.0f ? w_one(v) : 0.0);
-      }
-      __syncthreads();
-      if (tid == 0) {
-        double cum = sh.sum;
-        for (uint32_t i = 0; i < c; ++i) {
-          if (sh.wd[i] < 0.0) {
-            sh.keep = t0 + i;
-            sh.done = 1;
-            break;
-          }
-          if (p.top_p < 1.0f) {
-            cum = __dadd_rn(cum, __ddiv_rn(sh.wd[i], total1));
-            if (cum >= top_p) {
-              sh.keep = t0 + i + 1;
-              sh.done = 1;
-              break;
-            }
-          }
-        }
-        sh.sum = cum;
-      }
-      __syncthreads();
-      if (sh.done) break;
-    }
-    if (sh.done) keep = sh.keep;
-    __syncthreads();
-  } else {
-    unfiltered = true;
-    keep = n;
-  }
-
-  // The draw: u = unit() * total, then the first rank whose cumulative weight exceeds u.
-  double total;
-  if (unfiltered)
-    total = seq_fold(sh, n, [&](uint32_t i) { return w_temp((double)value(i)); });
-  else
-    total = seq_fold(sh, keep, [&](uint32_t j) { return w_temp(rv(j)); });
-  const double u = __dmul_rn(sh.u01, total);
-  if (tid == 0) {
-    sh.done = 0;
-    sh.sum = 0.0;
-    sh.pick = keep - 1;  // sample.rs:197, 272, 288: the last kept when u is never passed
-  }
-  __syncthreads();
-  for (uint32_t t0 = 0; t0 < keep; t0 += kStage) {
-    const uint32_t c = min((uint32_t)kStage, keep - t0);
-    for (uint32_t i = tid; i < c; i += kThreads) sh.wd[i] = w_temp(rv(t0 + i));
-    __syncthreads();
-    if (tid == 0) {
-      double cum = sh.sum;
-      for (uint32_t i = 0; i < c; ++i) {
-        cum = __dadd_rn(cum, sh.wd[i]);
-        if (u < cum) {
-          sh.pick = t0 + i;
-          sh.done = 1;
-          break;
-        }
-      }
-      sh.sum = cum;
-    }
-    __syncthreads();
-    if (sh.done) break;
-  }
-  const uint32_t pick = sh.pick;
-  if (tid == 0) {
-    a.tokens[row] = idA[pick];
-    a.status[row] = AS_ROW_OK | AS_ROW_EXACT_PATH;
-    if (a.kept_count) a.kept_count[row] = keep;
-  }
-  if (a.kept_ids) {
-    const uint32_t m = min(keep, a.kept_cap);
-    for (uint32_t j = tid; j < m; j += kThreads) {
-      a.kept_ids[(uint64_t)row * a.kept_cap + j] = idA[j];
-      if (a.kept_probs) a.kept_probs[(uint64_t)row * a.kept_cap + j] = __ddiv_rn(w_temp(rv(j)), total);
-    }
-  }
-}
-
-// --- the fast path's sort and certified draw --------------------------------------------------
-
-constexpr uint32_t kBuckets = 1024;
-
-// Exclusive prefix sum of one u32 per thread over the block; *total gets the sum.
-__device__ uint32_t block_exclusive_scan_u32(uint32_t x, uint32_t* wave_tot, uint32_t* total) {
-  const int lane = threadIdx.x & (kWave - 1), w = threadIdx.x / kWave;
-  uint32_t incl = x;
-  for (int o = 1; o < kWave; o <<= 1) {
-    const uint32_t y = (uint32_t)__shfl_up((int)incl, o, kWave);
-    if (lane >= o) incl += y;
-  }
-  __syncthreads();
-  if (lane == kWave - 1) wave_tot[w] = incl;
-  __syncthreads();
-  uint32_t before = 0, all = 0;
-  for (int k = 0; k < kWaves; ++k) {
-    if (k < w) before += wave_tot[k];
-    all += wave_tot[k];
-  }
-  *total = all;
-  return before + incl - x;
-}
-
-// The row's total from the slices' sums: total1 (by_temp false: sum of exp(l - top)) or the
-// unfiltered total (sum of exp((l - top) / T)), with a bound eps on its distance to the reference's
-// left fold in index order (sample.rs:218-222, 274-282). Each slice's sum is rescaled from its own
-// reference (sum_ref) to the row's largest value (a host-exact exp and a product). The bound adds up:
-//   - the reference's own fold of n terms and its exp: (n + 1) * 2^-53 per unit of X, with the
-//     fold of the slices (n_seg) and 64 to spare;
-//   - each slice's own evaluation, at most err_rel * sum + err_abs * sum_abs (sum_abs moved to the
-//     row's largest value by adding |dm| * sum), and 4 * 2^-53 per unit for its rescale;
-//   - the reference's argument roundings, 2^-53 * |d| per term and per rounding (babs);
-//   - terms the scan's exp flushed to 0: below 2^-126 each.
-__device__ __forceinline__ void slices_total(const FinishArgs& a, Shared& sh, double top, double temp,
-                                             bool by_temp, double* X, double* eps) {
-  if (threadIdx.x == 0) {
-    double x = 0.0, babs = 0.0, own = 0.0;
-    for (uint32_t s = 0; s < a.n_seg; ++s) {
-      const SegStats& t = sh.seg[s];
-      if (t.sum == 0.0) continue;
-      const double ms = (double)t.sum_ref;
-      double dm = fabs(__dsub_rn(top, ms)), dd = __dsub_rn(ms, top);
-      if (by_temp) {
-        dm = __ddiv_rn(dm, temp);
-        dd = __ddiv_rn(dd, temp);
-      }
-      const double sc = as_exp::exp_with(sh.tab, dd);
-      const double part = __dmul_rn(t.sum, sc);
-      const double pabs = __dmul_rn(sc, __dadd_rn(t.sum_abs, __dmul_rn(dm, t.sum)));
-      x = __dadd_rn(x, part);
-      babs = __dadd_rn(babs, pabs);
-      own = __dadd_rn(own, __dadd_rn(__dmul_rn(part, (double)t.err_rel + 4.0 * kU), __dmul_rn(pabs, (double)t.err_abs)));
-    }
-    const double terms = (double)a.n + (double)a.n_seg + 64.0;
-    sh.x = x;
-    sh.eps = 1.02 * (kU * ((by_temp ? 2.1 : 1.1) * babs + terms * x) + own) + (double)a.n * 0x1p-126;
-  }
-  __syncthreads();
-  *X = sh.x;
-  *eps = sh.eps;
-  __syncthreads();
-}
-
-
-// Sorts the candidates sh.sk[0..total) whose packed rank is >= R into rank order (packed
-// descending) and returns how many there are, P. Only the first `need` ranks are guaranteed placed:
-// a bucket that starts at or past `need` is left unsorted. A bucket sort: buckets by distance from
-// the row's largest key kmax, then each value's place inside its bucket by counting the bucket's
-// values above it (quadratic in a bucket's size, which heavy ties make large).
-__device__ __forceinline__ uint32_t sort_candidates(Shared& sh, uint32_t total, uint64_t R,
-                                                    uint32_t kmax, uint32_t need) {
-  const uint32_t tid = threadIdx.x;
-  uint64_t* out2 = reinterpret_cast<uint64_t*>(sh.wd);
-  constexpr int kPerT = kCap / kThreads;
-  uint64_t xs[kPerT];
-  uint32_t kmin = 0xFFFFFFFFu, mine = 0;
-#pragma unroll
-  for (int q = 0; q < kPerT; ++q) {
-    const uint32_t i = tid + q * kThreads;
-    xs[q] = (i < total) ? sh.sk[i] : 0ull;
-    if (i < total && xs[q] >= R) {
-      kmin = min(kmin, (uint32_t)(xs[q] >> 32));
-      ++mine;
-    }
-  }
-  kmin = block_min_u32<kWaves>(kmin, sh.red_u);
-  const uint32_t P = block_sum_u32<kWaves>(mine, sh.red_u);
-  const uint32_t range = kmax - kmin;
-  uint32_t shift = 0;
-  while ((range >> shift) >= kBuckets) ++shift;
-  sh.bcnt[tid] = 0;
-  __syncthreads();
-  uint32_t slot[kPerT];
-#pragma unroll
-  for (int q = 0; q < kPerT; ++q) {
-    const uint32_t i = tid + q * kThreads;
-    slot[q] = 0;
-    if (i < total && xs[q] >= R) slot[q] = atomicAdd(&sh.bcnt[(kmax - (uint32_t)(xs[q] >> 32)) >> shift], 1u);
-  }
-  __syncthreads();
-  const uint32_t c = sh.bcnt[tid];
-  uint32_t all;
-  sh.bstart[tid] = block_exclusive_scan_u32(c, sh.red_u, &all);
-  __syncthreads();
-#pragma unroll
-  for (int q = 0; q < kPerT; ++q) {
-    const uint32_t i = tid + q * kThreads;
-    if (i < total && xs[q] >= R) {
-      const uint32_t b = (kmax - (uint32_t)(xs[q] >> 32)) >> shift;
-      out2[sh.bstart[b] + slot[q]] = xs[q];
-    }
-  }
-  __syncthreads();
-  for (uint32_t i = tid; i < P; i += kThreads) {
-    const uint64_t x = out2[i];
-    const uint32_t b = (kmax - (uint32_t)(x >> 32)) >> shift;
-    const uint32_t s0 = sh.bstart[b], nb = sh.bcnt[b];
-    if (s0 >= need) continue;
-    uint32_t r = 0;
-    for (uint32_t j = 0; j < nb; ++j) r += (out2[s0 + j] > x) ? 1u : 0u;
-    sh.sk[s0 + r] = x;
-  }
-  __syncthreads();
-  return P;
-}
-
-// Inclusive prefix sums of sh.wd[0..m) (m <= kCap), eight per thread in loc[], the thread's
-// offset in *off; returns the sum of all m to every thread. Parallel: each sum is within
-// gamma(40) of the exact sum of its (positive) terms.
-__device__ __forceinline__ double prefix_scan(Shared& sh, uint32_t m, double loc[8], double* off) {
-  const uint32_t i0 = threadIdx.x * 8;
-  double run = 0.0;
-#pragma unroll
-  for (int q = 0; q < 8; ++q) {
-    run = __dadd_rn(run, (i0 + q < m) ? sh.wd[i0 + q] : 0.0);
-    loc[q] = run;
-  }
-  *off = block_exclusive_scan_f64(run, sh.red_d);
-#pragma unroll
-  for (int q = 0; q < 8; ++q)
-    if (i0 + q == m - 1) sh.x = __dadd_rn(*off, loc[q]);
-  __syncthreads();
-  const double s = sh.x;
-  __syncthreads();
-  return s;
-}
-
-// The draw's decision from bounds: u (the reference's unit() * total) lies in [ulo, uhi], and the
-// reference's cumulative c_j (its left fold of w_0..w_j) is within gamma(j+1) + gamma(40) of our
-// scanned prefix. Returns the first j < m with c_j > u when the bounds settle it, m when u is
-// certainly past every c_j of the m, kNone when they cannot decide.
-__device__ __forceinline__ uint32_t decide_draw(Shared& sh, uint32_t m, const double loc[8], double off, double ulo,
-                                double uhi) {
-  const uint32_t i0 = threadIdx.x * 8;
-  const double g40 = gamma_n(40.0);
-  uint32_t fp = m, fc = m;
-#pragma unroll
-  for (int q = 0; q < 8; ++q) {
-    const uint32_t i = i0 + q;
-    if (i < m) {
-      const double Rv = __dadd_rn(off, loc[q]);
-      const double rel = gamma_n((double)i + 1.0) + g40 + 4.0 * kU;
-      if (Rv * (1.0 + rel) > ulo) fp = min(fp, i);
-      if (Rv * (1.0 - rel) > uhi) fc = min(fc, i);
-    }
-  }
-  const uint32_t jp = block_min_u32<kWaves>(fp, sh.red_u);
-  const uint32_t jc = block_min_u32<kWaves>(fc, sh.red_u);
-  if (jp == jc) return jc;  // jc < m, or both m: past every c_j
-  return kNone;
-}
-
-// --- the deep path ------------------------------------------------------------------------------
-//
-// For a row whose cut or draw lies past the fast path's sorted candidates: one pass over the row
-// histograms its values into bins (fine near the row's largest value; each bin's count and its
-// weight in fixed point, added with integer LDS atomics), which fixes the lowest bin that can hold
-// the cut (or the draw), with a margin; a second pass collects every value down to that bin; a
-// bucket sort in HBM scratch puts them in rank order; and the same certified decisions as the fast
-// path run while streaming through them. The row's exact total in index order is computed only
-// when the slices' certified sums leave a decision open. When a bound still cannot decide, the
-// exact-order path runs.
-
-constexpr uint32_t kDeepBins = 4096;
-constexpr uint32_t kDeepBucketMax = 4096;
-
-// Streams the sorted values buf[c0 .. c0+m) through LDS in chunks: sh.sk gets the values, sh.wd
-// their weight(value), then a block prefix scan; f(chunk_start, count, loc, base) sees the chunk,
-// with the global inclusive prefix of chunk value q at base + loc[q], and returns true to stop.
-// Returns the sum of every weight streamed (within gamma(80) of the exact sum).
-template <class W, class F>
-__device__ __forceinline__ double stream_scan(Shared& sh, const uint64_t* buf, uint32_t m, W weight, F f) {
-  double carry = 0.0;
-  for (uint32_t c0 = 0; c0 < m; c0 += kCap) {
-    const uint32_t cn = min((uint32_t)kCap, m - c0);
-    for (uint32_t i = threadIdx.x; i < cn; i += kThreads) {
-      const uint64_t x = buf[c0 + i];
-      sh.sk[i] = x;
-      sh.wd[i] = weight((double)packed_value(x));
-    }
-    __syncthreads();
-    double loc[8], off;
-    const double tot = prefix_scan(sh, cn, loc, &off);
-    const bool stop = f(c0, cn, loc, __dadd_rn(carry, off));
-    carry = __dadd_rn(carry, tot);
-    __syncthreads();
-    if (stop) break;
-  }
-  return carry;
-}
-
-// First rank j with lo/hi bounds of the reference's cumulative crossing `target`: fills *jl (first
-// j whose upper bound reaches it) and *jh (first j whose lower bound does), over m streamed values.
-// cum_j = R_j / total with total in [x - eps, x + eps]; rel(j) bounds the rank-order fold.
-template <class W>
-__device__ __forceinline__ void stream_cross(Shared& sh, const uint64_t* buf, uint32_t m, W weight,
-                                             double x, double eps, double target, uint32_t* jl,
-                                             uint32_t* jh) {
-  uint32_t fl = kNone, fh = kNone;
-  stream_scan(sh, buf, m, weight, [&](uint32_t c0, uint32_t cn, const double loc[8], double base) {
-    const uint32_t i0 = threadIdx.x * 8;
-    uint32_t a = kNone, b = kNone;
-#pragma unroll
-    for (int q = 0; q < 8; ++q) {
-      const uint32_t i = i0 + q;
-      if (i < cn) {
-        const double Rv = __dadd_rn(base, loc[q]);
-        const double rel = 2.0 * gamma_n(80.0) + gamma_n(2.0 * (double)(c0 + i) + 4.0) + 10.0 * kU;
-        if (Rv * (1.0 + rel) / (x - eps) >= target) a = min(a, c0 + i);
-        if (Rv * (1.0 - rel) / (x + eps) >= target) b = min(b, c0 + i);
-      }
-    }
-    a = block_min_u32<kWaves>(a, sh.red_u);
-    b = block_min_u32<kWaves>(b, sh.red_u);
-    if (fl == kNone) fl = a;
-    if (fh == kNone) fh = b;
-    return fl != kNone && fh != kNone;
-  });
-  *jl = (fl == kNone) ? m : fl;
-  *jh = (fh == kNone) ? m : fh;
-}
-
-// The draw over the first m streamed values with u in [ulo, uhi]: the first j with the
-// reference's cumulative c_j > u when the bounds settle it, m when u is certainly past all of
-// them, kNone when they cannot decide.
-template <class W>
-__device__ __forceinline__ uint32_t stream_draw(Shared& sh, const uint64_t* buf, uint32_t m, W weight,
-                                                double ulo, double uhi) {
-  uint32_t res = m;
-  bool done = false;
-  stream_scan(sh, buf, m, weight, [&](uint32_t c0, uint32_t cn, const double loc[8], double base) {
-    const uint32_t i0 = threadIdx.x * 8;
-    uint32_t a = kNone, b = kNone;
-#pragma unroll
-    for (int q = 0; q < 8; ++q) {
-      const uint32_t i = i0 + q;
-      if (i < cn) {
-        const double Rv = __dadd_rn(base, loc[q]);
-        const double rel = gamma_n((double)(c0 + i) + 1.0) + gamma_n(80.0) + 4.0 * kU;
-        if (Rv * (1.0 + rel) > ulo) a = min(a, c0 + i);
-        if (Rv * (1.0 - rel) > uhi) b = min(b, c0 + i);
-      }
-    }
-    a = block_min_u32<kWaves>(a, sh.red_u);
-    b = block_min_u32<kWaves>(b, sh.red_u);
-    if (a != kNone) {
-      res = (a == b) ? a : kNone;
-      done = true;
-    }
-    return done;
-  });
-  return res;
-}
-
-// The deep path's passes over a row: 16 values per thread per step, with their history counts
-// (cnt, 0 when null), all loads of a step issued before any value is used (16-byte loads, scalar
-// ones for an unaligned row or the ragged end). f(i, v, c) runs for each value.
-template <class F>
-__device__ __forceinline__ void for_each_value(const float* x, const uint32_t* cnt, uint32_t n, bool vec, F f) {
-  typedef float f32x4 __attribute__((ext_vector_type(4)));
-  typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
-  constexpr uint32_t kStep = 16 * kThreads;
-  const uint32_t tid = threadIdx.x;
-  for (uint32_t b0 = 0; b0 < n; b0 += kStep) {
-    if (vec && b0 + kStep <= n) {
-      f32x4 q[4];
-      u32x4 k[4];
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const uint32_t e = b0 + (j * kThreads + tid) * 4;
-        q[j] = *reinterpret_cast<const f32x4*>(x + e);
-        k[j] = cnt ? *reinterpret_cast<const u32x4*>(cnt + e) : u32x4{0u, 0u, 0u, 0u};
-      }
-#pragma unroll
-      for (int j = 0; j < 4; ++j)
-#pragma unroll
-        for (int c = 0; c < 4; ++c) f(b0 + (j * kThreads + tid) * 4 + c, q[j][c], k[j][c]);
-    } else {
-      float q[16];
-      uint32_t k[16];
-#pragma unroll
-      for (int j = 0; j < 16; ++j) {
-        const uint32_t i = b0 + j * kThreads + tid;
-        q[j] = (i < n) ? x[i] : 0.0f;
-        k[j] = (cnt && i < n) ? cnt[i] : 0u;
-      }
-#pragma unroll
-      for (int j = 0; j < 16; ++j) {
-        const uint32_t i = b0 + j * kThreads + tid;
-        if (i < n) f(i, q[j], k[j]);
-      }
-    }
-  }
-}
-
-__device__ __noinline__ float penalize_out(float x, uint32_t c, const RowParams& p) { return penalize(x, c, p); }
-
-// Returns true when it settled the row.
-__device__ __noinline__ bool deep_row(const FinishArgs& a, const RowParams& p, uint32_t row) {
-  Shared& sh = g_sh;
-  const uint32_t n = a.n, tid = threadIdx.x, lane = tid & (kWave - 1);
-  uint32_t* S = a.scratch + (uint64_t)row * a.scratch_stride;
-  uint32_t* cnt = S;
-  uint64_t* bufA = reinterpret_cast<uint64_t*>(S + ((n + 1) & ~1u));
-  uint64_t* bufB = bufA + n;
-  const float* x = a.logits + (uint64_t)row * a.row_stride;
-
-  uint32_t hb;
-  const uint32_t he = history_bounds(a, p, row, &hb);
-  const uint32_t extra = a.extra_ids ? p.extra : 0;
-  const bool pen = (p.flags & kFlagPenalties) && (he > hb || extra > 0);
-  if (pen) {
-    for (uint32_t i = tid; i < n; i += kThreads) cnt[i] = 0;
-    __syncthreads();
-    for (uint32_t h = hb + tid; h < he; h += kThreads) {
-      const uint32_t id = a.hist_ids[h];
-      if (id < n) atomicAdd(&cnt[id], 1u);
-    }
-    for (uint32_t h = tid; h < extra; h += kThreads) {
-      const uint32_t id = a.extra_ids[h];
-      if (id < n) atomicAdd(&cnt[id], 1u);
-    }
-    __syncthreads();
-  }
-  // The counts start 16-byte aligned (the scratch stride is a multiple of 4 words). History values
-  // are few: their penalty runs out of line, so that the passes do not evaluate it for every value.
-  const uint32_t* pcnt = pen ? cnt : nullptr;
-  auto pvalue = [&](float v, uint32_t c) -> float { return __builtin_expect(c != 0, 0) ? penalize_out(v, c, p) : v; };
-  const bool vec = a.vec && a.row_stride % 4 == 0;
-
-  if (p.mode == kModeGreedy) {
-    // greedy / greedy_penalized (sample.rs:9-17, 378-396) over the whole row.
-    float gv = 0.0f;
-    uint32_t gi = kNone;
-    for_each_value(x, pcnt, n, vec, [&](uint32_t i, float v, uint32_t c) { greedy_merge(gv, gi, pvalue(v, c), i); });
-    wave_greedy(gv, gi);
-    if (lane == 0) {
-      sh.wd[tid / kWave] = (double)gv;
-      sh.red_u[tid / kWave] = gi;
-    }
-    __syncthreads();
-    if (tid == 0) {
-      for (int w = 1; w < kWaves; ++w) greedy_merge(gv, gi, (float)sh.wd[w], sh.red_u[w]);
-      a.tokens[row] = gi;
-      a.status[row] = AS_ROW_OK | AS_ROW_DEEP_PATH;
-      if (a.kept_count) a.kept_count[row] = 1;
-      if (a.kept_ids && a.kept_cap > 0) {
-        a.kept_ids[(uint64_t)row * a.kept_cap] = gi;
-        if (a.kept_probs) a.kept_probs[(uint64_t)row * a.kept_cap] = 1.0;
-      }
-    }
-    return true;
-  }
-
-  // A slice whose statistics the scan could not finish (too many distinct history ids or
-  // candidates) leaves the maxima and sums incomplete: the exact-order path recomputes everything.
-  if (sh.stats_bad) return false;
-
-  const uint32_t mk = sh.mk;
-  const double top = (double)key_value(mk);
-  const double temp = (double)p.temp, top_p = (double)p.top_p;
-  const bool has_floor = p.min_p > 0.0f;
-  const double floor = __dadd_rn(top, p.ln_min_p);
-  const uint32_t fk = total_key(floor_f32(floor));
-  const bool topk = (p.mode == kModeTopK || p.mode == kModeExactTopK);
-  const uint32_t k = p.top_k;
-  const bool cuts = p.top_p < 1.0f || has_floor;
-  const bool unfiltered = !topk && !cuts;
-  const uint64_t* tab = sh.tab;
-  auto w_temp = [&](double v) { return as_exp::exp_with(tab, __ddiv_rn(__dsub_rn(v, top), temp)); };
-  auto w_one = [&](double v) { return as_exp::exp_with(tab, __dsub_rn(v, top)); };
-
-  // The row's total, when the cut or the draw needs it: first the slices' certified sums (within
-  // about 1e-6 of the total); when a decision falls inside that bound (a cut this deep has
-  // neighbouring cumulative weights ~1e-5 of the total apart), exact_total() sums the host-exact exp
-  // of the reference's own f64 arguments, within (n + its fold's depth) * 2^-53 of the reference's
-  // left fold.
-  const bool need_total = !topk && (p.top_p < 1.0f || unfiltered);
-  double X = 0.0, eps = 0.0;
-  if (need_total) {
-    slices_total(a, sh, top, temp, unfiltered, &X, &eps);
-    if (!(X - eps > 0.0 && eps == eps)) return false;
-  }
-  bool exact = false;
-
-  // Pass 1: a histogram of the values by distance below the largest, kDeepBins bins over dspan
-  // (32, or 32 T for weights exp((l - top) / T): below it a value's weight is under e^-32 of the
-  // largest), the last bin holding everything further down; with f32 weight sums. The bin is
-  // monotone in the value, so every value ranking above the cut lies in a bin at or before its.
-  const float topf = key_value(mk), inv_t = 1.0f / p.temp;
-  const float bsc = (float)kDeepBins / (unfiltered ? 32.0f * p.temp : 32.0f);
-  auto bin_of = [&](float v) -> uint32_t {
-    const float t = (topf - v) * bsc;
-    return t < (float)(kDeepBins - 1) ? (uint32_t)t : kDeepBins - 1;
-  };
-  // Counts (u32) and weights in 2^-32 units (u64: LDS integer atomics; float ones serialise).
-  uint32_t* hc = reinterpret_cast<uint32_t*>(sh.wd);
-  uint64_t* hm = reinterpret_cast<uint64_t*>(sh.wd) + kDeepBins / 2;
-  static_assert(kDeepBins * 12 <= sizeof(sh.wd), "histogram room");
-  for (uint32_t b = tid; b < kDeepBins; b += kThreads) {
-    hc[b] = 0;
-    hm[b] = 0ull;
-  }
-  __syncthreads();
-  // One value into the histogram: its bin and (for the cut's bin) its weight, exp(d) <= 1 in 2^-32
-  // units rounded down.
-  auto count = [&](float v) {
-    const uint32_t b = bin_of(v);
-    atomicAdd(&hc[b], 1u);
-    if (need_total) {
-      const float f = unfiltered ? __expf((v - topf) * inv_t) : __expf(v - topf);
-      atomicAdd(reinterpret_cast<unsigned long long*>(&hm[b]), (unsigned long long)(f * 0x1p32f));
-    }
-  };
-  // The stream leaves history positions (count c != 0) out; each history id is then counted once,
-  // penalised, by the thread that sets its count's top bit first.
-  for_each_value(x, pcnt, n, vec, [&](uint32_t, float v, uint32_t c) {
-    if (__builtin_expect(c == 0, 1)) count(v);
-  });
-  if (pen) {
-    auto hist_one = [&](uint32_t id) {
-      if (id >= n) return;
-      const uint32_t old = atomicOr(&cnt[id], 0x80000000u);
-      if (!(old & 0x80000000u)) count(penalize(x[id], old, p));
-    };
-    for (uint32_t h = hb + tid; h < he; h += kThreads) hist_one(a.hist_ids[h]);
-    for (uint32_t h = tid; h < extra; h += kThreads) hist_one(a.extra_ids[h]);
-  }
-  __syncthreads();
-  {
-    // The cut's bin bc: the first whose running count reaches k (top-k), or whose running f32
-    // weight reaches the target with 5% to spare; four bins per thread, then block scans.
-    static_assert(kDeepBins == 4 * kThreads, "four bins per thread");
-    uint32_t c4[4], csum = 0;
-    double m4[4], msum = 0.0;
-#pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      c4[q] = hc[tid * 4 + q];
-      m4[q] = (double)hm[tid * 4 + q] * 0x1p-32;
-      csum += c4[q];
-      msum += m4[q];
-    }
-    uint32_t call;
-    uint32_t cb = block_exclusive_scan_u32(csum, sh.red_u, &call);
-    double mb = block_exclusive_scan_f64(msum, sh.red_d);
-    const double target = unfiltered ? sh.u01 * (X + eps) * 1.005 : (p.top_p < 1.0f ? top_p * (X + eps) * 1.005 : 0.0);
-    uint32_t first = kDeepBins - 1;
-#pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      cb += c4[q];
-      mb += m4[q];
-      const bool hit = topk ? (cb >= k) : (need_total && mb >= target);
-      if (hit) first = min(first, tid * 4 + q);
-    }
-    uint32_t bc = block_min_u32<kWaves>(first, sh.red_u);
-    if (!topk && has_floor) bc = min(bc, bin_of(key_value(fk)));
-    if (tid == 0) {
-      sh.keep = bc;
-      sh.pick = 0;
-    }
-  }
-  __syncthreads();
-  const uint32_t bc = sh.keep;
-
-  // Pass 2: every value in bins 0..bc, into bufA (any order): 16 values per thread per step,
-  // placed by ballots with one LDS atomic per wave and step.
-  {
-    constexpr uint32_t kStep = 16 * kThreads;
-    const uint64_t below = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
-    for (uint32_t b0 = 0; b0 < n; b0 += kStep) {
-      float q[16];
-      uint32_t idx[16], hc16[16];
-      if (vec && b0 + kStep <= n) {
-        typedef float f32x4 __attribute__((ext_vector_type(4)));
-        typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
-        f32x4 t[4];
-        u32x4 k[4];
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          const uint32_t e = b0 + (j * kThreads + tid) * 4;
-          t[j] = *reinterpret_cast<const f32x4*>(x + e);
-          k[j] = pcnt ? *reinterpret_cast<const u32x4*>(pcnt + e) : u32x4{0u, 0u, 0u, 0u};
-        }
-#pragma unroll
-        for (int j = 0; j < 4; ++j)
-#pragma unroll
-          for (int c = 0; c < 4; ++c) {
-            q[4 * j + c] = t[j][c];
-            hc16[4 * j + c] = k[j][c];
-            idx[4 * j + c] = b0 + (j * kThreads + tid) * 4 + c;
-          }
-      } else {
-#pragma unroll
-        for (int j = 0; j < 16; ++j) {
-          idx[j] = b0 + j * kThreads + tid;
-          q[j] = (idx[j] < n) ? x[idx[j]] : 0.0f;
-          hc16[j] = (pcnt && idx[j] < n) ? pcnt[idx[j]] : 0u;
-        }
-      }
-      uint32_t keys[16];
-      uint64_t m[16];
-      uint32_t tot = 0;
-#pragma unroll
-      for (int j = 0; j < 16; ++j) {
-        keys[j] = (idx[j] < n) ? total_key(q[j]) : 0u;
-        const bool take = idx[j] < n && hc16[j] == 0 && bin_of(q[j]) <= bc;
-        m[j] = __ballot(take);
-        tot += (uint32_t)__popcll(m[j]);
-      }
-      uint32_t base = 0;
-      if (lane == 0 && tot) base = atomicAdd(&sh.pick, tot);
-      base = __shfl(base, 0, kWave);
-#pragma unroll
-      for (int j = 0; j < 16; ++j) {
-        if ((m[j] >> lane) & 1ull) bufA[base + __popcll(m[j] & below)] = pack(keys[j], idx[j]);
-        base += (uint32_t)__popcll(m[j]);
-      }
-    }
-    if (pen) {
-      // Each history id once more, penalised, by the thread that clears its count's top bit.
-      auto hist_two = [&](uint32_t id) {
-        if (id >= n) return;
-        const uint32_t old = atomicAnd(&cnt[id], 0x7fffffffu);
-        if (!(old & 0x80000000u)) return;
-        const float v = penalize(x[id], old & 0x7fffffffu, p);
-        if (bin_of(v) <= bc) bufA[atomicAdd(&sh.pick, 1u)] = pack(total_key(v), id);
-      };
-      for (uint32_t h = hb + tid; h < he; h += kThreads) hist_two(a.hist_ids[h]);
-      for (uint32_t h = tid; h < extra; h += kThreads) hist_two(a.extra_ids[h]);
-    }
-  }
-  __syncthreads();
-  const uint32_t D = sh.pick;
-  const bool complete = (D == n);
-
-  // Bucket sort of bufA[0..D) into rank order (through bufB): kDeepBins value buckets over the range
-  // the collected values span (monotone in the value, so bucket order is rank order).
-  uint32_t kmin = 0xFFFFFFFFu;
-  for (uint32_t i = tid; i < D; i += kThreads) kmin = min(kmin, (uint32_t)(bufA[i] >> 32));
-  kmin = block_min_u32<kWaves>(kmin, sh.red_u);
-  const float span2 = topf - key_value(kmin);
-  const float bsc2 = span2 > 0.0f ? (float)(kDeepBins - 1) / span2 : 0.0f;
-  auto bin_p = [&](uint64_t x) {
-    const float t = (topf - packed_value(x)) * bsc2;
-    return t < (float)(kDeepBins - 1) ? (uint32_t)t : kDeepBins - 1;
-  };
-  {
-    for (uint32_t b = tid; b < kDeepBins; b += kThreads) hc[b] = 0;
-    __syncthreads();
-    for (uint32_t i = tid; i < D; i += kThreads) atomicAdd(&hc[bin_p(bufA[i])], 1u);
-    __syncthreads();
-    // Exclusive scan of the 4096 counts: four per thread, then the block.
-    uint32_t* bs = hc + kDeepBins;  // bucket starts (over hm's space)
-    uint32_t c4[4], run = 0, big = 0;
-#pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      c4[q] = hc[tid * 4 + q];
-      big = max(big, c4[q]);
-      run += c4[q];
-    }
-    uint32_t all;
-    uint32_t off = block_exclusive_scan_u32(run, sh.red_u, &all);
-#pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      bs[tid * 4 + q] = off;
-      off += c4[q];
-    }
-    big = block_max_u32<kWaves>(big, sh.red_u);
-    if (big > kDeepBucketMax) return false;  // heavy ties: the exact-order path's stable sort
-    // Scatter: a value's slot in its bucket from an LDS counter (reusing the counts, now zeroed
-    // by subtraction as slots are taken).
-    for (uint32_t i = tid; i < D; i += kThreads) {
-      const uint64_t v = bufA[i];
-      const uint32_t b = bin_p(v);
-      const uint32_t slot = atomicSub(&hc[b], 1u) - 1u;
-      bufB[bs[b] + slot] = v;
-    }
-    __syncthreads();
-    for (uint32_t i = tid; i < D; i += kThreads) {
-      const uint64_t v = bufB[i];
-      const uint32_t b = bin_p(v);
-      const uint32_t s0 = bs[b];
-      const uint32_t e0 = (b + 1 < kDeepBins) ? bs[b + 1] : D;
-      uint32_t r = 0;
-      for (uint32_t j = s0; j < e0; ++j) r += (bufB[j] > v) ? 1u : 0u;
-      bufA[s0 + r] = v;
-    }
-    __syncthreads();
-  }
-  auto val_at = [&](uint32_t j) -> double { return (double)packed_value(bufA[j]); };
-
-  // The exact total: exp_core per value streamed (arguments at or below -512 give terms under
-  // 1e-222 of a total of at least 1, left out, far inside eps), then the history ids penalised (each
-  // claimed by setting its count's top bit, which pass 2 cleared). One loop per case, so that no
-  // division is evaluated where none is needed.
-  auto exact_total = [&]() {
-    const uint64_t* t = g_sh.tab;
-    double acc = 0.0;
-    if (unfiltered) {
-      for_each_value(x, pcnt, n, vec, [&](uint32_t, float v, uint32_t c) {
-        if (__builtin_expect(c == 0, 1)) {
-          const double d = __ddiv_rn(__dsub_rn((double)v, top), temp);
-          acc = __dadd_rn(acc, d > -512.0 ? as_exp::exp_core(t, d) : 0.0);
-        }
-      });
-    } else {
-      for_each_value(x, pcnt, n, vec, [&](uint32_t, float v, uint32_t c) {
-        if (__builtin_expect(c == 0, 1)) {
-          const double d = __dsub_rn((double)v, top);
-          acc = __dadd_rn(acc, d > -512.0 ? as_exp::exp_core(t, d) : 0.0);
-        }
-      });
-    }
-    if (pen) {
-      auto hist_three = [&](uint32_t id) {
-        if (id >= n) return;
-        const uint32_t old = atomicOr(&cnt[id], 0x80000000u);
-        if (old & 0x80000000u) return;
-        double d = __dsub_rn((double)penalize(x[id], old, p), top);
-        if (unfiltered) d = __ddiv_rn(d, temp);
-        acc = __dadd_rn(acc, as_exp::exp_with(t, d));
-      };
-      for (uint32_t h = hb + tid; h < he; h += kThreads) hist_three(a.hist_ids[h]);
-      for (uint32_t h = tid; h < extra; h += kThreads) hist_three(a.extra_ids[h]);
-    }
-    X = block_sum_f64<kWaves>(acc, sh.red_d);
-    eps = kU * 1.02 * ((double)n + (double)(n / kThreads) + 32.0) * X;
-    exact = true;
-    return X - eps > 0.0 && eps == eps;
-  };
-
-  // The cut.
-  uint32_t keep = kNone;
-  if (topk) {
-    keep = k;
-    if (p.top_p < 1.0f) {
-      const double Tk = stream_scan(sh, bufA, k, w_one, [](uint32_t, uint32_t, const double*, double) { return false; });
-      const double ek = Tk * (gamma_n((double)k) + 2.0 * gamma_n(80.0) + 4.0 * kU);
-      uint32_t jl, jh;
-      stream_cross(sh, bufA, k, w_one, Tk, ek, top_p, &jl, &jh);
-      if (jl == jh) keep = (jl < k) ? jl + 1 : k;
-      else return false;
-    }
-    if (has_floor) {
-      uint32_t first = keep;
-      for (uint32_t j = tid; j < keep; j += kThreads)
-        if (!(val_at(j) >= floor)) first = min(first, j);
-      keep = block_min_u32<kWaves>(first, sh.red_u);
-    }
-  } else if (cuts) {
-    uint32_t im = D;
-    if (has_floor) {
-      uint32_t first = D;
-      for (uint32_t j = tid; j < D; j += kThreads)
-        if (!(val_at(j) >= floor)) first = min(first, j);
-      im = block_min_u32<kWaves>(first, sh.red_u);
-    }
-    const bool im_exact = (im < D) || complete;
-    for (;;) {
-      uint32_t jl = D, jh = D;
-      if (p.top_p < 1.0f) stream_cross(sh, bufA, D, w_one, X, eps, top_p, &jl, &jh);
-      if (im_exact && im <= jl) keep = im;
-      else if (jl < D && jl == jh) keep = jh + 1;
-      else if (jl == D && complete) keep = n;
-      else if (!exact && p.top_p < 1.0f) {
-        if (!exact_total()) return false;
-        continue;
-      } else return false;
-      break;
-    }
-  }
-
-  // The draw.
-  uint32_t pick;
-  double tot;
-  if (unfiltered) {
-    for (;;) {
-      const uint32_t j = stream_draw(sh, bufA, D, w_temp, sh.u01 * (X - eps) * (1.0 - 3.0 * kU),
-                                     sh.u01 * (X + eps) * (1.0 + 3.0 * kU));
-      if (j != kNone && j < D) pick = j;
-      else if (j == D && complete) pick = n - 1;
-      else if (!exact) {
-        if (!exact_total()) return false;
-        continue;
-      } else return false;
-      break;
-    }
-    keep = n;
-    tot = X;
-  } else {
-    const double Sk = stream_scan(sh, bufA, keep, w_temp, [](uint32_t, uint32_t, const double*, double) { return false; });
-    const double d = gamma_n((double)keep) + 2.0 * gamma_n(80.0) + 4.0 * kU;
-    const uint32_t j = stream_draw(sh, bufA, keep, w_temp, sh.u01 * Sk * (1.0 - d), sh.u01 * Sk * (1.0 + d));
-    if (j == kNone) return false;
-    pick = (j < keep) ? j : keep - 1;
-    tot = Sk;
-  }
-  if (tid == 0) {
-    a.tokens[row] = packed_id(bufA[pick]);
-    a.status[row] = AS_ROW_OK | AS_ROW_DEEP_PATH;
-    if (a.kept_count) a.kept_count[row] = keep;
-  }
-  if (a.kept_ids) {
-    const uint32_t m = min(min(keep, a.kept_cap), D);
-    for (uint32_t j = tid; j < m; j += kThreads) {
-      a.kept_ids[(uint64_t)row * a.kept_cap + j] = packed_id(bufA[j]);
-      if (a.kept_probs) a.kept_probs[(uint64_t)row * a.kept_cap + j] = __ddiv_rn(w_temp(val_at(j)), tot);
-    }
-  }
-  return true;
-}
-
-// --- the draw's unsorted tail --------------------------------------------------------------------
-//
-// Bounds [sh.w_lo, sh.w_hi] on W, the sum of exp((l - top) / T) over S: the row's values that rank below
-// R and are >= fl (min-p's floor as an f32, or -inf), and [sh.m_lo, sh.m_hi] on M, the sum of
-// exp(l - top) over S. One pass over the row; the history's ids are
-// marked in an LDS bitmap and counted in an LDS hash, left out of the stream and added penalised.
-// Each term comes from the hardware's exp2: for |t| <= 126 its error (the instruction's, and four
-// roundings of t of 2^-24 |t| each) is below 3e-5 relative, and below that terms are under 2^-126
-// each; terms add in f32 in runs of at most 16 (under 1e-6 relative), then in f64. Returns false when
-// the history does not fit the tables.
-constexpr uint32_t kTailHash = 1024;
-
-__device__ __noinline__ bool tail_sums(const FinishArgs& a, const RowParams& p, uint32_t row, uint64_t R,
-                                       float fl, float topf) {
-  Shared& sh = g_sh;
-  const uint32_t n = a.n, tid = threadIdx.x;
-  const float* x = a.logits + (uint64_t)row * a.row_stride;
-  uint32_t hb;
-  const uint32_t he = history_bounds(a, p, row, &hb);
-  const uint32_t extra = a.extra_ids ? p.extra : 0;
-  const bool pen = (p.flags & kFlagPenalties) && (he > hb || extra > 0);
-  // The bitmap over sh.wd, the hash over the sort's bucket tables (both free here).
-  uint32_t* bm = reinterpret_cast<uint32_t*>(sh.wd);
-  uint32_t* hid = sh.bcnt;
-  uint32_t* hcnt = sh.bstart;
-  static_assert(kTailHash <= sizeof(sh.bcnt) / 4 && kTailHash <= sizeof(sh.bstart) / 4, "hash room");
-  if (pen) {
-    const uint32_t words = (n + 31) / 32;
-    if (words > sizeof(sh.wd) / 4) return false;
-    for (uint32_t i = tid; i < words; i += kThreads) bm[i] = 0;
-    for (uint32_t i = tid; i < kTailHash; i += kThreads) {
-      hid[i] = kNone;
-      hcnt[i] = 0;
-    }
-    if (tid == 0) sh.tail_over = 0;
-    __syncthreads();
-    auto mark = [&](uint32_t id) {
-      if (id >= n) return;
-      atomicOr(&bm[id >> 5], 1u << (id & 31u));
-      uint32_t h = (id * 0x9E3779B1u) >> (32 - 10);
-      static_assert(kTailHash == 1u << 10, "the hash's top bits");
-      for (uint32_t probe = 0; probe < kTailHash; ++probe) {
-        const uint32_t prev = atomicCAS(&hid[h], kNone, id);
-        if (prev == kNone || prev == id) {
-          atomicAdd(&hcnt[h], 1u);
-          return;
-        }
-        h = (h + 1) & (kTailHash - 1);
-      }
-      sh.tail_over = 1;
-    };
-    for (uint32_t h = hb + tid; h < he; h += kThreads) mark(a.hist_ids[h]);
-    for (uint32_t h = tid; h < extra; h += kThreads) mark(a.extra_ids[h]);
-    __syncthreads();
-    if (sh.tail_over) return false;
-  }
-  // In S: v >= fl, and v ranks below R: v < R's value, or (rarely) equal to it and below in the
-  // packed order (which also orders -0 below +0).
-  const float rv = key_value((uint32_t)(R >> 32));
-  const float s1 = 1.44269502f, sw = (1.0f / p.temp) * s1;
-  double w = 0.0, m = 0.0;
-  // v's terms into (tw, tm) when v is in S.
-  auto term = [&](float v, uint32_t id, float& tw, float& tm) {
-    bool in = v >= fl && v < rv;
-    if (__builtin_expect(v == rv, 0)) in = v >= fl && pack(total_key(v), id) < R;
-    if (in) {
-      const float d = v - topf;
-      tw += __builtin_amdgcn_exp2f(d * sw);
-      tm += __builtin_amdgcn_exp2f(d * s1);
-    }
-  };
-  auto one = [&](float v, uint32_t id) {
-    float tw = 0.0f, tm = 0.0f;
-    term(v, id, tw, tm);
-    w += (double)tw;
-    m += (double)tm;
-  };
-  typedef float f32x4 __attribute__((ext_vector_type(4)));
-  auto masked = [&](uint32_t i) { return pen && ((bm[i >> 5] >> (i & 31u)) & 1u); };
-  if (a.vec && a.row_stride % 4 == 0) {
-    // 16-byte groups, kG per thread per batch, two batches in flight: batch b+1's loads are issued
-    // before batch b is summed.
-    constexpr uint32_t kG = 4, kS = kG * kThreads;
-    const uint32_t ng = n / 4;
-    const f32x4* xv = reinterpret_cast<const f32x4*>(x);
-    f32x4 qa[kG], qb[kG];
-    auto load = [&](f32x4 (&q)[kG], uint32_t g0) {
-#pragma unroll
-      for (uint32_t k = 0; k < kG; ++k) {
-        const uint32_t g = g0 + k * kThreads + tid;
-        q[k] = (g < ng) ? xv[g] : f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-      }
-    };
-    auto sum = [&](const f32x4 (&q)[kG], uint32_t g0) {
-      float tw = 0.0f, tm = 0.0f;
-#pragma unroll
-      for (uint32_t k = 0; k < kG; ++k) {
-        const uint32_t g = g0 + k * kThreads + tid;
-        const uint32_t mask = (g >= ng) ? 15u : pen ? (bm[g >> 3] >> ((4 * g) & 31u)) & 15u : 0u;
-#pragma unroll
-        for (int c = 0; c < 4; ++c)
-          if (!((mask >> c) & 1u)) term(q[k][c], 4 * g + c, tw, tm);
-      }
-      w += (double)tw;
-      m += (double)tm;
-    };
-    load(qa, 0);
-    for (uint32_t g0 = 0; g0 < ng; g0 += 2 * kS) {
-      load(qb, g0 + kS);
-      sum(qa, g0);
-      load(qa, g0 + 2 * kS);
-      sum(qb, g0 + kS);
-    }
-    for (uint32_t i = 4 * ng + tid; i < n; i += kThreads)
-      if (!masked(i)) one(x[i], i);
-  } else {
-    for (uint32_t i = tid; i < n; i += kThreads)
-      if (!masked(i)) one(x[i], i);
-  }
-  if (pen)
-    for (uint32_t s = tid; s < kTailHash; s += kThreads)
-      if (hid[s] != kNone) one(penalize(x[hid[s]], hcnt[s], p), hid[s]);
-  w = block_sum_f64<kWaves>(w, sh.red_d);
-  m = block_sum_f64<kWaves>(m, sh.red_d);
-  const double flush = (double)n * 0x1p-125;
-  if (tid == 0) {
-    sh.w_lo = fmax(0.0, w * (1.0 - 1e-4) - flush);
-    sh.w_hi = w * (1.0 + 1e-4) + flush;
-    sh.m_lo = fmax(0.0, m * (1.0 - 1e-4) - flush);
-    sh.m_hi = m * (1.0 + 1e-4) + flush;
-  }
-  __syncthreads();
-  return true;
-}
-
-// The draw when neither filter stops among the P sorted values, so that the kept set runs past
-// them (draw_partial, sample.rs:260-272). The draw is still settled when u falls among the sorted
-// values with the unsorted tail's weight bounded. First from the sorted values alone: each unsorted
-// weight is at most the last sorted one, and for T <= 1 with top-p's total known, w = e^(1/T) <=
-// e * e_last^(1/T - 1) with e = exp(l - top) <= e_last, so the tail is at most e_last^(1/T - 1)
-// times total1's unsorted part. When u falls within that bound of a cumulative weight, one pass
-// over the row bounds S's weight W (S: the values below R, and above the floor). The kept tail is
-// S's first values in rank order: its weight is at most W; all of W when only the floor cuts; and
-// for T <= 1 at least K / M of W, with K the kept tail's mass at T = 1 and M S's (the ratio of the
-// two weights, exp(l - top)^(1/T - 1), falls with the rank). K >= top-p's cumulative mass past the
-// sorted values, or K = M when the floor cuts first. sh.x1 +- sh.eps1 is total1 and sh.r_prefix the
-// sorted values' mass at T = 1 (top-p rows); with_tail: [sh.w_lo, sh.w_hi] bounds W and [sh.m_lo,
-// sh.m_hi] bounds M. With bins (the tail kernel's histogram of S, TailBins), the cut is placed
-// within S by the bins' cumulative mass at T = 1: every bin whose cumulative mass stays below top-p's
-// least target is kept whole, and no bin past the first whose cumulative mass reaches its largest
-// target is kept at all, which bounds the kept tail's weight by sums of whole bins. Returns the rank
-// drawn (P: past every sorted value; kNone: undecided); sh.sum gets the sorted weight.
-__device__ __noinline__ uint32_t draw_past(const FinishArgs& a, const RowParams& p, uint32_t row, uint32_t P,
-                                           bool with_tail, bool bins) {
-  Shared& sh = g_sh;
-  const double x1 = sh.x1, eps1 = sh.eps1, r_prefix = sh.r_prefix;
-  const uint32_t n = a.n, tid = threadIdx.x;
-  const uint64_t* tab = sh.tab;
-  const double top = (double)key_value(sh.mk), temp = (double)p.temp, top_p = (double)p.top_p;
-  auto val = [&](uint32_t i) -> double { return (double)packed_value(sh.sk[i]); };
-  const double g40 = gamma_n(40.0), gn = gamma_n((double)n);
-  double lo = 0.0, w_hi = __builtin_inf();
-  if (with_tail) {
-    const double w_lo = sh.w_lo, m_lo = sh.m_lo, m_hi = sh.m_hi;
-    w_hi = sh.w_hi;
-    // Top-p's target past the sorted values, at least kp: when S's whole mass is below it, the
-    // floor cuts first (or nothing but the floor cuts) and the kept tail is all of S.
-    const double kp = (p.top_p < 1.0f) ? top_p * (x1 - eps1) * (1.0 - 1e-9) - r_prefix * (1.0 + 1e-9)
-                                       : __builtin_inf();
-    if (m_hi < kp) {
-      lo = w_lo;
-    } else if (p.temp <= 1.0f) {
-      const double k1 = fmin(kp, m_lo);
-      if (k1 > 0.0 && m_hi > 0.0) lo = k1 / m_hi * w_lo;
-    }
-    if (bins && p.top_p < 1.0f) {
-      // Top-p's target past the sorted values lies in [kp, kq]. Each bin's sums are within 1e-4
-      // relative (as RowTail's) plus its flushed terms; their prefix sums add at most gamma(256).
-      const double kq = top_p * (x1 + eps1) * (1.0 + 1e-9) - r_prefix * (1.0 - 1e-9);
-      const double fl_b = (double)n * 0x1p-125, slack = 1e-4 + gamma_n(300.0);
-      const as_dev::TailBins& tb = a.tail_bins[row];
-      double bm = 0.0, bw = 0.0;
-      if (tid < as_dev::kTailBins) {
-        bm = tb.m[tid];
-        bw = tb.w[tid];
-      }
-      const double mlo = fmax(0.0, bm * (1.0 - slack) - fl_b), mhi = bm * (1.0 + slack) + fl_b;
-      const double wlo = fmax(0.0, bw * (1.0 - slack) - fl_b), whi = bw * (1.0 + slack) + fl_b;
-      const double cm_hi = __dadd_rn(block_exclusive_scan_f64(mhi, sh.red_d), mhi);
-      const double cm_lo = __dadd_rn(block_exclusive_scan_f64(mlo, sh.red_d), mlo);
-      const bool valid = tid < as_dev::kTailBins;
-      // b_min: the first bin whose cumulative mass can reach kp (the bins before it are kept whole);
-      // b_max: the first whose cumulative mass surely reaches kq (no later bin is kept).
-      const uint32_t b_min = block_min_u32<kWaves>(valid && cm_hi >= kp ? tid : kNone, sh.red_u);
-      const uint32_t b_max = block_min_u32<kWaves>(valid && cm_lo >= kq ? tid : kNone, sh.red_u);
-      const double before = block_sum_f64<kWaves>(valid && tid < b_min ? wlo : 0.0, sh.red_d);
-      const double upto = block_sum_f64<kWaves>(valid && tid <= b_max ? whi : 0.0, sh.red_d);
-      lo = fmax(lo, before * (1.0 - gamma_n(300.0)));
-      if (b_max != kNone) w_hi = fmin(w_hi, upto * (1.0 + gamma_n(300.0)));
-    }
-  }
-  for (uint32_t i = tid; i < P; i += kThreads)
-    sh.wd[i] = as_exp::exp_with(tab, __ddiv_rn(__dsub_rn(val(i), top), temp));
-  __syncthreads();
-  double loc[8], off;
-  const double SP = prefix_scan(sh, P, loc, &off);
-  double tail = (double)(n - P) * sh.wd[P - 1] * (1.0 + 4.0 * kU);
-  if (p.top_p < 1.0f && p.temp <= 1.0f) {
-    const double e_last = as_exp::exp_with(tab, __dsub_rn(val(P - 1), top));
-    const double rest = (x1 + eps1) - r_prefix * (1.0 - 2.0 * g40);
-    const double t2 = pow(e_last, 1.0 / temp - 1.0) * (1.0 + 1e-9) * (rest > 0.0 ? rest : 0.0);
-    if (t2 < tail) tail = t2;
-  }
-  tail = fmin(tail, w_hi);
-  const double slo = (SP * (1.0 - g40 - 4.0 * kU) + lo) * (1.0 - gn);
-  const double shi = (SP * (1.0 + g40 + 4.0 * kU) + tail) * (1.0 + gn);
-  const uint32_t j = decide_draw(sh, P, loc, off, sh.u01 * slo * (1.0 - 3.0 * kU), sh.u01 * shi * (1.0 + 3.0 * kU));
-  if (tid == 0) sh.sum = SP;
-  return j;
-}
-
-// --- the kernel ---------------------------------------------------------------------------------
-
-__device__ __forceinline__ void finish_row(const FinishArgs& a) {
-  Shared& sh = g_sh;
-  const uint32_t row = blockIdx.x, tid = threadIdx.x;
-  const RowParams p = a.params[row];
-  const SegStats* gst = a.stats + (uint64_t)row * a.n_seg;
-  const uint32_t n = a.n;
-  if (tid < 256) sh.tab[tid] = as_exp::kTable[tid];
-  // The host learns that the scan no longer reads the call's parameter block; the tail kernel's
-  // list empties for the next call's scan (this call's tail kernel has ended).
-  if (row == 0 && tid == 0) {
-    __hip_atomic_store(a.done, a.call, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
-    a.tail_list->count = 0u;
-  }
-  // The tail kernel's sums for the row: whole when every part of a flagged row added its own (within
-  // 3e-5 relative per term; 1e-4 to spare, and terms under 2^-126 that may have flushed to 0).
-  if (tid == 0) {
-    const RowTail t = a.tail[row];
-    const uint32_t parts = (n + as_launch::kTailLen - 1) / as_launch::kTailLen;
-    sh.have_tail = (a.share[row].gave_up != 0u && t.parts == parts && t.failed == 0u) ? 1u : 0u;
-    const double flush = (double)n * 0x1p-125;
-    sh.w_lo = fmax(0.0, t.w * (1.0 - 1e-4) - flush);
-    sh.w_hi = t.w * (1.0 + 1e-4) + flush;
-    sh.m_lo = fmax(0.0, t.m * (1.0 - 1e-4) - flush);
-    sh.m_hi = t.m * (1.0 + 1e-4) + flush;
-    sh.tail_count = t.count;
-    sh.tail_listed = (t.lost == 0u && t.count <= kTailKeep) ? 1u : 0u;
-    sh.tail_parts = t.parts;
-  }
-  // The slices' results, all loads in flight at once.
-  for (uint32_t s = tid; s < a.n_seg; s += kThreads) sh.seg[s] = gst[s];
-  __syncthreads();
-  // The row's shared words and tail sums go back to zero for the next call (this call's scan and
-  // tail kernel have ended, and their words were read above).
-  if (tid < sizeof(RowShare) / 4) reinterpret_cast<uint32_t*>(a.share + row)[tid] = 0u;
-  if (tid >= 64 && tid < 64 + sizeof(RowTail) / 4) reinterpret_cast<uint32_t*>(a.tail + row)[tid - 64] = 0u;
-  const SegStats* st = sh.seg;
-
-  if (tid == 0) {
-    uint32_t bad = kNone, gi = kNone, mk = 0, total = 0, trunc = 0, long_hist = 0;
-    float gv = 0.0f;
-    uint64_t bound = 0;
-    for (uint32_t s = 0; s < a.n_seg; ++s) {
-      const SegStats t = st[s];
-      bad = min(bad, t.nonfinite);
-      greedy_merge(gv, gi, t.greedy_val, t.greedy_idx);
-      mk = max(mk, t.max_key);
-      sh.seg_off[s] = total;
-      total += t.n_cand;
-      if (t.truncated & 1u) {
-        trunc = 1;
-        bound = max(bound, t.bound);
-      }
-      if (t.truncated & 2u) long_hist = 1;
-    }
-    sh.seg_off[a.n_seg] = total;
-    sh.bad = bad;
-    sh.gi = gi;
-    sh.mk = mk;
-    sh.total = total;
-    sh.trunc = trunc;
-    sh.bound_key = bound;
-    sh.exact = long_hist;
-    sh.stats_bad = long_hist;
-    sh.nsk = 0;
-    sh.u01 = 0.0;
-    uint32_t hb = 0;
-    const uint32_t he = as_launch::history_bounds(a, p, row, &hb);
-    sh.hist_over = (he - hb > a.max_history) ? he - hb : 0u;
-    if (bad == kNone && p.mode != kModeGreedy && !sh.hist_over) {
-      // One unit() per sampled row (sample.rs:189, 264, 276), after the row's skipped draws.
-      uint64_t s4[4];
-      uint64_t* src = a.rng_state + 4ull * p.rng_index;
-      for (int k = 0; k < 4; ++k) s4[k] = src[k];
-      for (uint32_t k = 0; k < p.rng_skip; ++k) rng_next(s4);
-      sh.u01 = rng_unit(s4);
-      if (p.flags & kFlagRngWrite)
-        for (int k = 0; k < 4; ++k) src[k] = s4[k];
-    }
-  }
-  __syncthreads();
-
-  if (sh.hist_over) {
-    if (tid == 0) {
-      a.tokens[row] = kNone;
-      a.status[row] = AS_ROW_HISTORY;
-      if (a.kept_count) a.kept_count[row] = sh.hist_over;
-    }
-    return;
-  }
-  if (sh.bad != kNone) {
-    if (tid == 0) {
-      a.tokens[row] = kNone;
-      a.status[row] = AS_ROW_NONFINITE;
-      if (a.kept_count) a.kept_count[row] = sh.bad;
-    }
-    return;
-  }
-  if (p.mode == kModeGreedy && !sh.exact) {
-    if (tid == 0) {
-      a.tokens[row] = sh.gi;
-      a.status[row] = AS_ROW_OK;
-      if (a.kept_count) a.kept_count[row] = 1;
-      if (a.kept_ids && a.kept_cap > 0) {
-        a.kept_ids[(uint64_t)row * a.kept_cap] = sh.gi;
-        if (a.kept_probs) a.kept_probs[(uint64_t)row * a.kept_cap] = 1.0;
-      }
-    }
-    return;
-  }
-
-  if ((p.mode == kModeTopK || p.mode == kModePartial) && !sh.exact) {
-    const double top = (double)key_value(sh.mk);
-    const double temp = (double)p.temp;
-    const double top_p = (double)p.top_p;
-    const bool has_floor = p.min_p > 0.0f;
-    const double floor = __dadd_rn(top, p.ln_min_p);
-    const uint64_t* tab = sh.tab;
-    auto val = [&](uint32_t i) -> double { return (double)packed_value(sh.sk[i]); };
-    auto w_temp = [&](double v) { return as_exp::exp_with(tab, __ddiv_rn(__dsub_rn(v, top), temp)); };
-    auto w_one = [&](double v) { return as_exp::exp_with(tab, __dsub_rn(v, top)); };
-
-    // The values that can matter, sorted: every value of the row ranking at or above R is a
-    // candidate (R is the largest bound of a truncated segment; for a top-k row that segment also
-    // holds k values >= R), and nothing below min-p's floor is ever kept.
-    uint64_t R = sh.trunc ? sh.bound_key : 0ull;
-    bool floor_cut = false;  // R is the floor: the value after the sorted ones is below it
-    if (p.mode == kModePartial && has_floor) {
-      const uint64_t F = (uint64_t)total_key(floor_f32(floor)) << 32;
-      if (F >= R) {
-        R = F;
-        floor_cut = true;
-      }
-    }
-    {
-      // The slices' candidates ranking >= R into sh.sk, in any order: candidate g of the row is
-      // slot g - seg_off[s] of slice s. Those below R (spilled before a slice's bound rose) drop.
-      const uint64_t* src = a.cands + (uint64_t)row * a.n_seg * a.cand_stride;
-      const uint32_t all = sh.total, lane = tid & (kWave - 1);
-      constexpr int kLoad = 4;
-      for (uint32_t g0 = 0; g0 < all; g0 += kLoad * kThreads) {
-        uint64_t tmp[kLoad];
-#pragma unroll
-        for (int q = 0; q < kLoad; ++q) {
-          const uint32_t g = g0 + tid + q * kThreads;
-          tmp[q] = 0ull;
-          if (g < all) {
-            uint32_t lo = 0, hi = a.n_seg;  // seg_off[lo] <= g < seg_off[hi]
-            while (hi - lo > 1) {
-              const uint32_t mid = (lo + hi) / 2;
-              if (sh.seg_off[mid] <= g) lo = mid;
-              else hi = mid;
-            }
-            tmp[q] = src[(uint64_t)lo * a.cand_stride + (g - sh.seg_off[lo])];
-          }
-        }
-#pragma unroll
-        for (int q = 0; q < kLoad; ++q) {
-          const bool keep = tmp[q] != 0ull && tmp[q] >= R;
-          const uint64_t m = __ballot(keep);
-          uint32_t base = 0;
-          if (lane == 0 && m) base = atomicAdd(&sh.nsk, (uint32_t)__popcll(m));
-          base = __builtin_amdgcn_readfirstlane(base);
-          const uint32_t pos = base + __builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32),
-                                                                 __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0u));
-          if (keep && pos < (uint32_t)kCap) sh.sk[pos] = tmp[q];
-        }
-      }
-      __syncthreads();
-    }
-    const uint32_t total = min(sh.nsk, (uint32_t)kCap);
-    const bool too_many = sh.nsk > (uint32_t)kCap;  // more candidates >= R than the finish holds
-    // A row whose floor set the tail kernel listed (S: every value below R and at or above the floor),
-    // and whose whole floor set's mass at T = 1 is short of top-p's target: top-p never stops inside it
-    // and min-p's floor cuts first (sample.rs:237-251), so the kept set is the candidates and all of S,
-    // sorted once, together. The candidates' mass needs no order: a parallel sum of positive terms,
-    // within gamma(40) of exact, and the margins below are far wider.
-    bool floor_set = false;
-    if (p.mode == kModePartial && has_floor && !floor_cut && !too_many && sh.have_tail && sh.tail_listed &&
-        total + sh.tail_count <= (uint32_t)kCap) {
-      bool cuts_first = true;
-      if (p.top_p < 1.0f) {
-        double X, eps;
-        slices_total(a, sh, top, temp, false, &X, &eps);
-        double mc = 0.0;
-        for (uint32_t i = tid; i < total; i += kThreads) mc += w_one(val(i));
-        mc = block_sum_f64<kWaves>(mc, sh.red_d);
-        cuts_first = (X - eps > 0.0) && (eps == eps) &&
-                     sh.m_hi < top_p * (X - eps) * (1.0 - 1e-9) - mc * (1.0 + 1e-9);
-      }
-      if (cuts_first) {
-        const uint64_t* list = reinterpret_cast<const uint64_t*>(a.scratch + (uint64_t)row * a.scratch_stride);
-        const uint32_t cnt = sh.tail_count;
-        for (uint32_t i = tid; i < cnt; i += kThreads) sh.sk[total + i] = list[i];
-        __syncthreads();
-        floor_set = true;
-      }
-    }
-    const uint32_t P = floor_set ? sort_candidates(sh, total + sh.tail_count, 0ull, sh.mk, kNone)
-                                 : sort_candidates(sh, total, R, sh.mk, p.mode == kModeTopK ? p.top_k : kNone);
-    if (tid == 0) sh.prefix = P;
-    const bool complete = (P == n);  // every value of the row is sorted
-    // A top-k row's k best are among the sorted values only when at least k rank at or above R.
-    const bool short_topk = p.mode == kModeTopK && P < p.top_k;
-
-    uint32_t keep = kNone;
-    uint32_t status = AS_ROW_OK;
-    bool drawn = false;
-    double r_prefix = 0.0;  // the top-p scan's sum of exp(l - top) over the P sorted values
-    double x1 = 0.0, eps1 = 0.0;  // total1 and its bound
-    if (floor_set) {
-      keep = P;  // every value at or above the floor
-      status |= AS_ROW_TAIL_PASS;
-    } else if (short_topk || too_many) {
-      keep = kNone;
-    } else if (p.mode == kModeTopK) {
-      // draw_full_sort over the k best (sample.rs:157-183).
-      const uint32_t k = p.top_k;
-      keep = k;
-      if (p.top_p < 1.0f) {
-        for (uint32_t i = tid; i < k; i += kThreads) sh.wd[i] = w_one(val(i));
-        __syncthreads();
-        if (tid == 0) {
-          double tot = 0.0;
-          for (uint32_t i = 0; i < k; ++i) tot = __dadd_rn(tot, sh.wd[i]);
-          double cum = 0.0;
-          uint32_t kk = k;
-          for (uint32_t i = 0; i < k; ++i) {
-            cum = __dadd_rn(cum, __ddiv_rn(sh.wd[i], tot));
-            if (cum >= top_p) {
-              kk = i + 1;
-              break;
-            }
-          }
-          sh.keep = kk;
-        }
-        __syncthreads();
-        keep = sh.keep;
-      }
-      if (has_floor) {
-        uint32_t first = keep;
-        for (uint32_t i = tid; i < keep; i += kThreads)
-          if (!(val(i) >= floor)) first = min(first, i);
-        keep = block_min_u32<kWaves>(first, sh.red_u);
-      }
-    } else if (p.top_p < 1.0f || has_floor) {
-      // draw_partial's cut (sample.rs:230-259): the first rank below min-p's floor, or the rank at
-      // which the top-p cumulative reaches top_p, whichever comes first.
-      uint32_t im = P;  // first sorted rank below the floor (P: none among the sorted)
-      if (has_floor && !floor_cut) {
-        uint32_t first = P;
-        for (uint32_t i = tid; i < P; i += kThreads)
-          if (!(val(i) >= floor)) first = min(first, i);
-        im = block_min_u32<kWaves>(first, sh.red_u);
-      }
-      // min-p's cut is known exactly when it falls among the sorted values, or right after them.
-      const bool im_exact = (im < P) || floor_cut;
-      uint32_t jl = P, jh = P;  // top-p: possible and certain trigger ranks among the sorted
-      bool ok = true;
-      if (p.top_p < 1.0f) {
-        // total1 = sum of exp(l - top) over the row in index order (sample.rs:218-222): the
-        // segments' sums rescaled, with |result - reference's left fold| <= eps.
-        double X, eps;
-        slices_total(a, sh, top, temp, false, &X, &eps);
-        x1 = X;
-        eps1 = eps;
-        ok = (X - eps > 0.0) && (eps == eps);
-        if (ok) {
-          for (uint32_t i = tid; i < P; i += kThreads) sh.wd[i] = w_one(val(i));
-          __syncthreads();
-          double loc[8], off;
-          r_prefix = prefix_scan(sh, P, loc, &off);
-          const double g40 = 2.0 * gamma_n(40.0);
-          uint32_t fl = P, fh = P;
-          const uint32_t i0 = tid * 8;
-#pragma unroll
-          for (int q = 0; q < 8; ++q) {
-            const uint32_t i = i0 + q;
-            if (i < P) {
-              const double Rv = __dadd_rn(off, loc[q]);
-              const double rel = g40 + gamma_n(2.0 * (double)i + 4.0) + 10.0 * kU;
-              const double hi = Rv * (1.0 + rel) / (X - eps);
-              const double lo = Rv * (1.0 - rel) / (X + eps);
-              if (hi >= top_p) fl = min(fl, i);
-              if (lo >= top_p) fh = min(fh, i);
-            }
-          }
-          jl = block_min_u32<kWaves>(fl, sh.red_u);
-          jh = block_min_u32<kWaves>(fh, sh.red_u);
-        }
-      }
-      if (!ok) {
-        keep = kNone;
-      } else if (im_exact && im <= jl) {
-        keep = im;  // min-p's cut, at or before any rank top-p could stop at
-      } else if (jl < P && jl == jh) {
-        keep = jh + 1;  // top-p's cut, certainly, and min-p's comes later
-      } else if (jl == P && complete) {
-        keep = n;  // neither filter stops: every value
-      } else if (jl == P && !im_exact && sh.have_tail && sh.tail_listed && P + sh.tail_count <= (uint32_t)kCap &&
-                 sh.m_hi < (p.top_p < 1.0f ? top_p * (x1 - eps1) * (1.0 - 1e-9) - r_prefix * (1.0 + 1e-9)
-                                           : __builtin_inf())) {
-        // Neither filter stops among the sorted values, and S's whole mass is short of top-p's
-        // target past them, so the floor cuts first: the kept set is the sorted values and all of
-        // S, which the tail kernel listed. Sorted in with the candidates, they take the exact draw.
-        const uint64_t* list = reinterpret_cast<const uint64_t*>(a.scratch + (uint64_t)row * a.scratch_stride);
-        const uint32_t cnt = sh.tail_count;
-        for (uint32_t i = tid; i < cnt; i += kThreads) sh.sk[P + i] = list[i];
-        __syncthreads();
-        const uint32_t P2 = sort_candidates(sh, P + cnt, 0ull, sh.mk, kNone);
-        if (tid == 0) sh.prefix = P2;
-        keep = P2;
-        status |= AS_ROW_TAIL_PASS;
-        __syncthreads();
-      } else if (jl == P && !im_exact && !a.kept_ids) {
-        // Neither filter stops among the P sorted values: the kept set runs past them.
-        if (tid == 0) {
-          sh.x1 = x1;
-          sh.eps1 = eps1;
-          sh.r_prefix = r_prefix;
-        }
-        __syncthreads();
-        // The tail kernel's sums when it took the row; else the sorted values alone first, and one
-        // pass over the row when they cannot settle the draw.
-        uint32_t j;
-        if (sh.have_tail) {
-          status |= AS_ROW_TAIL_PASS;
-          j = draw_past(a, a.params[row], row, P, true, true);
-        } else {
-          j = draw_past(a, a.params[row], row, P, false, false);
-          if (j == kNone && tail_sums(a, a.params[row], row, R, has_floor ? floor_f32(floor) : -__builtin_inff(),
-                                      key_value(sh.mk))) {
-            status |= AS_ROW_TAIL_PASS;
-            j = draw_past(a, a.params[row], row, P, true, false);
-          }
-        }
-        if (j != kNone && j < P) {
-          if (tid == 0) sh.pick = j;  // sh.sum holds the sorted weight
-          drawn = true;
-          keep = P;  // a lower bound: the kept set's full size is not known
-          status |= AS_ROW_KEPT_PARTIAL;
-        } else {
-          keep = kNone;
-        }
-        __syncthreads();
-      } else {
-        keep = kNone;
-      }
-    } else {
-      // No filter (sample.rs:274-292): the total over the row in index order, from the segments'
-      // sums with an error bound, then the first rank whose cumulative weight passes u.
-      double X, eps;
-      slices_total(a, sh, top, temp, true, &X, &eps);
-      for (uint32_t i = tid; i < P; i += kThreads) sh.wd[i] = w_temp(val(i));
-      __syncthreads();
-      keep = kNone;
-      if (X - eps > 0.0 && eps == eps) {
-        double loc[8], off;
-        prefix_scan(sh, P, loc, &off);
-        const uint32_t j = decide_draw(sh, P, loc, off, sh.u01 * (X - eps) * (1.0 - 3.0 * kU),
-                                       sh.u01 * (X + eps) * (1.0 + 3.0 * kU));
-        uint32_t pick = kNone;
-        if (j != kNone && j < P) pick = j;
-        else if (j == P && complete) pick = n - 1;  // u past every cumulative: the last value
-        if (pick != kNone) {
-          if (tid == 0) {
-            sh.pick = pick;
-            sh.sum = X;
-          }
-          drawn = true;
-          keep = n;
-        }
-        __syncthreads();
-      }
-    }
-
-    if (keep != kNone && !drawn) {
-      // The draw over the kept prefix (sample.rs:184-197, 260-272): u = unit() * sum(w), then the
-      // first rank whose cumulative weight exceeds u. Both sums are the reference's left folds in
-      // rank order; past a few hundred tokens they come from a parallel scan with an error bound,
-      // and the sequential folds run only when the bound cannot decide.
-      for (uint32_t i = tid; i < keep; i += kThreads) sh.wd[i] = w_temp(val(i));
-      __syncthreads();
-      if (keep > 256) {
-        double loc[8], off;
-        const double S = prefix_scan(sh, keep, loc, &off);
-        const double d = gamma_n((double)keep) + gamma_n(40.0) + 4.0 * kU;
-        const uint32_t j = decide_draw(sh, keep, loc, off, sh.u01 * S * (1.0 - d), sh.u01 * S * (1.0 + d));
-        if (j != kNone) {
-          if (tid == 0) {
-            sh.pick = (j < keep) ? j : keep - 1;  // past every cumulative: the last kept
-            sh.sum = S;
-          }
-          drawn = true;
-        }
-        __syncthreads();
-      }
-      if (!drawn) {
-        if (tid == 0) {
-          double tot = 0.0;
-          for (uint32_t i = 0; i < keep; ++i) tot = __dadd_rn(tot, sh.wd[i]);
-          const double u = __dmul_rn(sh.u01, tot);
-          double cum = 0.0;
-          uint32_t pick = keep - 1;
-          for (uint32_t i = 0; i < keep; ++i) {
-            cum = __dadd_rn(cum, sh.wd[i]);
-            if (u < cum) {
-              pick = i;
-              break;
-            }
-          }
-          sh.pick = pick;
-          sh.sum = tot;
-        }
-        __syncthreads();
-      }
-    }
-
-    if (keep == kNone) {
-      if (tid == 0) sh.exact = 1;
-    } else {
-      const uint32_t pick = sh.pick;
-      const double tot = sh.sum;
-      if (tid == 0) {
-        a.tokens[row] = packed_id(sh.sk[pick]);
-        a.status[row] = status;
-        if (a.kept_count) a.kept_count[row] = keep;
-      }
-      if (a.kept_ids) {
-        const uint32_t m = min(min(keep, a.kept_cap), sh.prefix);
-        for (uint32_t j = tid; j < m; j += kThreads) {
-          a.kept_ids[(uint64_t)row * a.kept_cap + j] = packed_id(sh.sk[j]);
-          if (a.kept_probs) a.kept_probs[(uint64_t)row * a.kept_cap + j] = __ddiv_rn(sh.wd[j], tot);
-        }
-      }
-    }
-    __syncthreads();
-  } else {
-    if (tid == 0) sh.exact = 1;
-    __syncthreads();
-  }
-
-  if (sh.exact) {
-    __syncthreads();
-    if (!deep_row(a, a.params[row], row)) {
-      __syncthreads();
-      exact_row(a, a.params[row], row);
-    }
-  }
-}
-
-__global__ __launch_bounds__(kThreads) void finish_kernel(const FinishArgs* __restrict__ ap) {
+__global__ __launch_bounds__(1024) void finish_kernel(const FinishArgs* __restrict__ ap) {
   const FinishArgs& a = *ap;
-  finish_row(a);
+  as_fin_sliced::finish_row(a, blockIdx.x);
   // The row's tail histogram goes back to zero for the next call once this row is done with it
   // (every path above has ended, in every thread).
   __syncthreads();
-  if (g_sh.tail_parts != 0u && threadIdx.x < as_dev::kTailBins) {
+  if (as_fin_sliced::shm().tail_parts != 0u && threadIdx.x < as_dev::kTailBins) {
     a.tail_bins[blockIdx.x].m[threadIdx.x] = 0.0;
     a.tail_bins[blockIdx.x].w[threadIdx.x] = 0.0;
   }
@@ -1789,7 +49,7 @@ __global__ __launch_bounds__(kThreads) void finish_kernel(const FinishArgs* __re
 namespace as_launch {
 
 hipError_t finish(hipStream_t stream, uint32_t n_rows, const FinishArgs* a) {
-  hipLaunchKernelGGL(finish_kernel, dim3(n_rows), dim3(kThreads), 0, stream, a);
+  hipLaunchKernelGGL(finish_kernel, dim3(n_rows), dim3(1024), 0, stream, a);
   return hipGetLastError();
 }
 

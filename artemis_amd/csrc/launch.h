@@ -67,6 +67,8 @@ struct FinishArgs {
   as_dev::TailBins* tail_bins;  // per row: the tail kernel's histogram of S
   as_dev::TailList* tail_list;  // the rows the scan flagged for the tail kernel
   uint32_t max_history;     // a row with more history ids than this is refused (AS_ROW_HISTORY)
+  uint32_t fused;           // the row kernel: each workgroup scans and finishes its own row
+  uint32_t* fused_count;    // the row kernel: workgroups that have ended (the last writes `done`)
 };
 
 // The row's history ids are hist_ids[*hb, return value), from the CSR offsets or the row's range.
@@ -113,6 +115,19 @@ hipError_t scan(hipStream_t stream, bool vec, const float* logits, const float* 
                 as_dev::TailList* tail_list, const RowOrder& order);
 
 hipError_t finish(hipStream_t stream, uint32_t n_rows, const FinishArgs* a);
+
+// The row kernel (fused.hip): one 512-thread workgroup scans a whole row and chooses its token, for
+// rows of at most kRowMaxVocab values (its history bitmap lives in LDS). Batches of at least
+// kRowMinRows rows would take it by default; that is off (the sliced scan is faster on mixed batches,
+// where rows whose draw runs past their sorted values need a second pass that one workgroup makes
+// slowly), so it runs when a caller asks for it (as_debug_path).
+constexpr uint32_t kRowMaxVocab = 262144;
+constexpr uint32_t kRowMinRows = 0xFFFFFFFFu;
+hipError_t sample_rows(hipStream_t stream, bool vec, const float* logits, const float* zero, uint64_t row_stride,
+                       uint32_t n, uint32_t n_rows, const void* block_in, void* block_out, as_dev::RowShare* share,
+                       const uint32_t* hist_off, const uint32_t* hist_ids, const uint32_t* extra_ids,
+                       as_dev::SegStats* stats, uint64_t* cands, uint32_t cand_stride, const FinishArgs& a);
+size_t row_kernel_lds();
 
 // Between the scan and the finish: the weights of S for min-p rows whose scan gave up keeping the
 // floor set whole (a no-op for the other rows).

@@ -19,12 +19,19 @@ PROB_RTOL = 1e-5
 VOCAB = 248_320
 
 
-@pytest.fixture(scope="module")
-def ctx():
+# Every test runs on both kernel paths: rows spread over several workgroups (the sliced scan, then
+# the finish kernel) and one workgroup per row (the row kernel), whatever the batch size.
+PATHS = {"sliced": 1, "row": 2}
+
+
+@pytest.fixture(scope="module", params=list(PATHS), ids=list(PATHS))
+def ctx(request):
     if not torch.cuda.is_available():
         pytest.skip("no GPU")
     from artemis_amd import Context
     c = Context(max_rows=1024, max_vocab=VOCAB)
+    c.debug_path(PATHS[request.param])
+    c.test_path = request.param
     yield c
     c.close()
 
@@ -283,8 +290,11 @@ def test_tail_histogram_draws_match_the_oracle(ctx):
     # At the row's own T (0.36) every draw took the tail kernel's sums and bins, and the bins
     # settle nearly all of them (the first bound alone left about 1 in 20 to the deep path). At
     # T = 1.3 the draw usually lands past the sorted values, which only the deep path can take.
-    assert seen[()] == 128, seen
-    assert deep[()] <= 3, deep
+    # The row kernel has no tail kernel: its rows bound the unsorted tail with the finish's own
+    # pass when the sorted values alone cannot (the tokens above are checked on both paths).
+    if ctx.test_path == "sliced":
+        assert seen[()] == 128, seen
+        assert deep[()] <= 3, deep
 
 
 def test_large_floor_sets_match_the_oracle(ctx):
@@ -308,8 +318,9 @@ def test_large_floor_sets_match_the_oracle(ctx):
     want = oracle_rows(rows, params, seeds, hists, kept_cap=16)
     check_rows(g, want, params, kept_cap=16, label="floor sets")
     # The tail kernel takes the first 16 rows the scan flags (in the order it flags them); the finish
-    # kernel settles the rest.
-    assert ((g["status"] & AS_ROW_TAIL_PASS) != 0).sum() >= 16, g["status"]
+    # kernel settles the rest. (The row kernel's sixteen waves keep such floor sets whole.)
+    if ctx.test_path == "sliced":
+        assert ((g["status"] & AS_ROW_TAIL_PASS) != 0).sum() >= 16, g["status"]
 
 
 def test_whole_vocabulary_plants(ctx):
