@@ -113,6 +113,124 @@ __device__ __forceinline__ double wave_seq_total(const double* w, uint32_t m) {
   return carry;
 }
 
+// draw_full_sort's top-p cut (sample.rs:166-179) over w[0..m) in the reference's order: the total,
+// then cum += w_i / total until cum reaches top_p; returns the kept count (m when it never does).
+__device__ __forceinline__ uint32_t wave_seq_cut(const double* w, uint32_t m, double top_p) {
+  const uint32_t lane = threadIdx.x & (kWave - 1);
+  const double tot = wave_seq_total(w, m);
+  double carry = 0.0;
+  for (uint32_t b0 = 0; b0 < m; b0 += kWave) {
+    const uint32_t i = b0 + lane;
+    const double q = (i < m) ? __ddiv_rn(w[i], tot) : 0.0;
+    const double cum = wave_seq_prefix(q, carry);
+    const uint64_t hit = __ballot(i < m && cum >= top_p);
+    if (hit) return b0 + (uint32_t)__builtin_ctzll(hit) + 1;
+    carry = wave_lane63(cum);
+  }
+  return m;
+}
+// The draw over w[0..m) in the reference's order (sample.rs:184-197, 260-272): u = u01 * total,
+// then the first rank whose cumulative weight passes u (the last when none does). *tot gets the total.
+__device__ __forceinline__ uint32_t wave_seq_draw(const double* w, uint32_t m, double u01, double* tot) {
+  const uint32_t lane = threadIdx.x & (kWave - 1);
+  const double t = wave_seq_total(w, m);
+  const double u = __dmul_rn(u01, t);
+  *tot = t;
+  double carry = 0.0;
+  for (uint32_t b0 = 0; b0 < m; b0 += kWave) {
+    const uint32_t i = b0 + lane;
+    const double cum = wave_seq_prefix((i < m) ? w[i] : 0.0, carry);
+    const uint64_t hit = __ballot(i < m && u < cum);
+    if (hit) return b0 + (uint32_t)__builtin_ctzll(hit);
+    carry = wave_lane63(cum);
+  }
+  return m - 1;
+}
+
+// --- certified decisions on one wave ----------------------------------------------------------
+//
+// Up to kWPer * 64 sorted values, lane l holding ranks kWPer*l .. kWPer*l + kWPer-1 in registers.
+// Their prefix sums come from a fold of kWPer in the lane and a scan over the lanes: each is a sum
+// of positive terms through at most kWPer + 7 roundings, within gamma(kWPer + 7) of its exact value,
+// as the reference's left fold of j + 1 terms is within gamma(j) of it. A decision the two bounds
+// agree on is the reference's; otherwise the caller takes the sequential fold above.
+constexpr int kWPer = 4;
+constexpr uint32_t kWaveMax = kWPer * kWave;
+
+// Inclusive prefix sums pre[] of the values w[] in rank order; returns the total to every lane.
+__device__ __forceinline__ double wave_prefix(const double (&w)[kWPer], double (&pre)[kWPer]) {
+  const uint32_t lane = threadIdx.x & (kWave - 1);
+  double run = 0.0;
+#pragma unroll
+  for (int q = 0; q < kWPer; ++q) {
+    run = __dadd_rn(run, w[q]);
+    pre[q] = run;
+  }
+  double incl = run;
+#pragma unroll
+  for (int o = 1; o < kWave; o <<= 1) {
+    const double y = __shfl_up(incl, o, kWave);
+    if (lane >= (uint32_t)o) incl = __dadd_rn(incl, y);
+  }
+  double excl = __shfl_up(incl, 1, kWave);
+  if (lane == 0) excl = 0.0;
+#pragma unroll
+  for (int q = 0; q < kWPer; ++q) pre[q] = __dadd_rn(excl, pre[q]);
+  return __shfl(incl, kWave - 1, kWave);
+}
+// The first rank below m whose flag is set (m when none).
+__device__ __forceinline__ uint32_t wave_first(const bool (&f)[kWPer], uint32_t m) {
+  const uint32_t i0 = (threadIdx.x & (kWave - 1)) * kWPer;
+  uint32_t first = m;
+#pragma unroll
+  for (int q = kWPer - 1; q >= 0; --q)
+    if (f[q] && i0 + q < m) first = i0 + q;
+  return wave_min_u32(first);
+}
+// draw_full_sort's top-p cut over the m values' weights w (zero past m): the kept count, or kNone
+// when the bounds cannot decide. The reference's cumulative at rank j, its left fold of
+// fl(w_i / total), lies within gamma(j + 1) of exact / its total, which is within gamma(m) of exact;
+// ours (prefix / total) within gamma(kWPer + 8) of exact.
+__device__ __forceinline__ uint32_t wave_topp_cut(const double (&w)[kWPer], uint32_t m, double top_p) {
+  double pre[kWPer];
+  const double S = wave_prefix(w, pre);
+  const uint32_t i0 = (threadIdx.x & (kWave - 1)) * kWPer;
+  const double base = 2.0 * gamma_n(2.0 * kWPer + 16.0) + gamma_n(2.0 * (double)m + 4.0) + 10.0 * kU;
+  bool lo[kWPer], hi[kWPer];
+#pragma unroll
+  for (int q = 0; q < kWPer; ++q) {
+    const double c = __ddiv_rn(pre[q], S);
+    const double rel = base + gamma_n(2.0 * (double)(i0 + q) + 4.0);
+    lo[q] = c * (1.0 + rel) >= top_p;  // the reference's cumulative may have reached top_p
+    hi[q] = c * (1.0 - rel) >= top_p;  // it certainly has
+  }
+  const uint32_t jl = wave_first(lo, m), jh = wave_first(hi, m);
+  if (jl != jh) return kNone;
+  return jh < m ? jh + 1 : m;
+}
+// The draw over the m values' weights w (zero past m) with u = u01 * total (sample.rs:184-197,
+// 260-272): the first rank whose cumulative passes u (m - 1 when none does), or kNone when the
+// bounds cannot decide. *tot gets our total (within gamma(m) + gamma(kWPer + 8) of the reference's).
+__device__ __forceinline__ uint32_t wave_draw(const double (&w)[kWPer], uint32_t m, double u01, double* tot) {
+  double pre[kWPer];
+  const double S = wave_prefix(w, pre);
+  *tot = S;
+  const uint32_t i0 = (threadIdx.x & (kWave - 1)) * kWPer;
+  const double g = gamma_n(2.0 * kWPer + 16.0);
+  const double d = gamma_n((double)m + 1.0) + g + 4.0 * kU;
+  const double ulo = u01 * S * (1.0 - d) * (1.0 - 3.0 * kU), uhi = u01 * S * (1.0 + d) * (1.0 + 3.0 * kU);
+  bool may[kWPer], sure[kWPer];
+#pragma unroll
+  for (int q = 0; q < kWPer; ++q) {
+    const double rel = gamma_n((double)(i0 + q) + 1.0) + g + 4.0 * kU;
+    may[q] = pre[q] * (1.0 + rel) > ulo;
+    sure[q] = pre[q] * (1.0 - rel) > uhi;
+  }
+  const uint32_t jp = wave_first(may, m), jc = wave_first(sure, m);
+  if (jp != jc) return kNone;
+  return jc < m ? jc : m - 1;
+}
+
 // --- the exact-order path ---------------------------------------------------------------------
 
 // Thread 0's left-to-right f64 fold of term(i), i in [0, m), staged through LDS in tiles that all
@@ -415,11 +533,13 @@ __device__ uint32_t block_exclusive_scan_u32(uint32_t x, uint32_t* wave_tot, uin
 //     row's largest value by adding |dm| * sum), and 4 * 2^-53 per unit for its rescale;
 //   - the reference's argument roundings, 2^-53 * |d| per term and per rounding (babs);
 //   - terms the scan's exp flushed to 0: below 2^-126 each.
+// Wave 0 adds the slices' parts, one slice per lane, in a wave reduction: any order of adding n_seg
+// positive parts is within n_seg * 2^-53 of their left fold, which the bound's n_seg term covers.
 __device__ __forceinline__ void slices_total(const FinishArgs& a, Shared& sh, double top, double temp,
                                              bool by_temp, double* X, double* eps) {
-  if (threadIdx.x == 0) {
+  if (threadIdx.x < kWave) {
     double x = 0.0, babs = 0.0, own = 0.0;
-    for (uint32_t s = 0; s < a.n_seg; ++s) {
+    for (uint32_t s = threadIdx.x; s < a.n_seg; s += kWave) {
       const SegStats& t = sh.seg[s];
       if (t.sum == 0.0) continue;
       const double ms = (double)t.sum_ref;
@@ -435,9 +555,14 @@ __device__ __forceinline__ void slices_total(const FinishArgs& a, Shared& sh, do
       babs = __dadd_rn(babs, pabs);
       own = __dadd_rn(own, __dadd_rn(__dmul_rn(part, (double)t.err_rel + 4.0 * kU), __dmul_rn(pabs, (double)t.err_abs)));
     }
-    const double terms = (double)a.n + (double)a.n_seg + 64.0;
-    sh.x = x;
-    sh.eps = 1.02 * (kU * ((by_temp ? 2.1 : 1.1) * babs + terms * x) + own) + (double)a.n * 0x1p-126;
+    x = wave_sum_f64(x);
+    babs = wave_sum_f64(babs);
+    own = wave_sum_f64(own);
+    if (threadIdx.x == 0) {
+      const double terms = (double)a.n + (double)a.n_seg + 64.0;
+      sh.x = x;
+      sh.eps = 1.02 * (kU * ((by_temp ? 2.1 : 1.1) * babs + terms * x) + own) + (double)a.n * 0x1p-126;
+    }
   }
   __syncthreads();
   *X = sh.x;
@@ -467,13 +592,26 @@ __device__ __forceinline__ uint32_t sort_candidates(Shared& sh, uint32_t total, 
       ++mine;
     }
   }
-  kmin = block_min_u32<kWaves>(kmin, sh.red_u);
-  const uint32_t P = block_sum_u32<kWaves>(mine, sh.red_u);
+  // One barrier pair gives every thread the smallest key and the count; the buckets clear before it.
+  for (uint32_t b = tid; b < kBuckets; b += kThreads) sh.bcnt[b] = 0;
+  kmin = wave_min_u32(kmin);
+  mine = wave_sum_u32(mine);
+  __syncthreads();
+  if ((tid & (kWave - 1)) == 0) {
+    sh.red_u[tid / kWave] = kmin;
+    sh.base[tid / kWave] = mine;
+  }
+  __syncthreads();
+  uint32_t P = 0;
+  kmin = 0xFFFFFFFFu;
+#pragma unroll
+  for (int w = 0; w < kWaves; ++w) {
+    kmin = min(kmin, sh.red_u[w]);
+    P += sh.base[w];
+  }
   const uint32_t range = kmax - kmin;
   uint32_t shift = 0;
   while ((range >> shift) >= kBuckets) ++shift;
-  for (uint32_t b = tid; b < kBuckets; b += kThreads) sh.bcnt[b] = 0;
-  __syncthreads();
   uint32_t slot[kPerT];
 #pragma unroll
   for (int q = 0; q < kPerT; ++q) {
@@ -482,20 +620,25 @@ __device__ __forceinline__ uint32_t sort_candidates(Shared& sh, uint32_t total, 
     if (i < total && xs[q] >= R) slot[q] = atomicAdd(&sh.bcnt[(kmax - (uint32_t)(xs[q] >> 32)) >> shift], 1u);
   }
   __syncthreads();
-  {
-    // Bucket starts: kBPer consecutive buckets per thread, then the block's scan.
-    constexpr uint32_t kBPer = kBuckets / kThreads;
-    uint32_t cs[kBPer], run = 0;
+  if (tid < kWave) {
+    // Bucket starts on wave 0: kB consecutive buckets per lane, then a scan over the lanes.
+    constexpr uint32_t kB = kBuckets / kWave;
+    uint32_t cs[kB], run = 0;
 #pragma unroll
-    for (uint32_t q = 0; q < kBPer; ++q) {
-      cs[q] = sh.bcnt[tid * kBPer + q];
+    for (uint32_t q = 0; q < kB; ++q) {
+      cs[q] = sh.bcnt[tid * kB + q];
       run += cs[q];
     }
-    uint32_t all;
-    uint32_t off = block_exclusive_scan_u32(run, sh.red_u, &all);
+    uint32_t incl = run;
 #pragma unroll
-    for (uint32_t q = 0; q < kBPer; ++q) {
-      sh.bstart[tid * kBPer + q] = off;
+    for (int o = 1; o < kWave; o <<= 1) {
+      const uint32_t y = (uint32_t)__shfl_up((int)incl, o, kWave);
+      if (tid >= (uint32_t)o) incl += y;
+    }
+    uint32_t off = incl - run;
+#pragma unroll
+    for (uint32_t q = 0; q < kB; ++q) {
+      sh.bstart[tid * kB + q] = off;
       off += cs[q];
     }
   }
@@ -1381,7 +1524,17 @@ __device__ __forceinline__ void finish_row(const FinishArgs& a, uint32_t row) {
     sh.tail_listed = (t.lost == 0u && t.count <= kTailKeep) ? 1u : 0u;
     sh.tail_parts = t.parts;
   }
-  // The slices' results, all loads in flight at once.
+  // The slices' results, all loads in flight at once, with the row's RNG state and history bounds
+  // (thread 0 keeps them in registers for the merge below).
+  const bool draws = p.mode != kModeGreedy;
+  uint64_t s4[4] = {0ull, 0ull, 0ull, 0ull};
+  uint64_t* src = a.rng_state + 4ull * p.rng_index;
+  uint32_t hb = 0, he = 0;
+  if (tid == 0) {
+    if (draws)
+      for (int k = 0; k < 4; ++k) s4[k] = src[k];
+    he = as_launch::history_bounds(a, p, row, &hb);
+  }
   for (uint32_t s = tid; s < a.n_seg; s += kThreads) sh.seg[s] = gst[s];
   __syncthreads();
   // The row's shared words and tail sums go back to zero for the next call (this call's scan and
@@ -1390,46 +1543,64 @@ __device__ __forceinline__ void finish_row(const FinishArgs& a, uint32_t row) {
   if (tid >= 64 && tid < 64 + sizeof(RowTail) / 4) reinterpret_cast<uint32_t*>(a.tail + row)[tid - 64] = 0u;
   const SegStats* st = sh.seg;
 
-  if (tid == 0) {
-    uint32_t bad = kNone, gi = kNone, mk = 0, total = 0, trunc = 0, long_hist = 0;
+  if (tid < kWave) {
+    // Wave 0 merges the slices' results, one slice per lane (a row has at most a few hundred): the
+    // non-finite index and the largest key by reductions, the greedy pick by its total order (a row
+    // holding a NaN or an infinity is refused before that pick matters), and each slice's first
+    // candidate's place by a prefix of the counts in slice order.
+    const uint32_t lane = tid;
+    uint32_t bad = kNone, gi = kNone, mk = 0, trunc = 0, long_hist = 0, run = 0;
     float gv = 0.0f;
     uint64_t bound = 0;
-    for (uint32_t s = 0; s < a.n_seg; ++s) {
-      const SegStats t = st[s];
-      bad = min(bad, t.nonfinite);
-      greedy_merge(gv, gi, t.greedy_val, t.greedy_idx);
-      mk = max(mk, t.max_key);
-      sh.seg_off[s] = total;
-      total += t.n_cand;
-      if (t.truncated & 1u) {
-        trunc = 1;
-        bound = max(bound, t.bound);
+    for (uint32_t b0 = 0; b0 < a.n_seg; b0 += kWave) {
+      const uint32_t s = b0 + lane;
+      uint32_t c = 0;
+      if (s < a.n_seg) {
+        const SegStats& t = st[s];
+        bad = min(bad, t.nonfinite);
+        greedy_merge(gv, gi, t.greedy_val, t.greedy_idx);
+        mk = max(mk, t.max_key);
+        c = t.n_cand;
+        if (t.truncated & 1u) {
+          trunc = 1;
+          bound = max(bound, t.bound);
+        }
+        if (t.truncated & 2u) long_hist = 1;
       }
-      if (t.truncated & 2u) long_hist = 1;
+      uint32_t incl = c;
+      for (int o = 1; o < kWave; o <<= 1) {
+        const uint32_t y = (uint32_t)__shfl_up((int)incl, o, kWave);
+        if (lane >= (uint32_t)o) incl += y;
+      }
+      if (s < a.n_seg) sh.seg_off[s] = run + incl - c;
+      run += (uint32_t)__shfl((int)incl, kWave - 1, kWave);
     }
-    sh.seg_off[a.n_seg] = total;
-    sh.bad = bad;
-    sh.gi = gi;
-    sh.mk = mk;
-    sh.total = total;
-    sh.trunc = trunc;
-    sh.bound_key = bound;
-    sh.exact = long_hist;
-    sh.stats_bad = long_hist;
-    sh.nsk = 0;
-    sh.u01 = 0.0;
-    uint32_t hb = 0;
-    const uint32_t he = as_launch::history_bounds(a, p, row, &hb);
-    sh.hist_over = (he - hb > a.max_history) ? he - hb : 0u;
-    if (bad == kNone && p.mode != kModeGreedy && !sh.hist_over) {
-      // One unit() per sampled row (sample.rs:189, 264, 276), after the row's skipped draws.
-      uint64_t s4[4];
-      uint64_t* src = a.rng_state + 4ull * p.rng_index;
-      for (int k = 0; k < 4; ++k) s4[k] = src[k];
-      for (uint32_t k = 0; k < p.rng_skip; ++k) rng_next(s4);
-      sh.u01 = rng_unit(s4);
-      if (p.flags & kFlagRngWrite)
-        for (int k = 0; k < 4; ++k) src[k] = s4[k];
+    bad = wave_min_u32(bad);
+    mk = wave_max_u32(mk);
+    trunc = wave_max_u32(trunc);
+    long_hist = wave_max_u32(long_hist);
+    bound = wave_max_u64(bound);
+    wave_greedy(gv, gi);
+    if (lane == 0) {
+      sh.seg_off[a.n_seg] = run;
+      sh.bad = bad;
+      sh.gi = gi;
+      sh.mk = mk;
+      sh.total = run;
+      sh.trunc = trunc;
+      sh.bound_key = bound;
+      sh.exact = long_hist;
+      sh.stats_bad = long_hist;
+      sh.nsk = 0;
+      sh.u01 = 0.0;
+      sh.hist_over = (he - hb > a.max_history) ? he - hb : 0u;
+      if (bad == kNone && draws && !sh.hist_over) {
+        // One unit() per sampled row (sample.rs:189, 264, 276), after the row's skipped draws.
+        for (uint32_t k = 0; k < p.rng_skip; ++k) rng_next(s4);
+        sh.u01 = rng_unit(s4);
+        if (p.flags & kFlagRngWrite)
+          for (int k = 0; k < 4; ++k) src[k] = s4[k];
+      }
     }
   }
   __syncthreads();
@@ -1568,39 +1739,49 @@ __device__ __forceinline__ void finish_row(const FinishArgs& a, uint32_t row) {
     } else if (short_topk || too_many) {
       keep = kNone;
     } else if (p.mode == kModeTopK) {
-      // draw_full_sort over the k best (sample.rs:157-183).
+      // draw_full_sort over the k best (sample.rs:157-197), on wave 0 from registers: top-p's cut,
+      // min-p's floor (the ranks are sorted, so it keeps a prefix) and the draw, each decided by
+      // bounds and by the reference's sequential folds only when the bounds cannot.
+      static_assert(as_launch::kTopKMax <= kWaveMax, "one wave holds a top-k");
       const uint32_t k = p.top_k;
-      keep = k;
-      if (p.top_p < 1.0f) {
-        for (uint32_t i = tid; i < k; i += kThreads) sh.wd[i] = w_one(val(i));
-        __syncthreads();
-        if (tid < kWave) {
-          // total, then cum += w_i / total until it reaches top_p (sample.rs:169-178), on wave 0.
-          const double tot = wave_seq_total(sh.wd, k);
-          double carry = 0.0;
-          uint32_t kk = k;
-          for (uint32_t b0 = 0; b0 < k; b0 += kWave) {
-            const uint32_t i = b0 + tid;
-            const double q = (i < k) ? __ddiv_rn(sh.wd[i], tot) : 0.0;
-            const double cum = wave_seq_prefix(q, carry);
-            const uint64_t hit = __ballot(i < k && cum >= top_p);
-            if (hit) {
-              kk = b0 + (uint32_t)__builtin_ctzll(hit) + 1;
-              break;
-            }
-            carry = wave_lane63(cum);
+      if (tid < kWave) {
+        const uint32_t i0 = tid * kWPer;
+        uint32_t kk = k;
+        if (p.top_p < 1.0f) {
+          double w[kWPer];
+#pragma unroll
+          for (int q = 0; q < kWPer; ++q) w[q] = (i0 + q < k) ? w_one(val(i0 + q)) : 0.0;
+          kk = wave_topp_cut(w, k, top_p);
+          if (kk == kNone) {
+#pragma unroll
+            for (int q = 0; q < kWPer; ++q)
+              if (i0 + q < k) sh.wd[i0 + q] = w[q];
+            kk = wave_seq_cut(sh.wd, k, top_p);
           }
-          if (tid == 0) sh.keep = kk;
         }
-        __syncthreads();
-        keep = sh.keep;
+        if (has_floor) {
+          bool below[kWPer];
+#pragma unroll
+          for (int q = 0; q < kWPer; ++q) below[q] = (i0 + q < kk) && !(val(i0 + q) >= floor);
+          kk = wave_first(below, kk);
+        }
+        double w[kWPer], tot = 0.0;
+#pragma unroll
+        for (int q = 0; q < kWPer; ++q) {
+          w[q] = (i0 + q < kk) ? w_temp(val(i0 + q)) : 0.0;
+          if (i0 + q < kk) sh.wd[i0 + q] = w[q];  // the kept probabilities' weights
+        }
+        uint32_t pick = wave_draw(w, kk, sh.u01, &tot);
+        if (pick == kNone) pick = wave_seq_draw(sh.wd, kk, sh.u01, &tot);
+        if (tid == 0) {
+          sh.keep = kk;
+          sh.pick = pick;
+          sh.sum = tot;
+        }
       }
-      if (has_floor) {
-        uint32_t first = keep;
-        for (uint32_t i = tid; i < keep; i += kThreads)
-          if (!(val(i) >= floor)) first = min(first, i);
-        keep = block_min_u32<kWaves>(first, sh.red_u);
-      }
+      __syncthreads();
+      keep = sh.keep;
+      drawn = true;
     } else if (p.top_p < 1.0f || has_floor) {
       // draw_partial's cut (sample.rs:230-259): the first rank below min-p's floor, or the rank at
       // which the top-p cumulative reaches top_p, whichever comes first.
@@ -1756,21 +1937,18 @@ __device__ __forceinline__ void finish_row(const FinishArgs& a, uint32_t row) {
       if (!drawn) {
         if (tid < kWave) {
           // u = unit() * sum(w), then the first rank whose cumulative weight passes u
-          // (sample.rs:184-197, 260-272), on wave 0.
-          const double tot = wave_seq_total(sh.wd, keep);
-          const double u = __dmul_rn(sh.u01, tot);
-          double carry = 0.0;
-          uint32_t pick = keep - 1;
-          for (uint32_t b0 = 0; b0 < keep; b0 += kWave) {
-            const uint32_t i = b0 + tid;
-            const double cum = wave_seq_prefix((i < keep) ? sh.wd[i] : 0.0, carry);
-            const uint64_t hit = __ballot(i < keep && u < cum);
-            if (hit) {
-              pick = b0 + (uint32_t)__builtin_ctzll(hit);
-              break;
-            }
-            carry = wave_lane63(cum);
+          // (sample.rs:184-197, 260-272), on wave 0: by bounds for up to kWaveMax kept values, else
+          // (or when they cannot decide) by the reference's sequential folds.
+          double tot = 0.0;
+          uint32_t pick = kNone;
+          if (keep <= kWaveMax) {
+            const uint32_t i0 = tid * kWPer;
+            double w[kWPer];
+#pragma unroll
+            for (int q = 0; q < kWPer; ++q) w[q] = (i0 + q < keep) ? sh.wd[i0 + q] : 0.0;
+            pick = wave_draw(w, keep, sh.u01, &tot);
           }
+          if (pick == kNone) pick = wave_seq_draw(sh.wd, keep, sh.u01, &tot);
           if (tid == 0) {
             sh.pick = pick;
             sh.sum = tot;
