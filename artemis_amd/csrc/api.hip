@@ -306,7 +306,7 @@ int run_rows(as_ctx* c, const Plan& pl, const RowParams* rows, const float* logi
   bool floor_rows = false;
   for (uint32_t r = 0; r < n_rows && !floor_rows; ++r)
     floor_rows = rows[r].mode == as_dev::kModePartial && rows[r].min_p > 0.0f;
-  if (floor_rows) AS_HIP(c, as_launch::tail(c->stream, n_rows, n, a));
+  if (floor_rows) AS_HIP(c, as_launch::tail(c->stream, n_rows, n, c->d_args));
   AS_HIP(c, as_launch::finish(c->stream, n_rows, c->d_args));
   c->share_dirty = false;
   if (e2) AS_HIP(c, hipEventRecord(e2, c->stream));

@@ -32,6 +32,8 @@ using as_launch::FinishArgs;
 
 namespace {
 
+// The arguments are read from device memory (the scan's copy of the pinned block), which costs each
+// workgroup less than a large kernel-argument block.
 __global__ __launch_bounds__(1024) void finish_kernel(const FinishArgs* __restrict__ ap) {
   const FinishArgs& a = *ap;
   as_fin_sliced::finish_row(a, blockIdx.x);

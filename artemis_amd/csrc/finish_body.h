@@ -22,6 +22,10 @@ constexpr int kStage = 4096;
 constexpr double kU = 1.1102230246251565e-16;  // 2^-53, the unit roundoff
 
 __device__ __forceinline__ double gamma_n(double n) { return n * kU / (1.0 - n * kU); }
+// An upper bound of gamma_n with no division, for n * kU below 2^-30 (n below 2^22 here):
+// gamma_n = n u (1 + n u + ...) <= n u (1 + 2 n u), and the margin 1e-9 also covers the products'
+// own roundings.
+__device__ __forceinline__ double gamma_ub(double n) { return n * (kU * (1.0 + 1e-9)); }
 
 struct Shared {
   uint64_t sk[kCap];  // candidates (exact path: per-wave digit counts)
@@ -42,6 +46,7 @@ struct Shared {
       tail_listed, tail_parts;
   uint64_t bound_key;
   double u01, sum, x, eps, x1, eps1, r_prefix, w_lo, w_hi, m_lo, m_hi;
+  uint32_t draw_rng;  // the row draws: its stream advances once the candidates are in flight
 };
 // The workgroup's LDS, at file scope so that the out-of-line paths below address it as LDS: a static
 // array, or the kernel's dynamic LDS (AS_DYNAMIC_LDS) when another body shares it.
@@ -195,14 +200,16 @@ __device__ __forceinline__ uint32_t wave_topp_cut(const double (&w)[kWPer], uint
   double pre[kWPer];
   const double S = wave_prefix(w, pre);
   const uint32_t i0 = (threadIdx.x & (kWave - 1)) * kWPer;
-  const double base = 2.0 * gamma_n(2.0 * kWPer + 16.0) + gamma_n(2.0 * (double)m + 4.0) + 10.0 * kU;
+  const double base = 2.0 * gamma_ub(2.0 * kWPer + 16.0) + gamma_ub(2.0 * (double)m + 4.0) + 10.0 * kU;
+  // pre / S against top_p as pre against top_p * S (S > 0): the products' roundings are within the
+  // 10 u of base.
+  const double t = top_p * S;
   bool lo[kWPer], hi[kWPer];
 #pragma unroll
   for (int q = 0; q < kWPer; ++q) {
-    const double c = __ddiv_rn(pre[q], S);
-    const double rel = base + gamma_n(2.0 * (double)(i0 + q) + 4.0);
-    lo[q] = c * (1.0 + rel) >= top_p;  // the reference's cumulative may have reached top_p
-    hi[q] = c * (1.0 - rel) >= top_p;  // it certainly has
+    const double rel = base + gamma_ub(2.0 * (double)(i0 + q) + 4.0);
+    lo[q] = pre[q] * (1.0 + rel) >= t;  // the reference's cumulative may have reached top_p
+    hi[q] = pre[q] * (1.0 - rel) >= t;  // it certainly has
   }
   const uint32_t jl = wave_first(lo, m), jh = wave_first(hi, m);
   if (jl != jh) return kNone;
@@ -216,13 +223,13 @@ __device__ __forceinline__ uint32_t wave_draw(const double (&w)[kWPer], uint32_t
   const double S = wave_prefix(w, pre);
   *tot = S;
   const uint32_t i0 = (threadIdx.x & (kWave - 1)) * kWPer;
-  const double g = gamma_n(2.0 * kWPer + 16.0);
-  const double d = gamma_n((double)m + 1.0) + g + 4.0 * kU;
+  const double g = gamma_ub(2.0 * kWPer + 16.0);
+  const double d = gamma_ub((double)m + 1.0) + g + 4.0 * kU;
   const double ulo = u01 * S * (1.0 - d) * (1.0 - 3.0 * kU), uhi = u01 * S * (1.0 + d) * (1.0 + 3.0 * kU);
   bool may[kWPer], sure[kWPer];
 #pragma unroll
   for (int q = 0; q < kWPer; ++q) {
-    const double rel = gamma_n((double)(i0 + q) + 1.0) + g + 4.0 * kU;
+    const double rel = gamma_ub((double)(i0 + q) + 1.0) + g + 4.0 * kU;
     may[q] = pre[q] * (1.0 + rel) > ulo;
     sure[q] = pre[q] * (1.0 - rel) > uhi;
   }
@@ -576,9 +583,27 @@ __device__ __forceinline__ void slices_total(const FinishArgs& a, Shared& sh, do
 // a bucket that starts at or past `need` is left unsorted. A bucket sort: buckets by distance from
 // the row's largest key kmax, then each value's place inside its bucket by counting the bucket's
 // values above it (quadratic in a bucket's size, which heavy ties make large).
+// At most kRankSort values are sorted by counting: thread i takes value i's rank, the number of
+// values above it (the packed keys are distinct), in one pass over the LDS copy.
+constexpr uint32_t kRankSort = 256;
+static_assert(kRankSort <= (uint32_t)kThreads, "one value per thread");
 __device__ __forceinline__ uint32_t sort_candidates(Shared& sh, uint32_t total, uint64_t R,
                                                     uint32_t kmax, uint32_t need) {
   const uint32_t tid = threadIdx.x;
+  if (total <= kRankSort) {
+    const uint64_t x = (tid < total) ? sh.sk[tid] : 0ull;
+    const bool mine = tid < total && x >= R;
+    uint32_t r = 0;
+    if (mine)
+      for (uint32_t j = 0; j < total; ++j) {
+        const uint64_t y = sh.sk[j];
+        r += (y > x) ? 1u : 0u;  // every y > x >= R is kept
+      }
+    const uint32_t P = (uint32_t)__syncthreads_count(mine);
+    if (mine) sh.sk[r] = x;
+    __syncthreads();
+    return P;
+  }
   uint64_t* out2 = reinterpret_cast<uint64_t*>(sh.wd);
   constexpr int kPerT = kCap / kThreads;
   uint64_t xs[kPerT];
@@ -700,7 +725,7 @@ __device__ __forceinline__ uint32_t decide_draw(Shared& sh, uint32_t m, const do
     const uint32_t i = i0 + q;
     if (i < m) {
       const double Rv = __dadd_rn(off, loc[q]);
-      const double rel = gamma_n((double)i + 1.0) + g40 + 4.0 * kU;
+      const double rel = gamma_ub((double)i + 1.0) + g40 + 4.0 * kU;
       if (Rv * (1.0 + rel) > ulo) fp = min(fp, i);
       if (Rv * (1.0 - rel) > uhi) fc = min(fc, i);
     }
@@ -1594,15 +1619,20 @@ __device__ __forceinline__ void finish_row(const FinishArgs& a, uint32_t row) {
       sh.nsk = 0;
       sh.u01 = 0.0;
       sh.hist_over = (he - hb > a.max_history) ? he - hb : 0u;
-      if (bad == kNone && draws && !sh.hist_over) {
-        // One unit() per sampled row (sample.rs:189, 264, 276), after the row's skipped draws.
-        for (uint32_t k = 0; k < p.rng_skip; ++k) rng_next(s4);
-        sh.u01 = rng_unit(s4);
-        if (p.flags & kFlagRngWrite)
-          for (int k = 0; k < 4; ++k) src[k] = s4[k];
-      }
+      sh.draw_rng = (bad == kNone && draws && !sh.hist_over) ? 1u : 0u;
     }
   }
+  // One unit() per sampled row (sample.rs:189, 264, 276), after the row's skipped draws: thread 0
+  // advances the stream (its state loaded above) once the row's next loads are in flight, before the
+  // barrier that follows them; nothing reads u01 earlier.
+  auto take_u01 = [&]() {
+    if (tid == 0 && sh.draw_rng) {
+      for (uint32_t k = 0; k < p.rng_skip; ++k) rng_next(s4);
+      sh.u01 = rng_unit(s4);
+      if (p.flags & kFlagRngWrite)
+        for (int k = 0; k < 4; ++k) src[k] = s4[k];
+    }
+  };
   __syncthreads();
 
   if (sh.hist_over) {
@@ -1691,6 +1721,7 @@ __device__ __forceinline__ void finish_row(const FinishArgs& a, uint32_t row) {
           if (keep && pos < (uint32_t)kCap) sh.sk[pos] = tmp[q];
         }
       }
+      take_u01();
       __syncthreads();
     }
     const uint32_t total = min(sh.nsk, (uint32_t)kCap);
@@ -1743,21 +1774,26 @@ __device__ __forceinline__ void finish_row(const FinishArgs& a, uint32_t row) {
       // min-p's floor (the ranks are sorted, so it keeps a prefix) and the draw, each decided by
       // bounds and by the reference's sequential folds only when the bounds cannot.
       static_assert(as_launch::kTopKMax <= kWaveMax, "one wave holds a top-k");
+      static_assert(2 * as_launch::kTopKMax <= (uint32_t)kCap && as_launch::kTopKMax <= (uint32_t)kThreads,
+                    "the weights of a top-k, one per thread");
       const uint32_t k = p.top_k;
+      // Every weight first, one value per thread: sh.wd[i] = w at T, sh.wd[kTopKMax + i] = w at T = 1.
+      double* w1s = sh.wd + as_launch::kTopKMax;
+      if (tid < k) {
+        const double v = val(tid);
+        sh.wd[tid] = w_temp(v);
+        if (p.top_p < 1.0f) w1s[tid] = w_one(v);
+      }
+      __syncthreads();
       if (tid < kWave) {
         const uint32_t i0 = tid * kWPer;
         uint32_t kk = k;
         if (p.top_p < 1.0f) {
           double w[kWPer];
 #pragma unroll
-          for (int q = 0; q < kWPer; ++q) w[q] = (i0 + q < k) ? w_one(val(i0 + q)) : 0.0;
+          for (int q = 0; q < kWPer; ++q) w[q] = (i0 + q < k) ? w1s[i0 + q] : 0.0;
           kk = wave_topp_cut(w, k, top_p);
-          if (kk == kNone) {
-#pragma unroll
-            for (int q = 0; q < kWPer; ++q)
-              if (i0 + q < k) sh.wd[i0 + q] = w[q];
-            kk = wave_seq_cut(sh.wd, k, top_p);
-          }
+          if (kk == kNone) kk = wave_seq_cut(w1s, k, top_p);
         }
         if (has_floor) {
           bool below[kWPer];
@@ -1767,10 +1803,7 @@ __device__ __forceinline__ void finish_row(const FinishArgs& a, uint32_t row) {
         }
         double w[kWPer], tot = 0.0;
 #pragma unroll
-        for (int q = 0; q < kWPer; ++q) {
-          w[q] = (i0 + q < kk) ? w_temp(val(i0 + q)) : 0.0;
-          if (i0 + q < kk) sh.wd[i0 + q] = w[q];  // the kept probabilities' weights
-        }
+        for (int q = 0; q < kWPer; ++q) w[q] = (i0 + q < kk) ? sh.wd[i0 + q] : 0.0;  // also the kept weights
         uint32_t pick = wave_draw(w, kk, sh.u01, &tot);
         if (pick == kNone) pick = wave_seq_draw(sh.wd, kk, sh.u01, &tot);
         if (tid == 0) {
@@ -1810,6 +1843,7 @@ __device__ __forceinline__ void finish_row(const FinishArgs& a, uint32_t row) {
           double loc[kScanPer], off;
           r_prefix = prefix_scan(sh, P, loc, &off);
           const double g40 = 2.0 * gamma_n(40.0);
+          const double tp_lo = top_p * (X - eps), tp_hi = top_p * (X + eps);
           uint32_t fl = P, fh = P;
           const uint32_t i0 = tid * kScanPer;
 #pragma unroll
@@ -1817,11 +1851,11 @@ __device__ __forceinline__ void finish_row(const FinishArgs& a, uint32_t row) {
             const uint32_t i = i0 + q;
             if (i < P) {
               const double Rv = __dadd_rn(off, loc[q]);
-              const double rel = g40 + gamma_n(2.0 * (double)i + 4.0) + 10.0 * kU;
-              const double hi = Rv * (1.0 + rel) / (X - eps);
-              const double lo = Rv * (1.0 - rel) / (X + eps);
-              if (hi >= top_p) fl = min(fl, i);
-              if (lo >= top_p) fh = min(fh, i);
+              const double rel = g40 + gamma_ub(2.0 * (double)i + 4.0) + 10.0 * kU;
+              // Rv / (X -+ eps) against top_p as Rv against top_p * (X -+ eps): the products'
+              // roundings are within the 10 u of rel.
+              if (Rv * (1.0 + rel) >= tp_lo) fl = min(fl, i);
+              if (Rv * (1.0 - rel) >= tp_hi) fh = min(fh, i);
             }
           }
           jl = block_min_u32<kWaves>(fl, sh.red_u);
@@ -1978,6 +2012,7 @@ __device__ __forceinline__ void finish_row(const FinishArgs& a, uint32_t row) {
     }
     __syncthreads();
   } else {
+    take_u01();
     if (tid == 0) sh.exact = 1;
     __syncthreads();
   }

@@ -131,7 +131,7 @@ size_t row_kernel_lds();
 
 // Between the scan and the finish: the weights of S for min-p rows whose scan gave up keeping the
 // floor set whole (a no-op for the other rows).
-hipError_t tail(hipStream_t stream, uint32_t n_rows, uint32_t n, const FinishArgs& a);
+hipError_t tail(hipStream_t stream, uint32_t n_rows, uint32_t n, const FinishArgs* a);
 
 // Log-probabilities (logprobs.hip): rows in parts of kLpPart values, each part's 20 best and sums.
 constexpr uint32_t kLpPart = 8192;

@@ -243,9 +243,10 @@ __device__ __forceinline__ void tail_part(const FinishArgs& a, uint32_t row, uin
   if (tid == 0) __hip_atomic_fetch_add(&t.parts, 1u, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-// The workgroups take the (flagged row, part) items in turn. The arguments come by value: the rows
-// to cover are known after one load (the scan's list).
-__global__ __launch_bounds__(kThreads) void tail_kernel(const FinishArgs a) {
+// The workgroups take the (flagged row, part) items in turn. The arguments are the scan's device copy
+// of the call's block: a large kernel-argument block costs every workgroup more than that load.
+__global__ __launch_bounds__(kThreads) void tail_kernel(const FinishArgs* __restrict__ ap) {
+  const FinishArgs& a = *ap;
   const uint32_t parts = (a.n + kLen - 1) / kLen;
   for (uint32_t item = blockIdx.x; item < as_launch::kTailRows * parts; item += gridDim.x) {
     // The list's count and this item's entry, loaded together (an entry past the count is unused).
@@ -261,7 +262,7 @@ __global__ __launch_bounds__(kThreads) void tail_kernel(const FinishArgs a) {
 
 namespace as_launch {
 
-hipError_t tail(hipStream_t stream, uint32_t n_rows, uint32_t n, const FinishArgs& a) {
+hipError_t tail(hipStream_t stream, uint32_t n_rows, uint32_t n, const FinishArgs* a) {
   const uint32_t items = min(n_rows, kTailRows) * ((n + kTailLen - 1) / kTailLen);
   hipLaunchKernelGGL(tail_kernel, dim3(min(items, kTailGroups)), dim3(kThreads), 0, stream, a);
   return hipGetLastError();
