@@ -84,3 +84,33 @@ def test_row_bytes_matches_the_oracle(L):
     assert row_bytes(WTYPE["Q6_K"], 2048) == 8 * 210
     with pytest.raises(Exception):
         row_bytes(WTYPE["Q4_K"], 100)
+
+
+def _rust_block(text, start):
+    i = text.index(start)
+    return text[i:text.index("\n}", i)]
+
+
+def test_integration_binding_matches_the_header(L):
+    """INTEGRATION.md's Rust AsSampling has the header's fields in the header's order, its From impl
+    passes both new penalties through, and the check messages it quotes are as_check's."""
+    doc = open(os.path.join(ROOT, "INTEGRATION.md")).read()
+    header = open(HEADER).read()
+    c_struct = header[:header.index("} as_sampling;")]
+    c_struct = c_struct[c_struct.rindex("typedef struct {"):]
+    c_fields = re.findall(r"^\s*(?:float|uint32_t)\s+(\w+);", c_struct, re.M)
+    rust = _rust_block(doc, "pub struct AsSampling {")
+    r_fields = re.findall(r"pub (\w+): (f32|u32),", rust)
+    assert [f for f, _ in r_fields] == c_fields
+    assert [t for _, t in r_fields] == ["u32" if f in ("top_k", "reserved") else "f32" for f in c_fields]
+    conv = _rust_block(doc, "impl From<&engine::Sampling> for AsSampling {")
+    assert "frequency: s.frequency_penalty" in conv and "repetition: s.repetition_penalty" in conv
+    from artemis_amd import Sampling
+    for kw, flag in ((dict(frequency_penalty=float("nan")), "--frequency-penalty"),
+                     (dict(repetition_penalty=0.0), "--repetition-penalty")):
+        with pytest.raises(ValueError) as e:
+            Sampling(temp=1.0, top_k=0, top_p=1.0, min_p=0.0, **kw).check()
+        msg = str(e.value)
+        assert msg.startswith(flag)
+        tail = msg.split(" ", 2)[2]  # "must be ..."
+        assert f'"{flag} {{}} {tail}"' in doc, (flag, tail)

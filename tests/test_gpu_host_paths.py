@@ -1,0 +1,106 @@
+"""Host-side paths of as_sample on the GPU, each checked against the oracle through the C ABI:
+
+- back-to-back calls with different settings and no host synchronisation between them, which
+  exercises the two pinned parameter blocks the calls alternate between (a call reuses a block only
+  once the call two before it has finished reading it);
+- histories with more distinct ids per slice than the scan's LDS hash counts (512), which send the
+  row to the finish kernel's passes over the whole row (the deep path, then the exact-order path).
+"""
+import numpy as np
+import pytest
+
+from test_gpu_sampler import GRID, check_rows, csr, oracle_rows, random_logits
+
+pytestmark = pytest.mark.gpu
+
+torch = pytest.importorskip("torch")
+
+AS_ROW_EXACT_PATH = 0x100
+AS_ROW_DEEP_PATH = 0x400
+
+
+@pytest.fixture(scope="module")
+def ctx():
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU")
+    from artemis_amd import Context
+    c = Context(max_rows=64, max_vocab=248_320, max_history=65_535)
+    yield c
+    c.close()
+
+
+def settings(p):
+    from artemis_amd import Sampling
+    return Sampling(p["temp"], p["top_k"], p["top_p"], p["min_p"], p.get("presence", 0.0),
+                    p.get("frequency", 0.0), p.get("repetition", 1.0))
+
+
+def test_back_to_back_calls_with_different_settings(ctx):
+    from artemis_amd import states_tensor
+    dev = torch.device("cuda:0")
+    rows, n, calls = 16, 20_000, 50
+    rng = np.random.default_rng(11)
+    logits = np.stack([random_logits(rng, n, i % 3) for i in range(rows)])
+    hists = [rng.integers(0, n, size=40).astype(np.uint32) for _ in range(rows)]
+    off, ids = csr(hists, rows)
+    d_lg = torch.from_numpy(logits).to(dev)
+    d_off, d_ids = torch.from_numpy(off).to(dev), torch.from_numpy(ids).to(dev)
+    plan = []
+    for c in range(calls):
+        # Every call has its own settings (the grid rotated, penalties varied) and seeds.
+        params = []
+        for r in range(rows):
+            q = dict(GRID[(c * 7 + r * 13) % len(GRID)])
+            if (c + r) % 3 == 1:
+                q.update(presence=0.5 + 0.1 * (c % 4))
+            if (c + r) % 3 == 2:
+                q.update(presence=0.25, frequency=0.1 * (c % 5), repetition=1.0 + 0.05 * (r % 3))
+            params.append(q)
+        seeds = [1000 * c + r for r in range(rows)]
+        plan.append((params, seeds, states_tensor(seeds, dev), ctx.outputs(rows, 8, dev)))
+    torch.cuda.synchronize()
+    # Every call is issued before any result is read.
+    for params, _, st, out in plan:
+        ctx.sample_batch(d_lg, [settings(p) for p in params], st, d_off, d_ids, kept_cap=8, out=out)
+    torch.cuda.synchronize()
+    for c, (params, seeds, st, out) in enumerate(plan):
+        tok, status, kept, kept_ids, kept_probs = out
+        g = dict(tokens=tok.cpu().numpy().astype(np.uint32), status=status.cpu().numpy().astype(np.uint32),
+                 kept=kept.cpu().numpy().astype(np.uint32), kept_ids=kept_ids.cpu().numpy().astype(np.uint32),
+                 kept_probs=kept_probs.cpu().numpy(), rng=st.cpu().numpy().view(np.uint64))
+        want = oracle_rows(logits, params, seeds, hists, kept_cap=8)
+        check_rows(g, want, params, kept_cap=8, label=f"call {c}")
+
+
+@pytest.mark.parametrize("rows", [1, 4])
+def test_histories_past_the_slice_hash_take_the_exact_path(ctx, rows):
+    from artemis_amd import states_tensor
+    dev = torch.device("cuda:0")
+    n = 248_320
+    rng = np.random.default_rng(20 + rows)
+    logits = (rng.standard_normal((rows, n)) * 2.5).astype(np.float32)
+    # 20,000 history ids over the first 30,000 ids (about 14,000 distinct, each seen one to a few
+    # times): every slice that covers that range holds far more than 512 distinct ids.
+    hists = [rng.integers(0, 30_000, size=20_000).astype(np.uint32) for _ in range(rows)]
+    for r, h in enumerate(hists):
+        logits[r, int(h[0])] += 6.0  # a history id among the best
+    kinds = [dict(temp=0.7, top_k=40, top_p=0.9, min_p=0.05, presence=0.5, frequency=0.3, repetition=1.05),
+             dict(temp=0.0, top_k=0, top_p=1.0, min_p=0.0, presence=1.5),
+             dict(temp=0.8, top_k=0, top_p=0.9, min_p=0.02, presence=0.5, frequency=0.3, repetition=1.05),
+             dict(temp=1.0, top_k=20, top_p=1.0, min_p=0.0, frequency=0.4)]
+    params = [kinds[r % len(kinds)] for r in range(rows)]
+    seeds = [77 + r for r in range(rows)]
+    off, ids = csr(hists, rows)
+    st = states_tensor(seeds, dev)
+    tok, status, kept, kept_ids, kept_probs = ctx.sample_batch(
+        torch.from_numpy(logits).to(dev), [settings(p) for p in params], st,
+        torch.from_numpy(off).to(dev), torch.from_numpy(ids).to(dev), kept_cap=16)
+    torch.cuda.synchronize()
+    g = dict(tokens=tok.cpu().numpy().astype(np.uint32), status=status.cpu().numpy().astype(np.uint32),
+             kept=kept.cpu().numpy().astype(np.uint32), kept_ids=kept_ids.cpu().numpy().astype(np.uint32),
+             kept_probs=kept_probs.cpu().numpy(), rng=st.cpu().numpy().view(np.uint64))
+    want = oracle_rows(logits, params, seeds, hists, kept_cap=16)
+    check_rows(g, want, params, kept_cap=16, label=f"rows={rows}")
+    # The slices could not count the history: every row was settled by a pass of the finish kernel
+    # over the whole row (the deep path, then the exact-order path when a bound leaves it open).
+    assert all(int(s) & (AS_ROW_EXACT_PATH | AS_ROW_DEEP_PATH) for s in g["status"]), [hex(int(s)) for s in g["status"]]
