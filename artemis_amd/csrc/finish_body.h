@@ -881,16 +881,424 @@ __device__ __forceinline__ void for_each_value(const float* x, const uint32_t* c
 
 __device__ __noinline__ float penalize_out(float x, uint32_t c, const RowParams& p) { return penalize(x, c, p); }
 
-// Returns true when it settled the row.
-__device__ __noinline__ bool deep_row(const FinishArgs& a, const RowParams& p, uint32_t row) {
-  Shared& sh = shm();
-  const uint32_t n = a.n, tid = threadIdx.x, lane = tid & (kWave - 1);
-  uint32_t* S = a.scratch + (uint64_t)row * a.scratch_stride;
-  uint32_t* cnt = S;
-  uint64_t* bufA = reinterpret_cast<uint64_t*>(S + ((n + 1) & ~1u));
-  uint64_t* bufB = bufA + n;
-  const float* x = a.logits + (uint64_t)row * a.row_stride;
+// --- the deep path by deciding bins ---------------------------------------------------------------
+//
+// A row without a top-k whose cut or draw lies past the fast path's candidates needs the rank order
+// only where a decision falls: at top-p's cut (the cumulative weight at T = 1 reaching top_p of the
+// total), at min-p's floor, and at the draw (the cumulative weight at T passing u times the kept
+// weight). One pass over the row histograms every value by its distance below the largest into
+// kDeepBins bins (the bin is monotone in the value, so bins follow the rank order) and adds each
+// value's weights, the host-exact exp of the reference's own f64 arguments (exp_core): every term
+// has the reference's bits, and any sum of them differs from the reference's ordered folds only by
+// rounding. The bins' prefix sums fix, with certified bounds, the few bins that can hold each
+// decision; a second pass collects only those bins' values into LDS, a sort orders them, and each
+// one's rank is the count before its run of collected bins plus its place in the run. The decisions
+// compare the reference's cumulatives, bounded by the prefix before the run plus the run's terms,
+// with targets bounded by the exact totals. Returns false, with nothing written, when a bound cannot
+// decide or the bins hold more values than LDS does; the caller then takes the full deep path.
+constexpr uint32_t kBinRanges = 3;
+// Element k of a run's three values, by selects (the runs' few values stay in registers).
+template <class T>
+__device__ __forceinline__ T sel3(uint32_t k, T v0, T v1, T v2) {
+  return k == 0 ? v0 : (k == 1 ? v1 : v2);
+}
 
+__device__ __noinline__ bool deep_bins(const FinishArgs& a, const RowParams& p, uint32_t row, bool pen) {
+  Shared& sh = shm();
+  const uint32_t n = a.n, tid = threadIdx.x;
+  uint32_t* cnt = a.scratch + (uint64_t)row * a.scratch_stride;
+  uint32_t hb;
+  const uint32_t he = history_bounds(a, p, row, &hb);
+  const uint32_t extra = a.extra_ids ? p.extra : 0;
+  const float* x = a.logits + (uint64_t)row * a.row_stride;
+  const uint32_t* pcnt = pen ? cnt : nullptr;
+  const bool vec = a.vec && a.row_stride % 4 == 0;
+  const uint64_t* tab = sh.tab;
+  const uint32_t mk = sh.mk;
+  const double top = (double)key_value(mk), temp = (double)p.temp, top_p = (double)p.top_p;
+  const float topf = key_value(mk);
+  const bool has_floor = p.min_p > 0.0f, by_top_p = p.top_p < 1.0f;
+  const bool unfiltered = !by_top_p && !has_floor;
+  const float floorf = floor_f32(__dadd_rn(top, p.ln_min_p));
+  // Bins of distance below the largest value, kDeepBins over span, everything further down in the
+  // last: below span a weight is under e^-32 of the largest's (span is 32 T above T = 1).
+  const float span = 32.0f * fmaxf(1.0f, p.temp);
+  const float bsc = (float)kDeepBins / span;
+  auto bin_of = [&](float v) -> uint32_t {
+    const float t = (topf - v) * bsc;
+    return t < (float)(kDeepBins - 1) ? (uint32_t)t : kDeepBins - 1;
+  };
+  // The reference's weights exp(l - top) (top-p's) and exp((l - top) / T); arguments at or below
+  // -512 (terms under 1e-222) are left out, far inside the bounds below.
+  auto e_core = [&](double d) -> double { return d > -512.0 ? as_exp::exp_core(tab, d) : 0.0; };
+  auto w1 = [&](float v) -> double { return e_core(__dsub_rn((double)v, top)); };
+  auto wt = [&](float v) -> double { return e_core(__ddiv_rn(__dsub_rn((double)v, top), temp)); };
+
+  // Pass 1: counts (hc), weights at T = 1 (hm, top-p rows) and at T (hw). hc and hm share sh.wd,
+  // hw lies in sh.sk.
+  uint32_t* hc = reinterpret_cast<uint32_t*>(sh.wd);
+  double* hm = sh.wd + kDeepBins / 2;
+  double* hw = reinterpret_cast<double*>(sh.sk);
+  static_assert(kDeepBins * 12 <= sizeof(sh.wd) && kDeepBins * 8 <= sizeof(sh.sk), "histogram room");
+  for (uint32_t b = tid; b < kDeepBins; b += kThreads) {
+    hc[b] = 0;
+    hm[b] = 0.0;
+    hw[b] = 0.0;
+  }
+  __syncthreads();
+  auto count = [&](float v) {
+    const uint32_t b = bin_of(v);
+    atomicAdd(&hc[b], 1u);
+    if (by_top_p) atomicAdd(&hm[b], w1(v));
+    atomicAdd(&hw[b], wt(v));
+  };
+  for_each_value(x, pcnt, n, vec, [&](uint32_t, float v, uint32_t c) {
+    if (__builtin_expect(c == 0, 1)) count(v);
+  });
+  if (pen) {
+    // Each history id once, penalised, by the thread that sets its count's top bit first (pass 2
+    // clears it again).
+    auto hist_one = [&](uint32_t id) {
+      if (id >= n) return;
+      const uint32_t old = atomicOr(&cnt[id], 0x80000000u);
+      if (!(old & 0x80000000u)) count(penalize(x[id], old, p));
+    };
+    for (uint32_t h = hb + tid; h < he; h += kThreads) hist_one(a.hist_ids[h]);
+    for (uint32_t h = tid; h < extra; h += kThreads) hist_one(a.extra_ids[h]);
+  }
+  __syncthreads();
+
+  // Inclusive prefixes over the bins, in place: kDPer bins per thread, then the block.
+  constexpr int kDPer = kDeepBins / kThreads;
+  static_assert(kDeepBins % kThreads == 0, "whole bins per thread");
+  {
+    uint32_t c4[kDPer], cs = 0;
+    double m4[kDPer], w4[kDPer], ms = 0.0, ws = 0.0;
+#pragma unroll
+    for (int q = 0; q < kDPer; ++q) {
+      const uint32_t b = tid * kDPer + q;
+      cs += hc[b];
+      ms = __dadd_rn(ms, hm[b]);
+      ws = __dadd_rn(ws, hw[b]);
+      c4[q] = cs;
+      m4[q] = ms;
+      w4[q] = ws;
+    }
+    uint32_t call;
+    const uint32_t cb = block_exclusive_scan_u32(cs, sh.red_u, &call);
+    const double mb = block_exclusive_scan_f64(ms, sh.red_d);
+    const double wb = block_exclusive_scan_f64(ws, sh.red_d);
+#pragma unroll
+    for (int q = 0; q < kDPer; ++q) {
+      const uint32_t b = tid * kDPer + q;
+      hc[b] = cb + c4[q];
+      hm[b] = __dadd_rn(mb, m4[q]);
+      hw[b] = __dadd_rn(wb, w4[q]);
+    }
+  }
+  __syncthreads();
+  // Every prefix (and the totals) is within E of the exact sum of its terms: a term goes through one
+  // f64 atomic add and at most kDPer + 2 log2(kThreads) + 2 more adds; the reference's own folds of
+  // the same terms (total1 and the unfiltered total in index order, the cumulatives in rank order,
+  // the kept weight) are within gamma(n) of the same exact sums, and gj covers their ratios.
+  const double M_all = hm[kDeepBins - 1], W_all = hw[kDeepBins - 1];
+  const double g_all = gamma_ub(2.0 * (double)n + 128.0);
+  const double Em = g_all * M_all, Ew = g_all * W_all;
+  const double gj = gamma_ub(2.0 * (double)n + 4.0) + 10.0 * kU;
+  auto C = [&](uint32_t b) -> uint32_t { return b == kNone ? 0u : hc[b]; };  // through bin b; kNone: none
+  auto Mc = [&](uint32_t b) -> double { return b == kNone ? 0.0 : hm[b]; };
+  auto Wc = [&](uint32_t b) -> double { return b == kNone ? 0.0 : hw[b]; };
+  auto before = [](uint32_t b) -> uint32_t { return b == 0 ? kNone : b - 1; };
+
+  // top-p's cut: the first rank whose reference cumulative reaches top_p, i.e. whose prefix S_j
+  // reaches top_p * total1. Bins before c_lo cannot hold it (their prefixes cannot reach the least
+  // target); at the end of c_hi it has surely been reached.
+  const double tp_lo = top_p * (M_all - Em), tp_hi = top_p * (M_all + Em);
+  uint32_t c_lo = kNone, c_hi = kNone;
+  if (by_top_p) {
+    uint32_t a0 = kNone, a1 = kNone;
+#pragma unroll
+    for (int q = 0; q < kDPer; ++q) {
+      const uint32_t b = tid * kDPer + q;
+      if ((hm[b] + Em) * (1.0 + gj) >= tp_lo) a0 = min(a0, b);
+      if ((hm[b] - Em) * (1.0 - gj) >= tp_hi) a1 = min(a1, b);
+    }
+    c_lo = block_min_u32<kWaves>(a0, sh.red_u);
+    c_hi = block_min_u32<kWaves>(a1, sh.red_u);
+    if (c_hi == kNone) c_hi = kDeepBins - 1;
+    if (c_lo == kNone) c_lo = c_hi;
+  }
+  // min-p's cut, the first rank below the floor, lies in the floor value's bin f (or at its ends).
+  const uint32_t f = has_floor ? bin_of(floorf) : kNone;
+  const bool need_c = by_top_p && !(has_floor && f < c_lo);  // else min-p surely cuts first
+  const bool need_f = has_floor && !(by_top_p && f > c_hi);  // else top-p surely cuts first
+  // The kept set ends in bins [k_lo, k_hi] (the last bin when nothing cuts).
+  uint32_t k_lo = kDeepBins - 1, k_hi = kDeepBins - 1;
+  if (need_c) {
+    k_lo = c_lo;
+    k_hi = c_hi;
+  }
+  if (need_f) {
+    k_lo = min(k_lo, f);
+    k_hi = need_c ? min(k_hi, f) : f;
+  }
+  // The draw: u = unit() * W, W the kept weight at T, in [Wc(k_lo - 1), Wc(k_hi)] (all of it when
+  // nothing cuts); the bins that can hold the first cumulative above u, at most the kept set's.
+  const double Wk_lo = unfiltered ? W_all : Wc(before(k_lo)), Wk_hi = unfiltered ? W_all : Wc(k_hi);
+  const double u_lo = sh.u01 * (Wk_lo - Ew) * (1.0 - gj) * (1.0 - 4.0 * kU);
+  const double u_hi = sh.u01 * (Wk_hi + Ew) * (1.0 + gj) * (1.0 + 4.0 * kU);
+  uint32_t d_lo, d_hi;
+  {
+    uint32_t a0 = kNone, a1 = kNone;
+#pragma unroll
+    for (int q = 0; q < kDPer; ++q) {
+      const uint32_t b = tid * kDPer + q;
+      if ((hw[b] + Ew) * (1.0 + gj) > u_lo) a0 = min(a0, b);
+      if ((hw[b] - Ew) * (1.0 - gj) > u_hi) a1 = min(a1, b);
+    }
+    d_lo = min(block_min_u32<kWaves>(a0, sh.red_u), k_hi);
+    d_hi = min(block_min_u32<kWaves>(a1, sh.red_u), k_hi);  // past the kept set: its last value
+  }
+  // The runs of bins to collect, in bin order, merged where they touch.
+  uint32_t r0[kBinRanges], r1[kBinRanges], nr = 0;
+  {
+    // The draw's, the cut's and the floor's (kNone: not needed), sorted by start with three
+    // compare-exchanges (kNone last), then merged.
+    uint32_t lo[kBinRanges] = {d_lo, need_c ? c_lo : kNone, need_f ? f : kNone};
+    uint32_t hi[kBinRanges] = {d_hi, need_c ? c_hi : kNone, need_f ? f : kNone};
+    auto cx = [&](int i, int j) {
+      if (lo[j] < lo[i]) {
+        const uint32_t t0 = lo[i], t1 = hi[i];
+        lo[i] = lo[j];
+        hi[i] = hi[j];
+        lo[j] = t0;
+        hi[j] = t1;
+      }
+    };
+    cx(0, 1);
+    cx(1, 2);
+    cx(0, 1);
+#pragma unroll
+    for (uint32_t i = 0; i < kBinRanges; ++i) {
+      r0[i] = kNone;
+      r1[i] = kNone;
+    }
+#pragma unroll
+    for (uint32_t i = 0; i < kBinRanges; ++i) {
+      if (lo[i] == kNone) continue;
+      if (nr > 0 && lo[i] <= sel3(nr - 1, r1[0], r1[1], r1[2]) + 1) {
+        const uint32_t e = max(sel3(nr - 1, r1[0], r1[1], r1[2]), hi[i]);
+#pragma unroll
+        for (uint32_t k = 0; k < kBinRanges; ++k)
+          if (k + 1 == nr) r1[k] = e;
+      } else {
+#pragma unroll
+        for (uint32_t k = 0; k < kBinRanges; ++k)
+          if (k == nr) {
+            r0[k] = lo[i];
+            r1[k] = hi[i];
+          }
+        ++nr;
+      }
+    }
+  }
+  // Per run: the count and weights before it, and where its values start among the collected ones.
+  uint32_t cbr[kBinRanges], first[kBinRanges];
+  double mbr[kBinRanges], wbr[kBinRanges];
+  uint32_t collected = 0;
+#pragma unroll
+  for (uint32_t k = 0; k < kBinRanges; ++k) {
+    cbr[k] = 0;
+    mbr[k] = 0.0;
+    wbr[k] = 0.0;
+    first[k] = kNone;  // past every collected value: no run
+    if (k < nr) {
+      cbr[k] = C(before(r0[k]));
+      mbr[k] = Mc(before(r0[k]));
+      wbr[k] = Wc(before(r0[k]));
+      first[k] = collected;
+      collected += C(r1[k]) - cbr[k];
+    }
+  }
+  const uint32_t cf_before = need_f ? C(before(f)) : 0u, cf_through = need_f ? C(f) : 0u;
+  const double wf_before = need_f ? Wc(before(f)) : 0.0, wf_through = need_f ? Wc(f) : 0.0;
+  const bool fits = collected <= (uint32_t)kCap;
+  if (tid == 0) sh.pick = 0;
+  __syncthreads();  // every thread has read the prefixes: sh.sk takes the collected values
+
+  // Pass 2: the runs' values into sh.sk (any order); the history ids once more, which clears their
+  // counts' top bits (also when the values do not fit).
+  auto in_runs = [&](uint32_t b) {
+    bool in = false;
+#pragma unroll
+    for (uint32_t k = 0; k < kBinRanges; ++k) in = in || (b >= r0[k] && b <= r1[k]);  // unused: kNone
+    return in;
+  };
+  if (fits) {
+    for_each_value(x, pcnt, n, vec, [&](uint32_t i, float v, uint32_t c) {
+      if (__builtin_expect(c == 0, 1) && in_runs(bin_of(v))) {
+        const uint32_t s = atomicAdd(&sh.pick, 1u);
+        if (s < (uint32_t)kCap) sh.sk[s] = pack(total_key(v), i);
+      }
+    });
+  }
+  if (pen) {
+    auto hist_two = [&](uint32_t id) {
+      if (id >= n) return;
+      const uint32_t old = atomicAnd(&cnt[id], 0x7fffffffu);
+      if (!(old & 0x80000000u) || !fits) return;
+      const float v = penalize(x[id], old & 0x7fffffffu, p);
+      if (in_runs(bin_of(v))) {
+        const uint32_t s = atomicAdd(&sh.pick, 1u);
+        if (s < (uint32_t)kCap) sh.sk[s] = pack(total_key(v), id);
+      }
+    };
+    for (uint32_t h = hb + tid; h < he; h += kThreads) hist_two(a.hist_ids[h]);
+    for (uint32_t h = tid; h < extra; h += kThreads) hist_two(a.extra_ids[h]);
+  }
+  __syncthreads();
+  if (!fits || sh.pick != collected || collected == 0) return false;
+  const uint32_t P = sort_candidates(sh, collected, 0ull, mk, kNone);
+  if (P != collected) return false;
+  auto val = [&](uint32_t i) -> float { return packed_value(sh.sk[i]); };
+  auto run_of = [&](uint32_t i) -> uint32_t { return (i >= first[2]) ? 2u : (i >= first[1] ? 1u : 0u); };
+  auto rank_of = [&](uint32_t i, uint32_t k) -> uint32_t { return sel3(k, cbr[0], cbr[1], cbr[2]) + (i - sel3(k, first[0], first[1], first[2])); };
+  // A scan of the collected values' weights in sh.wd: each thread's inclusive prefixes, and per run
+  // the scan just before it (a run's terms through i are the difference, within 2 gamma(40) of the
+  // scan's total).
+  double loc[kScanPer], off;
+  double* run_base = sh.red_d;  // one slot per run (kWaves >= kBinRanges)
+  static_assert(kWaves >= (int)kBinRanges, "a slot per run");
+  auto scan_runs = [&]() {
+    prefix_scan(sh, P, loc, &off);
+    if (tid < kBinRanges) run_base[tid] = 0.0;
+    __syncthreads();
+#pragma unroll
+    for (int q = 0; q < kScanPer; ++q) {
+      const uint32_t i = tid * kScanPer + q;
+#pragma unroll
+      for (uint32_t k = 1; k < kBinRanges; ++k)
+        if (i < P && i + 1 == first[k]) run_base[k] = __dadd_rn(off, loc[q]);
+    }
+    __syncthreads();
+  };
+  const double g40 = 2.0 * gamma_n(40.0);
+
+  // The cut (sample.rs:230-252): at the first rank below the floor, or one past the first whose
+  // cumulative reaches top_p, whichever comes first.
+  uint32_t keep = n;
+  double Wkeep = W_all, Wkeep_err = Ew;
+  if (need_c || need_f) {
+    for (uint32_t i = tid; i < P; i += kThreads) sh.wd[i] = need_c ? w1(val(i)) : 0.0;
+    __syncthreads();
+    scan_runs();
+    uint32_t jl = kNone, jh = kNone, jf = kNone;
+    const double err = Em + g40 * M_all;
+#pragma unroll
+    for (int q = 0; q < kScanPer; ++q) {
+      const uint32_t i = tid * kScanPer + q;
+      if (i >= P) continue;
+      const uint32_t k = run_of(i), r = rank_of(i, k);
+      if (need_f && !(val(i) >= floorf)) jf = min(jf, r);
+      if (need_c) {
+        const double S = __dadd_rn(sel3(k, mbr[0], mbr[1], mbr[2]), __dsub_rn(__dadd_rn(off, loc[q]), run_base[k]));
+        if ((S + err) * (1.0 + gj) >= tp_lo) jl = min(jl, r);
+        if ((S - err) * (1.0 - gj) >= tp_hi) jh = min(jh, r);
+      }
+    }
+    jl = block_min_u32<kWaves>(jl, sh.red_u);
+    jh = block_min_u32<kWaves>(jh, sh.red_u);
+    jf = block_min_u32<kWaves>(jf, sh.red_u);
+    uint32_t k_topp = kNone, k_floor = kNone;
+    if (need_c) {
+      if (jl != jh || jh == kNone) return false;
+      k_topp = jh + 1;
+    }
+    // The first value past the floor's bin is below the floor: min-p cuts there at the latest.
+    if (need_f) k_floor = min(jf, cf_through);
+    keep = min(k_topp, k_floor);
+    // The kept weight at T: a prefix of whole bins when min-p cuts at its bin's ends, else a run's
+    // prefix plus its terms through rank keep - 1.
+    __syncthreads();
+    for (uint32_t i = tid; i < P; i += kThreads) sh.wd[i] = wt(val(i));
+    __syncthreads();
+    if (need_f && keep == k_floor && keep == cf_through) {
+      Wkeep = wf_through;
+    } else if (need_f && keep == k_floor && keep == cf_before) {
+      Wkeep = wf_before;
+    } else {
+      uint32_t home = kNone;
+      for (uint32_t i = tid; i < P; i += kThreads) {
+        const uint32_t k = run_of(i);
+        if (rank_of(i, k) + 1 == keep) home = k;
+      }
+      home = block_min_u32<kWaves>(home, sh.red_u);
+      if (home == kNone) return false;
+      double part = 0.0;
+      for (uint32_t i = tid; i < P; i += kThreads)
+        if (run_of(i) == home && rank_of(i, home) < keep) part += sh.wd[i];
+      part = block_sum_f64<kWaves>(part, sh.red_d);
+      Wkeep = __dadd_rn(sel3(home, wbr[0], wbr[1], wbr[2]), part);
+    }
+    Wkeep_err = Ew + 2.0 * gamma_n(64.0) * W_all;
+  } else {
+    for (uint32_t i = tid; i < P; i += kThreads) sh.wd[i] = wt(val(i));
+    __syncthreads();
+  }
+
+  // The draw (sample.rs:260-272, 274-292): u = unit() * (the kept weight), then the first kept rank
+  // whose cumulative at T passes u, or the last kept one when none does.
+  scan_runs();
+  const double ulo = sh.u01 * (Wkeep - Wkeep_err) * (1.0 - gj) * (1.0 - 4.0 * kU);
+  const double uhi = sh.u01 * (Wkeep + Wkeep_err) * (1.0 + gj) * (1.0 + 4.0 * kU);
+  const double err = Ew + g40 * W_all;
+  uint32_t jp = kNone, jc = kNone, last = kNone;
+#pragma unroll
+  for (int q = 0; q < kScanPer; ++q) {
+    const uint32_t i = tid * kScanPer + q;
+    if (i >= P) continue;
+    const uint32_t k = run_of(i), r = rank_of(i, k);
+    if (r >= keep) continue;
+    if (r + 1 == keep) last = i;
+    const double S = __dadd_rn(sel3(k, wbr[0], wbr[1], wbr[2]), __dsub_rn(__dadd_rn(off, loc[q]), run_base[k]));
+    if ((S + err) * (1.0 + gj) > ulo) jp = min(jp, r);
+    if ((S - err) * (1.0 - gj) > uhi) jc = min(jc, r);
+  }
+  jp = block_min_u32<kWaves>(jp, sh.red_u);
+  jc = block_min_u32<kWaves>(jc, sh.red_u);
+  last = block_min_u32<kWaves>(last, sh.red_u);
+  // Ranks before the draw's first bin cannot pass u (their bins' prefixes cannot reach u_lo), and
+  // every kept rank from there on was collected; so the first collected rank that may pass u is
+  // the first of all.
+  uint32_t pick_rank;
+  if (jp == kNone) {
+    if (last == kNone) return false;  // the last kept value was not collected
+    pick_rank = keep - 1;
+  } else if (jp == jc) {
+    pick_rank = jc;
+  } else {
+    return false;
+  }
+  uint32_t pi = kNone;
+  for (uint32_t i = tid; i < P; i += kThreads)
+    if (rank_of(i, run_of(i)) == pick_rank) pi = i;
+  pi = block_min_u32<kWaves>(pi, sh.red_u);
+  if (pi == kNone) return false;
+  if (tid == 0) {
+    a.tokens[row] = packed_id(sh.sk[pi]);
+    a.status[row] = AS_ROW_OK | AS_ROW_DEEP_PATH;
+    if (a.kept_count) a.kept_count[row] = keep;
+  }
+  return true;
+}
+
+
+// Returns true when it settled the row.
+// The row's history counts in its scratch (u32 per id), for the passes over the whole row: whether
+// penalties act (false: no counts).
+__device__ __noinline__ bool deep_prep(const FinishArgs& a, const RowParams& p, uint32_t row) {
+  const uint32_t n = a.n, tid = threadIdx.x;
+  uint32_t* cnt = a.scratch + (uint64_t)row * a.scratch_stride;
   uint32_t hb;
   const uint32_t he = history_bounds(a, p, row, &hb);
   const uint32_t extra = a.extra_ids ? p.extra : 0;
@@ -908,6 +1316,22 @@ __device__ __noinline__ bool deep_row(const FinishArgs& a, const RowParams& p, u
     }
     __syncthreads();
   }
+  return pen;
+}
+
+// The full deep path, after deep_prep: returns true when it settled the row.
+__device__ __noinline__ bool deep_row(const FinishArgs& a, const RowParams& p, uint32_t row, bool pen) {
+  Shared& sh = shm();
+  const uint32_t n = a.n, tid = threadIdx.x, lane = tid & (kWave - 1);
+  uint32_t* S = a.scratch + (uint64_t)row * a.scratch_stride;
+  uint32_t* cnt = S;
+  uint64_t* bufA = reinterpret_cast<uint64_t*>(S + ((n + 1) & ~1u));
+  uint64_t* bufB = bufA + n;
+  const float* x = a.logits + (uint64_t)row * a.row_stride;
+
+  uint32_t hb;
+  const uint32_t he = history_bounds(a, p, row, &hb);
+  const uint32_t extra = a.extra_ids ? p.extra : 0;
   // The counts start 16-byte aligned (the scratch stride is a multiple of 4 words). History values
   // are few: their penalty runs out of line, so that the passes do not evaluate it for every value.
   const uint32_t* pcnt = pen ? cnt : nullptr;
@@ -941,6 +1365,7 @@ __device__ __noinline__ bool deep_row(const FinishArgs& a, const RowParams& p, u
   // A slice whose statistics the scan could not finish (too many distinct history ids or
   // candidates) leaves the maxima and sums incomplete: the exact-order path recomputes everything.
   if (sh.stats_bad) return false;
+
 
   const uint32_t mk = sh.mk;
   const double top = (double)key_value(mk);
@@ -2018,10 +2443,20 @@ __device__ __forceinline__ void finish_row(const FinishArgs& a, uint32_t row) {
   }
 
   if (sh.exact) {
+    // Rows without a top-k first try collecting only the bins their decisions fall in (kept lists
+    // need every kept value in order: those rows take the full deep path). Each path is called at
+    // the same depth, so that the kernel's stack is the largest of theirs, not their sum.
     __syncthreads();
-    if (!deep_row(a, a.params[row], row)) {
+    const RowParams& pr = a.params[row];
+    const bool pen = deep_prep(a, pr, row);
+    bool done = false;
+    if (!sh.stats_bad && pr.mode != kModeTopK && pr.mode != kModeExactTopK && !a.kept_ids) {
+      done = deep_bins(a, pr, row, pen);
       __syncthreads();
-      exact_row(a, a.params[row], row);
+    }
+    if (!done && !deep_row(a, pr, row, pen)) {
+      __syncthreads();
+      exact_row(a, pr, row);
     }
   }
 }

@@ -6,7 +6,8 @@ A step is one as_sample call over the 256-row batch, inputs already in HBM. Thre
 batch rotate between steps so no step finds its rows in the 256 MB Infinity Cache. The JSON line
 also carries batch-1 latency (configs 1-4: greedy, stochastic, penalised, and as_verify over 6 rows),
 the roofline of the whole chain (every kernel of one as_sample call, HIP events on the library's
-stream) with the scan kernel's share beside it, and the CPU oracle timed on this host per
+stream) with the scan kernel's share beside it, two worst-case 256-row batches (no filter at T = 1,
+and min-p 0.002), and the CPU oracle timed on this host per
 configuration, with and without the reference's device-to-host copy of each row.
 
     python bench.py [--gpus 1] [--steps K] [--warmup W]
@@ -159,6 +160,43 @@ def gpu_batch1(reps=200):
     out["config4"] = dict(rows=int(rows.shape[0]), read=int(res[0]), accepted=int(res[1]),
                           us_per_call_median=round(float(np.median(t)), 2), us_per_call_best=round(float(t.min()), 2),
                           kernel_us=round((scan_ms + rest_ms) / calls * 1e3, 2))
+    return out
+
+
+def gpu_worst(reps=10):
+    """Batches that config 5 does not reach: 256 rows of config 5's logits (no history) with no
+    filter at T = 1 (every draw's total is the whole row's, and a draw may land past the sorted
+    candidates), and 256 rows with min-p 0.002 and no top-k (floor sets of thousands of values).
+    Per call: the chain's kernel time (HIP events on the library's stream) and how many rows took
+    the rare paths."""
+    import torch
+
+    from artemis_amd import Context, PackedSampling, Sampling, states_tensor, workloads
+
+    w = workloads.config5()
+    dev = torch.device("cuda:0")
+    rows, n = w.logits.shape
+    host = torch.from_numpy(w.logits)
+    sets = [host.to(dev) for _ in range(3)]
+    ctx = Context(max_rows=rows, max_vocab=n)
+    out = {}
+    for name, s in [("unfiltered_t1", Sampling(1.0, 0, 1.0, 0.0)), ("minp_0.002", Sampling(0.7, 0, 1.0, 0.002))]:
+        packed, res = PackedSampling([s] * rows), ctx.outputs(rows)
+        rng = states_tensor(w.seeds, dev)
+        for i in range(2):
+            ctx.sample_batch(sets[i % 3], packed, rng, out=res)
+        _, st, *_ = ctx.sample_batch(sets[0], packed, rng, out=res)
+        status = st.cpu().numpy()
+        ctx.profile(True)
+        for i in range(reps):
+            ctx.sample_batch(sets[i % 3], packed, rng, out=res)
+        scan_ms, rest_ms, calls = ctx.profile_read()
+        ctx.profile(False)
+        out[name] = dict(us_per_call=round((scan_ms + rest_ms) / calls * 1e3, 2),
+                         scan_us=round(scan_ms / calls * 1e3, 2), after_scan_us=round(rest_ms / calls * 1e3, 2),
+                         deep_rows=int(((status & 0x400) != 0).sum()), exact_rows=int(((status & 0x100) != 0).sum()),
+                         tail_pass_rows=int(((status & 0x800) != 0).sum()))
+    ctx.close()
     return out
 
 
@@ -355,10 +393,12 @@ def main():
         sys.exit(2)
 
     g = gpu_config5(a.steps, a.warmup)
-    b1 = lpb = head = None
+    b1 = lpb = head = worst = None
     if not a.only_config5:
         log("bench: batch-1 latency")
         b1 = gpu_batch1()
+        log("bench: worst-case batches")
+        worst = gpu_worst()
         log("bench: log-probabilities")
         lpb = gpu_logprobs()
         log("bench: output head")
@@ -409,6 +449,7 @@ def main():
         "exact_path_rows": g["exact_rows"],
         "deep_path_rows": g["deep_rows"],
         "batch1": b1,
+        "worst_case_batches": worst,
         "logprobs_top20": lpb,
         "head_q6k_248320x2048": head,
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",

@@ -43,8 +43,10 @@ extern "C" {
  * deeper than the fast path's candidates. Informational; the token is the same either way. */
 #define AS_ROW_EXACT_PATH 0x100u
 /* OR-ed into the status: the kept set runs deeper than the values the fast path sorted; the token
- * is exact (the unsorted tail's weight is bounded and cannot change it), kept_count is a lower
- * bound and the kept lists hold the first kept_count ids with weights over that prefix. */
+ * is exact (the unsorted tail's weight is bounded and cannot change it) and kept_count is a lower
+ * bound. Only a call without kept lists (kept_ids null) takes this shortcut: with kept lists, such
+ * a row is settled by the deep or exact-order path, so its kept_count, ids and probabilities are the
+ * reference's. */
 #define AS_ROW_KEPT_PARTIAL 0x200u
 /* OR-ed into the status: the cut or the draw lay past the fast path's candidates and a second pass
  * over the row settled it (informational; the token is the reference's either way). */
