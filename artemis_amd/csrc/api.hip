@@ -33,7 +33,8 @@ struct as_ctx {
   RowShare* d_share = nullptr;
   as_dev::RowTail* d_tail = nullptr;
   as_dev::TailBins* d_tail_bins = nullptr;
-  as_dev::TailList* d_tail_list = nullptr;
+  as_dev::TailList* d_tail_list = nullptr;  // two lists: call c takes list c mod 2
+  uint64_t* d_tail_claims = nullptr;         // one per finish workgroup: max(max_rows, kTailGroups)
   bool share_dirty = false;  // a scan ran without its finish (a failed launch): the context is unusable
   int force_path = 0;        // as_debug_path: 0 automatic, 1 the sliced scan, 2 the row kernel
   uint32_t* d_fused_count = nullptr;  // the row kernel's count of ended workgroups
@@ -235,7 +236,6 @@ int run_rows(as_ctx* c, const Plan& pl, const RowParams* rows, const float* logi
   a.share = c->d_share;
   a.tail = c->d_tail;
   a.tail_bins = c->d_tail_bins;
-  a.tail_list = c->d_tail_list;
   a.hist_off = hist_off;
   a.hist_ids = hist_ids;
   a.extra_ids = extra_ids;
@@ -254,6 +254,10 @@ int run_rows(as_ctx* c, const Plan& pl, const RowParams* rows, const float* logi
   a.scratch_stride = c->scratch_stride;
   a.done = c->h_done;
   a.call = ++c->calls;
+  a.tail_list = c->d_tail_list + (a.call & 1);
+  a.tail_next = c->d_tail_list + ((a.call + 1) & 1);
+  a.tail_claims = c->d_tail_claims;
+  a.n_rows = n_rows;
   a.max_history = c->max_history;
   a.fused = pl.row_kernel ? 1u : 0u;
   a.fused_count = c->d_fused_count;
@@ -299,15 +303,16 @@ int run_rows(as_ctx* c, const Plan& pl, const RowParams* rows, const float* logi
   order_rows(rows, n_rows, &c->order, c->order_cost);
   AS_HIP(c, as_launch::scan(c->stream, vec, logits, c->d_zero, row_stride, n, n_rows, n_seg, pl.slice_len,
                             h, c->d_block, c->d_share, hist_off, hist_ids, extra_ids, c->d_stats, c->d_cands,
-                            pl.stride, c->d_tail_list, c->order));
+                            pl.stride, a.tail_list, c->order));
   if (e1) AS_HIP(c, hipEventRecord(e1, c->stream));
-  // The tail kernel serves only rows without a top-k that have min-p's floor (the scan flags no
-  // other row for it): a call with none skips its launch.
-  bool floor_rows = false;
-  for (uint32_t r = 0; r < n_rows && !floor_rows; ++r)
-    floor_rows = rows[r].mode == as_dev::kModePartial && rows[r].min_p > 0.0f;
-  if (floor_rows) AS_HIP(c, as_launch::tail(c->stream, n_rows, n, c->d_args));
-  AS_HIP(c, as_launch::finish(c->stream, n_rows, c->d_args));
+  // Only rows without a top-k that have min-p's floor can be flagged for S's sums: with any, the
+  // finish kernel runs enough workgroups to take their parts at once.
+  uint32_t floor_rows = 0;
+  for (uint32_t r = 0; r < n_rows; ++r)
+    floor_rows += (rows[r].mode == as_dev::kModePartial && rows[r].min_p > 0.0f) ? 1u : 0u;
+  const uint32_t tail_items = std::min(floor_rows, as_launch::kTailRows) * as_launch::tail_parts(n);
+  const uint32_t groups = std::max(n_rows, std::min(tail_items, as_launch::kTailGroups));
+  AS_HIP(c, as_launch::finish(c->stream, groups, c->d_args));
   c->share_dirty = false;
   if (e2) AS_HIP(c, hipEventRecord(e2, c->stream));
   return AS_OK;
@@ -366,6 +371,7 @@ int as_destroy(as_ctx* c) {
   (void)hipFree(c->d_tail);
   (void)hipFree(c->d_tail_bins);
   (void)hipFree(c->d_tail_list);
+  (void)hipFree(c->d_tail_claims);
   (void)hipFree(c->d_cands);
   (void)hipFree(c->d_scratch);
   (void)hipFree(c->d_vstatus);
@@ -413,8 +419,11 @@ int as_create(int device, void* hip_stream, uint32_t max_rows, uint32_t max_voca
   if (e == hipSuccess) e = hipMemset(c->d_tail, 0, sizeof(as_dev::RowTail) * max_rows);
   if (e == hipSuccess) e = hipMalloc(&c->d_tail_bins, sizeof(as_dev::TailBins) * max_rows);
   if (e == hipSuccess) e = hipMemset(c->d_tail_bins, 0, sizeof(as_dev::TailBins) * max_rows);
-  if (e == hipSuccess) e = hipMalloc(&c->d_tail_list, sizeof(as_dev::TailList));
-  if (e == hipSuccess) e = hipMemset(c->d_tail_list, 0, sizeof(as_dev::TailList));
+  if (e == hipSuccess) e = hipMalloc(&c->d_tail_list, 2 * sizeof(as_dev::TailList));
+  if (e == hipSuccess) e = hipMemset(c->d_tail_list, 0, 2 * sizeof(as_dev::TailList));
+  const size_t claims = sizeof(uint64_t) * std::max(max_rows, as_launch::kTailGroups);
+  if (e == hipSuccess) e = hipMalloc(&c->d_tail_claims, claims);
+  if (e == hipSuccess) e = hipMemset(c->d_tail_claims, 0, claims);
   if (e == hipSuccess)
     e = hipMalloc(&c->d_cands, sizeof(uint64_t) * (uint64_t)max_rows * as_launch::kCandCap);
   if (e == hipSuccess) e = hipMalloc(&c->d_scratch, sizeof(uint32_t) * (uint64_t)max_rows * c->scratch_stride);

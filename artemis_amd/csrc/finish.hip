@@ -33,25 +33,27 @@ using as_launch::FinishArgs;
 namespace {
 
 // The arguments are read from device memory (the scan's copy of the pinned block), which costs each
-// workgroup less than a large kernel-argument block.
+// workgroup less than a large kernel-argument block. Workgroup b finishes row b; those past the
+// call's rows only take parts of S's sums (tail_start), which every workgroup whose row is not
+// flagged does first.
 __global__ __launch_bounds__(1024) void finish_kernel(const FinishArgs* __restrict__ ap) {
   const FinishArgs& a = *ap;
-  as_fin_sliced::finish_row(a, blockIdx.x);
-  // The row's tail histogram goes back to zero for the next call once this row is done with it
-  // (every path above has ended, in every thread).
+  const uint32_t row = blockIdx.x;
+  as_fin_sliced::tail_start(a, row, gridDim.x);
+  if (row >= a.n_rows) return;
+  as_fin_sliced::finish_row(a, row);
+  // A flagged row's S sums and histogram go back to zero for the next call once every part has
+  // ended and every path above is done with them.
   __syncthreads();
-  if (as_fin_sliced::shm().tail_parts != 0u && threadIdx.x < as_dev::kTailBins) {
-    a.tail_bins[blockIdx.x].m[threadIdx.x] = 0.0;
-    a.tail_bins[blockIdx.x].w[threadIdx.x] = 0.0;
-  }
+  if (as_fin_sliced::shm().tail_slot != kNone) as_fin_sliced::tail_end(a, row);
 }
 
 }  // namespace
 
 namespace as_launch {
 
-hipError_t finish(hipStream_t stream, uint32_t n_rows, const FinishArgs* a) {
-  hipLaunchKernelGGL(finish_kernel, dim3(n_rows), dim3(1024), 0, stream, a);
+hipError_t finish(hipStream_t stream, uint32_t groups, const FinishArgs* a) {
+  hipLaunchKernelGGL(finish_kernel, dim3(groups), dim3(1024), 0, stream, a);
   return hipGetLastError();
 }
 

@@ -47,6 +47,8 @@ struct Shared {
   uint64_t bound_key;
   double u01, sum, x, eps, x1, eps1, r_prefix, w_lo, w_hi, m_lo, m_hi;
   uint32_t draw_rng;  // the row draws: its stream advances once the candidates are in flight
+  // S's sums (tail_start, tail_wait): this call's flagged rows, this row's place among them.
+  uint32_t tl_n, tl_rows[kTailListMax], tail_slot, tail_waited, tail_won;
 };
 // The workgroup's LDS, at file scope so that the out-of-line paths below address it as LDS: a static
 // array, or the kernel's dynamic LDS (AS_DYNAMIC_LDS) when another body shares it.
@@ -58,6 +60,22 @@ __device__ __forceinline__ Shared& shm() { return g_sh_static; }
 #endif
 
 // --- block helpers ------------------------------------------------------------------------------
+
+// Device-coherent loads and stores (relaxed, agent scope): what other workgroups of the kernel write
+// with device atomics or such stores, whatever this XCD's L2 holds.
+__device__ __forceinline__ uint32_t ld_agent(const uint32_t* p) {
+  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ uint64_t ld_agent(const uint64_t* p) {
+  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ double ld_agent(const double* p) {
+  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void st_agent(uint64_t* p, uint64_t v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
 
 // Exclusive prefix sum of one f64 per thread over the block.
 __device__ double block_exclusive_scan_f64(double x, double* wave_tot) {
@@ -839,42 +857,73 @@ __device__ __forceinline__ uint32_t stream_draw(Shared& sh, const uint64_t* buf,
 }
 
 // The deep path's passes over a row: 16 values per thread per step, with their history counts
-// (cnt, 0 when null), all loads of a step issued before any value is used (16-byte loads, scalar
-// ones for an unaligned row or the ragged end). f(i, v, c) runs for each value.
-template <class F>
+// (cnt, 0 when null). One workgroup streams a whole row, so its loads' latency, not HBM, bounds a
+// pass. With kPipe and without counts, whole 16-byte steps run two at a time, each step's loads
+// issued before the previous step's values are used (the last of them reloads a step rather than
+// branch); otherwise (counts take as many registers again, and some callers have none to spare) a
+// step's loads are all issued before any value is used. Scalar loads cover an unaligned row and the
+// ragged end. f(i, v, c) runs for each value.
+template <bool kPipe = false, class F>
 __device__ __forceinline__ void for_each_value(const float* x, const uint32_t* cnt, uint32_t n, bool vec, F f) {
   typedef float f32x4 __attribute__((ext_vector_type(4)));
   typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
   constexpr uint32_t kStep = 16 * kThreads;
   const uint32_t tid = threadIdx.x;
-  for (uint32_t b0 = 0; b0 < n; b0 += kStep) {
-    if (vec && b0 + kStep <= n) {
-      f32x4 q[4];
-      u32x4 k[4];
+  auto at = [&](uint32_t s, int j) { return s * kStep + (j * kThreads + tid) * 4; };
+  uint32_t b0 = 0;
+  if (vec) {
+    const uint32_t whole = n / kStep;
+    if (kPipe && !cnt && whole > 0) {
+      f32x4 qa[4], qb[4];
+      auto load = [&](f32x4 (&q)[4], uint32_t s) {
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const uint32_t e = b0 + (j * kThreads + tid) * 4;
-        q[j] = *reinterpret_cast<const f32x4*>(x + e);
-        k[j] = cnt ? *reinterpret_cast<const u32x4*>(cnt + e) : u32x4{0u, 0u, 0u, 0u};
+        for (int j = 0; j < 4; ++j) q[j] = *reinterpret_cast<const f32x4*>(x + at(s, j));
+      };
+      auto use = [&](const f32x4 (&q)[4], uint32_t s) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+#pragma unroll
+          for (int c = 0; c < 4; ++c) f(at(s, j) + c, q[j][c], 0u);
+      };
+      load(qa, 0);
+      uint32_t s = 0;
+      for (; s + 2 <= whole; s += 2) {
+        load(qb, s + 1);
+        use(qa, s);
+        load(qa, min(s + 2, whole - 1));
+        use(qb, s + 1);
       }
-#pragma unroll
-      for (int j = 0; j < 4; ++j)
-#pragma unroll
-        for (int c = 0; c < 4; ++c) f(b0 + (j * kThreads + tid) * 4 + c, q[j][c], k[j][c]);
+      if (s < whole) use(qa, s);
     } else {
-      float q[16];
-      uint32_t k[16];
+      for (uint32_t s = 0; s < whole; ++s) {
+        f32x4 q[4];
+        u32x4 k[4];
 #pragma unroll
-      for (int j = 0; j < 16; ++j) {
-        const uint32_t i = b0 + j * kThreads + tid;
-        q[j] = (i < n) ? x[i] : 0.0f;
-        k[j] = (cnt && i < n) ? cnt[i] : 0u;
-      }
+        for (int j = 0; j < 4; ++j) {
+          q[j] = *reinterpret_cast<const f32x4*>(x + at(s, j));
+          k[j] = cnt ? *reinterpret_cast<const u32x4*>(cnt + at(s, j)) : u32x4{0u, 0u, 0u, 0u};
+        }
 #pragma unroll
-      for (int j = 0; j < 16; ++j) {
-        const uint32_t i = b0 + j * kThreads + tid;
-        if (i < n) f(i, q[j], k[j]);
+        for (int j = 0; j < 4; ++j)
+#pragma unroll
+          for (int c = 0; c < 4; ++c) f(at(s, j) + c, q[j][c], k[j][c]);
       }
+    }
+    b0 = whole * kStep;
+  }
+  for (; b0 < n; b0 += kStep) {
+    float q[16];
+    uint32_t k[16];
+#pragma unroll
+    for (int j = 0; j < 16; ++j) {
+      const uint32_t i = b0 + j * kThreads + tid;
+      q[j] = (i < n) ? x[i] : 0.0f;
+      k[j] = (cnt && i < n) ? cnt[i] : 0u;
+    }
+#pragma unroll
+    for (int j = 0; j < 16; ++j) {
+      const uint32_t i = b0 + j * kThreads + tid;
+      if (i < n) f(i, q[j], k[j]);
     }
   }
 }
@@ -952,7 +1001,7 @@ __device__ __noinline__ bool deep_bins(const FinishArgs& a, const RowParams& p, 
     if (by_top_p) atomicAdd(&hm[b], w1(v));
     atomicAdd(&hw[b], wt(v));
   };
-  for_each_value(x, pcnt, n, vec, [&](uint32_t, float v, uint32_t c) {
+  for_each_value<true>(x, pcnt, n, vec, [&](uint32_t, float v, uint32_t c) {
     if (__builtin_expect(c == 0, 1)) count(v);
   });
   if (pen) {
@@ -1135,7 +1184,7 @@ __device__ __noinline__ bool deep_bins(const FinishArgs& a, const RowParams& p, 
     return in;
   };
   if (fits) {
-    for_each_value(x, pcnt, n, vec, [&](uint32_t i, float v, uint32_t c) {
+    for_each_value<true>(x, pcnt, n, vec, [&](uint32_t i, float v, uint32_t c) {
       if (__builtin_expect(c == 0, 1) && in_runs(bin_of(v))) {
         const uint32_t s = atomicAdd(&sh.pick, 1u);
         if (s < (uint32_t)kCap) sh.sk[s] = pack(total_key(v), i);
@@ -1870,7 +1919,7 @@ __device__ __noinline__ bool tail_sums(const FinishArgs& a, const RowParams& p, 
 // two weights, exp(l - top)^(1/T - 1), falls with the rank). K >= top-p's cumulative mass past the
 // sorted values, or K = M when the floor cuts first. sh.x1 +- sh.eps1 is total1 and sh.r_prefix the
 // sorted values' mass at T = 1 (top-p rows); with_tail: [sh.w_lo, sh.w_hi] bounds W and [sh.m_lo,
-// sh.m_hi] bounds M. With bins (the tail kernel's histogram of S, TailBins), the cut is placed
+// sh.m_hi] bounds M. With bins (S's histogram, TailBins), the cut is placed
 // within S by the bins' cumulative mass at T = 1: every bin whose cumulative mass stays below top-p's
 // least target is kept whole, and no bin past the first whose cumulative mass reaches its largest
 // target is kept at all, which bounds the kept tail's weight by sums of whole bins. Returns the rank
@@ -1906,8 +1955,8 @@ __device__ __noinline__ uint32_t draw_past(const FinishArgs& a, const RowParams&
       const as_dev::TailBins& tb = a.tail_bins[row];
       double bm = 0.0, bw = 0.0;
       if (tid < as_dev::kTailBins) {
-        bm = tb.m[tid];
-        bw = tb.w[tid];
+        bm = ld_agent(&tb.m[tid]);
+        bw = ld_agent(&tb.w[tid]);
       }
       const double mlo = fmax(0.0, bm * (1.0 - slack) - fl_b), mhi = bm * (1.0 + slack) + fl_b;
       const double wlo = fmax(0.0, bw * (1.0 - slack) - fl_b), whi = bw * (1.0 + slack) + fl_b;
@@ -1944,6 +1993,358 @@ __device__ __noinline__ uint32_t draw_past(const FinishArgs& a, const RowParams&
   return j;
 }
 
+// --- S's sums in the finish kernel ---------------------------------------------------------------
+//
+// A min-p row without a top-k whose scan did not keep every value above its floor (a slice flagged
+// it in the call's TailList) may need the weights of S, the values ranking below the candidates'
+// bound R and at or above the floor: W = sum of exp((l - top) / T), M = sum of exp(l - top), |S|,
+// S's histogram (TailBins) and, when S is small, its values (in the row's scratch). The flagged rows
+// are cut into parts of kTailLen values, item i being part i mod parts of the list's row i / parts.
+// The H workgroups whose row is not flagged (and those past the call's rows) are the helpers: helper
+// h takes items h, h + H, ..., first of all (tail_start), once it has claimed that set by raising
+// its claim word to the call's number (an atomic max: a lower number is an earlier call's; the
+// claim is issued with the first item's loads and checked before anything is written). A flagged
+// row's workgroup, when it needs the sums (tail_wait), claims the sets holding its row's items that
+// no helper has claimed (helpers not yet running) and takes them itself, then waits only for sets
+// that running workgroups hold. With no helper, each flagged row takes its own items. An item adds
+// its sums with device atomics and stores its values with device-coherent stores, and counts itself
+// in RowTail::ended once they are complete; the row's workgroup reads them with device-coherent
+// loads, and clears them after its row (tail_end).
+
+// An item's tables, over sh.wd (free whenever an item runs: before the row's work, or while its
+// workgroup waits with the row's candidates in sh.sk).
+constexpr uint32_t kPartHash = 512;   // distinct history ids in a part
+constexpr uint32_t kTailStage = 2048; // values of S a part stages before they go to scratch
+struct TailLds {
+  double bin_m[kTailBins];
+  double bin_w[kTailBins];
+  float vals[as_launch::kTailLen];  // the part's raw values (the history's are read here)
+  uint32_t bitmap[as_launch::kTailLen / 32];
+  uint32_t hid[kPartHash];
+  uint32_t hcnt[kPartHash];
+  uint64_t stage[kTailStage];
+  double red_w[kWaves], red_m[kWaves];
+  uint32_t red_c[kWaves];
+  uint32_t overflow, staged, base, skip, top, bad;
+  uint64_t R;
+};
+static_assert(sizeof(TailLds) <= sizeof(double) * kCap, "an item's tables fit in sh.wd");
+static_assert(as_launch::kTailLen % (4 * kThreads) == 0, "whole 16-byte groups per thread");
+static_assert(kPartHash % kWave == 0 && kPartHash <= (uint32_t)kThreads, "whole waves take the history's slots, one each");
+
+// One item: part `part` of flagged row `row`. With `claim`, thread 0 first claims the helper's set
+// through that word; the claim is lost (returns false, nothing written) when a flagged row's
+// workgroup took the set first. Loads that need only the row go out at once (the claim, the part's
+// values, the row's parameters, history bounds and slice statistics), then the history's ids (whose
+// raw values are read from the part's values, staged in LDS). S's count is reserved in the row's
+// list while the terms are computed.
+__device__ __noinline__ bool tail_item(const FinishArgs& a, uint32_t row, uint32_t part, uint64_t* claim) {
+  Shared& sh = shm();
+  TailLds& t = *reinterpret_cast<TailLds*>(sh.wd);
+  constexpr uint32_t kLen = as_launch::kTailLen, kPer = kLen / kThreads;
+  const uint32_t tid = threadIdx.x, lane = tid & (kWave - 1), wave = tid / kWave;
+  const uint32_t n = a.n, b0 = part * kLen, b1 = min(b0 + kLen, n), len = b1 - b0;
+  const float* x = a.logits + (uint64_t)row * a.row_stride;
+  const bool vec = a.vec && a.row_stride % 4 == 0 && len == kLen;
+  typedef float f32x4 __attribute__((ext_vector_type(4)));
+  uint64_t old = 0;
+  if (claim && tid == 0)
+    old = __hip_atomic_fetch_max(claim, a.call, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  // Value k of this thread is at offset at(k) of the part.
+  auto at = [&](uint32_t k) { return vec ? ((k / 4) * kThreads + tid) * 4 + (k % 4) : k * kThreads + tid; };
+  float v[kPer];
+  if (vec) {
+#pragma unroll
+    for (uint32_t j = 0; j < kPer / 4; ++j) {
+      const f32x4 q = *reinterpret_cast<const f32x4*>(x + b0 + (j * kThreads + tid) * 4);
+#pragma unroll
+      for (int c = 0; c < 4; ++c) v[4 * j + c] = q[c];
+    }
+  } else {
+#pragma unroll
+    for (uint32_t k = 0; k < kPer; ++k) v[k] = at(k) < len ? x[b0 + at(k)] : 0.0f;
+  }
+  const RowParams& p = a.params[row];
+  uint32_t hb;
+  const uint32_t he = as_launch::history_bounds(a, p, row, &hb);
+  const uint32_t extra = a.extra_ids ? p.extra : 0;
+  const bool pen = (p.flags & kFlagPenalties) && (he > hb || extra > 0);
+  // The row's largest value and bound, and whether its statistics are whole, from its slices.
+  uint32_t top = 0, bad = 0;
+  uint64_t bound = 0;
+  for (uint32_t s = tid; s < a.n_seg; s += kThreads) {
+    const SegStats& g = a.stats[(uint64_t)row * a.n_seg + s];
+    top = max(top, g.max_key);
+    if (g.truncated & 1u) bound = max(bound, g.bound);
+    if ((g.truncated & 2u) || g.nonfinite != kNone) bad = 1;
+  }
+#pragma unroll
+  for (uint32_t k = 0; k < kPer; ++k)
+    if (at(k) < kLen) t.vals[at(k)] = v[k];
+  if (pen) {
+    for (uint32_t i = tid; i < kLen / 32; i += kThreads) t.bitmap[i] = 0;
+    for (uint32_t i = tid; i < kPartHash; i += kThreads) {
+      t.hid[i] = kNone;
+      t.hcnt[i] = 0;
+    }
+  }
+  for (uint32_t b = tid; b < kTailBins; b += kThreads) {
+    t.bin_m[b] = 0.0;
+    t.bin_w[b] = 0.0;
+  }
+  if (tid == 0) {
+    t.top = 0;
+    t.bad = 0;
+    t.R = 0;
+    t.overflow = 0;
+    t.staged = 0;
+  }
+  __syncthreads();
+  if (tid < a.n_seg) {
+    atomicMax(&t.top, top);
+    if (bound) atomicMax(reinterpret_cast<unsigned long long*>(&t.R), (unsigned long long)bound);
+    if (bad) t.bad = 1;
+  }
+  if (pen) {
+    auto mark = [&](uint32_t id) {
+      const uint32_t off = id - b0;
+      if (off >= len) return;
+      atomicOr(&t.bitmap[off >> 5], 1u << (off & 31u));
+      uint32_t h = (id * 0x9E3779B1u) >> (32 - 9);
+      static_assert(kPartHash == 1u << 9, "the hash's top bits");
+      for (uint32_t probe = 0; probe < kPartHash; ++probe) {
+        const uint32_t prev = atomicCAS(&t.hid[h], kNone, id);
+        if (prev == kNone || prev == id) {
+          atomicAdd(&t.hcnt[h], 1u);
+          return;
+        }
+        h = (h + 1) & (kPartHash - 1);
+      }
+      t.overflow = 1;
+    };
+    for (uint32_t h = hb + tid; h < he; h += kThreads) mark(a.hist_ids[h]);
+    for (uint32_t h = tid; h < extra; h += kThreads) mark(a.extra_ids[h]);
+  }
+  if (tid == 0) t.skip = (claim && old >= a.call) ? 1u : 0u;
+  __syncthreads();
+  if (t.skip) return false;
+  RowTail& rt = a.tail[row];
+  const float topf = key_value(t.top);
+  const float fl = floor_f32(__dadd_rn((double)topf, p.ln_min_p));
+  const uint64_t R = t.R;
+  // S is defined for a min-p row without a top-k whose statistics are whole and whose bound lies
+  // above its floor; otherwise the item only ends.
+  const bool defined = p.mode == kModePartial && p.min_p > 0.0f && t.bad == 0u &&
+                       ((uint64_t)total_key(fl) << 32) < R;
+  if (defined && t.overflow == 0u) {
+    // In S: v >= fl, and v ranks below R: v < R's value, or (rarely) equal to it and below in the
+    // packed order (which also orders -0 below +0).
+    const float rv = key_value((uint32_t)(R >> 32));
+    auto in_s = [&](float val, uint32_t id) {
+      bool in = val >= fl && val < rv;
+      if (__builtin_expect(val == rv, 0)) in = val >= fl && pack(total_key(val), id) < R;
+      return in;
+    };
+    bool in[kPer];
+    uint32_t cnt = 0;
+#pragma unroll
+    for (uint32_t k = 0; k < kPer; ++k) {
+      const uint32_t off = at(k);
+      const bool valid = off < len && !(pen && ((t.bitmap[off >> 5] >> (off & 31u)) & 1u));
+      in[k] = valid && in_s(v[k], b0 + off);
+      cnt += in[k] ? 1u : 0u;
+    }
+    // The history's ids in the part, penalised (one slot of the hash per thread).
+    float hv = 0.0f;
+    uint32_t hid = kNone;
+    bool hin = false;
+    if (pen && tid < kPartHash) {
+      hid = t.hid[tid];
+      if (hid != kNone) {
+        hv = penalize(t.vals[hid - b0], t.hcnt[tid], p);
+        hin = in_s(hv, hid);
+        cnt += hin ? 1u : 0u;
+      }
+    }
+    cnt = block_sum_u32<kWaves>(cnt, t.red_c);
+    // The part's place in the row's list, reserved now and read once the terms are in.
+    uint32_t base = 0;
+    if (tid == 0) {
+      base = __hip_atomic_fetch_add(&rt.count, cnt, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      if (cnt > kTailStage) __hip_atomic_fetch_or(&rt.lost, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    const float s1 = 1.44269502f, sw = (1.0f / p.temp) * s1;
+    // The histogram's scale: (rv - v) * bscale is monotone in v, so bins follow the rank order.
+    const float span = rv - fl;
+    const float bscale = (span > 0.0f && span < __builtin_inff()) ? (float)kTailBins / span : 0.0f;
+    float gw = 0.0f, gm = 0.0f;
+    // Called by every lane of the wave at once: the values in S add their terms and bins, and are
+    // staged with one LDS atomic per wave.
+    auto add = [&](bool in_, float val, uint32_t id) {
+      if (in_) {
+        const float d = val - topf;
+        const float tw = __builtin_amdgcn_exp2f(d * sw), tm = __builtin_amdgcn_exp2f(d * s1);
+        gw += tw;
+        gm += tm;
+        const uint32_t b = (uint32_t)fminf((rv - val) * bscale, (float)(kTailBins - 1));
+        atomicAdd(&t.bin_w[b], (double)tw);
+        atomicAdd(&t.bin_m[b], (double)tm);
+      }
+      const uint64_t mk = __ballot(in_);
+      if (mk) {
+        uint32_t sbase = 0;
+        if (lane == 0) sbase = atomicAdd(&t.staged, (uint32_t)__popcll(mk));
+        sbase = __builtin_amdgcn_readfirstlane(sbase);
+        const uint32_t i =
+            sbase + __builtin_amdgcn_mbcnt_hi((uint32_t)(mk >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)mk, 0u));
+        if (in_ && i < kTailStage) t.stage[i] = pack(total_key(val), id);
+      }
+    };
+#pragma unroll
+    for (uint32_t k = 0; k < kPer; ++k) add(in[k], v[k], b0 + at(k));
+    double w = (double)gw, m = (double)gm;
+    if (pen && tid < kPartHash) {
+      gw = 0.0f;
+      gm = 0.0f;
+      add(hin, hv, hid);
+      w += (double)gw;
+      m += (double)gm;
+    }
+    // Both sums over the block in one round (wave sums, then the waves' in order).
+    w = wave_sum_f64(w);
+    m = wave_sum_f64(m);
+    if (lane == 0) {
+      t.red_w[wave] = w;
+      t.red_m[wave] = m;
+    }
+    if (tid == 0) t.base = base;
+    __syncthreads();  // also: the LDS bins and the staged values are whole
+    if (tid == 0) {
+      double sw_ = t.red_w[0], sm_ = t.red_m[0];
+      for (int k = 1; k < kWaves; ++k) {
+        sw_ = __dadd_rn(sw_, t.red_w[k]);
+        sm_ = __dadd_rn(sm_, t.red_m[k]);
+      }
+      __hip_atomic_fetch_add(&rt.w, sw_, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      __hip_atomic_fetch_add(&rt.m, sm_, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      __hip_atomic_fetch_add(&rt.parts, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    // The part's bins into the row's.
+    as_dev::TailBins& tb = a.tail_bins[row];
+    for (uint32_t b = tid; b < kTailBins; b += kThreads) {
+      if (t.bin_w[b] != 0.0) __hip_atomic_fetch_add(&tb.w[b], t.bin_w[b], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      if (t.bin_m[b] != 0.0) __hip_atomic_fetch_add(&tb.m[b], t.bin_m[b], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    // The staged values to scratch, at the part's place in the row's list, when the list can hold
+    // them.
+    const uint32_t at0 = t.base, staged = min(cnt, kTailStage);
+    uint64_t* list = reinterpret_cast<uint64_t*>(a.scratch + (uint64_t)row * a.scratch_stride);
+    if (at0 + staged <= kTailKeep)
+      for (uint32_t i = tid; i < staged; i += kThreads) st_agent(list + at0 + i, t.stage[i]);
+  } else if (defined && tid == 0) {
+    __hip_atomic_fetch_or(&rt.failed, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+  // Every write above has completed (in every thread) before the item counts itself ended.
+  __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  __syncthreads();
+  if (tid == 0) __hip_atomic_fetch_add(&rt.ended, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  return true;
+}
+
+// First thing in every workgroup of the sliced finish: this call's flagged rows (the first
+// kTailRows) into LDS, this workgroup's row's place among them, and, for a helper, its set of items.
+__device__ __attribute__((unused)) void tail_start(const FinishArgs& a, uint32_t wg, uint32_t groups) {
+  Shared& sh = shm();
+  const uint32_t tid = threadIdx.x;
+  if (tid == 0) {
+    sh.tl_n = min(a.tail_list->count, as_launch::kTailRows);
+    sh.tail_slot = kNone;
+    sh.tail_waited = 0;
+  }
+  __syncthreads();
+  const uint32_t nl = sh.tl_n;
+  if (nl == 0) return;
+  if (tid < nl) {
+    const uint32_t r = a.tail_list->rows[tid];
+    sh.tl_rows[tid] = r;
+    if (r == wg) sh.tail_slot = tid;
+  }
+  __syncthreads();
+  const uint32_t helpers = groups - nl;
+  if (sh.tail_slot != kNone || helpers == 0) return;
+  uint32_t below = 0;  // flagged rows before this workgroup's
+  for (uint32_t k = 0; k < nl; ++k) below += sh.tl_rows[k] < wg ? 1u : 0u;
+  const uint32_t parts = as_launch::tail_parts(a.n), items = nl * parts, h = wg - below;
+  for (uint32_t i = h; i < items; i += helpers)
+    if (!tail_item(a, sh.tl_rows[i / parts], i % parts, i == h ? a.tail_claims + h : nullptr)) break;
+  __syncthreads();
+}
+
+// The flagged row's workgroup: takes the sets holding its row's items that no helper has claimed
+// (all its items when there is no helper), waits for the sets running helpers hold, and reads S's
+// sums (within 1e-4 relative: each term is within 3e-5, and terms under 2^-126 may have flushed to
+// 0). Once per row; sh.bcnt is free (the candidates are not yet sorted).
+constexpr uint32_t kTailSpin = 1u << 24;  // a guard: every set claimed is being summed by a running workgroup
+__device__ __noinline__ void tail_wait(const FinishArgs& a, uint32_t row) {
+  Shared& sh = shm();
+  const uint32_t tid = threadIdx.x, slot = sh.tail_slot, parts = as_launch::tail_parts(a.n);
+  const uint32_t nl = sh.tl_n, items = nl * parts, helpers = gridDim.x - nl;
+  if (helpers == 0) {
+    for (uint32_t q = 0; q < parts; ++q) tail_item(a, row, q, nullptr);
+  } else {
+    // One claim per thread (the won sets listed in sh.bcnt; of two threads claiming the same set
+    // only one wins), up to kThreads at a time.
+    static_assert(sizeof(sh.bcnt) / 4 >= (uint32_t)kThreads, "a list slot per thread");
+    for (uint32_t q0 = 0; q0 < parts; q0 += kThreads) {
+      __syncthreads();
+      if (tid == 0) sh.tail_won = 0;
+      __syncthreads();
+      const uint32_t q = q0 + tid, h = (slot * parts + q) % helpers;
+      if (q < parts &&
+          __hip_atomic_fetch_max(a.tail_claims + h, a.call, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < a.call)
+        sh.bcnt[atomicAdd(&sh.tail_won, 1u)] = h;
+      __syncthreads();
+      const uint32_t won = sh.tail_won;
+      for (uint32_t k = 0; k < won; ++k) {
+        const uint32_t hk = sh.bcnt[k];
+        for (uint32_t i = hk; i < items; i += helpers) tail_item(a, sh.tl_rows[i / parts], i % parts, nullptr);
+      }
+    }
+  }
+  RowTail& rt = a.tail[row];
+  if (tid == 0) {
+    for (uint32_t k = 0; ld_agent(&rt.ended) < parts && k < kTailSpin; ++k) __builtin_amdgcn_s_sleep(2);
+    const bool whole = ld_agent(&rt.ended) == parts;
+    const double w = ld_agent(&rt.w), m = ld_agent(&rt.m);
+    const uint32_t count = ld_agent(&rt.count), summed = ld_agent(&rt.parts);
+    const uint32_t failed = ld_agent(&rt.failed), lost = ld_agent(&rt.lost);
+    sh.have_tail = (whole && summed == parts && failed == 0u) ? 1u : 0u;
+    const double flush = (double)a.n * 0x1p-125;
+    sh.w_lo = fmax(0.0, w * (1.0 - 1e-4) - flush);
+    sh.w_hi = w * (1.0 + 1e-4) + flush;
+    sh.m_lo = fmax(0.0, m * (1.0 - 1e-4) - flush);
+    sh.m_hi = m * (1.0 + 1e-4) + flush;
+    sh.tail_count = count;
+    sh.tail_listed = (lost == 0u && count <= kTailKeep) ? 1u : 0u;
+    sh.tail_parts = summed;
+    sh.tail_waited = 1;
+  }
+  __syncthreads();
+}
+
+// After a flagged row: its items have all ended (waiting for them if the row did not need them);
+// its sums and bins go back to zero for the next call.
+__device__ __noinline__ __attribute__((unused)) void tail_end(const FinishArgs& a, uint32_t row) {
+  Shared& sh = shm();
+  if (!sh.tail_waited) tail_wait(a, row);
+  const uint32_t tid = threadIdx.x;
+  if (tid < sizeof(RowTail) / 4) reinterpret_cast<uint32_t*>(a.tail + row)[tid] = 0u;
+  if (tid < kTailBins) {
+    a.tail_bins[row].m[tid] = 0.0;
+    a.tail_bins[row].w[tid] = 0.0;
+  }
+}
+
 // --- the kernel ---------------------------------------------------------------------------------
 
 __device__ __forceinline__ void finish_row(const FinishArgs& a, uint32_t row) {
@@ -1953,26 +2354,18 @@ __device__ __forceinline__ void finish_row(const FinishArgs& a, uint32_t row) {
   const SegStats* gst = a.stats + (uint64_t)row * a.n_seg;
   const uint32_t n = a.n;
   if (tid < 256) sh.tab[tid] = as_exp::kTable[tid];
-  // The host learns that the scan no longer reads the call's parameter block; the tail kernel's
-  // list empties for the next call's scan (this call's tail kernel has ended).
-  if (!a.fused && row == 0 && tid == 0) {
-    __hip_atomic_store(a.done, a.call, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
-    a.tail_list->count = 0u;
+  // The host learns that the scan no longer reads the call's parameter block; the next call's list
+  // of flagged rows empties (this call's scan and the call before it have ended).
+  if (row == 0 && tid == 0) {
+    if (!a.fused) __hip_atomic_store(a.done, a.call, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+    a.tail_next->count = 0u;
   }
-  // The tail kernel's sums for the row: whole when every part of a flagged row added its own (within
-  // 3e-5 relative per term; 1e-4 to spare, and terms under 2^-126 that may have flushed to 0).
+  // S's sums: none until a flagged row waits for them (tail_wait).
   if (tid == 0) {
-    const RowTail t = a.tail[row];
-    const uint32_t parts = (n + as_launch::kTailLen - 1) / as_launch::kTailLen;
-    sh.have_tail = (a.share[row].gave_up != 0u && t.parts == parts && t.failed == 0u) ? 1u : 0u;
-    const double flush = (double)n * 0x1p-125;
-    sh.w_lo = fmax(0.0, t.w * (1.0 - 1e-4) - flush);
-    sh.w_hi = t.w * (1.0 + 1e-4) + flush;
-    sh.m_lo = fmax(0.0, t.m * (1.0 - 1e-4) - flush);
-    sh.m_hi = t.m * (1.0 + 1e-4) + flush;
-    sh.tail_count = t.count;
-    sh.tail_listed = (t.lost == 0u && t.count <= kTailKeep) ? 1u : 0u;
-    sh.tail_parts = t.parts;
+    sh.have_tail = 0;
+    sh.tail_count = 0;
+    sh.tail_listed = 0;
+    sh.tail_parts = 0;
   }
   // The slices' results, all loads in flight at once, with the row's RNG state and history bounds
   // (thread 0 keeps them in registers for the merge below).
@@ -1987,10 +2380,9 @@ __device__ __forceinline__ void finish_row(const FinishArgs& a, uint32_t row) {
   }
   for (uint32_t s = tid; s < a.n_seg; s += kThreads) sh.seg[s] = gst[s];
   __syncthreads();
-  // The row's shared words and tail sums go back to zero for the next call (this call's scan and
-  // tail kernel have ended, and their words were read above).
+  // The row's shared words go back to zero for the next call (this call's scan has ended, and their
+  // words were read above).
   if (tid < sizeof(RowShare) / 4) reinterpret_cast<uint32_t*>(a.share + row)[tid] = 0u;
-  if (tid >= 64 && tid < 64 + sizeof(RowTail) / 4) reinterpret_cast<uint32_t*>(a.tail + row)[tid - 64] = 0u;
   const SegStats* st = sh.seg;
 
   if (tid < kWave) {
@@ -2149,9 +2541,11 @@ __device__ __forceinline__ void finish_row(const FinishArgs& a, uint32_t row) {
       take_u01();
       __syncthreads();
     }
+    // A flagged row's S sums, before anything reads them (its candidates stay in sh.sk).
+    if (!a.fused && sh.tail_slot != kNone) tail_wait(a, row);
     const uint32_t total = min(sh.nsk, (uint32_t)kCap);
     const bool too_many = sh.nsk > (uint32_t)kCap;  // more candidates >= R than the finish holds
-    // A row whose floor set the tail kernel listed (S: every value below R and at or above the floor),
+    // A row whose floor set S's parts listed (S: every value below R and at or above the floor),
     // and whose whole floor set's mass at T = 1 is short of top-p's target: top-p never stops inside it
     // and min-p's floor cuts first (sample.rs:237-251), so the kept set is the candidates and all of S,
     // sorted once, together. The candidates' mass needs no order: a parallel sum of positive terms,
@@ -2172,7 +2566,7 @@ __device__ __forceinline__ void finish_row(const FinishArgs& a, uint32_t row) {
       if (cuts_first) {
         const uint64_t* list = reinterpret_cast<const uint64_t*>(a.scratch + (uint64_t)row * a.scratch_stride);
         const uint32_t cnt = sh.tail_count;
-        for (uint32_t i = tid; i < cnt; i += kThreads) sh.sk[total + i] = list[i];
+        for (uint32_t i = tid; i < cnt; i += kThreads) sh.sk[total + i] = ld_agent(list + i);
         __syncthreads();
         floor_set = true;
       }
@@ -2300,10 +2694,10 @@ __device__ __forceinline__ void finish_row(const FinishArgs& a, uint32_t row) {
                                            : __builtin_inf())) {
         // Neither filter stops among the sorted values, and S's whole mass is short of top-p's
         // target past them, so the floor cuts first: the kept set is the sorted values and all of
-        // S, which the tail kernel listed. Sorted in with the candidates, they take the exact draw.
+        // S, which S's parts listed. Sorted in with the candidates, they take the exact draw.
         const uint64_t* list = reinterpret_cast<const uint64_t*>(a.scratch + (uint64_t)row * a.scratch_stride);
         const uint32_t cnt = sh.tail_count;
-        for (uint32_t i = tid; i < cnt; i += kThreads) sh.sk[P + i] = list[i];
+        for (uint32_t i = tid; i < cnt; i += kThreads) sh.sk[P + i] = ld_agent(list + i);
         __syncthreads();
         const uint32_t P2 = sort_candidates(sh, P + cnt, 0ull, sh.mk, kNone);
         if (tid == 0) sh.prefix = P2;
@@ -2318,7 +2712,7 @@ __device__ __forceinline__ void finish_row(const FinishArgs& a, uint32_t row) {
           sh.r_prefix = r_prefix;
         }
         __syncthreads();
-        // The tail kernel's sums when it took the row; else the sorted values alone first, and one
+        // S's sums when the row was flagged; else the sorted values alone first, and one
         // pass over the row when they cannot settle the draw.
         uint32_t j;
         if (sh.have_tail) {
@@ -2447,6 +2841,8 @@ __device__ __forceinline__ void finish_row(const FinishArgs& a, uint32_t row) {
     // need every kept value in order: those rows take the full deep path). Each path is called at
     // the same depth, so that the kernel's stack is the largest of theirs, not their sum.
     __syncthreads();
+    // A flagged row's parts write its scratch: they have all ended before the passes below use it.
+    if (!a.fused && sh.tail_slot != kNone && !sh.tail_waited) tail_wait(a, row);
     const RowParams& pr = a.params[row];
     const bool pen = deep_prep(a, pr, row);
     bool done = false;

@@ -5,7 +5,7 @@
 // waves share lives in LDS and is read every other chunk. The two bodies share the workgroup's LDS
 // (dynamic LDS, the larger of the two). Eight waves (two per SIMD) leave each wave the registers the
 // stream needs without spilling; sixteen would spill inside the stream loop, and every reload's wait
-// on the vector-memory counter would also wait for the chunk loads in flight. There is no tail kernel and no separate finish launch: a min-p row whose floor set
+// on the vector-memory counter would also wait for the chunk loads in flight. S is not summed in parts and there is no separate finish launch: a min-p row whose floor set
 // overflows its waves' buffers bounds its unsorted tail with the finish's own pass over the row.
 //
 // Used for batches large enough to occupy the GPU with one workgroup per row (a CU each: the LDS

@@ -63,12 +63,16 @@ struct FinishArgs {
   uint64_t scratch_stride;  // u32 per row
   uint64_t* done;           // pinned host word: the call number whose scan has ended (the host
   uint64_t call;            //   reuses a parameter block once its call's scan is over)
-  as_dev::RowTail* tail;    // per row: the tail kernel's sums (min-p rows whose scan gave up)
-  as_dev::TailBins* tail_bins;  // per row: the tail kernel's histogram of S
-  as_dev::TailList* tail_list;  // the rows the scan flagged for the tail kernel
+  as_dev::RowTail* tail;    // per row: S's sums (min-p rows whose scan gave up)
+  as_dev::TailBins* tail_bins;  // per row: S's histogram
+  as_dev::TailList* tail_list;  // the rows this call's scan flagged for S's sums
+  as_dev::TailList* tail_next;  // the next call's list (cleared by this call's finish kernel)
+  uint64_t* tail_claims;    // per helper of S's sums: the number of the last call that claimed its set
   uint32_t max_history;     // a row with more history ids than this is refused (AS_ROW_HISTORY)
   uint32_t fused;           // the row kernel: each workgroup scans and finishes its own row
   uint32_t* fused_count;    // the row kernel: workgroups that have ended (the last writes `done`)
+  uint32_t n_rows;          // rows of the call
+  uint32_t pad_;
 };
 
 // The row's history ids are hist_ids[*hb, return value), from the CSR offsets or the row's range.
@@ -88,11 +92,13 @@ __device__ __forceinline__ uint32_t history_bounds(const FinishArgs& a, const as
   return e;
 }
 
-// The tail kernel covers each of the first kTailRows flagged rows in parts of kTailLen values (16
-// values per thread of a 256-thread workgroup); at most kTailGroups workgroups take the parts in turn.
+// The finish kernel covers S for each of the first kTailRows flagged rows in parts of kTailLen
+// values; a call with rows that may be flagged runs at least min(kTailGroups, their parts)
+// workgroups, the ones past its rows only taking parts.
 constexpr uint32_t kTailLen = 4096;
 constexpr uint32_t kTailRows = as_dev::kTailListMax;
 constexpr uint32_t kTailGroups = 256;
+__host__ __device__ constexpr uint32_t tail_parts(uint32_t n) { return (n + kTailLen - 1) / kTailLen; }
 
 // The order in which the scan's workgroups take rows: the workgroups of launch row y (grid y) scan
 // row r[y]. Workgroups launched earlier hold the older waves of their CU, which the hardware serves
@@ -114,7 +120,8 @@ hipError_t scan(hipStream_t stream, bool vec, const float* logits, const float* 
                 const uint32_t* extra_ids, as_dev::SegStats* stats, uint64_t* cands, uint32_t cand_stride,
                 as_dev::TailList* tail_list, const RowOrder& order);
 
-hipError_t finish(hipStream_t stream, uint32_t n_rows, const FinishArgs* a);
+// groups: the call's rows, or more (the workgroups past them only take parts of S's sums).
+hipError_t finish(hipStream_t stream, uint32_t groups, const FinishArgs* a);
 
 // The row kernel (fused.hip): one 512-thread workgroup scans a whole row and chooses its token, for
 // rows of at most kRowMaxVocab values (its history bitmap lives in LDS). Batches of at least
@@ -128,10 +135,6 @@ hipError_t sample_rows(hipStream_t stream, bool vec, const float* logits, const 
                        const uint32_t* hist_off, const uint32_t* hist_ids, const uint32_t* extra_ids,
                        as_dev::SegStats* stats, uint64_t* cands, uint32_t cand_stride, const FinishArgs& a);
 size_t row_kernel_lds();
-
-// Between the scan and the finish: the weights of S for min-p rows whose scan gave up keeping the
-// floor set whole (a no-op for the other rows).
-hipError_t tail(hipStream_t stream, uint32_t n_rows, uint32_t n, const FinishArgs* a);
 
 // Log-probabilities (logprobs.hip): rows in parts of kLpPart values, each part's 20 best and sums.
 constexpr uint32_t kLpPart = 8192;

@@ -64,8 +64,9 @@ struct RowShare {
 };
 
 // A min-p row whose candidates do not hold its whole floor set: the weights of S, the row's values
-// that rank below the candidates' bound and lie at or above the floor, summed by the tail kernel
-// (sums of f32 terms from the hardware's exp2, each within 3e-5 relative; zero between calls).
+// that rank below the candidates' bound and lie at or above the floor, summed in parts by the finish
+// kernel's workgroups (sums of f32 terms from the hardware's exp2, each within 3e-5 relative; zero
+// between calls: the row's own workgroup clears it once every part has ended).
 struct RowTail {
   double w;        // sum of exp((l - top) / T) over S
   double m;        // sum of exp(l - top) over S
@@ -73,9 +74,11 @@ struct RowTail {
   uint32_t parts;  // parts of the row summed (the sums cover S once every part has added)
   uint32_t failed; // a part could not (more distinct history ids than its table holds)
   uint32_t lost;   // a part held more of S than it could stage (the scratch list is incomplete)
+  uint32_t ended;  // parts that have ended, summed or not (their writes complete before they count)
+  uint32_t pad_;
 };
 constexpr uint32_t kTailKeep = 8192;
-// The tail kernel's histogram of S by value: bin b holds the values v with
+// The histogram of S by value: bin b holds the values v with
 // floor(min(rv - v) * kTailBins / (rv - fl), kTailBins - 1) = b (rv: the value of the candidates' bound,
 // fl: the floor), so that every value of bin b ranks above every value of bin b + 1; per bin the
 // sums of exp(l - top) (m) and exp((l - top) / T) (w), each term as in RowTail. Zero between calls.
@@ -85,8 +88,9 @@ struct TailBins {
   double w[kTailBins];
 };
 
-// The rows a call's scan flagged for the tail kernel (RowShare::gave_up), in the order the scan
-// flagged them: the first kTailListMax of them. The finish kernel clears the count after each call.
+// The rows a call's scan flagged for S's sums (RowShare::gave_up), in the order the scan flagged
+// them: the first kTailListMax of them. A context holds two lists and call c takes list c mod 2; the
+// finish kernel of call c clears the other list's count for the next call.
 constexpr uint32_t kTailListMax = 16;
 struct TailList {
   uint32_t count;  // rows flagged (may exceed kTailListMax)

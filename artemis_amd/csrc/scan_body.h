@@ -943,8 +943,8 @@ __device__ __forceinline__ void scan_slice(
     }
     st.max_key = mk;
     // A min-p row's slice whose bound lies above its floor (from the largest value it knows the row
-    // to hold) did not keep every value above the floor: the row is flagged for the tail kernel.
-    // The first slice to flag the row lists it for the tail kernel.
+    // to hold) did not keep every value above the floor: the row is flagged for S's sums.
+    // The first slice to flag the row lists it.
     if (sl.floor_on && tid == 0 && bound > floor_tau(max(mk, shared_top), sl.ln_min_p)) {
       const uint32_t was = __hip_atomic_fetch_max(&reinterpret_cast<RowShare*>(sl.share)->gave_up, 1u,
                                                   __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);

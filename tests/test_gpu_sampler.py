@@ -254,7 +254,7 @@ def test_draws_past_the_sorted_values_match_the_oracle(ctx):
 
 
 def test_tail_histogram_draws_match_the_oracle(ctx):
-    # The tail kernel takes the first 16 flagged rows of a call and, with S's sums, bins S by value;
+    # The finish kernel sums S for the first 16 flagged rows of a call and bins S by value;
     # the finish kernel places top-p's cut within one bin and draws past the sorted values from
     # those bounds. Config 5's row 111 (top-p keeps ~16,500 values, min-p's floor ~111,000) under
     # many seeds, 16 rows a call so that every row takes that path (and with T > 1, where the bins
@@ -287,10 +287,10 @@ def test_tail_histogram_draws_match_the_oracle(ctx):
             st = g["status"]
             seen[key] += int(((st & AS_ROW_TAIL_PASS) != 0).sum())
             deep[key] += int(((st & AS_ROW_DEEP_PATH) != 0).sum())
-    # At the row's own T (0.36) every draw took the tail kernel's sums and bins, and the bins
+    # At the row's own T (0.36) every draw took S's sums and bins, and the bins
     # settle nearly all of them (the first bound alone left about 1 in 20 to the deep path). At
     # T = 1.3 the draw usually lands past the sorted values, which only the deep path can take.
-    # The row kernel has no tail kernel: its rows bound the unsorted tail with the finish's own
+    # The row kernel does not sum S in parts: its rows bound the unsorted tail with the finish's own
     # pass when the sorted values alone cannot (the tokens above are checked on both paths).
     if ctx.test_path == "sliced":
         assert seen[()] == 128, seen
@@ -300,7 +300,7 @@ def test_tail_histogram_draws_match_the_oracle(ctx):
 def test_large_floor_sets_match_the_oracle(ctx):
     # min-p rows whose floor set holds thousands of values (config 5's rows 254 and 151: 4,302 and
     # 3,365 values above the floor, top-p far deeper): the scan keeps a few thousand candidates and
-    # the tail kernel lists the rest of the floor set, which the finish kernel sorts in. Tokens,
+    # S's parts list the rest of the floor set, which the finish kernel sorts in. Tokens,
     # streams, kept counts and kept lists must be the oracle's, under many seeds.
     from artemis_amd import AS_ROW_TAIL_PASS, workloads
     w = workloads.config5()
@@ -317,7 +317,7 @@ def test_large_floor_sets_match_the_oracle(ctx):
     g = gpu_batch(ctx, rows, params, seeds, hists, kept_cap=16)
     want = oracle_rows(rows, params, seeds, hists, kept_cap=16)
     check_rows(g, want, params, kept_cap=16, label="floor sets")
-    # The tail kernel takes the first 16 rows the scan flags (in the order it flags them); the finish
+    # S is summed in parts for the first 16 rows the scan flags (in the order it flags them); the finish
     # kernel settles the rest. (The row kernel's sixteen waves keep such floor sets whole.)
     if ctx.test_path == "sliced":
         assert ((g["status"] & AS_ROW_TAIL_PASS) != 0).sum() >= 16, g["status"]
