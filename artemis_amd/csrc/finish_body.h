@@ -596,29 +596,30 @@ __device__ __forceinline__ void slices_total(const FinishArgs& a, Shared& sh, do
 }
 
 
-// Sorts the candidates sh.sk[0..total) whose packed rank is >= R into rank order (packed
-// descending) and returns how many there are, P. Only the first `need` ranks are guaranteed placed:
+// Sorts the candidates sk[off..off + total) whose packed rank is >= R into rank order (packed
+// descending), in place from sk[off], and returns how many there are, P (off + total <= kCap). Only the first `need` ranks are guaranteed placed:
 // a bucket that starts at or past `need` is left unsorted. A bucket sort: buckets by distance from
-// the row's largest key kmax, then each value's place inside its bucket by counting the bucket's
+// kmax (at least every key sorted: the row's largest), then each value's place inside its bucket by counting the bucket's
 // values above it (quadratic in a bucket's size, which heavy ties make large).
 // At most kRankSort values are sorted by counting: thread i takes value i's rank, the number of
 // values above it (the packed keys are distinct), in one pass over the LDS copy.
 constexpr uint32_t kRankSort = 256;
 static_assert(kRankSort <= (uint32_t)kThreads, "one value per thread");
 __device__ __forceinline__ uint32_t sort_candidates(Shared& sh, uint32_t total, uint64_t R,
-                                                    uint32_t kmax, uint32_t need) {
+                                                    uint32_t kmax, uint32_t need, uint32_t off = 0) {
   const uint32_t tid = threadIdx.x;
+  uint64_t* sk = sh.sk + off;
   if (total <= kRankSort) {
-    const uint64_t x = (tid < total) ? sh.sk[tid] : 0ull;
+    const uint64_t x = (tid < total) ? sk[tid] : 0ull;
     const bool mine = tid < total && x >= R;
     uint32_t r = 0;
     if (mine)
       for (uint32_t j = 0; j < total; ++j) {
-        const uint64_t y = sh.sk[j];
+        const uint64_t y = sk[j];
         r += (y > x) ? 1u : 0u;  // every y > x >= R is kept
       }
     const uint32_t P = (uint32_t)__syncthreads_count(mine);
-    if (mine) sh.sk[r] = x;
+    if (mine) sk[r] = x;
     __syncthreads();
     return P;
   }
@@ -629,7 +630,7 @@ __device__ __forceinline__ uint32_t sort_candidates(Shared& sh, uint32_t total, 
 #pragma unroll
   for (int q = 0; q < kPerT; ++q) {
     const uint32_t i = tid + q * kThreads;
-    xs[q] = (i < total) ? sh.sk[i] : 0ull;
+    xs[q] = (i < total) ? sk[i] : 0ull;
     if (i < total && xs[q] >= R) {
       kmin = min(kmin, (uint32_t)(xs[q] >> 32));
       ++mine;
@@ -702,7 +703,7 @@ __device__ __forceinline__ uint32_t sort_candidates(Shared& sh, uint32_t total, 
     if (s0 >= need) continue;
     uint32_t r = 0;
     for (uint32_t j = 0; j < nb; ++j) r += (out2[s0 + j] > x) ? 1u : 0u;
-    sh.sk[s0 + r] = x;
+    sk[s0 + r] = x;
   }
   __syncthreads();
   return P;
@@ -2283,7 +2284,7 @@ __device__ __attribute__((unused)) void tail_start(const FinishArgs& a, uint32_t
 // The flagged row's workgroup: takes the sets holding its row's items that no helper has claimed
 // (all its items when there is no helper), waits for the sets running helpers hold, and reads S's
 // sums (within 1e-4 relative: each term is within 3e-5, and terms under 2^-126 may have flushed to
-// 0). Once per row; sh.bcnt is free (the candidates are not yet sorted).
+// 0). Once per row; sh.bcnt and sh.wd are free (the candidates' sort is done with them).
 constexpr uint32_t kTailSpin = 1u << 24;  // a guard: every set claimed is being summed by a running workgroup
 __device__ __noinline__ void tail_wait(const FinishArgs& a, uint32_t row) {
   Shared& sh = shm();
@@ -2541,24 +2542,27 @@ __device__ __forceinline__ void finish_row(const FinishArgs& a, uint32_t row) {
       take_u01();
       __syncthreads();
     }
-    // A flagged row's S sums, before anything reads them (its candidates stay in sh.sk).
-    if (!a.fused && sh.tail_slot != kNone) tail_wait(a, row);
     const uint32_t total = min(sh.nsk, (uint32_t)kCap);
     const bool too_many = sh.nsk > (uint32_t)kCap;  // more candidates >= R than the finish holds
+    // The candidates in rank order; a flagged row's parts of S are summed meanwhile, and its sums
+    // are read after (tail_wait).
+    uint32_t P = sort_candidates(sh, total, R, sh.mk, p.mode == kModeTopK ? p.top_k : kNone);
+    if (!a.fused && sh.tail_slot != kNone) tail_wait(a, row);
     // A row whose floor set S's parts listed (S: every value below R and at or above the floor),
     // and whose whole floor set's mass at T = 1 is short of top-p's target: top-p never stops inside it
-    // and min-p's floor cuts first (sample.rs:237-251), so the kept set is the candidates and all of S,
-    // sorted once, together. The candidates' mass needs no order: a parallel sum of positive terms,
-    // within gamma(40) of exact, and the margins below are far wider.
+    // and min-p's floor cuts first (sample.rs:237-251), so the kept set is the candidates and all of S.
+    // Every value of S ranks below every candidate: S sorted on its own follows them. The
+    // candidates' mass needs no order: a parallel sum of positive terms, within gamma(40) of exact,
+    // and the margins below are far wider.
     bool floor_set = false;
     if (p.mode == kModePartial && has_floor && !floor_cut && !too_many && sh.have_tail && sh.tail_listed &&
-        total + sh.tail_count <= (uint32_t)kCap) {
+        P + sh.tail_count <= (uint32_t)kCap) {
       bool cuts_first = true;
       if (p.top_p < 1.0f) {
         double X, eps;
         slices_total(a, sh, top, temp, false, &X, &eps);
         double mc = 0.0;
-        for (uint32_t i = tid; i < total; i += kThreads) mc += w_one(val(i));
+        for (uint32_t i = tid; i < P; i += kThreads) mc += w_one(val(i));
         mc = block_sum_f64<kWaves>(mc, sh.red_d);
         cuts_first = (X - eps > 0.0) && (eps == eps) &&
                      sh.m_hi < top_p * (X - eps) * (1.0 - 1e-9) - mc * (1.0 + 1e-9);
@@ -2566,13 +2570,12 @@ __device__ __forceinline__ void finish_row(const FinishArgs& a, uint32_t row) {
       if (cuts_first) {
         const uint64_t* list = reinterpret_cast<const uint64_t*>(a.scratch + (uint64_t)row * a.scratch_stride);
         const uint32_t cnt = sh.tail_count;
-        for (uint32_t i = tid; i < cnt; i += kThreads) sh.sk[total + i] = ld_agent(list + i);
+        for (uint32_t i = tid; i < cnt; i += kThreads) sh.sk[P + i] = ld_agent(list + i);
         __syncthreads();
+        P += sort_candidates(sh, cnt, 0ull, (uint32_t)(R >> 32), kNone, P);
         floor_set = true;
       }
     }
-    const uint32_t P = floor_set ? sort_candidates(sh, total + sh.tail_count, 0ull, sh.mk, kNone)
-                                 : sort_candidates(sh, total, R, sh.mk, p.mode == kModeTopK ? p.top_k : kNone);
     if (tid == 0) sh.prefix = P;
     const bool complete = (P == n);  // every value of the row is sorted
     // A top-k row's k best are among the sorted values only when at least k rank at or above R.
@@ -2699,7 +2702,8 @@ __device__ __forceinline__ void finish_row(const FinishArgs& a, uint32_t row) {
         const uint32_t cnt = sh.tail_count;
         for (uint32_t i = tid; i < cnt; i += kThreads) sh.sk[P + i] = ld_agent(list + i);
         __syncthreads();
-        const uint32_t P2 = sort_candidates(sh, P + cnt, 0ull, sh.mk, kNone);
+        // S ranks below every candidate: sorted on its own, it follows them.
+        const uint32_t P2 = P + sort_candidates(sh, cnt, 0ull, (uint32_t)(R >> 32), kNone, P);
         if (tid == 0) sh.prefix = P2;
         keep = P2;
         status |= AS_ROW_TAIL_PASS;
