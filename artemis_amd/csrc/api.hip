@@ -204,6 +204,21 @@ void order_rows(const RowParams* rows, uint32_t n_rows, as_launch::RowOrder* o,
 
 static_assert(sizeof(as_launch::FinishArgs) <= kArgsSlot && kArgsSlot % 16 == 0, "FinishArgs slot");
 
+// Each row's place among the finish kernel's helpers of S's sums (RowParams::help), the rows whose own
+// finish costs least first: greedy rows, then top-k rows, then rows without a top-k and without
+// min-p's floor, then those with it (the ones S is summed for); in row order within a kind.
+void help_ranks(const RowParams* rows, uint32_t n_rows, RowParams* out) {
+  auto kind = [](const RowParams& r) -> uint32_t {
+    if (r.mode == as_dev::kModeTopK) return 1;
+    if (r.mode == as_dev::kModePartial) return r.min_p > 0.0f ? 3 : 2;
+    return r.mode == as_dev::kModeGreedy ? 0 : 2;
+  };
+  uint32_t start[4] = {0, 0, 0, 0};
+  for (uint32_t r = 0; r < n_rows; ++r)
+    for (uint32_t k = kind(rows[r]) + 1; k < 4; ++k) ++start[k];
+  for (uint32_t r = 0; r < n_rows; ++r) out[r].help = start[kind(rows[r])]++;
+}
+
 // The next profiling event (created on first use), or null when profiling is off.
 hipEvent_t next_event(as_ctx* c) {
   if (!c->profile) return nullptr;
@@ -282,6 +297,7 @@ int run_rows(as_ctx* c, const Plan& pl, const RowParams* rows, const float* logi
   std::memset(h, 0, kArgsSlot);
   std::memcpy(h, &a, sizeof a);
   std::memcpy(h + kArgsSlot, rows, sizeof(RowParams) * n_rows);
+  help_ranks(rows, n_rows, reinterpret_cast<RowParams*>(h + kArgsSlot));
 
   hipEvent_t e0 = nullptr, e1 = nullptr, e2 = nullptr;
   if (c->profile && c->ev_used + 3 <= 3 * 4096) {

@@ -45,10 +45,10 @@ struct Shared {
   uint32_t bad, gi, mk, total, trunc, keep, pick, done, exact, prefix, stats_bad, nsk, tail_over, have_tail, tail_count,
       tail_listed, tail_parts;
   uint64_t bound_key;
-  double u01, sum, x, eps, x1, eps1, r_prefix, w_lo, w_hi, m_lo, m_hi;
+  double u01, sum, x, eps, x1, eps1, r_prefix, w_lo, w_hi, m_lo, m_hi, dp_lo, dp_hi;
   uint32_t draw_rng;  // the row draws: its stream advances once the candidates are in flight
   // S's sums (tail_start, tail_wait): this call's flagged rows, this row's place among them.
-  uint32_t tl_n, tl_rows[kTailListMax], tail_slot, tail_waited, tail_won;
+  uint32_t tl_n, tl_rows[kTailListMax], tl_help[kTailListMax], tl_me, tail_slot, tail_waited, tail_won;
 };
 // The workgroup's LDS, at file scope so that the out-of-line paths below address it as LDS: a static
 // array, or the kernel's dynamic LDS (AS_DYNAMIC_LDS) when another body shares it.
@@ -596,11 +596,12 @@ __device__ __forceinline__ void slices_total(const FinishArgs& a, Shared& sh, do
 }
 
 
-// Sorts the candidates sk[off..off + total) whose packed rank is >= R into rank order (packed
-// descending), in place from sk[off], and returns how many there are, P (off + total <= kCap). Only the first `need` ranks are guaranteed placed:
-// a bucket that starts at or past `need` is left unsorted. A bucket sort: buckets by distance from
-// kmax (at least every key sorted: the row's largest), then each value's place inside its bucket by counting the bucket's
-// values above it (quadratic in a bucket's size, which heavy ties make large).
+// Sorts the candidates sh.sk[off..off + total) whose packed rank is >= R into rank order (packed
+// descending), in place from sh.sk[off], and returns how many there are, P (off + total <= kCap).
+// Only the first `need` ranks are guaranteed placed: a bucket that starts at or past `need` is left
+// unsorted. A bucket sort: buckets by distance from kmax (at least every key sorted: the row's
+// largest), then each value's place inside its bucket by counting the bucket's values above it
+// (quadratic in a bucket's size, which heavy ties make large).
 // At most kRankSort values are sorted by counting: thread i takes value i's rank, the number of
 // values above it (the packed keys are distinct), in one pass over the LDS copy.
 constexpr uint32_t kRankSort = 256;
@@ -1934,6 +1935,25 @@ __device__ __noinline__ uint32_t draw_past(const FinishArgs& a, const RowParams&
   const double top = (double)key_value(sh.mk), temp = (double)p.temp, top_p = (double)p.top_p;
   auto val = [&](uint32_t i) -> double { return (double)packed_value(sh.sk[i]); };
   const double g40 = gamma_n(40.0), gn = gamma_n((double)n);
+  // S's bins, kTailBins / kWave consecutive ones per lane of wave 0, loaded first: their latency
+  // passes while the sorted values' weights are computed and scanned.
+  constexpr uint32_t kBPer = as_dev::kTailBins / kWave;
+  static_assert(as_dev::kTailBins % kWave == 0, "whole bins per lane");
+  const bool use_bins = with_tail && bins && p.top_p < 1.0f;
+  double bm[kBPer], bw[kBPer];
+  if (use_bins && tid < kWave) {
+    const as_dev::TailBins& tb = a.tail_bins[row];
+#pragma unroll
+    for (uint32_t q = 0; q < kBPer; ++q) {
+      bm[q] = ld_agent(&tb.m[tid * kBPer + q]);
+      bw[q] = ld_agent(&tb.w[tid * kBPer + q]);
+    }
+  }
+  for (uint32_t i = tid; i < P; i += kThreads)
+    sh.wd[i] = as_exp::exp_with(tab, __ddiv_rn(__dsub_rn(val(i), top), temp));
+  __syncthreads();
+  double loc[kScanPer], off;
+  const double SP = prefix_scan(sh, P, loc, &off);
   double lo = 0.0, w_hi = __builtin_inf();
   if (with_tail) {
     const double w_lo = sh.w_lo, m_lo = sh.m_lo, m_hi = sh.m_hi;
@@ -1948,42 +1968,71 @@ __device__ __noinline__ uint32_t draw_past(const FinishArgs& a, const RowParams&
       const double k1 = fmin(kp, m_lo);
       if (k1 > 0.0 && m_hi > 0.0) lo = k1 / m_hi * w_lo;
     }
-    if (bins && p.top_p < 1.0f) {
+    if (use_bins) {
       // Top-p's target past the sorted values lies in [kp, kq]. Each bin's sums are within 1e-4
       // relative (as RowTail's) plus its flushed terms; their prefix sums add at most gamma(256).
-      const double kq = top_p * (x1 + eps1) * (1.0 + 1e-9) - r_prefix * (1.0 - 1e-9);
-      const double fl_b = (double)n * 0x1p-125, slack = 1e-4 + gamma_n(300.0);
-      const as_dev::TailBins& tb = a.tail_bins[row];
-      double bm = 0.0, bw = 0.0;
-      if (tid < as_dev::kTailBins) {
-        bm = ld_agent(&tb.m[tid]);
-        bw = ld_agent(&tb.w[tid]);
+      // On wave 0: b_min, the first bin whose cumulative mass can reach kp (the bins before it are
+      // kept whole); b_max, the first whose cumulative mass surely reaches kq (no later bin is kept).
+      if (tid < kWave) {
+        const double kq = top_p * (x1 + eps1) * (1.0 + 1e-9) - r_prefix * (1.0 - 1e-9);
+        const double fl_b = (double)n * 0x1p-125, slack = 1e-4 + gamma_n(300.0);
+        double mhi[kBPer], mlo[kBPer], whi[kBPer], wlo[kBPer], rh = 0.0, rl = 0.0;
+#pragma unroll
+        for (uint32_t q = 0; q < kBPer; ++q) {
+          mlo[q] = fmax(0.0, bm[q] * (1.0 - slack) - fl_b);
+          mhi[q] = bm[q] * (1.0 + slack) + fl_b;
+          wlo[q] = fmax(0.0, bw[q] * (1.0 - slack) - fl_b);
+          whi[q] = bw[q] * (1.0 + slack) + fl_b;
+          rh = __dadd_rn(rh, mhi[q]);
+          rl = __dadd_rn(rl, mlo[q]);
+          mhi[q] = rh;  // the lane's inclusive prefixes
+          mlo[q] = rl;
+        }
+        // The lanes before this one, by an inclusive scan over the lanes.
+        double ih = rh, il = rl;
+        for (int o = 1; o < kWave; o <<= 1) {
+          const double yh = __shfl_up(ih, o, kWave), yl = __shfl_up(il, o, kWave);
+          if (tid >= (uint32_t)o) {
+            ih = __dadd_rn(ih, yh);
+            il = __dadd_rn(il, yl);
+          }
+        }
+        const double ph = __shfl_up(ih, 1, kWave), pl = __shfl_up(il, 1, kWave);
+        const double eh = tid == 0 ? 0.0 : ph, el = tid == 0 ? 0.0 : pl;
+        uint32_t a_min = kNone, a_max = kNone;
+#pragma unroll
+        for (uint32_t q = 0; q < kBPer; ++q) {
+          const uint32_t b = tid * kBPer + q;
+          if (a_min == kNone && __dadd_rn(eh, mhi[q]) >= kp) a_min = b;
+          if (a_max == kNone && __dadd_rn(el, mlo[q]) >= kq) a_max = b;
+        }
+        const uint32_t b_min = wave_min_u32(a_min), b_max = wave_min_u32(a_max);
+        double before = 0.0, upto = 0.0;
+#pragma unroll
+        for (uint32_t q = 0; q < kBPer; ++q) {
+          const uint32_t b = tid * kBPer + q;
+          before += b < b_min ? wlo[q] : 0.0;
+          upto += (b_max != kNone && b <= b_max) ? whi[q] : 0.0;
+        }
+        before = wave_sum_f64(before);
+        upto = wave_sum_f64(upto);
+        if (tid == 0) {
+          sh.dp_lo = fmax(lo, before * (1.0 - gamma_n(300.0)));
+          sh.dp_hi = b_max != kNone ? fmin(w_hi, upto * (1.0 + gamma_n(300.0))) : w_hi;
+        }
       }
-      const double mlo = fmax(0.0, bm * (1.0 - slack) - fl_b), mhi = bm * (1.0 + slack) + fl_b;
-      const double wlo = fmax(0.0, bw * (1.0 - slack) - fl_b), whi = bw * (1.0 + slack) + fl_b;
-      const double cm_hi = __dadd_rn(block_exclusive_scan_f64(mhi, sh.red_d), mhi);
-      const double cm_lo = __dadd_rn(block_exclusive_scan_f64(mlo, sh.red_d), mlo);
-      const bool valid = tid < as_dev::kTailBins;
-      // b_min: the first bin whose cumulative mass can reach kp (the bins before it are kept whole);
-      // b_max: the first whose cumulative mass surely reaches kq (no later bin is kept).
-      const uint32_t b_min = block_min_u32<kWaves>(valid && cm_hi >= kp ? tid : kNone, sh.red_u);
-      const uint32_t b_max = block_min_u32<kWaves>(valid && cm_lo >= kq ? tid : kNone, sh.red_u);
-      const double before = block_sum_f64<kWaves>(valid && tid < b_min ? wlo : 0.0, sh.red_d);
-      const double upto = block_sum_f64<kWaves>(valid && tid <= b_max ? whi : 0.0, sh.red_d);
-      lo = fmax(lo, before * (1.0 - gamma_n(300.0)));
-      if (b_max != kNone) w_hi = fmin(w_hi, upto * (1.0 + gamma_n(300.0)));
+      __syncthreads();
+      lo = sh.dp_lo;
+      w_hi = sh.dp_hi;
     }
   }
-  for (uint32_t i = tid; i < P; i += kThreads)
-    sh.wd[i] = as_exp::exp_with(tab, __ddiv_rn(__dsub_rn(val(i), top), temp));
-  __syncthreads();
-  double loc[kScanPer], off;
-  const double SP = prefix_scan(sh, P, loc, &off);
   double tail = (double)(n - P) * sh.wd[P - 1] * (1.0 + 4.0 * kU);
   if (p.top_p < 1.0f && p.temp <= 1.0f) {
-    const double e_last = as_exp::exp_with(tab, __dsub_rn(val(P - 1), top));
+    // e_last^(1/T - 1) = exp(d (1/T - 1)), d = l_last - top (exact in f64): the product's rounding
+    // and the exp's move the bound by far less than its 1e-9 margin.
+    const double d = __dsub_rn(val(P - 1), top);
     const double rest = (x1 + eps1) - r_prefix * (1.0 - 2.0 * g40);
-    const double t2 = pow(e_last, 1.0 / temp - 1.0) * (1.0 + 1e-9) * (rest > 0.0 ? rest : 0.0);
+    const double t2 = as_exp::exp_with(tab, d * (1.0 / temp - 1.0)) * (1.0 + 1e-9) * (rest > 0.0 ? rest : 0.0);
     if (t2 < tail) tail = t2;
   }
   tail = fmin(tail, w_hi);
@@ -2254,28 +2303,36 @@ __device__ __noinline__ bool tail_item(const FinishArgs& a, uint32_t row, uint32
 
 // First thing in every workgroup of the sliced finish: this call's flagged rows (the first
 // kTailRows) into LDS, this workgroup's row's place among them, and, for a helper, its set of items.
+// Helpers are numbered in the order their own work is expected to cost: the workgroups past the
+// call's rows first, then the rows by RowParams::help (flagged rows left out), so that with fewer
+// items than helpers the items go to the cheapest rows.
 __device__ __attribute__((unused)) void tail_start(const FinishArgs& a, uint32_t wg, uint32_t groups) {
   Shared& sh = shm();
   const uint32_t tid = threadIdx.x;
-  if (tid == 0) {
-    sh.tl_n = min(a.tail_list->count, as_launch::kTailRows);
-    sh.tail_slot = kNone;
-    sh.tail_waited = 0;
+  // The list's count and entries (those past the count unused) and this row's rank, loaded at once.
+  if (tid < as_launch::kTailRows) {
+    const uint32_t r = a.tail_list->rows[tid], hr = a.tail_list->help[tid];
+    const uint32_t nl = min(a.tail_list->count, as_launch::kTailRows);
+    sh.tl_rows[tid] = r;
+    sh.tl_help[tid] = hr;
+    if (tid == 0) {
+      sh.tl_me = wg < a.n_rows ? a.params[wg].help : 0u;
+      sh.tl_n = nl;
+      sh.tail_slot = kNone;
+      sh.tail_waited = 0;
+    }
   }
   __syncthreads();
   const uint32_t nl = sh.tl_n;
   if (nl == 0) return;
-  if (tid < nl) {
-    const uint32_t r = a.tail_list->rows[tid];
-    sh.tl_rows[tid] = r;
-    if (r == wg) sh.tail_slot = tid;
-  }
+  if (tid < nl && sh.tl_rows[tid] == wg) sh.tail_slot = tid;
   __syncthreads();
   const uint32_t helpers = groups - nl;
   if (sh.tail_slot != kNone || helpers == 0) return;
-  uint32_t below = 0;  // flagged rows before this workgroup's
-  for (uint32_t k = 0; k < nl; ++k) below += sh.tl_rows[k] < wg ? 1u : 0u;
-  const uint32_t parts = as_launch::tail_parts(a.n), items = nl * parts, h = wg - below;
+  const uint32_t extra = groups - a.n_rows, me = wg >= a.n_rows ? wg - a.n_rows : extra + sh.tl_me;
+  uint32_t below = 0;  // flagged rows ranked before this workgroup
+  for (uint32_t k = 0; k < nl; ++k) below += extra + sh.tl_help[k] < me ? 1u : 0u;
+  const uint32_t parts = as_launch::tail_parts(a.n), items = nl * parts, h = me - below;
   for (uint32_t i = h; i < items; i += helpers)
     if (!tail_item(a, sh.tl_rows[i / parts], i % parts, i == h ? a.tail_claims + h : nullptr)) break;
   __syncthreads();

@@ -94,8 +94,9 @@ __device__ __forceinline__ uint32_t history_bounds(const FinishArgs& a, const as
 
 // The finish kernel covers S for each of the first kTailRows flagged rows in parts of kTailLen
 // values; a call with rows that may be flagged runs at least min(kTailGroups, their parts)
-// workgroups, the ones past its rows only taking parts.
-constexpr uint32_t kTailLen = 4096;
+// workgroups, the ones past its rows only taking parts. The parts go to the workgroups whose own
+// work is expected to cost least: those past the call's rows, then the rows by RowParams::help.
+constexpr uint32_t kTailLen = 8192;
 constexpr uint32_t kTailRows = as_dev::kTailListMax;
 constexpr uint32_t kTailGroups = 256;
 __host__ __device__ constexpr uint32_t tail_parts(uint32_t n) { return (n + kTailLen - 1) / kTailLen; }

@@ -46,7 +46,7 @@ struct RowParams {
   uint32_t hist_len;
   uint32_t extra;       // ids of the extra list appended to the history (verify drafts)
   uint32_t cap;         // candidate slots per slice (slices x cap fit the finish LDS)
-  uint32_t pad_;
+  uint32_t help;        // the row's place among the finish kernel's helpers of S's sums (cheapest first)
 };
 static_assert(sizeof(RowParams) % 16 == 0, "whole 16-byte words");
 
@@ -95,6 +95,7 @@ constexpr uint32_t kTailListMax = 16;
 struct TailList {
   uint32_t count;  // rows flagged (may exceed kTailListMax)
   uint32_t rows[kTailListMax];
+  uint32_t help[kTailListMax];  // each listed row's RowParams::help
 };
 
 // Per (row, slice) results of the scan.

@@ -950,7 +950,10 @@ __device__ __forceinline__ void scan_slice(
                                                   __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       if (was == 0u && tail_list) {
         const uint32_t i = __hip_atomic_fetch_add(&tail_list->count, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        if (i < kTailListMax) tail_list->rows[i] = row;
+        if (i < kTailListMax) {
+          tail_list->rows[i] = row;
+          tail_list->help[i] = sh.prm.help;
+        }
       }
     }
 
