@@ -34,12 +34,14 @@ namespace {
 
 // The arguments are read from device memory (the scan's copy of the pinned block), which costs each
 // workgroup less than a large kernel-argument block. Workgroup b finishes row b; those past the
-// call's rows only take parts of S's sums (tail_start), which every workgroup whose row is not
+// call's rows only take parts of S's sums (tail_help), which every workgroup whose row is not
 // flagged does first.
 __global__ __launch_bounds__(1024) void finish_kernel(const FinishArgs* __restrict__ ap) {
   const FinishArgs& a = *ap;
   const uint32_t row = blockIdx.x;
-  as_fin_sliced::tail_start(a, row, gridDim.x);
+  as_fin_sliced::tail_list_load(a, row);
+  __syncthreads();
+  as_fin_sliced::tail_help(a, row, gridDim.x);
   if (row >= a.n_rows) return;
   as_fin_sliced::finish_row(a, row);
   // A flagged row's S sums and histogram go back to zero for the next call once every part has

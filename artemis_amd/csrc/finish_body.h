@@ -47,7 +47,7 @@ struct Shared {
   uint64_t bound_key;
   double u01, sum, x, eps, x1, eps1, r_prefix, w_lo, w_hi, m_lo, m_hi, dp_lo, dp_hi;
   uint32_t draw_rng;  // the row draws: its stream advances once the candidates are in flight
-  // S's sums (tail_start, tail_wait): this call's flagged rows, this row's place among them.
+  // S's sums (tail_list_load, tail_help, tail_wait): this call's flagged rows, this row's place among them.
   uint32_t tl_n, tl_rows[kTailListMax], tl_help[kTailListMax], tl_me, tail_slot, tail_waited, tail_won;
 };
 // The workgroup's LDS, at file scope so that the out-of-line paths below address it as LDS: a static
@@ -611,16 +611,31 @@ __device__ __forceinline__ uint32_t sort_candidates(Shared& sh, uint32_t total, 
   const uint32_t tid = threadIdx.x;
   uint64_t* sk = sh.sk + off;
   if (total <= kRankSort) {
-    const uint64_t x = (tid < total) ? sk[tid] : 0ull;
-    const bool mine = tid < total && x >= R;
+    // kThreads / kRankSort threads per value, each counting the values above it in its share of
+    // the list (eight LDS reads in flight per step; every lane of a wave reads the same words),
+    // their counts added in sh.hist.
+    constexpr uint32_t kWays = (uint32_t)kThreads / kRankSort;
+    static_assert(kRankSort <= 256 && kWays >= 1, "a counter per value in sh.hist");
+    const uint32_t v = tid % kRankSort, way = tid / kRankSort;
+    const uint64_t x = (v < total) ? sk[v] : 0ull;
+    const bool mine = v < total && x >= R;
+    if (tid < kRankSort) sh.hist[tid] = 0;
+    const uint32_t share = (total + kWays - 1) / kWays, j0 = way * share, j1 = min(total, j0 + share);
+    uint32_t c[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+    if (mine) {
+      uint32_t j = j0;
+      for (; j + 8 <= j1; j += 8)
+#pragma unroll
+        for (int u = 0; u < 8; ++u) c[u] += (sk[j + u] > x) ? 1u : 0u;  // every y > x >= R is kept
+      for (; j < j1; ++j) c[0] += (sk[j] > x) ? 1u : 0u;
+    }
     uint32_t r = 0;
-    if (mine)
-      for (uint32_t j = 0; j < total; ++j) {
-        const uint64_t y = sk[j];
-        r += (y > x) ? 1u : 0u;  // every y > x >= R is kept
-      }
-    const uint32_t P = (uint32_t)__syncthreads_count(mine);
-    if (mine) sk[r] = x;
+#pragma unroll
+    for (int u = 0; u < 8; ++u) r += c[u];
+    const uint32_t P = (uint32_t)__syncthreads_count(mine && way == 0);
+    if (mine && r) atomicAdd(&sh.hist[v], r);
+    __syncthreads();
+    if (mine && way == 0) sk[sh.hist[v]] = x;
     __syncthreads();
     return P;
   }
@@ -702,9 +717,13 @@ __device__ __forceinline__ uint32_t sort_candidates(Shared& sh, uint32_t total, 
     const uint32_t b = (kmax - (uint32_t)(x >> 32)) >> shift;
     const uint32_t s0 = sh.bstart[b], nb = sh.bcnt[b];
     if (s0 >= need) continue;
-    uint32_t r = 0;
-    for (uint32_t j = 0; j < nb; ++j) r += (out2[s0 + j] > x) ? 1u : 0u;
-    sk[s0 + r] = x;
+    uint32_t c[4] = {0, 0, 0, 0};
+    uint32_t j = 0;
+    for (; j + 4 <= nb; j += 4)
+#pragma unroll
+      for (int u = 0; u < 4; ++u) c[u] += (out2[s0 + j + u] > x) ? 1u : 0u;
+    for (; j < nb; ++j) c[0] += (out2[s0 + j] > x) ? 1u : 0u;
+    sk[s0 + c[0] + c[1] + c[2] + c[3]] = x;
   }
   __syncthreads();
   return P;
@@ -2051,7 +2070,7 @@ __device__ __noinline__ uint32_t draw_past(const FinishArgs& a, const RowParams&
 // S's histogram (TailBins) and, when S is small, its values (in the row's scratch). The flagged rows
 // are cut into parts of kTailLen values, item i being part i mod parts of the list's row i / parts.
 // The H workgroups whose row is not flagged (and those past the call's rows) are the helpers: helper
-// h takes items h, h + H, ..., first of all (tail_start), once it has claimed that set by raising
+// h takes items h, h + H, ..., first of all (tail_help), once it has claimed that set by raising
 // its claim word to the call's number (an atomic max: a lower number is an earlier call's; the
 // claim is issued with the first item's loads and checked before anything is written). A flagged
 // row's workgroup, when it needs the sums (tail_wait), claims the sets holding its row's items that
@@ -2301,34 +2320,37 @@ __device__ __noinline__ bool tail_item(const FinishArgs& a, uint32_t row, uint32
   return true;
 }
 
-// First thing in every workgroup of the sliced finish: this call's flagged rows (the first
-// kTailRows) into LDS, this workgroup's row's place among them, and, for a helper, its set of items.
-// Helpers are numbered in the order their own work is expected to cost: the workgroups past the
-// call's rows first, then the rows by RowParams::help (flagged rows left out), so that with fewer
-// items than helpers the items go to the cheapest rows.
-__device__ __attribute__((unused)) void tail_start(const FinishArgs& a, uint32_t wg, uint32_t groups) {
+// First thing in every workgroup of the sliced finish, before its row: this call's flagged rows
+// (the first kTailRows) and their ranks into LDS, with this row's rank (no barrier).
+__device__ __forceinline__ void tail_list_load(const FinishArgs& a, uint32_t wg) {
   Shared& sh = shm();
   const uint32_t tid = threadIdx.x;
-  // The list's count and entries (those past the count unused) and this row's rank, loaded at once.
   if (tid < as_launch::kTailRows) {
-    const uint32_t r = a.tail_list->rows[tid], hr = a.tail_list->help[tid];
-    const uint32_t nl = min(a.tail_list->count, as_launch::kTailRows);
-    sh.tl_rows[tid] = r;
-    sh.tl_help[tid] = hr;
+    sh.tl_rows[tid] = a.tail_list->rows[tid];  // entries past the count are unused
+    sh.tl_help[tid] = a.tail_list->help[tid];
     if (tid == 0) {
       sh.tl_me = wg < a.n_rows ? a.params[wg].help : 0u;
-      sh.tl_n = nl;
-      sh.tail_slot = kNone;
+      sh.tl_n = min(a.tail_list->count, as_launch::kTailRows);
       sh.tail_waited = 0;
     }
   }
-  __syncthreads();
+}
+
+// After a barrier that follows tail_list_load: this workgroup's row's place in the list
+// (sh.tail_slot, read after later barriers), and, for a helper, its set of items, before its row. Helpers are
+// numbered in the order their own work is expected to cost: the workgroups past the call's rows
+// first, then the rows by RowParams::help (flagged rows left out), so that with fewer items than
+// helpers the items go to the cheapest rows.
+__device__ __attribute__((unused)) void tail_help(const FinishArgs& a, uint32_t wg, uint32_t groups) {
+  Shared& sh = shm();
   const uint32_t nl = sh.tl_n;
-  if (nl == 0) return;
-  if (tid < nl && sh.tl_rows[tid] == wg) sh.tail_slot = tid;
-  __syncthreads();
+  uint32_t slot = kNone;
+  for (uint32_t k = 0; k < nl; ++k)
+    if (sh.tl_rows[k] == wg) slot = k;
+  __syncthreads();  // every thread has read sh.tl_* before thread 0 writes the slot
+  if (threadIdx.x == 0) sh.tail_slot = slot;
   const uint32_t helpers = groups - nl;
-  if (sh.tail_slot != kNone || helpers == 0) return;
+  if (nl == 0 || slot != kNone || helpers == 0) return;
   const uint32_t extra = groups - a.n_rows, me = wg >= a.n_rows ? wg - a.n_rows : extra + sh.tl_me;
   uint32_t below = 0;  // flagged rows ranked before this workgroup
   for (uint32_t k = 0; k < nl; ++k) below += extra + sh.tl_help[k] < me ? 1u : 0u;
@@ -2427,6 +2449,9 @@ __device__ __forceinline__ void finish_row(const FinishArgs& a, uint32_t row) {
   }
   // The slices' results, all loads in flight at once, with the row's RNG state and history bounds
   // (thread 0 keeps them in registers for the merge below).
+  // The slices' statistics first (they need nothing loaded), then what needs the row's parameters,
+  // so that waiting for the statistics does not wait for the RNG state too.
+  for (uint32_t s = tid; s < a.n_seg; s += kThreads) sh.seg[s] = gst[s];
   const bool draws = p.mode != kModeGreedy;
   uint64_t s4[4] = {0ull, 0ull, 0ull, 0ull};
   uint64_t* src = a.rng_state + 4ull * p.rng_index;
@@ -2436,7 +2461,6 @@ __device__ __forceinline__ void finish_row(const FinishArgs& a, uint32_t row) {
       for (int k = 0; k < 4; ++k) s4[k] = src[k];
     he = as_launch::history_bounds(a, p, row, &hb);
   }
-  for (uint32_t s = tid; s < a.n_seg; s += kThreads) sh.seg[s] = gst[s];
   __syncthreads();
   // The row's shared words go back to zero for the next call (this call's scan has ended, and their
   // words were read above).
