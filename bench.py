@@ -454,7 +454,7 @@ def main():
         "head_q6k_248320x2048": head,
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,
-                     "kernel": "the as_sample chain: every kernel of one call (scan, tail, finish)",
+                     "kernel": "the as_sample chain: every kernel of one call (scan, finish)",
                      "bytes_per_launch": g["alg_bytes"],
                      "scan_only": {"achieved": round(scan_achieved, 1), "frac": round(scan_achieved / HBM_PEAK_GBS, 4)}},
         "cpu_baseline": cpu,
