@@ -35,6 +35,9 @@ struct as_ctx {
   as_dev::TailBins* d_tail_bins = nullptr;
   as_dev::TailList* d_tail_list = nullptr;  // two lists: call c takes list c mod 2
   uint64_t* d_tail_claims = nullptr;         // one per finish workgroup: max(max_rows, kTailGroups)
+  as_dev::DeepJob* d_deep_jobs = nullptr;    // per row
+  uint64_t* d_deep_done = nullptr;           // rows finished by calls that shared the deep passes
+  uint64_t deep_rows_done = 0;               // the host's count of the same
   bool share_dirty = false;  // a scan ran without its finish (a failed launch): the context is unusable
   int force_path = 0;        // as_debug_path: 0 automatic, 1 the sliced scan, 2 the row kernel
   uint32_t* d_fused_count = nullptr;  // the row kernel's count of ended workgroups
@@ -272,9 +275,20 @@ int run_rows(as_ctx* c, const Plan& pl, const RowParams* rows, const float* logi
   a.tail_list = c->d_tail_list + (a.call & 1);
   a.tail_next = c->d_tail_list + ((a.call + 1) & 1);
   a.tail_claims = c->d_tail_claims;
+  a.deep_jobs = c->d_deep_jobs;
+  a.deep_done = c->d_deep_done;
   a.n_rows = n_rows;
   a.max_history = c->max_history;
   a.fused = pl.row_kernel ? 1u : 0u;
+  // Small batches share the deep passes with idle workgroups: any row without a top-k may take them
+  // (rows with kept lists take the full deep path, which is not shared).
+  bool partial = false;
+  for (uint32_t r = 0; r < n_rows; ++r) partial = partial || rows[r].mode == as_dev::kModePartial;
+  a.deep_help = (!pl.row_kernel && n_rows <= as_launch::kDeepHelpRows && !kept_ids && partial) ? 1u : 0u;
+  if (a.deep_help) {
+    c->deep_rows_done += n_rows;
+    a.deep_target = c->deep_rows_done;
+  }
   a.fused_count = c->d_fused_count;
 
   if (c->share_dirty)
@@ -327,7 +341,8 @@ int run_rows(as_ctx* c, const Plan& pl, const RowParams* rows, const float* logi
   for (uint32_t r = 0; r < n_rows; ++r)
     floor_rows += (rows[r].mode == as_dev::kModePartial && rows[r].min_p > 0.0f) ? 1u : 0u;
   const uint32_t tail_items = std::min(floor_rows, as_launch::kTailRows) * as_launch::tail_parts(n);
-  const uint32_t groups = std::max(n_rows, std::min(tail_items, as_launch::kTailGroups));
+  uint32_t groups = std::max(n_rows, std::min(tail_items, as_launch::kTailGroups));
+  if (a.deep_help) groups = std::max(groups, as_launch::kTailGroups);
   AS_HIP(c, as_launch::finish(c->stream, groups, c->d_args));
   c->share_dirty = false;
   if (e2) AS_HIP(c, hipEventRecord(e2, c->stream));
@@ -388,6 +403,8 @@ int as_destroy(as_ctx* c) {
   (void)hipFree(c->d_tail_bins);
   (void)hipFree(c->d_tail_list);
   (void)hipFree(c->d_tail_claims);
+  (void)hipFree(c->d_deep_jobs);
+  (void)hipFree(c->d_deep_done);
   (void)hipFree(c->d_cands);
   (void)hipFree(c->d_scratch);
   (void)hipFree(c->d_vstatus);
@@ -419,9 +436,7 @@ int as_create(int device, void* hip_stream, uint32_t max_rows, uint32_t max_voca
   c->max_seg = max_seg;
   c->order_cost.reserve(std::min(max_rows, as_launch::kOrderMax));
   c->rows.resize(max_rows);
-  // Per row: u32 counts [n], then (8-byte aligned) two u64 buffers [n] each for the deep and
-  // exact-order paths; rounded to 4 words so every row's scratch starts 16-byte aligned.
-  c->scratch_stride = (5ull * max_vocab + 2 + 3) & ~3ull;
+  c->scratch_stride = as_launch::scratch_words(max_vocab);
   hipError_t e = hipSetDevice(device);
   if (e == hipSuccess) e = hipMalloc(&c->d_block, kArgsSlot + sizeof(RowParams) * max_rows);
   if (e == hipSuccess) {
@@ -440,6 +455,10 @@ int as_create(int device, void* hip_stream, uint32_t max_rows, uint32_t max_voca
   const size_t claims = sizeof(uint64_t) * std::max(max_rows, as_launch::kTailGroups);
   if (e == hipSuccess) e = hipMalloc(&c->d_tail_claims, claims);
   if (e == hipSuccess) e = hipMemset(c->d_tail_claims, 0, claims);
+  if (e == hipSuccess) e = hipMalloc(&c->d_deep_jobs, sizeof(as_dev::DeepJob) * max_rows);
+  if (e == hipSuccess) e = hipMemset(c->d_deep_jobs, 0, sizeof(as_dev::DeepJob) * max_rows);
+  if (e == hipSuccess) e = hipMalloc(&c->d_deep_done, sizeof(uint64_t));
+  if (e == hipSuccess) e = hipMemset(c->d_deep_done, 0, sizeof(uint64_t));
   if (e == hipSuccess)
     e = hipMalloc(&c->d_cands, sizeof(uint64_t) * (uint64_t)max_rows * as_launch::kCandCap);
   if (e == hipSuccess) e = hipMalloc(&c->d_scratch, sizeof(uint32_t) * (uint64_t)max_rows * c->scratch_stride);

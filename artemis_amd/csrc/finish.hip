@@ -42,12 +42,20 @@ __global__ __launch_bounds__(1024) void finish_kernel(const FinishArgs* __restri
   as_fin_sliced::tail_list_load(a, row);
   __syncthreads();
   as_fin_sliced::tail_help(a, row, gridDim.x);
-  if (row >= a.n_rows) return;
-  as_fin_sliced::finish_row(a, row);
-  // A flagged row's S sums and histogram go back to zero for the next call once every part has
-  // ended and every path above is done with them.
-  __syncthreads();
-  if (as_fin_sliced::shm().tail_slot != kNone) as_fin_sliced::tail_end(a, row);
+  if (row < a.n_rows) {
+    as_fin_sliced::finish_row(a, row);
+    // A flagged row's S sums and histogram go back to zero for the next call once every part has
+    // ended and every path above is done with them.
+    __syncthreads();
+    if (as_fin_sliced::shm().tail_slot != kNone) as_fin_sliced::tail_end(a, row);
+  }
+  // A small batch: the row is finished (it publishes no more deep passes); then this workgroup takes
+  // parts of the other rows' passes until every row is finished.
+  if (a.deep_help) {
+    if (row < a.n_rows && threadIdx.x == 0)
+      __hip_atomic_fetch_add(a.deep_done, 1ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    as_fin_sliced::deep_help(a, row);
+  }
 }
 
 }  // namespace

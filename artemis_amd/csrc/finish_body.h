@@ -49,6 +49,8 @@ struct Shared {
   uint32_t draw_rng;  // the row draws: its stream advances once the candidates are in flight
   // S's sums (tail_list_load, tail_help, tail_wait): this call's flagged rows, this row's place among them.
   uint32_t tl_n, tl_rows[kTailListMax], tl_help[kTailListMax], tl_me, tail_slot, tail_waited, tail_won;
+  // The shared deep passes (deep_run, deep_help, deep_part).
+  uint32_t dp_pick, dp_stop, dp_q, dp_base, dp_staged;
 };
 // The workgroup's LDS, at file scope so that the out-of-line paths below address it as LDS: a static
 // array, or the kernel's dynamic LDS (AS_DYNAMIC_LDS) when another body shares it.
@@ -973,7 +975,224 @@ __device__ __forceinline__ T sel3(uint32_t k, T v0, T v1, T v2) {
   return k == 0 ? v0 : (k == 1 ? v1 : v2);
 }
 
+// --- the deep passes shared with idle workgroups ----------------------------------------------
+//
+// In a small batch most of the finish kernel's workgroups have no row, or are done with theirs, while
+// a deep row's two passes over its values would take one workgroup hundreds of microseconds. Those
+// passes are shared: the row's workgroup publishes a pass (DeepJob) and every idle workgroup takes
+// parts of kTailLen values (deep_help), as does the row's own (deep_run), which then waits only for
+// parts that running workgroups took. The histogram pass adds each part's bins into the row's
+// histogram with device atomics; the collecting pass lists each part's values from the chosen bins.
+// Nothing waits on a workgroup that has not begun, and a helper stops once every row of the call is
+// finished.
+
+// The shared passes' data in a row's scratch, after its history counts (8-byte aligned): the
+// histogram (counts, weights at 1, weights at T; kDistBins each), the list's count, a pad word, and
+// the list (at most kCap packed values).
+__device__ __forceinline__ uint32_t* deep_shared(const FinishArgs& a, uint32_t row) {
+  return a.scratch + (uint64_t)row * a.scratch_stride + (((uint64_t)a.n + 1) & ~1ull);
+}
+
+// One part of a row's shared pass (pass 0: its histogram; pass 1: its values in the published runs
+// of bins), by the whole workgroup, then the part counts itself ended. The history's positions are
+// left out (the row's workgroup adds the history's values penalised). The bins are the row's
+// deep_bins<true> ones: distance below the largest value, kDistBins over 32 max(T, 1). sh.wd and
+// sh.sk are free: a helper's own row is done, and the row's own workgroup calls this only where
+// deep_bins has nothing there.
+__device__ __noinline__ void deep_part(const FinishArgs& a, uint32_t row, uint32_t q, uint32_t pass) {
+  Shared& sh = shm();
+  constexpr uint32_t kLen = as_launch::kTailLen, kPer = kLen / kThreads, kNB = as_launch::kDistBins;
+  const uint32_t tid = threadIdx.x, lane = tid & (kWave - 1);
+  DeepJob& jb = a.deep_jobs[row];
+  const uint32_t n = a.n, b0 = q * kLen, b1 = min(b0 + kLen, n), len = b1 - b0;
+  const float* x = a.logits + (uint64_t)row * a.row_stride;
+  const bool vec = a.vec && a.row_stride % 4 == 0 && len == kLen;
+  typedef float f32x4 __attribute__((ext_vector_type(4)));
+  auto at = [&](uint32_t k) { return vec ? ((k / 4) * kThreads + tid) * 4 + (k % 4) : k * kThreads + tid; };
+  float v[kPer];
+  if (vec) {
+#pragma unroll
+    for (uint32_t j = 0; j < kPer / 4; ++j) {
+      const f32x4 qv = *reinterpret_cast<const f32x4*>(x + b0 + (j * kThreads + tid) * 4);
+#pragma unroll
+      for (int c = 0; c < 4; ++c) v[4 * j + c] = qv[c];
+    }
+  } else {
+#pragma unroll
+    for (uint32_t k = 0; k < kPer; ++k) v[k] = at(k) < len ? x[b0 + at(k)] : 0.0f;
+  }
+  const RowParams& p = a.params[row];
+  uint32_t hb;
+  const uint32_t he = as_launch::history_bounds(a, p, row, &hb);
+  const uint32_t extra = a.extra_ids ? p.extra : 0;
+  const bool pen = (p.flags & kFlagPenalties) && (he > hb || extra > 0);
+  const uint32_t mk = ld_agent(&jb.mk);
+  uint32_t r0[kBinRanges], r1[kBinRanges];
+#pragma unroll
+  for (uint32_t k = 0; k < kBinRanges; ++k) {
+    r0[k] = pass ? ld_agent(&jb.r0[k]) : kNone;
+    r1[k] = pass ? ld_agent(&jb.r1[k]) : kNone;
+  }
+  uint32_t* bm = reinterpret_cast<uint32_t*>(sh.wd);  // the part's history positions
+  uint32_t* hc = bm + kLen / 32;
+  double* hm = reinterpret_cast<double*>(hc + kNB);
+  double* hw = hm + kNB;
+  static_assert((kLen / 32 + kNB) % 2 == 0 && (kLen / 32 + kNB) * 4 + kNB * 16 <= sizeof(sh.wd), "part tables");
+  if (pen)
+    for (uint32_t i = tid; i < kLen / 32; i += kThreads) bm[i] = 0;
+  if (pass == 0)
+    for (uint32_t b = tid; b < kNB; b += kThreads) {
+      hc[b] = 0;
+      hm[b] = 0.0;
+      hw[b] = 0.0;
+    }
+  if (tid == 0) sh.dp_staged = 0;
+  __syncthreads();
+  if (pen) {
+    auto mark = [&](uint32_t id) {
+      const uint32_t off = id - b0;
+      if (off < len) atomicOr(&bm[off >> 5], 1u << (off & 31u));
+    };
+    for (uint32_t h = hb + tid; h < he; h += kThreads) mark(a.hist_ids[h]);
+    for (uint32_t h = tid; h < extra; h += kThreads) mark(a.extra_ids[h]);
+    __syncthreads();
+  }
+  const float topf = key_value(mk);
+  const double top = (double)topf, temp = (double)p.temp;
+  const float bsc = (float)kNB / (32.0f * fmaxf(1.0f, p.temp));
+  auto bin_of = [&](float val) -> uint32_t {
+    const float t = (topf - val) * bsc;
+    return t < (float)(kNB - 1) ? (uint32_t)t : kNB - 1;
+  };
+  auto own = [&](uint32_t k) { return at(k) < len && !(pen && ((bm[at(k) >> 5] >> (at(k) & 31u)) & 1u)); };
+  uint32_t* sh_g = deep_shared(a, row);
+  if (pass == 0) {
+    const uint64_t* tab = sh.tab;
+    const bool by_top_p = p.top_p < 1.0f;
+    auto e_core = [&](double d) -> double { return d > -512.0 ? as_exp::exp_core(tab, d) : 0.0; };
+#pragma unroll
+    for (uint32_t k = 0; k < kPer; ++k) {
+      if (!own(k)) continue;
+      const uint32_t b = bin_of(v[k]);
+      const double d = __dsub_rn((double)v[k], top);
+      atomicAdd(&hc[b], 1u);
+      if (by_top_p) atomicAdd(&hm[b], e_core(d));
+      atomicAdd(&hw[b], e_core(__ddiv_rn(d, temp)));
+    }
+    __syncthreads();
+    double* gm = reinterpret_cast<double*>(sh_g + kNB);
+    double* gw = gm + kNB;
+    for (uint32_t b = tid; b < kNB; b += kThreads) {
+      if (hc[b] == 0u) continue;
+      __hip_atomic_fetch_add(sh_g + b, hc[b], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      if (by_top_p) __hip_atomic_fetch_add(gm + b, hm[b], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      __hip_atomic_fetch_add(gw + b, hw[b], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+  } else {
+    // The part's values in the runs, staged in sh.sk with one LDS atomic per wave, then listed.
+#pragma unroll
+    for (uint32_t k = 0; k < kPer; ++k) {
+      bool in = false;
+      if (own(k)) {
+        const uint32_t b = bin_of(v[k]);
+#pragma unroll
+        for (uint32_t r = 0; r < kBinRanges; ++r) in = in || (b >= r0[r] && b <= r1[r]);  // unused: kNone
+      }
+      const uint64_t m = __ballot(in);
+      if (m) {
+        uint32_t base = 0;
+        if (lane == 0) base = atomicAdd(&sh.dp_staged, (uint32_t)__popcll(m));
+        base = __builtin_amdgcn_readfirstlane(base);
+        const uint32_t i = base + __builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0u));
+        if (in) sh.sk[i] = pack(total_key(v[k]), b0 + at(k));
+      }
+    }
+    __syncthreads();
+    const uint32_t staged = sh.dp_staged;
+    if (tid == 0) sh.dp_base = __hip_atomic_fetch_add(sh_g + 5 * kNB, staged, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __syncthreads();
+    const uint32_t base = sh.dp_base;
+    uint64_t* list = reinterpret_cast<uint64_t*>(sh_g + 5 * kNB + 2);
+    if (base + staged <= (uint32_t)kCap)
+      for (uint32_t i = tid; i < staged; i += kThreads) st_agent(list + base + i, sh.sk[i]);
+  }
+  // Every write above has completed (in every thread) before the part counts itself ended.
+  __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  __syncthreads();
+  if (tid == 0) __hip_atomic_fetch_add(&jb.ended[pass], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// The row's own workgroup: publishes pass `pass` (the fields it needs were stored before, in every
+// thread), takes its parts until none is left, then waits for the parts other workgroups took.
+// False if that wait ran past its guard (it cannot when every running workgroup makes progress).
+constexpr uint32_t kDeepSpin = 1u << 24;
+__device__ bool deep_run(const FinishArgs& a, uint32_t row, uint32_t pass) {
+  Shared& sh = shm();
+  DeepJob& jb = a.deep_jobs[row];
+  const uint32_t parts = as_launch::tail_parts(a.n);
+  __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  __syncthreads();
+  if (threadIdx.x == 0) __hip_atomic_store(&jb.stamp, 2 * a.call + pass, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  for (;;) {
+    if (threadIdx.x == 0)
+      sh.dp_q = ld_agent(&jb.next[pass]) < parts
+                    ? __hip_atomic_fetch_add(&jb.next[pass], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
+                    : parts;
+    __syncthreads();
+    const uint32_t q = sh.dp_q;
+    __syncthreads();
+    if (q >= parts) break;
+    deep_part(a, row, q, pass);
+  }
+  if (threadIdx.x == 0) {
+    uint32_t k = 0;
+    for (; ld_agent(&jb.ended[pass]) < parts && k < kDeepSpin; ++k) __builtin_amdgcn_s_sleep(2);
+    sh.dp_stop = k < kDeepSpin ? 1u : 0u;
+  }
+  __syncthreads();
+  return sh.dp_stop != 0u;
+}
+
+// A workgroup with no row left: takes parts of the rows' published passes (starting from its own
+// index, so that helpers spread over the rows) until every row of the call is finished. Helpers are
+// optional (each row's workgroup takes the parts nobody took), so a helper also stops after
+// kHelpTicks of the device's 100 MHz clock, a guard no call reaches.
+constexpr uint64_t kHelpTicks = 5000000;  // 50 ms
+__device__ __attribute__((unused)) void deep_help(const FinishArgs& a, uint32_t wg) {
+  Shared& sh = shm();
+  const uint32_t tid = threadIdx.x, nr = a.n_rows, parts = as_launch::tail_parts(a.n);
+  if (tid < 256) sh.tab[tid] = as_exp::kTable[tid];  // the parts' exps read the table in LDS
+  const uint64_t s0 = 2 * a.call, t0 = wall_clock64();
+  for (;;) {
+    if (tid == 0) sh.dp_pick = kNone;
+    __syncthreads();
+    // Every row's job at once, one per thread: a published pass with parts left.
+    for (uint32_t r = tid; r < nr; r += kThreads) {
+      const DeepJob& jb = a.deep_jobs[r];
+      const uint64_t st = ld_agent(&jb.stamp);
+      const uint32_t left0 = ld_agent(&jb.next[0]), left1 = ld_agent(&jb.next[1]);
+      const uint32_t pass = st == s0 ? 0u : (st == s0 + 1 ? 1u : 2u);
+      if (pass < 2 && (pass ? left1 : left0) < parts) atomicMin(&sh.dp_pick, (((r + nr - wg % nr) % nr) << 1) | pass);
+    }
+    if (tid == 0) sh.dp_stop = (ld_agent(a.deep_done) >= a.deep_target || wall_clock64() - t0 > kHelpTicks) ? 1u : 0u;
+    __syncthreads();
+    const uint32_t pick = sh.dp_pick, stop = sh.dp_stop;
+    if (pick != kNone) {
+      const uint32_t r = ((pick >> 1) + wg % nr) % nr, pass = pick & 1u;
+      if (tid == 0) sh.dp_q = __hip_atomic_fetch_add(&a.deep_jobs[r].next[pass], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      __syncthreads();
+      const uint32_t q = sh.dp_q;
+      if (q < parts) deep_part(a, r, q, pass);
+      continue;
+    }
+    if (stop) break;
+    __builtin_amdgcn_s_sleep(8);
+  }
+}
+
+template <bool kDist>
 __device__ __noinline__ bool deep_bins(const FinishArgs& a, const RowParams& p, uint32_t row, bool pen) {
+  constexpr uint32_t kNB = kDist ? as_launch::kDistBins : kDeepBins;
   Shared& sh = shm();
   const uint32_t n = a.n, tid = threadIdx.x;
   uint32_t* cnt = a.scratch + (uint64_t)row * a.scratch_stride;
@@ -990,13 +1209,13 @@ __device__ __noinline__ bool deep_bins(const FinishArgs& a, const RowParams& p, 
   const bool has_floor = p.min_p > 0.0f, by_top_p = p.top_p < 1.0f;
   const bool unfiltered = !by_top_p && !has_floor;
   const float floorf = floor_f32(__dadd_rn(top, p.ln_min_p));
-  // Bins of distance below the largest value, kDeepBins over span, everything further down in the
+  // Bins of distance below the largest value, kNB over span, everything further down in the
   // last: below span a weight is under e^-32 of the largest's (span is 32 T above T = 1).
   const float span = 32.0f * fmaxf(1.0f, p.temp);
-  const float bsc = (float)kDeepBins / span;
+  const float bsc = (float)kNB / span;
   auto bin_of = [&](float v) -> uint32_t {
     const float t = (topf - v) * bsc;
-    return t < (float)(kDeepBins - 1) ? (uint32_t)t : kDeepBins - 1;
+    return t < (float)(kNB - 1) ? (uint32_t)t : kNB - 1;
   };
   // The reference's weights exp(l - top) (top-p's) and exp((l - top) / T); arguments at or below
   // -512 (terms under 1e-222) are left out, far inside the bounds below.
@@ -1007,10 +1226,10 @@ __device__ __noinline__ bool deep_bins(const FinishArgs& a, const RowParams& p, 
   // Pass 1: counts (hc), weights at T = 1 (hm, top-p rows) and at T (hw). hc and hm share sh.wd,
   // hw lies in sh.sk.
   uint32_t* hc = reinterpret_cast<uint32_t*>(sh.wd);
-  double* hm = sh.wd + kDeepBins / 2;
+  double* hm = sh.wd + kNB / 2;
   double* hw = reinterpret_cast<double*>(sh.sk);
-  static_assert(kDeepBins * 12 <= sizeof(sh.wd) && kDeepBins * 8 <= sizeof(sh.sk), "histogram room");
-  for (uint32_t b = tid; b < kDeepBins; b += kThreads) {
+  static_assert(kNB * 12 <= sizeof(sh.wd) && kNB * 8 <= sizeof(sh.sk), "histogram room");
+  for (uint32_t b = tid; b < kNB; b += kThreads) {
     hc[b] = 0;
     hm[b] = 0.0;
     hw[b] = 0.0;
@@ -1022,9 +1241,38 @@ __device__ __noinline__ bool deep_bins(const FinishArgs& a, const RowParams& p, 
     if (by_top_p) atomicAdd(&hm[b], w1(v));
     atomicAdd(&hw[b], wt(v));
   };
-  for_each_value<true>(x, pcnt, n, vec, [&](uint32_t, float v, uint32_t c) {
-    if (__builtin_expect(c == 0, 1)) count(v);
-  });
+  if (kDist) {
+    // The histogram pass shared: the row's histogram in its scratch is cleared, the pass published,
+    // and this workgroup takes parts with the others until none is left, then waits for the parts
+    // the others took (the history's positions are left out of every part: they are added below).
+    uint32_t* gc = deep_shared(a, row);
+    double* gm = reinterpret_cast<double*>(gc + kNB);
+    double* gw = gm + kNB;
+    DeepJob& jb = a.deep_jobs[row];
+    for (uint32_t b = tid; b < kNB; b += kThreads) {
+      __hip_atomic_store(gc + b, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      __hip_atomic_store(gm + b, 0.0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      __hip_atomic_store(gw + b, 0.0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    if (tid == 0) {
+      __hip_atomic_store(&jb.mk, mk, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      for (int k = 0; k < 2; ++k) {
+        __hip_atomic_store(&jb.next[k], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_store(&jb.ended[k], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      }
+    }
+    if (!deep_run(a, row, 0)) return false;
+    for (uint32_t b = tid; b < kNB; b += kThreads) {
+      hc[b] = ld_agent(gc + b);
+      hm[b] = ld_agent(gm + b);
+      hw[b] = ld_agent(gw + b);
+    }
+    __syncthreads();  // the bins are whole before the history's values add to them
+  } else {
+    for_each_value<true>(x, pcnt, n, vec, [&](uint32_t, float v, uint32_t c) {
+      if (__builtin_expect(c == 0, 1)) count(v);
+    });
+  }
   if (pen) {
     // Each history id once, penalised, by the thread that sets its count's top bit first (pass 2
     // clears it again).
@@ -1039,8 +1287,8 @@ __device__ __noinline__ bool deep_bins(const FinishArgs& a, const RowParams& p, 
   __syncthreads();
 
   // Inclusive prefixes over the bins, in place: kDPer bins per thread, then the block.
-  constexpr int kDPer = kDeepBins / kThreads;
-  static_assert(kDeepBins % kThreads == 0, "whole bins per thread");
+  constexpr int kDPer = kNB / kThreads;
+  static_assert(kNB % kThreads == 0, "whole bins per thread");
   {
     uint32_t c4[kDPer], cs = 0;
     double m4[kDPer], w4[kDPer], ms = 0.0, ws = 0.0;
@@ -1071,7 +1319,7 @@ __device__ __noinline__ bool deep_bins(const FinishArgs& a, const RowParams& p, 
   // f64 atomic add and at most kDPer + 2 log2(kThreads) + 2 more adds; the reference's own folds of
   // the same terms (total1 and the unfiltered total in index order, the cumulatives in rank order,
   // the kept weight) are within gamma(n) of the same exact sums, and gj covers their ratios.
-  const double M_all = hm[kDeepBins - 1], W_all = hw[kDeepBins - 1];
+  const double M_all = hm[kNB - 1], W_all = hw[kNB - 1];
   const double g_all = gamma_ub(2.0 * (double)n + 128.0);
   const double Em = g_all * M_all, Ew = g_all * W_all;
   const double gj = gamma_ub(2.0 * (double)n + 4.0) + 10.0 * kU;
@@ -1095,7 +1343,7 @@ __device__ __noinline__ bool deep_bins(const FinishArgs& a, const RowParams& p, 
     }
     c_lo = block_min_u32<kWaves>(a0, sh.red_u);
     c_hi = block_min_u32<kWaves>(a1, sh.red_u);
-    if (c_hi == kNone) c_hi = kDeepBins - 1;
+    if (c_hi == kNone) c_hi = kNB - 1;
     if (c_lo == kNone) c_lo = c_hi;
   }
   // min-p's cut, the first rank below the floor, lies in the floor value's bin f (or at its ends).
@@ -1103,7 +1351,7 @@ __device__ __noinline__ bool deep_bins(const FinishArgs& a, const RowParams& p, 
   const bool need_c = by_top_p && !(has_floor && f < c_lo);  // else min-p surely cuts first
   const bool need_f = has_floor && !(by_top_p && f > c_hi);  // else top-p surely cuts first
   // The kept set ends in bins [k_lo, k_hi] (the last bin when nothing cuts).
-  uint32_t k_lo = kDeepBins - 1, k_hi = kDeepBins - 1;
+  uint32_t k_lo = kNB - 1, k_hi = kNB - 1;
   if (need_c) {
     k_lo = c_lo;
     k_hi = c_hi;
@@ -1204,7 +1452,32 @@ __device__ __noinline__ bool deep_bins(const FinishArgs& a, const RowParams& p, 
     for (uint32_t k = 0; k < kBinRanges; ++k) in = in || (b >= r0[k] && b <= r1[k]);  // unused: kNone
     return in;
   };
-  if (fits) {
+  if (fits && kDist) {
+    // The collecting pass shared: the runs published, the parts' values listed in the row's scratch,
+    // then copied here (the list holds at most kCap: more and the values do not fit).
+    DeepJob& jb = a.deep_jobs[row];
+    uint32_t* lc = deep_shared(a, row) + 5 * kNB;
+    const uint64_t* list = reinterpret_cast<const uint64_t*>(lc + 2);
+    if (tid == 0) {
+#pragma unroll
+      for (uint32_t k = 0; k < kBinRanges; ++k) {
+        __hip_atomic_store(&jb.r0[k], sel3(k, r0[0], r0[1], r0[2]), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_store(&jb.r1[k], sel3(k, r1[0], r1[1], r1[2]), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      }
+      __hip_atomic_store(lc, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    if (!deep_run(a, row, 1)) return false;
+    if (tid == 0) sh.nsk = ld_agent(lc);
+    __syncthreads();
+    const uint32_t got = sh.nsk;
+    if (got <= (uint32_t)kCap) {
+      for (uint32_t i = tid; i < got; i += kThreads) sh.sk[i] = ld_agent(list + i);
+      if (tid == 0) sh.pick = got;
+    } else if (tid == 0) {
+      sh.pick = kCap + 1;  // more than fit: not collected
+    }
+    __syncthreads();
+  } else if (fits) {
     for_each_value<true>(x, pcnt, n, vec, [&](uint32_t i, float v, uint32_t c) {
       if (__builtin_expect(c == 0, 1) && in_runs(bin_of(v))) {
         const uint32_t s = atomicAdd(&sh.pick, 1u);
@@ -2932,7 +3205,7 @@ __device__ __forceinline__ void finish_row(const FinishArgs& a, uint32_t row) {
     const bool pen = deep_prep(a, pr, row);
     bool done = false;
     if (!sh.stats_bad && pr.mode != kModeTopK && pr.mode != kModeExactTopK && !a.kept_ids) {
-      done = deep_bins(a, pr, row, pen);
+      done = a.deep_help ? deep_bins<true>(a, pr, row, pen) : deep_bins<false>(a, pr, row, pen);
       __syncthreads();
     }
     if (!done && !deep_row(a, pr, row, pen)) {

@@ -32,11 +32,22 @@ constexpr uint32_t kTopKMax = 256;
 constexpr uint32_t kHistReserve = 64;
 // Distinct history ids a slice can count (an LDS hash); more send the row to the exact path.
 constexpr uint32_t kHistSlots = 512;
+// The deep passes shared with idle workgroups histogram a row into kDistBins bins.
+constexpr uint32_t kDistBins = 1024;
+// u32 words of scratch per row for rows of n values: the history counts [n], then (8-byte aligned)
+// either two u64 buffers [n] (the full deep and exact-order paths) or the shared deep passes'
+// histogram (a u32 count and two f64 weights per bin) and list (a count, a pad word, kFinishCap
+// packed values); a multiple of 4 words, so that every row's scratch starts 16-byte aligned.
+__host__ __device__ constexpr uint64_t scratch_words(uint32_t n) {
+  const uint64_t head = ((uint64_t)n + 1) & ~1ull;
+  const uint64_t bufs = 4ull * n, shared = 5ull * kDistBins + 2 + 2ull * kFinishCap;
+  return (head + (bufs > shared ? bufs : shared) + 3) & ~3ull;
+}
 
 // The finish kernel's arguments and the rows' parameter blocks travel together, in one pinned host
 // block: FinishArgs in the first kArgsSlot bytes, then RowParams per row. The scan reads it where
 // the host wrote it and copies it to device memory for the finish kernel.
-constexpr uint32_t kArgsSlot = 256;
+constexpr uint32_t kArgsSlot = 320;
 
 struct FinishArgs {
   const float* logits;
@@ -59,7 +70,7 @@ struct FinishArgs {
   uint32_t* kept_ids;
   double* kept_probs;
   uint32_t vec;             // the rows are 16-byte aligned (float4 loads)
-  uint32_t* scratch;        // deep and exact paths: 5 x n u32 (+ alignment) per row
+  uint32_t* scratch;        // deep and exact paths: scratch_words(n) u32 per row
   uint64_t scratch_stride;  // u32 per row
   uint64_t* done;           // pinned host word: the call number whose scan has ended (the host
   uint64_t call;            //   reuses a parameter block once its call's scan is over)
@@ -72,7 +83,10 @@ struct FinishArgs {
   uint32_t fused;           // the row kernel: each workgroup scans and finishes its own row
   uint32_t* fused_count;    // the row kernel: workgroups that have ended (the last writes `done`)
   uint32_t n_rows;          // rows of the call
-  uint32_t pad_;
+  uint32_t deep_help;       // the deep path's passes are shared with idle workgroups (small batches)
+  as_dev::DeepJob* deep_jobs;  // per row
+  uint64_t* deep_done;      // rows finished, over every call of the context
+  uint64_t deep_target;     // deep_done once this call's rows are finished
 };
 
 // The row's history ids are hist_ids[*hb, return value), from the CSR offsets or the row's range.
@@ -121,7 +135,12 @@ hipError_t scan(hipStream_t stream, bool vec, const float* logits, const float* 
                 const uint32_t* extra_ids, as_dev::SegStats* stats, uint64_t* cands, uint32_t cand_stride,
                 as_dev::TailList* tail_list, const RowOrder& order);
 
-// groups: the call's rows, or more (the workgroups past them only take parts of S's sums).
+// A call of at most kDeepHelpRows rows, any of which may take the deep path, runs kTailGroups
+// workgroups: those past its rows, and each row's once its row is done, take parts of the rows' deep
+// passes until every row is finished.
+constexpr uint32_t kDeepHelpRows = 16;
+// groups: the call's rows, or more (the workgroups past them only take parts of S's sums and of the
+// deep passes).
 hipError_t finish(hipStream_t stream, uint32_t groups, const FinishArgs* a);
 
 // The row kernel (fused.hip): one 512-thread workgroup scans a whole row and chooses its token, for

@@ -98,6 +98,19 @@ struct TailList {
   uint32_t help[kTailListMax];  // each listed row's RowParams::help
 };
 
+// A row's deep-path passes, shared with the finish kernel's idle workgroups (small batches): the
+// row's workgroup publishes each pass by stamping it (2 x the call's number for the histogram pass,
+// that + 1 for the collecting pass) once the fields it needs are stored; any workgroup takes the
+// pass's parts through `next`, and each part counts itself in `ended` once its writes are complete.
+struct DeepJob {
+  uint64_t stamp;
+  uint32_t mk;            // the row's largest key
+  uint32_t next[2];       // per pass: the next part to take
+  uint32_t ended[2];      // per pass: parts ended
+  uint32_t r0[3], r1[3];  // the collecting pass: the runs of bins to collect (kNone: none)
+  uint32_t pad_;
+};
+
 // Per (row, slice) results of the scan.
 struct SegStats {
   uint32_t nonfinite;   // first index holding NaN/inf in the raw logits, or kNone
