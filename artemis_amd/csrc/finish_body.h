@@ -50,7 +50,7 @@ struct Shared {
   // S's sums (tail_list_load, tail_help, tail_wait): this call's flagged rows, this row's place among them.
   uint32_t tl_n, tl_rows[kTailListMax], tl_help[kTailListMax], tl_me, tail_slot, tail_waited, tail_won;
   // The shared deep passes (deep_run, deep_help, deep_part).
-  uint32_t dp_pick, dp_stop, dp_q, dp_base, dp_staged;
+  uint32_t dp_pick, dp_stop, dp_q, dp_base, dp_staged, dp_mk, dp_r[2 * 3];
 };
 // The workgroup's LDS, at file scope so that the out-of-line paths below address it as LDS: a static
 // array, or the kernel's dynamic LDS (AS_DYNAMIC_LDS) when another body shares it.
@@ -1026,12 +1026,14 @@ __device__ __noinline__ void deep_part(const FinishArgs& a, uint32_t row, uint32
   const uint32_t he = as_launch::history_bounds(a, p, row, &hb);
   const uint32_t extra = a.extra_ids ? p.extra : 0;
   const bool pen = (p.flags & kFlagPenalties) && (he > hb || extra > 0);
-  const uint32_t mk = ld_agent(&jb.mk);
-  uint32_t r0[kBinRanges], r1[kBinRanges];
-#pragma unroll
-  for (uint32_t k = 0; k < kBinRanges; ++k) {
-    r0[k] = pass ? ld_agent(&jb.r0[k]) : kNone;
-    r1[k] = pass ? ld_agent(&jb.r1[k]) : kNone;
+  // The job's fields, read once by the workgroup (every workgroup reads the same words).
+  if (tid == 0) {
+    sh.dp_mk = ld_agent(&jb.mk);
+    if (pass)
+      for (uint32_t k = 0; k < kBinRanges; ++k) {
+        sh.dp_r[k] = ld_agent(&jb.r0[k]);
+        sh.dp_r[kBinRanges + k] = ld_agent(&jb.r1[k]);
+      }
   }
   uint32_t* bm = reinterpret_cast<uint32_t*>(sh.wd);  // the part's history positions
   uint32_t* hc = bm + kLen / 32;
@@ -1056,6 +1058,13 @@ __device__ __noinline__ void deep_part(const FinishArgs& a, uint32_t row, uint32
     for (uint32_t h = hb + tid; h < he; h += kThreads) mark(a.hist_ids[h]);
     for (uint32_t h = tid; h < extra; h += kThreads) mark(a.extra_ids[h]);
     __syncthreads();
+  }
+  const uint32_t mk = sh.dp_mk;
+  uint32_t r0[kBinRanges], r1[kBinRanges];
+#pragma unroll
+  for (uint32_t k = 0; k < kBinRanges; ++k) {
+    r0[k] = pass ? sh.dp_r[k] : kNone;
+    r1[k] = pass ? sh.dp_r[kBinRanges + k] : kNone;
   }
   const float topf = key_value(mk);
   const double top = (double)topf, temp = (double)p.temp;
@@ -3078,8 +3087,11 @@ __device__ __forceinline__ void finish_row(const FinishArgs& a, uint32_t row) {
           j = draw_past(a, a.params[row], row, P, true, true);
         } else {
           j = draw_past(a, a.params[row], row, P, false, false);
-          if (j == kNone && tail_sums(a, a.params[row], row, R, has_floor ? floor_f32(floor) : -__builtin_inff(),
-                                      key_value(sh.mk))) {
+          // With the deep passes shared (a small batch), a row they would settle takes them at once
+          // rather than one workgroup's pass over the row first.
+          if (j == kNone && !a.deep_help &&
+              tail_sums(a, a.params[row], row, R, has_floor ? floor_f32(floor) : -__builtin_inff(),
+                        key_value(sh.mk))) {
             status |= AS_ROW_TAIL_PASS;
             j = draw_past(a, a.params[row], row, P, true, false);
           }
