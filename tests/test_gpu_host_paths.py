@@ -4,7 +4,9 @@
   exercises the two pinned parameter blocks the calls alternate between (a call reuses a block only
   once the call two before it has finished reading it);
 - histories with more distinct ids per slice than the scan's LDS hash counts (512), which send the
-  row to the finish kernel's passes over the whole row (the deep path, then the exact-order path).
+  row to the finish kernel's passes over the whole row (the deep path, then the exact-order path);
+- small batches whose rows take the deep path with its passes shared among the finish kernel's
+  idle workgroups, alone and alternating with larger batches on one context.
 """
 import numpy as np
 import pytest
@@ -104,3 +106,68 @@ def test_histories_past_the_slice_hash_take_the_exact_path(ctx, rows):
     # The slices could not count the history: every row was settled by a pass of the finish kernel
     # over the whole row (the deep path, then the exact-order path when a bound leaves it open).
     assert all(int(s) & (AS_ROW_EXACT_PATH | AS_ROW_DEEP_PATH) for s in g["status"]), [hex(int(s)) for s in g["status"]]
+
+
+@pytest.mark.parametrize("rows", [1, 3, 16])
+def test_small_batches_share_the_deep_passes(ctx, rows):
+    # A batch of at most 16 rows runs the finish kernel with extra workgroups, and rows whose draw or
+    # cut lies past their candidates share the deep path's two passes with them (in parts taken by
+    # whichever workgroup is idle). Rows without a top-k at the model's width: unfiltered at T = 1,
+    # top-p 0.95 at T = 1 and 0.6, with and without a history; seeds chosen per row.
+    from artemis_amd import states_tensor
+    dev = torch.device("cuda:0")
+    n = 248_320
+    rng = np.random.default_rng(40 + rows)
+    # Flat rows (sigma 1): the candidates hold a small part of the mass, so top-p's cut and most draws
+    # lie far past them and every batch has deep rows.
+    logits = rng.standard_normal((rows, n)).astype(np.float32)
+    kinds = [dict(temp=1.0, top_k=0, top_p=0.95, min_p=0.0),
+             dict(temp=1.0, top_k=0, top_p=1.0, min_p=0.0),
+             dict(temp=0.6, top_k=0, top_p=0.95, min_p=0.0, presence=0.5, frequency=0.3, repetition=1.05),
+             dict(temp=1.0, top_k=0, top_p=0.99, min_p=0.001)]
+    params = [kinds[r % len(kinds)] for r in range(rows)]
+    hists = [rng.integers(0, n, size=300).astype(np.uint32) for _ in range(rows)]
+    seeds = [900 + 17 * r for r in range(rows)]
+    off, ids = csr(hists, rows)
+    st = states_tensor(seeds, dev)
+    tok, status, kept, kept_ids, kept_probs = ctx.sample_batch(
+        torch.from_numpy(logits).to(dev), [settings(p) for p in params], st,
+        torch.from_numpy(off).to(dev), torch.from_numpy(ids).to(dev))
+    torch.cuda.synchronize()
+    g = dict(tokens=tok.cpu().numpy().astype(np.uint32), status=status.cpu().numpy().astype(np.uint32),
+             kept=kept.cpu().numpy().astype(np.uint32), kept_ids=kept_ids.cpu().numpy().astype(np.uint32),
+             kept_probs=kept_probs.cpu().numpy(), rng=st.cpu().numpy().view(np.uint64))
+    want = oracle_rows(logits, params, seeds, hists)
+    check_rows(g, want, params, label=f"rows={rows}")
+    # Kept lists are not asked for (rows with them take the full deep path alone).
+    assert any(int(s) & AS_ROW_DEEP_PATH for s in g["status"]), [hex(int(s)) for s in g["status"]]
+
+
+def test_shared_deep_passes_between_calls(ctx):
+    # Calls alternate between a small batch (deep passes shared) and a larger one (each row alone) on
+    # one context, with no host synchronisation: the shared jobs are stamped with the call's number,
+    # so a pass published in one call is never taken in another.
+    from artemis_amd import states_tensor
+    dev = torch.device("cuda:0")
+    n = 248_320
+    rng = np.random.default_rng(77)
+    sizes = [2, 20, 1, 20, 4]
+    plan = []
+    for c, rows in enumerate(sizes):
+        logits = (rng.standard_normal((rows, n)) * 2.5).astype(np.float32)
+        params = [dict(temp=1.0, top_k=0, top_p=1.0 if r % 2 else 0.95, min_p=0.0) for r in range(rows)]
+        seeds = [5000 + 31 * c + r for r in range(rows)]
+        st = states_tensor(seeds, dev)
+        out = ctx.outputs(rows, 0, dev)
+        plan.append((logits, params, seeds, st, out, torch.from_numpy(logits).to(dev)))
+    torch.cuda.synchronize()
+    for logits, params, seeds, st, out, d_lg in plan:
+        ctx.sample_batch(d_lg, [settings(p) for p in params], st, out=out)
+    torch.cuda.synchronize()
+    for c, (logits, params, seeds, st, out, _) in enumerate(plan):
+        tok, status, kept, kept_ids, kept_probs = out
+        g = dict(tokens=tok.cpu().numpy().astype(np.uint32), status=status.cpu().numpy().astype(np.uint32),
+                 kept=kept.cpu().numpy().astype(np.uint32), kept_ids=kept_ids.cpu().numpy().astype(np.uint32),
+                 kept_probs=kept_probs.cpu().numpy(), rng=st.cpu().numpy().view(np.uint64))
+        want = oracle_rows(logits, params, seeds, None)
+        check_rows(g, want, params, label=f"call {c}")
