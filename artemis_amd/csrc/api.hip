@@ -280,6 +280,9 @@ int run_rows(as_ctx* c, const Plan& pl, const RowParams* rows, const float* logi
   a.n_rows = n_rows;
   a.max_history = c->max_history;
   a.fused = pl.row_kernel ? 1u : 0u;
+  bool own_states = true;
+  for (uint32_t r = 0; r < n_rows && own_states; ++r) own_states = rows[r].rng_index == r;
+  a.rng_rows = own_states ? 1u : 0u;
   // Small batches share the deep passes with idle workgroups: any row without a top-k may take them
   // (rows with kept lists take the full deep path, which is not shared).
   bool partial = false;

@@ -2739,8 +2739,12 @@ __device__ __forceinline__ void finish_row(const FinishArgs& a, uint32_t row) {
   uint64_t* src = a.rng_state + 4ull * p.rng_index;
   uint32_t hb = 0, he = 0;
   if (tid == 0) {
-    if (draws)
+    // A row drawing from its own state (a.rng_rows) loads it beside its parameters rather than after.
+    if (a.rng_rows) {
+      for (int k = 0; k < 4; ++k) s4[k] = a.rng_state[4ull * row + k];
+    } else if (draws) {
       for (int k = 0; k < 4; ++k) s4[k] = src[k];
+    }
     he = as_launch::history_bounds(a, p, row, &hb);
   }
   __syncthreads();

@@ -87,6 +87,8 @@ struct FinishArgs {
   as_dev::DeepJob* deep_jobs;  // per row
   uint64_t* deep_done;      // rows finished, over every call of the context
   uint64_t deep_target;     // deep_done once this call's rows are finished
+  uint32_t rng_rows;        // row r draws from RNG state r (as_sample): its state loads without its parameters
+  uint32_t pad2_;
 };
 
 // The row's history ids are hist_ids[*hb, return value), from the CSR offsets or the row's range.
