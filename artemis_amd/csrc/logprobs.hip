@@ -11,9 +11,9 @@
 //     values of the part at or above it; the few values there go into LDS, where a rank count of
 //     their (value, id) keys sorts them.
 //   - lp_row_kernel: one workgroup per row. M = max m_p; total = sum of S_p * exp(m_p - M);
-//     lse = M + ln(total) (logprobs.rs:14-16); the parts' entries at or above the largest of the
-//     parts' nt-th entries hold the row's nt best, and a rank count orders them; each output is
-//     (x - lse) rounded to f32 (logprobs.rs:18, 34).
+//     lse = M + ln(total) (logprobs.rs:14-16); the row's nt best come from a merge of the parts'
+//     sorted lists (a tournament on one wave); each output is (x - lse) rounded to f32
+//     (logprobs.rs:18, 34).
 //
 // The reference sums exp(x - M) left to right over the row; this sum is parallel, with a bound on
 // the distance between the two: gamma(n + 64) relative (both orders' rounding and the rescale of
@@ -40,6 +40,7 @@ constexpr uint32_t kPer = kPart / kThreads;  // values per thread
 constexpr uint32_t kTop = as_launch::kLpTop;
 constexpr uint32_t kList = 1024;             // a part's values at or above its threshold
 constexpr uint32_t kMerge = as_launch::kLpMerge;
+constexpr uint32_t kEntries = kMerge / kThreads;  // list slots per thread in a row's merge
 constexpr double kU = 1.1102230246251565e-16;  // 2^-53
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 static_assert(kPer % 4 == 0, "whole 16-byte groups per thread");
@@ -62,30 +63,33 @@ __device__ __forceinline__ uint32_t wave_qth_u32(uint32_t x, uint32_t q) {
 
 __device__ __forceinline__ double gamma_n(double n) { return n * kU / (1.0 - n * kU); }
 
-// Relative error of exp_neg against exp, per term: the polynomial's truncation (3.07e-13 for |f| <= 1/2),
-// the rounding of t = d * log2(e) (at most |t| <= 1022 times 2^-53, times ln 2) and of the Horner steps.
-constexpr double kExpRel = 5.0e-13;
+// Relative error of exp_neg against exp, per term: the polynomial's (1.064e-12 at most, at f = -1/2),
+// the rounding of t = d * log2(e) (|t| <= 1022 times 2^-52, times ln 2: 1.6e-13) and of the Horner
+// steps (about 1e-15).
+constexpr double kExpRel = 1.5e-12;
 
 // exp(d) for d <= 0 without a table (a table's gathers from LDS conflict across lanes): e^d = 2^t,
-// t = d log2(e) = k + f with k = rint(t) and |f| <= 1/2 (f = t - k exactly), 2^f by its Taylor
-// series in f to degree 10 (coefficients ln(2)^i / i!), 2^k by ldexp (ExpPoly::exp_neg). Within kExpRel
-// of exp(d); the parallel sum it feeds is bounded at gamma(n) ~ 2.7e-11 relative anyway, so a few
-// ulps more per term change nothing. Below d = -708 the argument is clamped (such a term is under
-// 2^-1021 of the row's largest, which is 1).
+// t = d log2(e) = k + f with k = rint(t) and |f| <= 1/2 (f = t - k exactly), 2^f by a polynomial of
+// degree 8, 2^k by ldexp (ExpPoly::exp_neg). Within kExpRel of exp(d); the parallel sum it feeds is
+// bounded at gamma(n) ~ 2.8e-11 relative, so a few ulps more per term change little. Below d = -708
+// the argument is clamped (such a term is under 2^-1021 of the row's largest, which is 1).
 //
-// The coefficients of 2^f, highest degree first. Read from constant memory once per thread, they stay
-// in scalar registers, which each fused multiply-add takes as an operand (as immediates, each step
-// would first rebuild its coefficient in two vector moves).
-__constant__ double kExp2Poly[11] = {
-    7.054911620801123e-09,  1.01780860092397e-07,  1.321548679014431e-06, 1.5252733804059841e-05,
-    0.0001540353039338161,  0.0013333558146428443, 0.009618129107628477,  0.05550410866482158,
-    0.24022650695910072,    0.6931471805599453,    1.0};
+// The coefficients of 2^f, highest degree first: the Chebyshev interpolant of 2^f on [-1/2, 1/2] at
+// degree 8 (mpmath.chebyfit at 40 digits), rounded to f64; with the rounded coefficients its relative
+// error peaks at 1.064e-12, at f = -1/2. Read from constant memory once per thread, they stay in
+// scalar registers, which each fused multiply-add takes as an operand (as immediates, each step would
+// first rebuild its coefficient in two vector moves).
+constexpr int kPolyLen = 9;
+__constant__ double kExp2Poly[kPolyLen] = {
+    1.3255224878668817e-06, 1.5310079402249296e-05, 0.00015403455852453838, 0.0013333450568000645,
+    0.009618129159402558,   0.05550410941205933,    0.2402265069581299,     0.6931471805459335,
+    1.0};
 
 struct ExpPoly {
-  double c[11];
+  double c[kPolyLen];
   __device__ __forceinline__ void load() {
 #pragma unroll
-    for (int i = 0; i < 11; ++i) c[i] = kExp2Poly[i];
+    for (int i = 0; i < kPolyLen; ++i) c[i] = kExp2Poly[i];
   }
   __device__ __forceinline__ double exp_neg(double d) const {
     const double t = fmax(d, -708.0) * 1.4426950408889634;
@@ -93,7 +97,7 @@ struct ExpPoly {
     const double f = t - k;
     double p = c[0];
 #pragma unroll
-    for (int i = 1; i < 11; ++i) p = __builtin_fma(p, f, c[i]);
+    for (int i = 1; i < kPolyLen; ++i) p = __builtin_fma(p, f, c[i]);
     return __builtin_amdgcn_ldexp(p, (int32_t)k);
   }
 };
@@ -208,9 +212,9 @@ __global__ __launch_bounds__(kThreads) void lp_part_kernel(const float* __restri
 
 struct RowShared {
   uint64_t tab[256];
-  uint64_t merged[kMerge];
+  uint64_t lists[kMerge];         // the parts' lists end to end, kTop slots each
   uint64_t top[kTop];
-  uint32_t n_merged;
+  uint32_t n_top[kMerge / kTop];  // per part: its list's length
   uint32_t overflow;
   uint32_t inexact;
   uint32_t red_u[kWaves];
@@ -227,6 +231,8 @@ __device__ __forceinline__ float lp_round(double xd, double lse, double e, bool*
   return r;
 }
 
+// One workgroup per row. Every load it needs (the parts' fields and lists, the token's logit) is
+// issued at once, before any is used: one round trip to HBM.
 __global__ __launch_bounds__(kThreads) void lp_row_kernel(const float* __restrict__ logits, uint64_t row_stride,
                                                           uint32_t n, const LpPart* __restrict__ parts,
                                                           uint32_t n_parts, const uint32_t* __restrict__ tokens,
@@ -237,34 +243,45 @@ __global__ __launch_bounds__(kThreads) void lp_row_kernel(const float* __restric
   const uint32_t row = blockIdx.x, tid = threadIdx.x;
   const float* x = logits + (uint64_t)row * row_stride;
   const LpPart* pp = parts + (uint64_t)row * n_parts;
+  const uint32_t tok = tokens[row];
+  const uint32_t nt = min(min(top, kTop), n);
+  // One part per thread (n_parts <= kMerge / kTop < kThreads), and list slots i = tid + k kThreads of
+  // the parts' lists laid end to end (those past a part's n_top are never read below). The
+  // addresses are clamped into the row's parts, so that every load is issued unconditionally.
+  const bool mine = tid < n_parts;
+  const LpPart& q = pp[min(tid, n_parts - 1)];
+  const float mx = q.max;
+  const double sum = q.sum;
+  const uint32_t nq = q.n_top, ovf = q.overflow;
+  const uint32_t nm = n_parts * kTop;
+  uint64_t ent[kEntries];
+  if (nt > 0) {
+#pragma unroll
+    for (uint32_t k = 0; k < kEntries; ++k) {
+      const uint32_t i = min(tid + k * kThreads, nm - 1);
+      ent[k] = pp[i / kTop].top[i % kTop];
+    }
+  }
+  const float xt = x[min(tok, n - 1)];
+
   sh.tab[tid] = as_exp::kTable[tid];
   if (tid == 0) {
-    sh.n_merged = 0;
     sh.overflow = 0;
     sh.inexact = 0;
   }
+  if (mine) sh.n_top[tid] = nq;
+  if (nt > 0) {
+#pragma unroll
+    for (uint32_t k = 0; k < kEntries; ++k)
+      if (tid + k * kThreads < nm) sh.lists[tid + k * kThreads] = ent[k];
+  }
   // M: the largest part maximum.
-  uint32_t kmax = 0;
-  for (uint32_t p = tid; p < n_parts; p += kThreads) kmax = max(kmax, total_key(pp[p].max));
-  kmax = block_max_u32<kWaves>(kmax, sh.red_u);
+  const uint32_t kmax = block_max_u32<kWaves>(mine ? total_key(mx) : 0u, sh.red_u);
+  if (mine && ovf) sh.overflow = 1;  // after the block's barriers: thread 0 has cleared it
   const double M = (double)key_value(kmax);
   // total = sum of S_p * exp(m_p - M).
-  const uint32_t nt = min(min(top, kTop), n);
-  double t = 0.0;
-  uint64_t cut = 0;
-  for (uint32_t p = tid; p < n_parts; p += kThreads) {
-    const LpPart& q = pp[p];
-    t += q.sum * as_exp::exp_with(sh.tab, (double)q.max - M);
-    if (q.overflow) sh.overflow = 1;
-    // A part listing nt entries has nt values at or above its nt-th: no value below the largest
-    // such entry is among the row's nt best.
-    if (nt > 0 && q.n_top >= nt) cut = max(cut, q.top[nt - 1]);
-  }
-  const double total = block_sum_f64<kWaves>(t, sh.red_d);
-  cut = wave_max_u64(cut);
-  if ((tid & (kWave - 1)) == 0) sh.red_k[tid / kWave] = cut;
-  __syncthreads();
-  for (int k = 0; k < kWaves; ++k) cut = max(cut, sh.red_k[k]);
+  const double t = mine ? sum * as_exp::exp_with(sh.tab, (double)mx - M) : 0.0;
+  const double total = block_sum_f64<kWaves>(t, sh.red_d);  // its barriers publish overflow and the lists
   const double lnt = log(total);
   const double lse = M + lnt;
   // The distance to the reference's lse: both sums' roundings (n terms each, the parts' rescales),
@@ -273,28 +290,31 @@ __global__ __launch_bounds__(kThreads) void lp_row_kernel(const float* __restric
 
   if (nt > 0) {
     if (!sh.overflow) {
-      // The parts' entries at or above the cut hold the row's nt best (each part's list holds its
-      // own best kTop); an entry's place among them is the count of larger ones.
-      const uint32_t nm = n_parts * kTop;
-      for (uint32_t i = tid; i < nm; i += kThreads) {
-        const LpPart& q = pp[i / kTop];
-        if (i % kTop < q.n_top) {
-          const uint64_t key = q.top[i % kTop];
-          if (key >= cut) sh.merged[atomicAdd(&sh.n_merged, 1u)] = key;
+      // The row's nt best, in order, from the parts' sorted lists: a tournament on wave 0, where lane
+      // l holds the heads of parts l and l + 64; the largest head is the next best (keys are
+      // distinct: they hold the ids), and its part's list moves on. The lists hold at least nt
+      // entries together (a part lists min(its values, kTop) or more).
+      static_assert(kMerge / kTop <= 2 * kWave, "two parts per lane");
+      if (tid < kWave) {
+        const uint32_t p0 = tid, p1 = tid + kWave;
+        const uint32_t n0 = p0 < n_parts ? sh.n_top[p0] : 0u, n1 = p1 < n_parts ? sh.n_top[p1] : 0u;
+        uint32_t h0 = 0, h1 = 0;
+        uint64_t k0 = n0 > 0 ? sh.lists[p0 * kTop] : 0ull, k1 = n1 > 0 ? sh.lists[p1 * kTop] : 0ull;
+        for (uint32_t r = 0; r < nt; ++r) {
+          const uint64_t m = wave_max_u64(max(k0, k1));
+          if (tid == 0) sh.top[r] = m;
+          if (m == k0) {
+            ++h0;
+            k0 = h0 < n0 ? sh.lists[p0 * kTop + h0] : 0ull;
+          } else if (m == k1) {
+            ++h1;
+            k1 = h1 < n1 ? sh.lists[p1 * kTop + h1] : 0ull;
+          }
         }
-      }
-      __syncthreads();
-      const uint32_t nc = sh.n_merged;
-      for (uint32_t i = tid; i < nc; i += kThreads) {
-        const uint64_t key = sh.merged[i];
-        uint32_t r = 0;
-        for (uint32_t j = 0; j < nc; ++j) r += sh.merged[j] > key ? 1u : 0u;
-        if (r < nt) sh.top[r] = key;
       }
     } else {
       // Heavy ties overflowed a part's list: the row's best, one full pass each (the largest key
       // below the one before).
-      __syncthreads();  // every thread has read the cut from red_k
       uint64_t prev = ~0ull;
       for (uint32_t r = 0; r < nt; ++r) {
         uint64_t b = 0;
@@ -314,19 +334,18 @@ __global__ __launch_bounds__(kThreads) void lp_row_kernel(const float* __restric
     }
     __syncthreads();
     for (uint32_t r = tid; r < nt; r += kThreads) {
-      const uint32_t id = packed_id(sh.top[r]);
+      // The key holds the logit (-0 as +0, which gives the same difference).
       bool exact;
-      const float lp = lp_round((double)x[id], lse, e, &exact);
-      top_ids[(uint64_t)row * top + r] = id;
+      const float lp = lp_round((double)packed_value(sh.top[r]), lse, e, &exact);
+      top_ids[(uint64_t)row * top + r] = packed_id(sh.top[r]);
       top_lps[(uint64_t)row * top + r] = lp;
       if (!exact) sh.inexact = 1;
     }
   }
   if (tid == 0) {
-    const uint32_t tok = tokens[row];
     bool exact = true;
     float lp = __builtin_nanf("");
-    if (tok < n) lp = lp_round((double)x[tok], lse, e, &exact);
+    if (tok < n) lp = lp_round((double)xt, lse, e, &exact);
     logprob[row] = lp;
     if (!exact) sh.inexact = 1;
     if (tok >= n) sh.inexact = 1;

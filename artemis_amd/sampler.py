@@ -333,7 +333,8 @@ class Context:
                  n_vocab: Optional[int] = None):
         """logprobs (logprobs.rs:12-38) on every row: (logprob [n] f32, top_ids [n, top] int32,
         top_logprobs [n, top] f32, status [n] int32) device tensors; the first min(top, 20, n_vocab)
-        columns of each row are written. `tokens`: [n] int32 on the device."""
+        columns of each row are written, any others hold -1 and NaN. `tokens`: [n] int32 on the
+        device."""
         if logits.dim() == 1:
             logits = logits.view(1, -1)
         assert logits.is_cuda and logits.dtype == torch.float32
@@ -344,8 +345,13 @@ class Context:
         dev = logits.device
         lp = torch.empty(rows, dtype=torch.float32, device=dev)
         cols = max(top, 1)
-        ids = torch.full((rows, cols), -1, dtype=torch.int32, device=dev)
-        lps = torch.full((rows, cols), float("nan"), dtype=torch.float32, device=dev)
+        if 0 < top <= min(LP_MAX_TOP, nv):
+            # The library writes every column.
+            ids = torch.empty((rows, cols), dtype=torch.int32, device=dev)
+            lps = torch.empty((rows, cols), dtype=torch.float32, device=dev)
+        else:
+            ids = torch.full((rows, cols), -1, dtype=torch.int32, device=dev)
+            lps = torch.full((rows, cols), float("nan"), dtype=torch.float32, device=dev)
         st = torch.empty(rows, dtype=torch.int32, device=dev)
         self._ok(lib().as_logprobs(self.h, logits.data_ptr(), stride, nv, rows, tokens.data_ptr(), top,
                                    lp.data_ptr(), ids.data_ptr() if top else None,

@@ -192,7 +192,7 @@ int as_head_argmax(as_ctx* ctx, const void* w, uint32_t wtype, uint32_t rows, ui
  * top is 0), status [n_rows] or NULL: AS_LP_OK (every value the reference's bits), or AS_LP_INEXACT
  * when the bound e on the parallel sum's distance to the reference's left-to-right sum could move a
  * value's rounding to f32, or a token is out of range (its logprob is NaN). The bound is absolute:
- * |lse - lse_ref| <= e = gamma(n + 64) + 5e-13 + 2^-51 |ln total| + 2^-52 |lse| (gamma(m) =
+ * |lse - lse_ref| <= e = gamma(n + 64) + 1.5e-12 + 2^-51 |ln total| + 2^-52 |lse| (gamma(m) =
  * m 2^-53 / (1 - m 2^-53); about 2.8e-11 at the model's vocabulary), so an inexact value is within
  * e + one f32 ulp of the reference's, and its exp within about e relative. Near lp = 0 (a
  * near-certain token) that can be many f32 ulps. */

@@ -3,7 +3,7 @@ restates the same function (oracle/sampler_oracle.cc, oc_logprobs). Top ids must
 must be bit-exact on rows whose status is AS_LP_OK. On a row marked AS_LP_INEXACT (the bound on the
 parallel sum's distance to the reference's left-to-right sum could move a rounding to f32) each value
 must be within the library's absolute bound of the oracle's: |lp - lp_ref| <= e + one f32 ulp, with
-e = gamma(n + 64) + 5e-13 + 2^-51 |ln total| + 2^-52 |lse| (include/artemis_sampler.h), so exp(lp) is
+e = gamma(n + 64) + 1.5e-12 + 2^-51 |ln total| + 2^-52 |lse| (include/artemis_sampler.h), so exp(lp) is
 within about 3e-11 relative of the reference's probability, far inside the 1e-5 the probabilities
 must meet. Near-certain tokens (lp close to 0) are where that is many f32 ulps."""
 import numpy as np
@@ -47,7 +47,7 @@ def lse_bound(row, lse):
     n = len(row)
     g = (n + 64) * U / (1 - (n + 64) * U)
     ln_total = lse - float(np.max(row))
-    return g + 5e-13 + 4 * U * abs(ln_total) + 2 * U * abs(lse)
+    return g + 1.5e-12 + 4 * U * abs(ln_total) + 2 * U * abs(lse)
 
 
 def same_or_within(got, want, exact, e):
