@@ -881,12 +881,12 @@ __device__ __forceinline__ uint32_t stream_draw(Shared& sh, const uint64_t* buf,
 
 // The deep path's passes over a row: 16 values per thread per step, with their history counts
 // (cnt, 0 when null). One workgroup streams a whole row, so its loads' latency, not HBM, bounds a
-// pass. With kPipe and without counts, whole 16-byte steps run two at a time, each step's loads
-// issued before the previous step's values are used (the last of them reloads a step rather than
-// branch); otherwise (counts take as many registers again, and some callers have none to spare) a
-// step's loads are all issued before any value is used. Scalar loads cover an unaligned row and the
-// ragged end. f(i, v, c) runs for each value.
-template <bool kPipe = false, class F>
+// pass. With kPipe and without counts, whole 16-byte steps go through a ring of kDepth steps' loads:
+// each step's loads are issued kDepth - 1 steps before its values are used (near the end they reload
+// the last step rather than branch); otherwise (counts take as many registers again, and some callers
+// have none to spare) a step's loads are all issued before any value is used. Scalar loads cover an
+// unaligned row and the ragged end. f(i, v, c) runs for each value.
+template <bool kPipe = false, int kDepth = 2, class F>
 __device__ __forceinline__ void for_each_value(const float* x, const uint32_t* cnt, uint32_t n, bool vec, F f) {
   typedef float f32x4 __attribute__((ext_vector_type(4)));
   typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
@@ -897,34 +897,41 @@ __device__ __forceinline__ void for_each_value(const float* x, const uint32_t* c
   if (vec) {
     const uint32_t whole = n / kStep;
     if (kPipe && !cnt && whole > 0) {
-      f32x4 qa[4], qb[4];
-      auto load = [&](f32x4 (&q)[4], uint32_t s) {
+      static_assert(kDepth >= 2, "a step in flight while another is used");
+      f32x4 q[kDepth][4];
+      auto load = [&](f32x4 (&r)[4], uint32_t s) {
 #pragma unroll
-        for (int j = 0; j < 4; ++j) q[j] = *reinterpret_cast<const f32x4*>(x + at(s, j));
+        for (int j = 0; j < 4; ++j) r[j] = gload(reinterpret_cast<const f32x4*>(x + at(s, j)));
       };
-      auto use = [&](const f32x4 (&q)[4], uint32_t s) {
+      auto use = [&](const f32x4 (&r)[4], uint32_t s) {
 #pragma unroll
         for (int j = 0; j < 4; ++j)
 #pragma unroll
-          for (int c = 0; c < 4; ++c) f(at(s, j) + c, q[j][c], 0u);
+          for (int c = 0; c < 4; ++c) f(at(s, j) + c, r[j][c], 0u);
       };
-      load(qa, 0);
+      // Slot d holds step s + d; before step s + d is used, the slot of the step used just before
+      // takes step s + d + kDepth - 1.
+#pragma unroll
+      for (int d = 0; d < kDepth - 1; ++d) load(q[d], min((uint32_t)d, whole - 1));
       uint32_t s = 0;
-      for (; s + 2 <= whole; s += 2) {
-        load(qb, s + 1);
-        use(qa, s);
-        load(qa, min(s + 2, whole - 1));
-        use(qb, s + 1);
+      for (; s + kDepth <= whole; s += kDepth) {
+#pragma unroll
+        for (int d = 0; d < kDepth; ++d) {
+          load(q[(d + kDepth - 1) % kDepth], min(s + d + kDepth - 1, whole - 1));
+          use(q[d], s + d);
+        }
       }
-      if (s < whole) use(qa, s);
+#pragma unroll
+      for (int d = 0; d < kDepth - 1; ++d)
+        if (s + d < whole) use(q[d], s + d);
     } else {
       for (uint32_t s = 0; s < whole; ++s) {
         f32x4 q[4];
         u32x4 k[4];
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
-          q[j] = *reinterpret_cast<const f32x4*>(x + at(s, j));
-          k[j] = cnt ? *reinterpret_cast<const u32x4*>(cnt + at(s, j)) : u32x4{0u, 0u, 0u, 0u};
+          q[j] = gload(reinterpret_cast<const f32x4*>(x + at(s, j)));
+          k[j] = cnt ? gload(reinterpret_cast<const u32x4*>(cnt + at(s, j))) : u32x4{0u, 0u, 0u, 0u};
         }
 #pragma unroll
         for (int j = 0; j < 4; ++j)
@@ -940,8 +947,8 @@ __device__ __forceinline__ void for_each_value(const float* x, const uint32_t* c
 #pragma unroll
     for (int j = 0; j < 16; ++j) {
       const uint32_t i = b0 + j * kThreads + tid;
-      q[j] = (i < n) ? x[i] : 0.0f;
-      k[j] = (cnt && i < n) ? cnt[i] : 0u;
+      q[j] = (i < n) ? gload(x + i) : 0.0f;
+      k[j] = (cnt && i < n) ? gload(cnt + i) : 0u;
     }
 #pragma unroll
     for (int j = 0; j < 16; ++j) {
@@ -960,15 +967,33 @@ __device__ __noinline__ float penalize_out(float x, uint32_t c, const RowParams&
 // total), at min-p's floor, and at the draw (the cumulative weight at T passing u times the kept
 // weight). One pass over the row histograms every value by its distance below the largest into
 // kDeepBins bins (the bin is monotone in the value, so bins follow the rank order) and adds each
-// value's weights, the host-exact exp of the reference's own f64 arguments (exp_core): every term
-// has the reference's bits, and any sum of them differs from the reference's ordered folds only by
-// rounding. The bins' prefix sums fix, with certified bounds, the few bins that can hold each
+// value's weights, each within kPassRel of the reference's term (the bounded exp of exp_poly.h, at
+// (l - top) / T computed as (l - top) * (1 / T)): any sum of them differs from the reference's ordered
+// folds by rounding and kPassRel of the sum. The bins' prefix sums fix, with certified bounds, the few bins that can hold each
 // decision; a second pass collects only those bins' values into LDS, a sort orders them, and each
 // one's rank is the count before its run of collected bins plus its place in the run. The decisions
 // compare the reference's cumulatives, bounded by the prefix before the run plus the run's terms,
 // with targets bounded by the exact totals. Returns false, with nothing written, when a bound cannot
 // decide or the bins hold more values than LDS does; the caller then takes the full deep path.
 constexpr uint32_t kBinRanges = 3;
+// The histogram passes' terms against the reference's: the bounded exp's kExpPolyRel and the argument
+// scaled by 1 / T instead of divided by T (two roundings, |(l - top) / T| <= 708 before the clamp:
+// 1.6e-13 more), rounded up.
+constexpr double kPassRel = 2.0e-12;
+static_assert(kPassRel >= kExpPolyRel + 1.6e-13, "the histogram terms' bound");
+// A histogram pass's weights of a value: exp(l - top) (top-p's) and exp((l - top) / T).
+struct PassWeights {
+  ExpPoly ep;
+  double top, inv_t;
+  __device__ __forceinline__ void init(double top_, double temp) {
+    ep.load();
+    top = top_;
+    inv_t = 1.0 / temp;
+  }
+  __device__ __forceinline__ double d(float v) const { return __dsub_rn((double)v, top); }
+  __device__ __forceinline__ double one(double dv) const { return ep.exp_neg(dv); }
+  __device__ __forceinline__ double at_t(double dv) const { return ep.exp_neg(__dmul_rn(dv, inv_t)); }
+};
 // Element k of a run's three values, by selects (the runs' few values stay in registers).
 template <class T>
 __device__ __forceinline__ T sel3(uint32_t k, T v0, T v1, T v2) {
@@ -1076,17 +1101,17 @@ __device__ __noinline__ void deep_part(const FinishArgs& a, uint32_t row, uint32
   auto own = [&](uint32_t k) { return at(k) < len && !(pen && ((bm[at(k) >> 5] >> (at(k) & 31u)) & 1u)); };
   uint32_t* sh_g = deep_shared(a, row);
   if (pass == 0) {
-    const uint64_t* tab = sh.tab;
     const bool by_top_p = p.top_p < 1.0f;
-    auto e_core = [&](double d) -> double { return d > -512.0 ? as_exp::exp_core(tab, d) : 0.0; };
+    PassWeights pw;
+    pw.init(top, temp);
 #pragma unroll
     for (uint32_t k = 0; k < kPer; ++k) {
       if (!own(k)) continue;
       const uint32_t b = bin_of(v[k]);
-      const double d = __dsub_rn((double)v[k], top);
+      const double d = pw.d(v[k]);
       atomicAdd(&hc[b], 1u);
-      if (by_top_p) atomicAdd(&hm[b], e_core(d));
-      atomicAdd(&hw[b], e_core(__ddiv_rn(d, temp)));
+      if (by_top_p) atomicAdd(&hm[b], pw.one(d));
+      atomicAdd(&hw[b], pw.at_t(d));
     }
     __syncthreads();
     double* gm = reinterpret_cast<double*>(sh_g + kNB);
@@ -1199,6 +1224,85 @@ __device__ __attribute__((unused)) void deep_help(const FinishArgs& a, uint32_t 
   }
 }
 
+// The deep path's two passes over a row, each streaming through a ring of three steps' loads (two in
+// flight while one is used: more would spill the caller's registers). Both leave out the history's
+// positions (cnt set): their values are penalised, which the caller adds. The bins: distance below
+// the largest value topf, bsc bins per unit, the last bin holding everything further down.
+__device__ __forceinline__ uint32_t deep_bin(float topf, float bsc, uint32_t nb, float v) {
+  const float t = (topf - v) * bsc;
+  return t < (float)(nb - 1) ? (uint32_t)t : nb - 1;
+}
+
+// Pass 1: each value's count and weights into the LDS histogram (hc counts, hm the weights at T = 1
+// when by_top_p, hw the weights at T).
+__device__ __forceinline__ void deep_hist(const float* x, const uint32_t* pcnt, uint32_t n, bool vec, uint32_t nb,
+                                       float topf, float bsc, double top, double temp, bool by_top_p, uint32_t* hc,
+                                       double* hm, double* hw) {
+  PassWeights pw;
+  pw.init(top, temp);
+  for_each_value<true, 3>(x, pcnt, n, vec, [&](uint32_t, float v, uint32_t c) {
+    if (__builtin_expect(c == 0, 1)) {
+      const uint32_t b = deep_bin(topf, bsc, nb, v);
+      const double d = pw.d(v);
+      atomicAdd(&hc[b], 1u);
+      if (by_top_p) atomicAdd(&hm[b], pw.one(d));
+      atomicAdd(&hw[b], pw.at_t(d));
+    }
+  });
+}
+
+// Pass 2: the values of the bins in the runs [a0, e0], [a1, e1], [a2, e2] (kNone: no run) into sk,
+// packed, in any order; *pick counts them (past cap they are counted, not kept). kb: 6 words of LDS.
+// The bin is a non-increasing function of the value, so the values whose bin lies in a run [a, e]
+// are those whose key lies in an interval [lo, hi]. Lanes 0-5 find the six bounds by bisection over
+// the keys at or below the largest value's (no value of the row lies above it; the keys below the
+// finite values, -inf's and the NaNs', fall in the last bin as -FLT_MAX does); each value then costs
+// its key and two compares per run instead of its bin and the runs' tests.
+__device__ __forceinline__ void deep_collect(const float* x, const uint32_t* pcnt, uint32_t n, bool vec, uint32_t nb,
+                                          float topf, float bsc, uint32_t a0, uint32_t e0, uint32_t a1, uint32_t e1,
+                                          uint32_t a2, uint32_t e2, uint32_t* pick, uint64_t* sk, uint32_t cap,
+                                          uint32_t* kb) {
+  static_assert(kBinRanges == 3, "three runs");
+  const uint32_t tid = threadIdx.x;
+  if (tid < 2 * kBinRanges) {
+    const uint32_t r = tid >> 1, a = sel3(r, a0, a1, a2), e = sel3(r, e0, e1, e2), ktop = total_key(topf);
+    auto bin = [&](uint32_t k) { return deep_bin(topf, bsc, nb, key_value(k)); };
+    uint32_t out;
+    if (a == kNone) {
+      out = (tid & 1u) ? 0u : 0xFFFFFFFFu;  // an empty interval: lo above hi
+    } else if ((tid & 1u) == 0) {
+      // lo: the least key whose bin is at most e (the largest value's bin, 0, is).
+      uint32_t lo = 0, hi = ktop;
+      while (lo < hi) {
+        const uint32_t mid = lo + (hi - lo) / 2;
+        if (bin(mid) <= e) hi = mid;
+        else lo = mid + 1;
+      }
+      out = lo;
+    } else {
+      // hi: the greatest key at or below ktop whose bin is at least a (key 0's, the last bin, is).
+      uint32_t lo = 0, hi = ktop;
+      while (lo < hi) {
+        const uint32_t mid = hi - (hi - lo) / 2;
+        if (bin(mid) >= a) lo = mid;
+        else hi = mid - 1;
+      }
+      out = lo;
+    }
+    kb[tid] = out;
+  }
+  __syncthreads();
+  const uint32_t l0 = kb[0], h0 = kb[1], l1 = kb[2], h1 = kb[3], l2 = kb[4], h2 = kb[5];
+  for_each_value<true, 3>(x, pcnt, n, vec, [&](uint32_t i, float v, uint32_t c) {
+    const uint32_t k = total_key(v);
+    const bool hit = ((k >= l0) & (k <= h0)) | ((k >= l1) & (k <= h1)) | ((k >= l2) & (k <= h2));
+    if (__builtin_expect(hit && c == 0, 0)) {
+      const uint32_t s = atomicAdd(pick, 1u);
+      if (s < cap) sk[s] = pack(k, i);
+    }
+  });
+}
+
 template <bool kDist>
 __device__ __noinline__ bool deep_bins(const FinishArgs& a, const RowParams& p, uint32_t row, bool pen) {
   constexpr uint32_t kNB = kDist ? as_launch::kDistBins : kDeepBins;
@@ -1244,11 +1348,14 @@ __device__ __noinline__ bool deep_bins(const FinishArgs& a, const RowParams& p, 
     hw[b] = 0.0;
   }
   __syncthreads();
+  PassWeights pw;
+  pw.init(top, temp);
   auto count = [&](float v) {
     const uint32_t b = bin_of(v);
+    const double d = pw.d(v);
     atomicAdd(&hc[b], 1u);
-    if (by_top_p) atomicAdd(&hm[b], w1(v));
-    atomicAdd(&hw[b], wt(v));
+    if (by_top_p) atomicAdd(&hm[b], pw.one(d));
+    atomicAdd(&hw[b], pw.at_t(d));
   };
   if (kDist) {
     // The histogram pass shared: the row's histogram in its scratch is cleared, the pass published,
@@ -1278,9 +1385,7 @@ __device__ __noinline__ bool deep_bins(const FinishArgs& a, const RowParams& p, 
     }
     __syncthreads();  // the bins are whole before the history's values add to them
   } else {
-    for_each_value<true>(x, pcnt, n, vec, [&](uint32_t, float v, uint32_t c) {
-      if (__builtin_expect(c == 0, 1)) count(v);
-    });
+    deep_hist(x, pcnt, n, vec, kNB, topf, bsc, top, temp, by_top_p, hc, hm, hw);
   }
   if (pen) {
     // Each history id once, penalised, by the thread that sets its count's top bit first (pass 2
@@ -1324,12 +1429,13 @@ __device__ __noinline__ bool deep_bins(const FinishArgs& a, const RowParams& p, 
     }
   }
   __syncthreads();
-  // Every prefix (and the totals) is within E of the exact sum of its terms: a term goes through one
-  // f64 atomic add and at most kDPer + 2 log2(kThreads) + 2 more adds; the reference's own folds of
-  // the same terms (total1 and the unfiltered total in index order, the cumulatives in rank order,
-  // the kept weight) are within gamma(n) of the same exact sums, and gj covers their ratios.
+  // Every prefix (and the totals) is within E of the exact sum of the reference's terms: each term is
+  // within kPassRel of the reference's and goes through one f64 atomic add and at most
+  // kDPer + 2 log2(kThreads) + 2 more adds; the reference's own folds of its terms (total1 and the
+  // unfiltered total in index order, the cumulatives in rank order, the kept weight) are within
+  // gamma(n) of the same exact sums, and gj covers their ratios.
   const double M_all = hm[kNB - 1], W_all = hw[kNB - 1];
-  const double g_all = gamma_ub(2.0 * (double)n + 128.0);
+  const double g_all = gamma_ub(2.0 * (double)n + 128.0) + kPassRel * (1.0 + 1e-6);
   const double Em = g_all * M_all, Ew = g_all * W_all;
   const double gj = gamma_ub(2.0 * (double)n + 4.0) + 10.0 * kU;
   auto C = [&](uint32_t b) -> uint32_t { return b == kNone ? 0u : hc[b]; };  // through bin b; kNone: none
@@ -1487,12 +1593,8 @@ __device__ __noinline__ bool deep_bins(const FinishArgs& a, const RowParams& p, 
     }
     __syncthreads();
   } else if (fits) {
-    for_each_value<true>(x, pcnt, n, vec, [&](uint32_t i, float v, uint32_t c) {
-      if (__builtin_expect(c == 0, 1) && in_runs(bin_of(v))) {
-        const uint32_t s = atomicAdd(&sh.pick, 1u);
-        if (s < (uint32_t)kCap) sh.sk[s] = pack(total_key(v), i);
-      }
-    });
+    deep_collect(x, pcnt, n, vec, kNB, topf, bsc, r0[0], r1[0], r0[1], r1[1], r0[2], r1[2], &sh.pick, sh.sk,
+                 (uint32_t)kCap, sh.base);
   }
   if (pen) {
     auto hist_two = [&](uint32_t id) {
@@ -2612,7 +2714,12 @@ __device__ __forceinline__ void tail_list_load(const FinishArgs& a, uint32_t wg)
     sh.tl_help[tid] = a.tail_list->help[tid];
     if (tid == 0) {
       sh.tl_me = wg < a.n_rows ? a.params[wg].help : 0u;
-      sh.tl_n = min(a.tail_list->count, as_launch::kTailRows);
+      // More flagged rows than the list holds, and no kept lists asked for: the rows past the list take
+      // their own pass over the row (tail_sums), which sets the batch's time, so nothing is shared
+      // (helping the listed rows would only delay every helper). With kept lists the rows past it
+      // take the deep path, and the listed rows keep their parts.
+      const uint32_t flagged = a.tail_list->count;
+      sh.tl_n = (flagged <= as_launch::kTailRows || a.kept_ids) ? min(flagged, as_launch::kTailRows) : 0u;
       sh.tail_waited = 0;
     }
   }

@@ -25,6 +25,7 @@
 #include <mutex>
 
 #include "sampler_device.h"
+#include "exp_poly.h"
 #include "launch.h"
 #include "../../include/artemis_sampler.h"
 
@@ -63,44 +64,8 @@ __device__ __forceinline__ uint32_t wave_qth_u32(uint32_t x, uint32_t q) {
 
 __device__ __forceinline__ double gamma_n(double n) { return n * kU / (1.0 - n * kU); }
 
-// Relative error of exp_neg against exp, per term: the polynomial's (1.064e-12 at most, at f = -1/2),
-// the rounding of t = d * log2(e) (|t| <= 1022 times 2^-52, times ln 2: 1.6e-13) and of the Horner
-// steps (about 1e-15).
-constexpr double kExpRel = 1.5e-12;
-
-// exp(d) for d <= 0 without a table (a table's gathers from LDS conflict across lanes): e^d = 2^t,
-// t = d log2(e) = k + f with k = rint(t) and |f| <= 1/2 (f = t - k exactly), 2^f by a polynomial of
-// degree 8, 2^k by ldexp (ExpPoly::exp_neg). Within kExpRel of exp(d); the parallel sum it feeds is
-// bounded at gamma(n) ~ 2.8e-11 relative, so a few ulps more per term change little. Below d = -708
-// the argument is clamped (such a term is under 2^-1021 of the row's largest, which is 1).
-//
-// The coefficients of 2^f, highest degree first: the Chebyshev interpolant of 2^f on [-1/2, 1/2] at
-// degree 8 (mpmath.chebyfit at 40 digits), rounded to f64; with the rounded coefficients its relative
-// error peaks at 1.064e-12, at f = -1/2. Read from constant memory once per thread, they stay in
-// scalar registers, which each fused multiply-add takes as an operand (as immediates, each step would
-// first rebuild its coefficient in two vector moves).
-constexpr int kPolyLen = 9;
-__constant__ double kExp2Poly[kPolyLen] = {
-    1.3255224878668817e-06, 1.5310079402249296e-05, 0.00015403455852453838, 0.0013333450568000645,
-    0.009618129159402558,   0.05550410941205933,    0.2402265069581299,     0.6931471805459335,
-    1.0};
-
-struct ExpPoly {
-  double c[kPolyLen];
-  __device__ __forceinline__ void load() {
-#pragma unroll
-    for (int i = 0; i < kPolyLen; ++i) c[i] = kExp2Poly[i];
-  }
-  __device__ __forceinline__ double exp_neg(double d) const {
-    const double t = fmax(d, -708.0) * 1.4426950408889634;
-    const double k = __builtin_rint(t);
-    const double f = t - k;
-    double p = c[0];
-#pragma unroll
-    for (int i = 1; i < kPolyLen; ++i) p = __builtin_fma(p, f, c[i]);
-    return __builtin_amdgcn_ldexp(p, (int32_t)k);
-  }
-};
+// Each term's relative error against the reference's exp (ExpPoly::exp_neg, exp_poly.h).
+constexpr double kExpRel = kExpPolyRel;
 
 // The value part of lp_key.
 __device__ __forceinline__ uint32_t lp_vkey(float x) { return total_key(x == 0.0f ? 0.0f : x); }

@@ -5,8 +5,19 @@
 #include <stdint.h>
 
 #include "exp_f64.h"
+#include "exp_poly.h"
 
 namespace as_dev {
+
+// A load through a pointer to global memory. A pointer the compiler cannot place in an address space
+// (one read from memory, as the finish kernel's arguments are) takes flat instructions, which count
+// against the LDS wait counter as well: every wait for an LDS access then also waits for the loads
+// in flight, and a loop that mixes the two streams its row one step at a time. Reading through a
+// global-address-space view takes global instructions instead.
+template <class T>
+__device__ __forceinline__ T gload(const T* p) {
+  return *(const __attribute__((address_space(1))) T*)p;
+}
 
 constexpr int kWave = 64;
 constexpr uint32_t kNone = 0xFFFFFFFFu;

@@ -303,6 +303,31 @@ def test_tail_histogram_draws_match_the_oracle(ctx):
         assert deep[()] <= 3, deep
 
 
+def test_more_flagged_rows_than_the_list_holds(ctx):
+    # 32 rows that the scan flags for S's sums (config 5's row 111 under many seeds), no kept lists:
+    # more than the 16 the list holds, so nothing is shared. Each row draws from its sorted values
+    # when they settle the draw, else sums S in its own pass over the row (some rows under these
+    # seeds do). Tokens and streams must be the oracle's, and no row may need the deep path.
+    from artemis_amd import AS_ROW_DEEP_PATH, AS_ROW_TAIL_PASS, workloads
+    w = workloads.config5()
+    r = 111
+    base = w.params[r]
+    row = np.ascontiguousarray(w.logits[r])
+    hist = w.histories[r]
+    params = [dict(temp=base.temp, top_k=0, top_p=base.top_p, min_p=base.min_p, presence=base.presence,
+                   frequency=base.frequency, repetition=base.repetition) for _ in range(32)]
+    seeds = [31000 + s for s in range(32)]
+    g = gpu_batch(ctx, row, params, seeds, [hist] * 32)
+    off, ids = csr([hist] * 32, 32)
+    want, rng = O.sample_rows(params, seeds, row, off, ids, threads=8, shared=True)
+    bad = np.nonzero(g["tokens"] != want)[0]
+    assert len(bad) == 0, [(int(i), int(g["tokens"][i]), int(want[i]), int(g["status"][i])) for i in bad[:5]]
+    assert (g["rng"] == rng).all()
+    if ctx.test_path == "sliced":
+        st = g["status"]
+        assert ((st & AS_ROW_TAIL_PASS) != 0).any() and not ((st & AS_ROW_DEEP_PATH) != 0).any(), st
+
+
 def test_large_floor_sets_match_the_oracle(ctx):
     # min-p rows whose floor set holds thousands of values (config 5's rows 254 and 151: 4,302 and
     # 3,365 values above the floor, top-p far deeper): the scan keeps a few thousand candidates and

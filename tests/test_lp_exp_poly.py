@@ -1,9 +1,10 @@
-"""The log-probability kernel's exp (artemis_amd/csrc/logprobs.hip, ExpPoly::exp_neg) takes 2^f for
-|f| <= 1/2 from a degree-8 polynomial whose coefficients are written in that source. Its documented
-per-term bound kExpRel (1.5e-12 relative, which include/artemis_sampler.h's e carries) rests on the
-polynomial's own relative error, 1.064e-12 at most: this checks that error, evaluated exactly (mpmath)
-with the coefficients as the source holds them, over a grid of the interval and at its ends. A wrong
-or mistyped coefficient shows up as an error many times larger."""
+"""The bounded exp (artemis_amd/csrc/exp_poly.h, ExpPoly::exp_neg) that the log-probability kernel and
+the finish kernel's histogram passes use takes 2^f for |f| <= 1/2 from a degree-8 polynomial whose
+coefficients are written in that source. Its documented per-term bound kExpPolyRel (1.5e-12 relative,
+which include/artemis_sampler.h's logprob bound e carries) rests on the polynomial's own relative
+error, 1.064e-12 at most: this checks that error, evaluated exactly (mpmath) with the coefficients as
+the source holds them, over a grid of the interval and at its ends. A wrong or mistyped coefficient
+shows up as an error many times larger."""
 import os
 import re
 
@@ -11,7 +12,7 @@ import pytest
 
 mp = pytest.importorskip("mpmath")
 
-SRC = os.path.join(os.path.dirname(__file__), "..", "artemis_amd", "csrc", "logprobs.hip")
+SRC = os.path.join(os.path.dirname(__file__), "..", "artemis_amd", "csrc", "exp_poly.h")
 
 
 def coefficients():
@@ -33,5 +34,5 @@ def test_the_polynomial_of_2_to_the_f_is_within_its_documented_error():
         worst = max(worst, abs(p / mp.power(2, t) - 1))
     assert worst < 1.07e-12, float(worst)
     # The kernel's kExpRel adds the rounding of t = d log2(e) and of the Horner steps.
-    kexprel = float(re.search(r"constexpr double kExpRel = ([0-9.e-]+);", open(SRC).read()).group(1))
+    kexprel = float(re.search(r"constexpr double kExpPolyRel = ([0-9.e-]+);", open(SRC).read()).group(1))
     assert worst + 1.6e-13 + 1e-15 <= kexprel
