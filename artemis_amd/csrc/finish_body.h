@@ -63,19 +63,26 @@ __device__ __forceinline__ Shared& shm() { return g_sh_static; }
 
 // --- block helpers ------------------------------------------------------------------------------
 
+// A pointer to global memory as such (gload explains why: flat instructions would share the LDS wait
+// counter). Every atomic and device-coherent access of the kernel's HBM goes through one.
+template <class T>
+__device__ __forceinline__ __attribute__((address_space(1))) T* gp(T* p) {
+  return (__attribute__((address_space(1))) T*)p;
+}
+
 // Device-coherent loads and stores (relaxed, agent scope): what other workgroups of the kernel write
 // with device atomics or such stores, whatever this XCD's L2 holds.
 __device__ __forceinline__ uint32_t ld_agent(const uint32_t* p) {
-  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  return __hip_atomic_load(gp(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 __device__ __forceinline__ uint64_t ld_agent(const uint64_t* p) {
-  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  return __hip_atomic_load(gp(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 __device__ __forceinline__ double ld_agent(const double* p) {
-  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  return __hip_atomic_load(gp(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 __device__ __forceinline__ void st_agent(uint64_t* p, uint64_t v) {
-  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  __hip_atomic_store(gp(p), v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 
@@ -357,11 +364,11 @@ __device__ __noinline__ void exact_row(const FinishArgs& a, const RowParams& p, 
     for (uint32_t i = tid; i < n; i += kThreads) cnt[i] = 0;
     __syncthreads();
     for (uint32_t h = hb + tid; h < he; h += kThreads) {
-      const uint32_t id = a.hist_ids[h];
+      const uint32_t id = gload(a.hist_ids + h);
       if (id < n) atomicAdd(&cnt[id], 1u);
     }
     for (uint32_t h = tid; h < extra; h += kThreads) {
-      const uint32_t id = a.extra_ids[h];
+      const uint32_t id = gload(a.extra_ids + h);
       if (id < n) atomicAdd(&cnt[id], 1u);
     }
     __syncthreads();
@@ -1080,8 +1087,8 @@ __device__ __noinline__ void deep_part(const FinishArgs& a, uint32_t row, uint32
       const uint32_t off = id - b0;
       if (off < len) atomicOr(&bm[off >> 5], 1u << (off & 31u));
     };
-    for (uint32_t h = hb + tid; h < he; h += kThreads) mark(a.hist_ids[h]);
-    for (uint32_t h = tid; h < extra; h += kThreads) mark(a.extra_ids[h]);
+    for (uint32_t h = hb + tid; h < he; h += kThreads) mark(gload(a.hist_ids + h));
+    for (uint32_t h = tid; h < extra; h += kThreads) mark(gload(a.extra_ids + h));
     __syncthreads();
   }
   const uint32_t mk = sh.dp_mk;
@@ -1118,9 +1125,9 @@ __device__ __noinline__ void deep_part(const FinishArgs& a, uint32_t row, uint32
     double* gw = gm + kNB;
     for (uint32_t b = tid; b < kNB; b += kThreads) {
       if (hc[b] == 0u) continue;
-      __hip_atomic_fetch_add(sh_g + b, hc[b], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      if (by_top_p) __hip_atomic_fetch_add(gm + b, hm[b], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      __hip_atomic_fetch_add(gw + b, hw[b], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      __hip_atomic_fetch_add(gp(sh_g + b), hc[b], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      if (by_top_p) __hip_atomic_fetch_add(gp(gm + b), hm[b], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      __hip_atomic_fetch_add(gp(gw + b), hw[b], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
   } else {
     // The part's values in the runs, staged in sh.sk with one LDS atomic per wave, then listed.
@@ -1143,7 +1150,7 @@ __device__ __noinline__ void deep_part(const FinishArgs& a, uint32_t row, uint32
     }
     __syncthreads();
     const uint32_t staged = sh.dp_staged;
-    if (tid == 0) sh.dp_base = __hip_atomic_fetch_add(sh_g + 5 * kNB, staged, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (tid == 0) sh.dp_base = __hip_atomic_fetch_add(gp(sh_g + 5 * kNB), staged, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     __syncthreads();
     const uint32_t base = sh.dp_base;
     uint64_t* list = reinterpret_cast<uint64_t*>(sh_g + 5 * kNB + 2);
@@ -1153,7 +1160,7 @@ __device__ __noinline__ void deep_part(const FinishArgs& a, uint32_t row, uint32
   // Every write above has completed (in every thread) before the part counts itself ended.
   __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");
   __syncthreads();
-  if (tid == 0) __hip_atomic_fetch_add(&jb.ended[pass], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  if (tid == 0) __hip_atomic_fetch_add(gp(&jb.ended[pass]), 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // The row's own workgroup: publishes pass `pass` (the fields it needs were stored before, in every
@@ -1166,11 +1173,11 @@ __device__ bool deep_run(const FinishArgs& a, uint32_t row, uint32_t pass) {
   const uint32_t parts = as_launch::tail_parts(a.n);
   __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");
   __syncthreads();
-  if (threadIdx.x == 0) __hip_atomic_store(&jb.stamp, 2 * a.call + pass, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  if (threadIdx.x == 0) __hip_atomic_store(gp(&jb.stamp), 2 * a.call + pass, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   for (;;) {
     if (threadIdx.x == 0)
       sh.dp_q = ld_agent(&jb.next[pass]) < parts
-                    ? __hip_atomic_fetch_add(&jb.next[pass], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
+                    ? __hip_atomic_fetch_add(gp(&jb.next[pass]), 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
                     : parts;
     __syncthreads();
     const uint32_t q = sh.dp_q;
@@ -1213,7 +1220,7 @@ __device__ __attribute__((unused)) void deep_help(const FinishArgs& a, uint32_t 
     const uint32_t pick = sh.dp_pick, stop = sh.dp_stop;
     if (pick != kNone) {
       const uint32_t r = ((pick >> 1) + wg % nr) % nr, pass = pick & 1u;
-      if (tid == 0) sh.dp_q = __hip_atomic_fetch_add(&a.deep_jobs[r].next[pass], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      if (tid == 0) sh.dp_q = __hip_atomic_fetch_add(gp(&a.deep_jobs[r].next[pass]), 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       __syncthreads();
       const uint32_t q = sh.dp_q;
       if (q < parts) deep_part(a, r, q, pass);
@@ -1366,15 +1373,15 @@ __device__ __noinline__ bool deep_bins(const FinishArgs& a, const RowParams& p, 
     double* gw = gm + kNB;
     DeepJob& jb = a.deep_jobs[row];
     for (uint32_t b = tid; b < kNB; b += kThreads) {
-      __hip_atomic_store(gc + b, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      __hip_atomic_store(gm + b, 0.0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      __hip_atomic_store(gw + b, 0.0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      __hip_atomic_store(gp(gc + b), 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      __hip_atomic_store(gp(gm + b), 0.0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      __hip_atomic_store(gp(gw + b), 0.0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
     if (tid == 0) {
-      __hip_atomic_store(&jb.mk, mk, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      __hip_atomic_store(gp(&jb.mk), mk, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       for (int k = 0; k < 2; ++k) {
-        __hip_atomic_store(&jb.next[k], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        __hip_atomic_store(&jb.ended[k], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_store(gp(&jb.next[k]), 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_store(gp(&jb.ended[k]), 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       }
     }
     if (!deep_run(a, row, 0)) return false;
@@ -1395,8 +1402,8 @@ __device__ __noinline__ bool deep_bins(const FinishArgs& a, const RowParams& p, 
       const uint32_t old = atomicOr(&cnt[id], 0x80000000u);
       if (!(old & 0x80000000u)) count(penalize(x[id], old, p));
     };
-    for (uint32_t h = hb + tid; h < he; h += kThreads) hist_one(a.hist_ids[h]);
-    for (uint32_t h = tid; h < extra; h += kThreads) hist_one(a.extra_ids[h]);
+    for (uint32_t h = hb + tid; h < he; h += kThreads) hist_one(gload(a.hist_ids + h));
+    for (uint32_t h = tid; h < extra; h += kThreads) hist_one(gload(a.extra_ids + h));
   }
   __syncthreads();
 
@@ -1576,10 +1583,10 @@ __device__ __noinline__ bool deep_bins(const FinishArgs& a, const RowParams& p, 
     if (tid == 0) {
 #pragma unroll
       for (uint32_t k = 0; k < kBinRanges; ++k) {
-        __hip_atomic_store(&jb.r0[k], sel3(k, r0[0], r0[1], r0[2]), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        __hip_atomic_store(&jb.r1[k], sel3(k, r1[0], r1[1], r1[2]), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_store(gp(&jb.r0[k]), sel3(k, r0[0], r0[1], r0[2]), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_store(gp(&jb.r1[k]), sel3(k, r1[0], r1[1], r1[2]), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       }
-      __hip_atomic_store(lc, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      __hip_atomic_store(gp(lc), 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
     if (!deep_run(a, row, 1)) return false;
     if (tid == 0) sh.nsk = ld_agent(lc);
@@ -1607,8 +1614,8 @@ __device__ __noinline__ bool deep_bins(const FinishArgs& a, const RowParams& p, 
         if (s < (uint32_t)kCap) sh.sk[s] = pack(total_key(v), id);
       }
     };
-    for (uint32_t h = hb + tid; h < he; h += kThreads) hist_two(a.hist_ids[h]);
-    for (uint32_t h = tid; h < extra; h += kThreads) hist_two(a.extra_ids[h]);
+    for (uint32_t h = hb + tid; h < he; h += kThreads) hist_two(gload(a.hist_ids + h));
+    for (uint32_t h = tid; h < extra; h += kThreads) hist_two(gload(a.extra_ids + h));
   }
   __syncthreads();
   if (!fits || sh.pick != collected || collected == 0) return false;
@@ -1761,11 +1768,11 @@ __device__ __noinline__ bool deep_prep(const FinishArgs& a, const RowParams& p, 
     for (uint32_t i = tid; i < n; i += kThreads) cnt[i] = 0;
     __syncthreads();
     for (uint32_t h = hb + tid; h < he; h += kThreads) {
-      const uint32_t id = a.hist_ids[h];
+      const uint32_t id = gload(a.hist_ids + h);
       if (id < n) atomicAdd(&cnt[id], 1u);
     }
     for (uint32_t h = tid; h < extra; h += kThreads) {
-      const uint32_t id = a.extra_ids[h];
+      const uint32_t id = gload(a.extra_ids + h);
       if (id < n) atomicAdd(&cnt[id], 1u);
     }
     __syncthreads();
@@ -1888,8 +1895,8 @@ __device__ __noinline__ bool deep_row(const FinishArgs& a, const RowParams& p, u
       const uint32_t old = atomicOr(&cnt[id], 0x80000000u);
       if (!(old & 0x80000000u)) count(penalize(x[id], old, p));
     };
-    for (uint32_t h = hb + tid; h < he; h += kThreads) hist_one(a.hist_ids[h]);
-    for (uint32_t h = tid; h < extra; h += kThreads) hist_one(a.extra_ids[h]);
+    for (uint32_t h = hb + tid; h < he; h += kThreads) hist_one(gload(a.hist_ids + h));
+    for (uint32_t h = tid; h < extra; h += kThreads) hist_one(gload(a.extra_ids + h));
   }
   __syncthreads();
   {
@@ -1991,8 +1998,8 @@ __device__ __noinline__ bool deep_row(const FinishArgs& a, const RowParams& p, u
         const float v = penalize(x[id], old & 0x7fffffffu, p);
         if (bin_of(v) <= bc) bufA[atomicAdd(&sh.pick, 1u)] = pack(total_key(v), id);
       };
-      for (uint32_t h = hb + tid; h < he; h += kThreads) hist_two(a.hist_ids[h]);
-      for (uint32_t h = tid; h < extra; h += kThreads) hist_two(a.extra_ids[h]);
+      for (uint32_t h = hb + tid; h < he; h += kThreads) hist_two(gload(a.hist_ids + h));
+      for (uint32_t h = tid; h < extra; h += kThreads) hist_two(gload(a.extra_ids + h));
     }
   }
   __syncthreads();
@@ -2087,8 +2094,8 @@ __device__ __noinline__ bool deep_row(const FinishArgs& a, const RowParams& p, u
         if (unfiltered) d = __ddiv_rn(d, temp);
         acc = __dadd_rn(acc, as_exp::exp_with(t, d));
       };
-      for (uint32_t h = hb + tid; h < he; h += kThreads) hist_three(a.hist_ids[h]);
-      for (uint32_t h = tid; h < extra; h += kThreads) hist_three(a.extra_ids[h]);
+      for (uint32_t h = hb + tid; h < he; h += kThreads) hist_three(gload(a.hist_ids + h));
+      for (uint32_t h = tid; h < extra; h += kThreads) hist_three(gload(a.extra_ids + h));
     }
     X = block_sum_f64<kWaves>(acc, sh.red_d);
     eps = kU * 1.02 * ((double)n + (double)(n / kThreads) + 32.0) * X;
@@ -2228,8 +2235,8 @@ __device__ __noinline__ bool tail_sums(const FinishArgs& a, const RowParams& p, 
       }
       sh.tail_over = 1;
     };
-    for (uint32_t h = hb + tid; h < he; h += kThreads) mark(a.hist_ids[h]);
-    for (uint32_t h = tid; h < extra; h += kThreads) mark(a.extra_ids[h]);
+    for (uint32_t h = hb + tid; h < he; h += kThreads) mark(gload(a.hist_ids + h));
+    for (uint32_t h = tid; h < extra; h += kThreads) mark(gload(a.extra_ids + h));
     __syncthreads();
     if (sh.tail_over) return false;
   }
@@ -2502,20 +2509,20 @@ __device__ __noinline__ bool tail_item(const FinishArgs& a, uint32_t row, uint32
   typedef float f32x4 __attribute__((ext_vector_type(4)));
   uint64_t old = 0;
   if (claim && tid == 0)
-    old = __hip_atomic_fetch_max(claim, a.call, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    old = __hip_atomic_fetch_max(gp(claim), a.call, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   // Value k of this thread is at offset at(k) of the part.
   auto at = [&](uint32_t k) { return vec ? ((k / 4) * kThreads + tid) * 4 + (k % 4) : k * kThreads + tid; };
   float v[kPer];
   if (vec) {
 #pragma unroll
     for (uint32_t j = 0; j < kPer / 4; ++j) {
-      const f32x4 q = *reinterpret_cast<const f32x4*>(x + b0 + (j * kThreads + tid) * 4);
+      const f32x4 q = gload(reinterpret_cast<const f32x4*>(x + b0 + (j * kThreads + tid) * 4));
 #pragma unroll
       for (int c = 0; c < 4; ++c) v[4 * j + c] = q[c];
     }
   } else {
 #pragma unroll
-    for (uint32_t k = 0; k < kPer; ++k) v[k] = at(k) < len ? x[b0 + at(k)] : 0.0f;
+    for (uint32_t k = 0; k < kPer; ++k) v[k] = at(k) < len ? gload(x + b0 + at(k)) : 0.0f;
   }
   const RowParams& p = a.params[row];
   uint32_t hb;
@@ -2526,7 +2533,7 @@ __device__ __noinline__ bool tail_item(const FinishArgs& a, uint32_t row, uint32
   uint32_t top = 0, bad = 0;
   uint64_t bound = 0;
   for (uint32_t s = tid; s < a.n_seg; s += kThreads) {
-    const SegStats& g = a.stats[(uint64_t)row * a.n_seg + s];
+    const SegStats g = gload(a.stats + (uint64_t)row * a.n_seg + s);
     top = max(top, g.max_key);
     if (g.truncated & 1u) bound = max(bound, g.bound);
     if ((g.truncated & 2u) || g.nonfinite != kNone) bad = 1;
@@ -2575,8 +2582,8 @@ __device__ __noinline__ bool tail_item(const FinishArgs& a, uint32_t row, uint32
       }
       t.overflow = 1;
     };
-    for (uint32_t h = hb + tid; h < he; h += kThreads) mark(a.hist_ids[h]);
-    for (uint32_t h = tid; h < extra; h += kThreads) mark(a.extra_ids[h]);
+    for (uint32_t h = hb + tid; h < he; h += kThreads) mark(gload(a.hist_ids + h));
+    for (uint32_t h = tid; h < extra; h += kThreads) mark(gload(a.extra_ids + h));
   }
   if (tid == 0) t.skip = (claim && old >= a.call) ? 1u : 0u;
   __syncthreads();
@@ -2623,8 +2630,8 @@ __device__ __noinline__ bool tail_item(const FinishArgs& a, uint32_t row, uint32
     // The part's place in the row's list, reserved now and read once the terms are in.
     uint32_t base = 0;
     if (tid == 0) {
-      base = __hip_atomic_fetch_add(&rt.count, cnt, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      if (cnt > kTailStage) __hip_atomic_fetch_or(&rt.lost, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      base = __hip_atomic_fetch_add(gp(&rt.count), cnt, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      if (cnt > kTailStage) __hip_atomic_fetch_or(gp(&rt.lost), 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
     const float s1 = 1.44269502f, sw = (1.0f / p.temp) * s1;
     // The histogram's scale: (rv - v) * bscale is monotone in v, so bins follow the rank order.
@@ -2678,15 +2685,15 @@ __device__ __noinline__ bool tail_item(const FinishArgs& a, uint32_t row, uint32
         sw_ = __dadd_rn(sw_, t.red_w[k]);
         sm_ = __dadd_rn(sm_, t.red_m[k]);
       }
-      __hip_atomic_fetch_add(&rt.w, sw_, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      __hip_atomic_fetch_add(&rt.m, sm_, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      __hip_atomic_fetch_add(&rt.parts, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      __hip_atomic_fetch_add(gp(&rt.w), sw_, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      __hip_atomic_fetch_add(gp(&rt.m), sm_, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      __hip_atomic_fetch_add(gp(&rt.parts), 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
     // The part's bins into the row's.
     as_dev::TailBins& tb = a.tail_bins[row];
     for (uint32_t b = tid; b < kTailBins; b += kThreads) {
-      if (t.bin_w[b] != 0.0) __hip_atomic_fetch_add(&tb.w[b], t.bin_w[b], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      if (t.bin_m[b] != 0.0) __hip_atomic_fetch_add(&tb.m[b], t.bin_m[b], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      if (t.bin_w[b] != 0.0) __hip_atomic_fetch_add(gp(&tb.w[b]), t.bin_w[b], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      if (t.bin_m[b] != 0.0) __hip_atomic_fetch_add(gp(&tb.m[b]), t.bin_m[b], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
     // The staged values to scratch, at the part's place in the row's list, when the list can hold
     // them.
@@ -2695,12 +2702,12 @@ __device__ __noinline__ bool tail_item(const FinishArgs& a, uint32_t row, uint32
     if (at0 + staged <= kTailKeep)
       for (uint32_t i = tid; i < staged; i += kThreads) st_agent(list + at0 + i, t.stage[i]);
   } else if (defined && tid == 0) {
-    __hip_atomic_fetch_or(&rt.failed, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __hip_atomic_fetch_or(gp(&rt.failed), 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
   // Every write above has completed (in every thread) before the item counts itself ended.
   __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");
   __syncthreads();
-  if (tid == 0) __hip_atomic_fetch_add(&rt.ended, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  if (tid == 0) __hip_atomic_fetch_add(gp(&rt.ended), 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   return true;
 }
 
@@ -2770,7 +2777,7 @@ __device__ __noinline__ void tail_wait(const FinishArgs& a, uint32_t row) {
       __syncthreads();
       const uint32_t q = q0 + tid, h = (slot * parts + q) % helpers;
       if (q < parts &&
-          __hip_atomic_fetch_max(a.tail_claims + h, a.call, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < a.call)
+          __hip_atomic_fetch_max(gp(a.tail_claims + h), a.call, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < a.call)
         sh.bcnt[atomicAdd(&sh.tail_won, 1u)] = h;
       __syncthreads();
       const uint32_t won = sh.tail_won;
@@ -2819,7 +2826,7 @@ __device__ __noinline__ __attribute__((unused)) void tail_end(const FinishArgs& 
 __device__ __forceinline__ void finish_row(const FinishArgs& a, uint32_t row) {
   Shared& sh = shm();
   const uint32_t tid = threadIdx.x;
-  const RowParams p = a.params[row];
+  const RowParams p = gload(a.params + row);
   const SegStats* gst = a.stats + (uint64_t)row * a.n_seg;
   const uint32_t n = a.n;
   if (tid < 256) sh.tab[tid] = as_exp::kTable[tid];
@@ -2840,7 +2847,7 @@ __device__ __forceinline__ void finish_row(const FinishArgs& a, uint32_t row) {
   // (thread 0 keeps them in registers for the merge below).
   // The slices' statistics first (they need nothing loaded), then what needs the row's parameters,
   // so that waiting for the statistics does not wait for the RNG state too.
-  for (uint32_t s = tid; s < a.n_seg; s += kThreads) sh.seg[s] = gst[s];
+  for (uint32_t s = tid; s < a.n_seg; s += kThreads) sh.seg[s] = gload(gst + s);
   const bool draws = p.mode != kModeGreedy;
   uint64_t s4[4] = {0ull, 0ull, 0ull, 0ull};
   uint64_t* src = a.rng_state + 4ull * p.rng_index;
@@ -2848,9 +2855,9 @@ __device__ __forceinline__ void finish_row(const FinishArgs& a, uint32_t row) {
   if (tid == 0) {
     // A row drawing from its own state (a.rng_rows) loads it beside its parameters rather than after.
     if (a.rng_rows) {
-      for (int k = 0; k < 4; ++k) s4[k] = a.rng_state[4ull * row + k];
+      for (int k = 0; k < 4; ++k) s4[k] = gload(a.rng_state + 4ull * row + k);
     } else if (draws) {
-      for (int k = 0; k < 4; ++k) s4[k] = src[k];
+      for (int k = 0; k < 4; ++k) s4[k] = gload(src + k);
     }
     he = as_launch::history_bounds(a, p, row, &hb);
   }
@@ -2998,7 +3005,7 @@ __device__ __forceinline__ void finish_row(const FinishArgs& a, uint32_t row) {
               if (sh.seg_off[mid] <= g) lo = mid;
               else hi = mid;
             }
-            tmp[q] = src[(uint64_t)lo * a.cand_stride + (g - sh.seg_off[lo])];
+            tmp[q] = gload(src + (uint64_t)lo * a.cand_stride + (g - sh.seg_off[lo]));
           }
         }
 #pragma unroll

@@ -16,7 +16,20 @@ namespace as_dev {
 // global-address-space view takes global instructions instead.
 template <class T>
 __device__ __forceinline__ T gload(const T* p) {
-  return *(const __attribute__((address_space(1))) T*)p;
+  if constexpr (__is_scalar(T) || __is_same(T, float __attribute__((ext_vector_type(4)))) ||
+                __is_same(T, uint32_t __attribute__((ext_vector_type(4))))) {
+    return *(const __attribute__((address_space(1))) T*)p;
+  } else {
+    // A structure, word by word (a global-address-space object has no copy constructor to bind).
+    static_assert(sizeof(T) % 4 == 0, "whole words");
+    struct Words {
+      uint32_t w[sizeof(T) / 4];
+    } r;
+    const __attribute__((address_space(1))) uint32_t* q = (const __attribute__((address_space(1))) uint32_t*)p;
+#pragma unroll
+    for (uint32_t i = 0; i < sizeof(T) / 4; ++i) r.w[i] = q[i];
+    return __builtin_bit_cast(T, r);
+  }
 }
 
 constexpr int kWave = 64;
