@@ -1619,7 +1619,13 @@ __device__ __noinline__ bool deep_bins(const FinishArgs& a, const RowParams& p, 
   }
   __syncthreads();
   if (!fits || sh.pick != collected || collected == 0) return false;
-  const uint32_t P = sort_candidates(sh, collected, 0ull, mk, kNone);
+  // The bucket sort spreads keys below its kmax over its buckets: the collected values' own largest
+  // key, since they lie in a few bins far below the row's largest (with that one most would share a
+  // few buckets).
+  uint32_t ck = 0;
+  for (uint32_t i = tid; i < collected; i += kThreads) ck = max(ck, (uint32_t)(sh.sk[i] >> 32));
+  ck = block_max_u32<kWaves>(ck, sh.red_u);
+  const uint32_t P = sort_candidates(sh, collected, 0ull, ck, kNone);
   if (P != collected) return false;
   auto val = [&](uint32_t i) -> float { return packed_value(sh.sk[i]); };
   auto run_of = [&](uint32_t i) -> uint32_t { return (i >= first[2]) ? 2u : (i >= first[1] ? 1u : 0u); };
