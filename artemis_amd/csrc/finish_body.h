@@ -51,6 +51,7 @@ struct Shared {
   uint32_t tl_n, tl_rows[kTailListMax], tl_help[kTailListMax], tl_me, tail_slot, tail_waited, tail_won;
   // The shared deep passes (deep_run, deep_help, deep_part).
   uint32_t dp_pick, dp_stop, dp_q, dp_base, dp_staged, dp_mk, dp_r[2 * 3];
+  uint32_t dp_pub;  // this row published its histogram pass early (deep_publish_hist)
 };
 // The workgroup's LDS, at file scope so that the out-of-line paths below address it as LDS: a static
 // array, or the kernel's dynamic LDS (AS_DYNAMIC_LDS) when another body shares it.
@@ -1167,6 +1168,33 @@ __device__ __noinline__ void deep_part(const FinishArgs& a, uint32_t row, uint32
 // thread), takes its parts until none is left, then waits for the parts other workgroups took.
 // False if that wait ran past its guard (it cannot when every running workgroup makes progress).
 constexpr uint32_t kDeepSpin = 1u << 24;
+// The shared histogram pass published: the row's histogram in its scratch cleared and the job's
+// fields set (its largest key, its counters), then its stamp, once they have completed. Workgroups
+// with no row left take its parts from then on.
+__device__ __noinline__ void deep_publish_hist(const FinishArgs& a, uint32_t row, uint32_t mk) {
+  constexpr uint32_t kNB = as_launch::kDistBins;
+  const uint32_t tid = threadIdx.x;
+  uint32_t* gc = deep_shared(a, row);
+  double* gm = reinterpret_cast<double*>(gc + kNB);
+  double* gw = gm + kNB;
+  DeepJob& jb = a.deep_jobs[row];
+  for (uint32_t b = tid; b < kNB; b += kThreads) {
+    __hip_atomic_store(gp(gc + b), 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __hip_atomic_store(gp(gm + b), 0.0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __hip_atomic_store(gp(gw + b), 0.0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+  if (tid == 0) {
+    __hip_atomic_store(gp(&jb.mk), mk, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    for (int k = 0; k < 2; ++k) {
+      __hip_atomic_store(gp(&jb.next[k]), 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      __hip_atomic_store(gp(&jb.ended[k]), 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+  }
+  __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  __syncthreads();
+  if (tid == 0) __hip_atomic_store(gp(&jb.stamp), 2 * a.call, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
 __device__ bool deep_run(const FinishArgs& a, uint32_t row, uint32_t pass) {
   Shared& sh = shm();
   DeepJob& jb = a.deep_jobs[row];
@@ -1371,19 +1399,7 @@ __device__ __noinline__ bool deep_bins(const FinishArgs& a, const RowParams& p, 
     uint32_t* gc = deep_shared(a, row);
     double* gm = reinterpret_cast<double*>(gc + kNB);
     double* gw = gm + kNB;
-    DeepJob& jb = a.deep_jobs[row];
-    for (uint32_t b = tid; b < kNB; b += kThreads) {
-      __hip_atomic_store(gp(gc + b), 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      __hip_atomic_store(gp(gm + b), 0.0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      __hip_atomic_store(gp(gw + b), 0.0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    }
-    if (tid == 0) {
-      __hip_atomic_store(gp(&jb.mk), mk, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      for (int k = 0; k < 2; ++k) {
-        __hip_atomic_store(gp(&jb.next[k]), 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        __hip_atomic_store(gp(&jb.ended[k]), 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      }
-    }
+    if (!sh.dp_pub) deep_publish_hist(a, row, mk);  // unless the row published it before its candidates
     if (!deep_run(a, row, 0)) return false;
     for (uint32_t b = tid; b < kNB; b += kThreads) {
       hc[b] = ld_agent(gc + b);
@@ -2848,6 +2864,7 @@ __device__ __forceinline__ void finish_row(const FinishArgs& a, uint32_t row) {
     sh.tail_count = 0;
     sh.tail_listed = 0;
     sh.tail_parts = 0;
+    sh.dp_pub = 0;
   }
   // The slices' results, all loads in flight at once, with the row's RNG state and history bounds
   // (thread 0 keeps them in registers for the merge below).
@@ -2967,6 +2984,14 @@ __device__ __forceinline__ void finish_row(const FinishArgs& a, uint32_t row) {
       }
     }
     return;
+  }
+  // A small batch's row without a top-k (and not flagged for S's sums) may have to draw past its
+  // candidates: it publishes its deep histogram pass now, so that the workgroups with no row left
+  // sum it while this one sorts and tries its candidates (when they settle the row, the pass goes
+  // unused).
+  if (a.deep_help && !a.fused && !a.kept_ids && p.mode == kModePartial && !sh.stats_bad && sh.tail_slot == kNone) {
+    deep_publish_hist(a, row, sh.mk);
+    if (tid == 0) sh.dp_pub = 1;  // read after later barriers
   }
 
   if ((p.mode == kModeTopK || p.mode == kModePartial) && !sh.exact) {
