@@ -39,6 +39,17 @@ struct ExpPoly {
     for (int i = 1; i < kPolyLen; ++i) p = __builtin_fma(p, f, c[i]);
     return __builtin_amdgcn_ldexp(p, (int32_t)k);
   }
+  // exp(d) for finite d <= 0 without the clamp: below d = -708 the result is 2^f 2^k rounded to a
+  // subnormal or 0 (k saturates at the least int), under 2^-1021 like exp(d) itself.
+  __device__ __forceinline__ double exp_le0(double d) const {
+    const double t = d * 1.4426950408889634;
+    const double k = __builtin_rint(t);
+    const double f = t - k;
+    double p = c[0];
+#pragma unroll
+    for (int i = 1; i < kPolyLen; ++i) p = __builtin_fma(p, f, c[i]);
+    return __builtin_amdgcn_ldexp(p, (int32_t)k);
+  }
 };
 
 }  // namespace as_dev

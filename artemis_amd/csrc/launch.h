@@ -159,7 +159,7 @@ hipError_t sample_rows(hipStream_t stream, bool vec, const float* logits, const 
 size_t row_kernel_lds();
 
 // Log-probabilities (logprobs.hip): rows in parts of kLpPart values, each part's 20 best and sums.
-constexpr uint32_t kLpPart = 8192;
+constexpr uint32_t kLpPart = 16384;
 constexpr uint32_t kLpTop = 20;     // logprobs.rs:7, MAX_TOP
 constexpr uint32_t kLpMerge = 2048; // the parts' lists a row merges: lp_parts(n) * kLpTop at most
 __host__ __device__ constexpr uint32_t lp_parts(uint32_t n) { return (n + kLpPart - 1) / kLpPart; }

@@ -6,10 +6,11 @@
 // Two kernels over the rows in HBM:
 //   - lp_part_kernel: one 256-thread workgroup per kLpPart values of a row. Its largest value m_p,
 //     S_p = sum of exp(x - m_p) in f64 (each term within kExpRel of the reference's exp, from a
-//     table-free polynomial: exp_neg), and its 20 best by the reference's order: each wave's 5th
+//     table-free polynomial: exp_le0), and its 20 best by the reference's order: each wave's 5th
 //     largest lane maximum (by value), the smallest of the four, is a threshold with at least 20
-//     values of the part at or above it; the few values there go into LDS, where a rank count of
-//     their (value, id) keys sorts them.
+//     values of the part at or above it; the few values there go into LDS (each wave's into a
+//     segment of its own, at places a ballot per value gives), where a rank count of their (value,
+//     id) keys sorts them.
 //   - lp_row_kernel: one workgroup per row. M = max m_p; total = sum of S_p * exp(m_p - M);
 //     lse = M + ln(total) (logprobs.rs:14-16); the row's nt best come from a merge of the parts'
 //     sorted lists (a tournament on one wave); each output is (x - lse) rounded to f32
@@ -44,27 +45,29 @@ constexpr uint32_t kMerge = as_launch::kLpMerge;
 constexpr uint32_t kEntries = kMerge / kThreads;  // list slots per thread in a row's merge
 constexpr double kU = 1.1102230246251565e-16;  // 2^-53
 typedef float f32x4 __attribute__((ext_vector_type(4)));
-static_assert(kPer % 4 == 0, "whole 16-byte groups per thread");
+static_assert(kPer % 8 == 0, "whole 16-byte groups per thread, in two halves");
+static_assert(kPer / 2 <= 32, "a thread's running sums stay 32 roundings deep");
 
 // The reference's order as one descending u64: the logit's rank key with -0 mapped to +0 (they tie),
 // then the lower id.
 __device__ __forceinline__ uint64_t lp_key(float x, uint32_t id) { return pack(total_key(x == 0.0f ? 0.0f : x), id); }
 
 // A key m such that at least q lanes hold a key at or above it (the q-th largest distinct key, or
-// lower when lanes tie), or 0 when fewer than q lanes hold one (0: an empty lane).
-__device__ __forceinline__ uint32_t wave_qth_u32(uint32_t x, uint32_t q) {
-  uint32_t m = 0;
-  for (uint32_t it = 0; it < q; ++it) {
-    m = wave_max_u32(x);
+// lower when lanes tie), or 0 when fewer than q lanes hold one (0: an empty lane). m0: the wave's
+// largest x.
+__device__ __forceinline__ uint32_t wave_qth_u32(uint32_t x, uint32_t m0, uint32_t q) {
+  uint32_t m = m0;
+  for (uint32_t it = 1; it < q; ++it) {
     if (m == 0) return 0;
     if (x == m) x = 0;
+    m = wave_max_u32(x);
   }
   return m;
 }
 
 __device__ __forceinline__ double gamma_n(double n) { return n * kU / (1.0 - n * kU); }
 
-// Each term's relative error against the reference's exp (ExpPoly::exp_neg, exp_poly.h).
+// Each term's relative error against the reference's exp (ExpPoly::exp_le0, exp_poly.h).
 constexpr double kExpRel = kExpPolyRel;
 
 // The value part of lp_key.
@@ -75,9 +78,12 @@ __device__ __forceinline__ uint32_t lp_vkey(float x) { return total_key(x == 0.0
 constexpr uint32_t kLaneQ = (kTop + kWaves - 1) / kWaves;
 static_assert(kLaneQ * kWaves >= kTop, "the waves' thresholds cover the part's best kTop");
 
+// Each wave lists its values at or above the part's threshold in a segment of its own.
+constexpr uint32_t kSeg = kList / kWaves;
+
 struct PartShared {
   uint64_t list[kList];
-  uint32_t n_list;
+  uint32_t n_seg[kWaves];
   uint32_t red_t[kWaves];
   uint32_t red_u[kWaves];
   double red_d[kWaves];
@@ -114,52 +120,81 @@ __device__ __forceinline__ void lp_part(PartShared& sh, const float* __restrict_
   const uint32_t bk = has ? lp_vkey(bv) : 0u;
 
   // The part's largest value (-0 and +0 alike: both give the same differences).
-  const uint32_t kmax = block_max_u32<kWaves>(bk, sh.red_u);
+  const uint32_t wk = wave_max_u32(bk);
+  if (lane == 0) sh.red_u[w] = wk;
+  __syncthreads();
+  uint32_t kmax = sh.red_u[0];
+  for (int k = 1; k < kWaves; ++k) kmax = max(kmax, sh.red_u[k]);
   const float m = key_value(kmax);
   const double md = (double)m;
 
-  // S_p, each term within kExpRel of the reference's exp(f64(x) - m).
+  // S_p, each term within kExpRel of the reference's exp(f64(x) - m). Each half of the thread's
+  // values has its own running sum (at most 32 roundings deep, as the bound on the row's sum counts).
   ExpPoly ep;
   ep.load();
-  double s = 0.0;
+  double s = 0.0, s2 = 0.0;
 #pragma unroll
-  for (uint32_t q = 0; q < kPer; ++q)
-    if (valid(q)) s += ep.exp_neg((double)v[q] - md);
+  for (uint32_t q = 0; q < kPer / 2; ++q) {
+    if (valid(q)) s += ep.exp_le0((double)v[q] - md);
+    if (valid(q + kPer / 2)) s2 += ep.exp_le0((double)v[q + kPer / 2] - md);
+  }
+  s += s2;
 
   // The threshold: the smallest of the waves' kLaneQ-th largest lane maxima (0 when a wave holds
   // fewer). Each wave has kLaneQ lanes whose maximum is at or above it, so at least kTop values of the
   // part are, and every value among the part's kTop best is.
-  const uint32_t tw = wave_qth_u32(bk, kLaneQ);
-  if (lane == 0) sh.red_t[w] = tw;
-  if (tid == 0) sh.n_list = 0;
-  s = block_sum_f64<kWaves>(s, sh.red_d);  // its barriers publish red_t and n_list
-  uint32_t T = sh.red_t[0];
-  for (int k = 1; k < kWaves; ++k) T = min(T, sh.red_t[k]);
-  // Every value at or above the threshold's value (all of them for T = 0), into the list.
-  const float t_val = T ? key_value(T) : -__builtin_inff();
-#pragma unroll
-  for (uint32_t q = 0; q < kPer; ++q) {
-    if (valid(q) && v[q] >= t_val) {
-      const uint32_t i = atomicAdd(&sh.n_list, 1u);
-      if (i < kList) sh.list[i] = pack(lp_vkey(v[q]), b0 + off(q));
-    }
+  const uint32_t tw = wave_qth_u32(bk, wk, kLaneQ);
+  s = wave_sum_f64(s);
+  if (lane == 0) {
+    sh.red_t[w] = tw;
+    sh.red_d[w] = s;
   }
   __syncthreads();
-  const uint32_t n_list = sh.n_list;
+  uint32_t T = sh.red_t[0];
+  for (int k = 1; k < kWaves; ++k) T = min(T, sh.red_t[k]);
+  // Every value at or above the threshold's value (all of them for T = 0), into the wave's segment:
+  // each lane's place is the number of lanes below it that list a value at the same step.
+  const float t_val = T ? key_value(T) : -__builtin_inff();
+  uint64_t* seg = sh.list + w * kSeg;
+  uint32_t nw = 0;
+#pragma unroll
+  for (uint32_t q = 0; q < kPer; ++q) {
+    const bool c = valid(q) && v[q] >= t_val;
+    const uint64_t b = __ballot(c);
+    if (b) {
+      const uint32_t i = nw + __builtin_amdgcn_mbcnt_hi((uint32_t)(b >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)b, 0u));
+      if (c && i < kSeg) seg[i] = pack(lp_vkey(v[q]), b0 + off(q));
+      nw += (uint32_t)__popcll(b);
+    }
+  }
+  if (lane == 0) sh.n_seg[w] = nw;
+  __syncthreads();
+  uint32_t n_list = 0;
+  bool overflow = false;
+#pragma unroll
+  for (int k = 0; k < kWaves; ++k) {
+    n_list += sh.n_seg[k];
+    overflow |= sh.n_seg[k] > kSeg;
+  }
   // The list's kTop best, in order: each entry's place is the number of entries above it.
-  if (n_list <= kList) {
+  if (!overflow) {
     for (uint32_t i = tid; i < n_list; i += kThreads) {
-      const uint64_t key = sh.list[i];
+      uint32_t k = 0, j = i;
+      while (j >= sh.n_seg[k]) j -= sh.n_seg[k++];
+      const uint64_t key = sh.list[k * kSeg + j];
       uint32_t r = 0;
-      for (uint32_t j = 0; j < n_list; ++j) r += sh.list[j] > key ? 1u : 0u;
+      for (uint32_t k2 = 0; k2 < kWaves; ++k2)
+        for (uint32_t j2 = 0; j2 < sh.n_seg[k2]; ++j2) r += sh.list[k2 * kSeg + j2] > key ? 1u : 0u;
       if (r < kTop) out.top[r] = key;
     }
   }
   if (tid == 0) {
-    out.sum = s;
+    double S = sh.red_d[0];
+    for (int k = 1; k < kWaves; ++k) S = __dadd_rn(S, sh.red_d[k]);
+    out.sum = S;
     out.max = m;
     out.n_top = min(n_list, kTop);
-    out.overflow = n_list > kList ? 1u : 0u;
+    out.overflow = overflow ? 1u : 0u;
   }
 }
 
@@ -249,8 +284,9 @@ __global__ __launch_bounds__(kThreads) void lp_row_kernel(const float* __restric
   const double total = block_sum_f64<kWaves>(t, sh.red_d);  // its barriers publish overflow and the lists
   const double lnt = log(total);
   const double lse = M + lnt;
-  // The distance to the reference's lse: both sums' roundings (n terms each, the parts' rescales),
-  // each term's exp, the logarithm's ulp and the final addition.
+  // The distance to the reference's lse: both sums' roundings (the reference's n in order; ours at
+  // most 55 deep: 33 in a thread, 6 in its wave, 3 across the part's waves, 3 in the part's rescale,
+  // 10 in the row's sum), each term's exp, the logarithm's ulp and the final addition.
   const double e = gamma_n((double)n + 64.0) + kExpRel + 4.0 * kU * fabs(lnt) + 2.0 * kU * fabs(lse);
 
   if (nt > 0) {
@@ -348,7 +384,7 @@ hipError_t logprobs(hipStream_t stream, bool vec, const float* logits, uint64_t 
 
 namespace {
 
-constexpr uint32_t kStaticParts = 2048;  // 66 rows of the model's 248,320 values (31 parts each)
+constexpr uint32_t kStaticParts = 2048;  // 128 rows of the model's 248,320 values (16 parts each)
 static __device__ __align__(256) as_launch::LpPart scratch[kStaticParts];
 
 constexpr int kMaxDevices = 64;

@@ -205,8 +205,8 @@ int as_logprobs(as_ctx* ctx, const float* logits, uint64_t row_stride, uint32_t 
  * callers that cannot allocate device memory (code under HIP graph capture, tight serving loops,
  * harnesses that forbid hipMalloc). It runs as_logprobs' kernels, with the same arguments and
  * results, on hip_stream (NULL = the null stream) on the current device. Their scratch is a static
- * device array each GPU holds for the life of the process (2,048 parts of 8,192 values, 368 KiB):
- * n_rows x ceil(n_vocab / 8192) must be at most 2,048 (66 rows at 248,320), else AS_ERR_CAPACITY.
+ * device array each GPU holds for the life of the process (2,048 parts of 16,384 values, 368 KiB):
+ * n_rows x ceil(n_vocab / 16384) must be at most 2,048 (128 rows at 248,320), else AS_ERR_CAPACITY.
  * Every call on one GPU shares that array: calls that overlap on one GPU (other streams, other host
  * threads) race and must be ordered by the caller. Nothing is allocated and nothing is freed; the
  * device's first call looks the array's address up. err (host, may be NULL) gets a one-line message

@@ -149,6 +149,23 @@ def test_heavy_ties(ctx):
     check(ctx, np.stack([same, spread]), [7, 11], 20, "ties")
 
 
+def test_wide_ranges_within_a_wave(ctx):
+    # Values spanning far more than exp's range inside one wave's share of a part: a masked stretch
+    # over every wave's first 16-byte groups (each wave's sum starts from those and must start again
+    # from its largest value), masked values between ordinary ones, single huge values, and a masked
+    # half row; at a width whose last part is partial and at the model's.
+    gen = np.random.default_rng(41)
+    for n in [20000, VOCAB]:
+        rows = (gen.standard_normal((4, n)) * 2.5).astype(np.float32)
+        rows[0, :1024] = -1e4
+        rows[0, n - 1000:] = -1e4
+        rows[1, ::7] = -1e30
+        rows[2, 5000] = 1e4
+        rows[2, n - 3] = 3e4
+        rows[3, : n // 2] = -3e38
+        check(ctx, rows, [1, 8, 5000, n - 1], 20, f"wide n={n}")
+
+
 def test_strided_and_shared_rows(ctx):
     # A padded row stride, and stride 0 (every row reads the same row).
     gen = np.random.default_rng(3)

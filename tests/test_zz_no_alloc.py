@@ -41,7 +41,7 @@ def test_static_logprobs_match_as_logprobs_on_two_calls_in_a_row():
     from artemis_amd import Context
     dev = torch.device("cuda:0")
     gen = np.random.default_rng(17)
-    n1, r1 = 248_320, 66   # the static scratch nearly full: 66 x 31 = 2,046 parts
+    n1, r1 = 248_320, 128  # the static scratch full: 128 x 16 = 2,048 parts
     n2, r2 = 100_000, 5
     x1 = torch.from_numpy((gen.standard_normal((r1, n1)) * 2.5).astype(np.float32)).to(dev)
     x1[3, 777] = 60.0  # a near-certain token
@@ -68,8 +68,8 @@ def test_static_logprobs_refuse_a_batch_past_the_scratch():
     if not torch.cuda.is_available():
         pytest.skip("no GPU")
     dev = torch.device("cuda:0")
-    lg = torch.zeros((67, 248_320), dtype=torch.float32, device=dev)  # 67 x 31 = 2,077 parts
-    tok = torch.zeros(67, dtype=torch.int32, device=dev)
+    lg = torch.zeros((129, 248_320), dtype=torch.float32, device=dev)  # 129 x 16 = 2,064 parts
+    tok = torch.zeros(129, dtype=torch.int32, device=dev)
     rc, msg, lp, *_ = static_call(lg, tok, 20, 248_320, 248_320)
     assert rc == AS_ERR_CAPACITY and "2048" in msg.replace(",", ""), (rc, msg)
     torch.cuda.synchronize()
