@@ -468,7 +468,7 @@ int as_create(int device, void* hip_stream, uint32_t max_rows, uint32_t max_voca
   if (e == hipSuccess) e = hipMalloc(&c->d_vstatus, sizeof(uint32_t) * max_rows);
   if (e == hipSuccess) e = hipMalloc(&c->d_mv_partials, sizeof(uint64_t) * as_launch::kMatvecGroups);
   if (e == hipSuccess)
-    e = hipMalloc(&c->d_lp, sizeof(as_launch::LpPart) * (uint64_t)max_rows * as_launch::lp_parts(max_vocab));
+    e = hipMalloc(&c->d_lp, sizeof(as_launch::LpPart) * as_launch::lp_capacity(max_rows, max_vocab));
   if (e == hipSuccess) e = hipMalloc(&c->d_fused_count, sizeof(uint32_t));
   if (e == hipSuccess) e = hipMemset(c->d_fused_count, 0, sizeof(uint32_t));
   if (e == hipSuccess) e = hipMalloc(&c->d_zero, sizeof(float) * 1024);

@@ -158,11 +158,29 @@ hipError_t sample_rows(hipStream_t stream, bool vec, const float* logits, const 
                        as_dev::SegStats* stats, uint64_t* cands, uint32_t cand_stride, const FinishArgs& a);
 size_t row_kernel_lds();
 
-// Log-probabilities (logprobs.hip): rows in parts of kLpPart values, each part's 20 best and sums.
+// Log-probabilities (logprobs.hip): rows in parts, each part's 20 best and sums. Parts of kLpPart
+// values spread a part kernel's per-wave work over the most values its registers hold; a call whose
+// parts of kLpPartSmall values number under kLpOneRound (the chip's part workgroups at once: 256 CUs,
+// 7 each) takes those instead, for twice the workgroups per row.
 constexpr uint32_t kLpPart = 16384;
+constexpr uint32_t kLpPartSmall = 8192;
+constexpr uint32_t kLpOneRound = 1792;
 constexpr uint32_t kLpTop = 20;     // logprobs.rs:7, MAX_TOP
-constexpr uint32_t kLpMerge = 2048; // the parts' lists a row merges: lp_parts(n) * kLpTop at most
+constexpr uint32_t kLpMerge = 2048; // the parts' lists a row merges: parts per row * kLpTop at most
 __host__ __device__ constexpr uint32_t lp_parts(uint32_t n) { return (n + kLpPart - 1) / kLpPart; }
+__host__ __device__ constexpr uint32_t lp_part_len(uint32_t n, uint32_t n_rows) {
+  return (uint64_t)n_rows * ((n + kLpPartSmall - 1) / kLpPartSmall) < kLpOneRound &&
+                 ((n + kLpPartSmall - 1) / kLpPartSmall) * kLpTop <= kLpMerge
+             ? kLpPartSmall
+             : kLpPart;
+}
+// A call's parts per row, and the parts a context holds for any call within its sizes.
+__host__ __device__ constexpr uint32_t lp_parts_of(uint32_t n, uint32_t n_rows) {
+  return (n + lp_part_len(n, n_rows) - 1) / lp_part_len(n, n_rows);
+}
+__host__ __device__ constexpr uint64_t lp_capacity(uint32_t max_rows, uint32_t max_vocab) {
+  return (uint64_t)max_rows * ((max_vocab + kLpPartSmall - 1) / kLpPartSmall);
+}
 struct LpPart {
   double sum;         // sum of exp(x - max) over the part
   float max;          // the part's largest value

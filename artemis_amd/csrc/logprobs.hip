@@ -4,7 +4,8 @@
 // the lower id (logprobs.rs:40-48). Rows must be finite (the reference's run_step guarantees it).
 //
 // Two kernels over the rows in HBM:
-//   - lp_part_kernel: one 256-thread workgroup per kLpPart values of a row. Its largest value m_p,
+//   - lp_part_kernel: one 256-thread workgroup per part of a row (kLpPart values, or kLpPartSmall
+//     for a call whose grid of those fills at most one round of the chip: lp_part_len). Its largest value m_p,
 //     S_p = sum of exp(x - m_p) in f64 (each term within kExpRel of the reference's exp, from a
 //     table-free polynomial: exp_le0), and its 20 best by the reference's order: each wave's 5th
 //     largest lane maximum (by value), the smallest of the four, is a threshold with at least 20
@@ -37,16 +38,12 @@ namespace {
 
 constexpr int kThreads = 256;
 constexpr int kWaves = kThreads / kWave;
-constexpr uint32_t kPart = as_launch::kLpPart;
-constexpr uint32_t kPer = kPart / kThreads;  // values per thread
 constexpr uint32_t kTop = as_launch::kLpTop;
 constexpr uint32_t kList = 1024;             // a part's values at or above its threshold
 constexpr uint32_t kMerge = as_launch::kLpMerge;
 constexpr uint32_t kEntries = kMerge / kThreads;  // list slots per thread in a row's merge
 constexpr double kU = 1.1102230246251565e-16;  // 2^-53
 typedef float f32x4 __attribute__((ext_vector_type(4)));
-static_assert(kPer % 8 == 0, "whole 16-byte groups per thread, in two halves");
-static_assert(kPer / 2 <= 32, "a thread's running sums stay 32 roundings deep");
 
 // The reference's order as one descending u64: the logit's rank key with -0 mapped to +0 (they tie),
 // then the lower id.
@@ -89,11 +86,13 @@ struct PartShared {
   double red_d[kWaves];
 };
 
-// One part, b0 .. b1 of row x. kV4: the part is whole and 16-byte aligned, each thread's values in
-// 16-byte groups.
-template <bool kV4>
+// One part, b0 .. b1 of row x, kPer values per thread. kV4: the part is whole and 16-byte aligned,
+// each thread's values in 16-byte groups.
+template <bool kV4, uint32_t kPer>
 __device__ __forceinline__ void lp_part(PartShared& sh, const float* __restrict__ x, uint32_t b0, uint32_t b1,
                                         LpPart& out) {
+  static_assert(kPer % 8 == 0, "whole 16-byte groups per thread, in two halves");
+  static_assert(kPer / 2 <= 32, "a thread's running sums stay 32 roundings deep");
   const uint32_t tid = threadIdx.x, lane = tid & (kWave - 1), w = tid / kWave;
   auto off = [&](uint32_t q) { return kV4 ? ((q / 4) * kThreads + tid) * 4 + (q % 4) : q * kThreads + tid; };
   auto valid = [&](uint32_t q) { return kV4 || b0 + off(q) < b1; };
@@ -198,6 +197,7 @@ __device__ __forceinline__ void lp_part(PartShared& sh, const float* __restrict_
   }
 }
 
+template <uint32_t kPart>
 __global__ __launch_bounds__(kThreads) void lp_part_kernel(const float* __restrict__ logits, uint64_t row_stride,
                                                            uint32_t n, uint32_t vec, LpPart* __restrict__ parts,
                                                            uint32_t n_parts) {
@@ -206,8 +206,8 @@ __global__ __launch_bounds__(kThreads) void lp_part_kernel(const float* __restri
   const float* x = logits + (uint64_t)row * row_stride;
   const uint32_t b0 = part * kPart, b1 = min(b0 + kPart, n);
   LpPart& out = parts[(uint64_t)row * n_parts + part];
-  if (vec && b1 - b0 == kPart) lp_part<true>(sh, x, b0, b1, out);
-  else lp_part<false>(sh, x, b0, b1, out);
+  if (vec && b1 - b0 == kPart) lp_part<true, kPart / kThreads>(sh, x, b0, b1, out);
+  else lp_part<false, kPart / kThreads>(sh, x, b0, b1, out);
 }
 
 struct RowShared {
@@ -362,9 +362,13 @@ namespace as_launch {
 hipError_t logprobs(hipStream_t stream, bool vec, const float* logits, uint64_t row_stride, uint32_t n,
                     uint32_t n_rows, LpPart* parts, const uint32_t* tokens, uint32_t top, float* logprob,
                     uint32_t* top_ids, float* top_lps, uint32_t* status) {
-  const uint32_t n_parts = lp_parts(n);
-  hipLaunchKernelGGL(lp_part_kernel, dim3(n_parts, n_rows), dim3(kThreads), 0, stream, logits, row_stride, n,
-                     vec ? 1u : 0u, parts, n_parts);
+  const uint32_t len = lp_part_len(n, n_rows), n_parts = (n + len - 1) / len;
+  if (len == kLpPartSmall)
+    hipLaunchKernelGGL(lp_part_kernel<kLpPartSmall>, dim3(n_parts, n_rows), dim3(kThreads), 0, stream, logits,
+                       row_stride, n, vec ? 1u : 0u, parts, n_parts);
+  else
+    hipLaunchKernelGGL(lp_part_kernel<kLpPart>, dim3(n_parts, n_rows), dim3(kThreads), 0, stream, logits,
+                       row_stride, n, vec ? 1u : 0u, parts, n_parts);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
   hipLaunchKernelGGL(lp_row_kernel, dim3(n_rows), dim3(kThreads), 0, stream, logits, row_stride, n, parts, n_parts,
@@ -423,7 +427,7 @@ extern "C" int as_logprobs_static(void* hip_stream, const float* logits, uint64_
     return static_fail(err, err_cap, AS_ERR_INVALID, "as_logprobs_static: top > 0 needs top_ids and top_logprobs");
   if (row_stride != 0 && row_stride < n_vocab)
     return static_fail(err, err_cap, AS_ERR_INVALID, "as_logprobs_static: row_stride below n_vocab");
-  const uint32_t parts = as_launch::lp_parts(n_vocab);
+  const uint32_t parts = as_launch::lp_parts_of(n_vocab, n_rows);
   if (parts * as_launch::kLpTop > as_launch::kLpMerge)
     return static_fail(err, err_cap, AS_ERR_CAPACITY, "as_logprobs_static: vocabulary wider than the merge holds");
   if ((uint64_t)n_rows * parts > kStaticParts) {

@@ -130,6 +130,21 @@ def test_config5_rows_match_the_oracle(ctx):
     assert inexact <= 2, inexact
 
 
+def test_batches_past_one_round_take_the_wide_parts(ctx):
+    # A call whose 8,192-value parts would not fit one round of the chip's workgroups takes parts of
+    # 16,384 values: 64 aligned rows at the model's width (the last part partial), and 58 rows of an
+    # odd width (no 16-byte loads), each against the oracle.
+    from artemis_amd import workloads
+    gen = np.random.default_rng(43)
+    rows = workloads.config5(rows=64).logits
+    tokens = gen.integers(0, rows.shape[1], size=rows.shape[0])
+    _, _, _, _, inexact = check(ctx, rows, tokens, 20, "wide parts")
+    assert inexact <= 2, inexact
+    rows = (gen.standard_normal((58, VOCAB - 1)) * 3.0).astype(np.float32)
+    rows[7, 1000] = 40.0
+    check(ctx, rows, gen.integers(0, VOCAB - 1, size=58), 20, "wide parts, odd width")
+
+
 def test_ragged_widths_and_tops(ctx):
     gen = np.random.default_rng(11)
     for n in [1, 2, 5, 63, 8191, 8192, 8193, 20000, 100003]:
