@@ -125,17 +125,17 @@ __device__ __forceinline__ float unit_dot(const uint8_t* __restrict__ row, uint3
     const uint32_t scs = b[96 + 4 * n + m], dh = b[104];
     const uint32_t shl = 4 * (m >> 1), shh = 2 * m;
     float sa = 0.0f, sbs = 0.0f;
-    // Four 6-bit quants at once, one a byte (the nibbles at shl, the 2-bit pairs at shh above them);
-    // float(q) - 32 is exactly float(q - 32), so the products are the reference's. The bias is kept
-    // opaque so that each value is one byte-to-float conversion and one subtraction.
-    float bias = 32.0f;
-    __asm__ volatile("" : "+s"(bias));
+    // Four 6-bit quants at once, one a byte (the nibbles at shl, the 2-bit pairs at shh above them),
+    // then q - 32 in each byte as a signed byte: q + 96 is below 256 (no carry into the next byte),
+    // and flipping its top bit subtracts 128. Each value is then one sign-extending byte-to-float
+    // conversion; float(q - 32) is exactly the reference's float(q) - 32, so the products are its.
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
       const uint32_t q4 = ((ql[i] >> shl) & 0x0F0F0F0Fu) | (((qh[i] >> shh) & 0x03030303u) << 4);
+      const uint32_t s4 = (q4 + 0x60606060u) ^ 0x80808080u;
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
-        const float prod = ((float)((q4 >> (8 * e)) & 0xFFu) - bias) * x[4 * i + e];
+        const float prod = (float)(int8_t)(uint8_t)(s4 >> (8 * e)) * x[4 * i + e];
         if (i < 4) sa = sa + prod;
         else sbs = sbs + prod;
       }
