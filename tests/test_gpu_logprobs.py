@@ -145,6 +145,27 @@ def test_batches_past_one_round_take_the_wide_parts(ctx):
     check(ctx, rows, gen.integers(0, VOCAB - 1, size=58), 20, "wide parts, odd width")
 
 
+def test_both_sides_of_the_part_layout_switch():
+    # 179 rows of 81,920 values make 1,790 parts of 8,192 (one round of the chip's workgroups: that
+    # layout), 180 rows 1,800 (past it: parts of 16,384); the rows the two calls share must agree,
+    # and every row must match the oracle.
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU")
+    from artemis_amd import Context
+    gen = np.random.default_rng(47)
+    n = 81_920
+    rows = (gen.standard_normal((180, n)) * 2.5).astype(np.float32)
+    rows[5, 100] = 30.0
+    tokens = gen.integers(0, n, size=180)
+    c = Context(max_rows=180, max_vocab=n)
+    try:
+        small = check(c, rows[:179], tokens[:179], 20, "8,192-value parts")
+        wide = check(c, rows, tokens, 20, "16,384-value parts")
+    finally:
+        c.close()
+    assert (small[1] == wide[1][:179]).all()
+
+
 def test_ragged_widths_and_tops(ctx):
     gen = np.random.default_rng(11)
     for n in [1, 2, 5, 63, 8191, 8192, 8193, 20000, 100003]:
