@@ -125,14 +125,15 @@ __device__ __forceinline__ float unit_dot(const uint8_t* __restrict__ row, uint3
     const uint32_t scs = b[96 + 4 * n + m], dh = b[104];
     const uint32_t shl = 4 * (m >> 1), shh = 2 * m;
     float sa = 0.0f, sbs = 0.0f;
-    // Four 6-bit quants at once, one a byte (the nibbles at shl, the 2-bit pairs at shh above them),
-    // then q - 32 in each byte as a signed byte: q + 96 is below 256 (no carry into the next byte),
-    // and flipping its top bit subtracts 128. Each value is then one sign-extending byte-to-float
-    // conversion; float(q - 32) is exactly the reference's float(q) - 32, so the products are its.
+    // Four 6-bit quants q = lo + 16 hi at once, one a byte (the nibbles at shl, the 2-bit pairs at
+    // shh), each byte holding q - 32 as a signed byte: lo in its low nibble and hi - 2 (mod 16) in its
+    // high one, which v_perm_b32 looks up per byte (byte hi of 0x1000F0E0: 0xE0, 0xF0, 0x00, 0x10).
+    // Each value is then one sign-extending byte-to-float conversion; float(q - 32) is exactly the
+    // reference's float(q) - 32, so the products are its.
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
-      const uint32_t q4 = ((ql[i] >> shl) & 0x0F0F0F0Fu) | (((qh[i] >> shh) & 0x03030303u) << 4);
-      const uint32_t s4 = (q4 + 0x60606060u) ^ 0x80808080u;
+      const uint32_t hi = __builtin_amdgcn_perm(0u, 0x1000F0E0u, (qh[i] >> shh) & 0x03030303u);
+      const uint32_t s4 = ((ql[i] >> shl) & 0x0F0F0F0Fu) | hi;
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
         const float prod = (float)(int8_t)(uint8_t)(s4 >> (8 * e)) * x[4 * i + e];
