@@ -15,7 +15,7 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(HERE, "csrc")
 OBJ = os.path.join(HERE, "_build")
 LIB = os.path.join(HERE, "libartemis_sampler.so")
-SOURCES = ["api.hip", "scan.hip", "finish.hip", "fused.hip", "misc.hip", "logprobs.hip", "embed.hip", "matvec.hip"]
+SOURCES = ["api.hip", "scan.hip", "finish.hip", "misc.hip", "logprobs.hip", "embed.hip", "matvec.hip"]
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 
 FLAGS = [

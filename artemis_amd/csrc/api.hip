@@ -26,8 +26,12 @@ struct as_ctx {
   RowParams* d_params = nullptr;           // after the FinishArgs slot of d_block
   as_launch::FinishArgs* d_args = nullptr;  // the start of d_block
   void* d_block = nullptr;
+  // The parameter blocks d_params holds (as the host last uploaded them): a call uploads only the
+  // range of rows whose blocks differ, from one of two pinned staging blocks.
+  std::vector<RowParams> dev_rows;
+  uint32_t dev_valid = 0;  // rows of dev_rows that hold an upload
   void* h_block[2] = {nullptr, nullptr};
-  uint64_t* h_done = nullptr;  // pinned: the last call whose scan has ended (the finish kernel writes it)
+  uint64_t* h_done = nullptr;  // pinned: the last call whose finish kernel has started (it writes it)
   uint64_t calls = 0;
   SegStats* d_stats = nullptr;
   RowShare* d_share = nullptr;
@@ -39,8 +43,6 @@ struct as_ctx {
   uint64_t* d_deep_done = nullptr;           // rows finished by calls that shared the deep passes
   uint64_t deep_rows_done = 0;               // the host's count of the same
   bool share_dirty = false;  // a scan ran without its finish (a failed launch): the context is unusable
-  int force_path = 0;        // as_debug_path: 0 automatic, 1 the sliced scan, 2 the row kernel
-  uint32_t* d_fused_count = nullptr;  // the row kernel's count of ended workgroups
   uint64_t* d_cands = nullptr;
   uint32_t* d_scratch = nullptr;
   uint64_t scratch_stride = 0;
@@ -94,7 +96,6 @@ uint32_t wanted_cand(const as_sampling& s, uint32_t n) {
 // kernel's candidate room allows for the largest per-wave count, and slices of at most kSliceMax.
 struct Plan {
   uint32_t n_seg, slice_len, stride, limit;
-  bool row_kernel;  // one workgroup scans and finishes each row (fused.hip)
 };
 Plan plan_slices(uint32_t n, uint32_t n_rows, uint32_t c_max) {
   const uint32_t s_min = (n + as_launch::kSliceMax - 1) / as_launch::kSliceMax;
@@ -110,27 +111,7 @@ Plan plan_slices(uint32_t n, uint32_t n_rows, uint32_t c_max) {
   p.n_seg = (n + len - 1) / len;
   p.stride = as_launch::kCandCap / p.n_seg;
   p.limit = p.stride > as_launch::kHistReserve ? (p.stride - as_launch::kHistReserve) / 4 : 0;
-  p.row_kernel = false;
   return p;
-}
-
-// The row kernel's plan: one slice per row with all of the row's candidate slots.
-Plan plan_row_kernel(uint32_t n) {
-  Plan p;
-  p.n_seg = 1;
-  p.slice_len = n;
-  p.stride = as_launch::kCandCap;
-  p.limit = (as_launch::kCandCap - as_launch::kHistReserve) / 4;
-  p.row_kernel = true;
-  return p;
-}
-
-// Which kernels a call takes: the row kernel for batches that occupy the GPU with one workgroup per
-// row (and rows its LDS bitmap covers), the sliced scan otherwise; `force` (as_debug_path) overrides.
-Plan choose_plan(int force, uint32_t n, uint32_t n_rows, uint32_t c_max) {
-  const bool fits = n <= as_launch::kRowMaxVocab;
-  const bool row = force == 2 ? fits : force == 1 ? false : (fits && n_rows >= as_launch::kRowMinRows);
-  return row ? plan_row_kernel(n) : plan_slices(n, n_rows, c_max);
 }
 
 // The row's mode and parameter block (Sampler::sample's dispatch, sample.rs:129-150).
@@ -205,8 +186,6 @@ void order_rows(const RowParams* rows, uint32_t n_rows, as_launch::RowOrder* o,
   o->on = 1;
 }
 
-static_assert(sizeof(as_launch::FinishArgs) <= kArgsSlot && kArgsSlot % 16 == 0, "FinishArgs slot");
-
 // Each row's place among the finish kernel's helpers of S's sums (RowParams::help), the rows whose own
 // finish costs least first: greedy rows, then top-k rows, then rows without a top-k and without
 // min-p's floor, then those with it (the ones S is summed for); in row order within a kind.
@@ -234,17 +213,19 @@ hipEvent_t next_event(as_ctx* c) {
   return c->ev[c->ev_used++];
 }
 
-// One call over n_rows rows: the finish kernel's arguments and the rows' parameter blocks are written
-// to one of two pinned host blocks (waiting only if the call that read that block two calls ago has
-// not finished); the scan reads them there and copies them to device memory for the finish kernel.
-// No copy is queued: a host-to-device copy of a few tens of KB goes through a DMA engine whose
-// hand-offs with the kernels cost more than the kernels' own reads of the block.
-int run_rows(as_ctx* c, const Plan& pl, const RowParams* rows, const float* logits, uint64_t row_stride,
+// One call over n_rows rows. The rows' parameter blocks go to device memory only where they differ
+// from the blocks already there (a copy from one of two pinned staging blocks, the host waiting only
+// if the call that last used that block has not reached its finish kernel); the finish kernel's
+// arguments travel as the scan's kernel argument. Nothing else crosses to the GPU before the scan.
+int run_rows(as_ctx* c, const Plan& pl, RowParams* rows, const float* logits, uint64_t row_stride,
              uint32_t n, uint32_t n_rows, const uint32_t* hist_off, const uint32_t* hist_ids,
              const uint32_t* extra_ids, uint64_t* rng, uint32_t* tokens, uint32_t* status,
              uint32_t* kept_count, uint32_t* kept_ids, double* kept_probs, uint32_t kept_cap) {
   const uint32_t n_seg = pl.n_seg;
   const bool vec = aligned16(logits) && (row_stride % 4 == 0);
+  if (c->share_dirty)
+    return fail(c, AS_ERR_HIP, "an earlier call launched its scan but not its finish kernel: the context's "
+                               "shared words are not clear; destroy it and create another");
   as_launch::FinishArgs a{};
   a.logits = logits;
   a.row_stride = row_stride;
@@ -271,15 +252,15 @@ int run_rows(as_ctx* c, const Plan& pl, const RowParams* rows, const float* logi
   a.scratch = c->d_scratch;
   a.scratch_stride = c->scratch_stride;
   a.done = c->h_done;
-  a.call = ++c->calls;
-  a.tail_list = c->d_tail_list + (a.call & 1);
-  a.tail_next = c->d_tail_list + ((a.call + 1) & 1);
+  const uint64_t call = c->calls + 1;  // committed once the scan is launched
+  a.call = call;
+  a.tail_list = c->d_tail_list + (call & 1);
+  a.tail_next = c->d_tail_list + ((call + 1) & 1);
   a.tail_claims = c->d_tail_claims;
   a.deep_jobs = c->d_deep_jobs;
   a.deep_done = c->d_deep_done;
   a.n_rows = n_rows;
   a.max_history = c->max_history;
-  a.fused = pl.row_kernel ? 1u : 0u;
   bool own_states = true;
   for (uint32_t r = 0; r < n_rows && own_states; ++r) own_states = rows[r].rng_index == r;
   a.rng_rows = own_states ? 1u : 0u;
@@ -287,34 +268,39 @@ int run_rows(as_ctx* c, const Plan& pl, const RowParams* rows, const float* logi
   // (rows with kept lists take the full deep path, which is not shared).
   bool partial = false;
   for (uint32_t r = 0; r < n_rows; ++r) partial = partial || rows[r].mode == as_dev::kModePartial;
-  a.deep_help = (!pl.row_kernel && n_rows <= as_launch::kDeepHelpRows && !kept_ids && partial) ? 1u : 0u;
-  if (a.deep_help) {
-    c->deep_rows_done += n_rows;
-    a.deep_target = c->deep_rows_done;
-  }
-  a.fused_count = c->d_fused_count;
+  a.deep_help = (n_rows <= as_launch::kDeepHelpRows && !kept_ids && partial) ? 1u : 0u;
+  const uint64_t deep_target = c->deep_rows_done + (a.deep_help ? n_rows : 0u);
+  a.deep_target = deep_target;
 
-  if (c->share_dirty)
-    return fail(c, AS_ERR_HIP, "an earlier call launched its scan but not its finish kernel: the context's "
-                               "shared words are not clear; destroy it and create another");
-  // Block b was last read by the scan of call a.call - 2; the finish kernel after it wrote its number.
-  const int b = (int)(a.call & 1);
-  // Waits while the GPU works through the calls before it (the host runs at most two calls ahead);
-  // past 50 ms (a stream held up elsewhere) it waits for the stream instead.
-  if (a.call > 2 && __atomic_load_n(c->h_done, __ATOMIC_ACQUIRE) < a.call - 2) {
-    const auto t0 = std::chrono::steady_clock::now();
-    while (__atomic_load_n(c->h_done, __ATOMIC_ACQUIRE) < a.call - 2) {
-      if (std::chrono::steady_clock::now() - t0 > std::chrono::milliseconds(50)) {
-        AS_HIP(c, hipStreamSynchronize(c->stream));
-        break;
+  // The range of rows whose blocks differ from the device's.
+  help_ranks(rows, n_rows, rows);
+  uint32_t lo = n_rows, hi = 0;
+  for (uint32_t r = 0; r < n_rows; ++r)
+    if (r >= c->dev_valid || std::memcmp(&rows[r], &c->dev_rows[r], sizeof(RowParams)) != 0) {
+      lo = std::min(lo, r);
+      hi = r + 1;
+    }
+  if (lo < hi) {
+    // Staging block b was last filled by call `call - 2` or earlier, whose finish kernel writes its
+    // number once that upload is over. Waits while the GPU works through the calls before it; past
+    // 50 ms (a stream held up elsewhere) it waits for the stream instead.
+    const int b = (int)(call & 1);
+    if (call > 2 && __atomic_load_n(c->h_done, __ATOMIC_ACQUIRE) < call - 2) {
+      const auto t0 = std::chrono::steady_clock::now();
+      while (__atomic_load_n(c->h_done, __ATOMIC_ACQUIRE) < call - 2) {
+        if (std::chrono::steady_clock::now() - t0 > std::chrono::milliseconds(50)) {
+          AS_HIP(c, hipStreamSynchronize(c->stream));
+          break;
+        }
       }
     }
+    RowParams* h = static_cast<RowParams*>(c->h_block[b]);
+    std::memcpy(h + lo, rows + lo, sizeof(RowParams) * (hi - lo));
+    AS_HIP(c, hipMemcpyAsync(c->d_params + lo, h + lo, sizeof(RowParams) * (hi - lo), hipMemcpyHostToDevice,
+                             c->stream));
+    std::memcpy(&c->dev_rows[lo], rows + lo, sizeof(RowParams) * (hi - lo));
+    c->dev_valid = std::max(c->dev_valid, hi);
   }
-  char* h = static_cast<char*>(c->h_block[b]);
-  std::memset(h, 0, kArgsSlot);
-  std::memcpy(h, &a, sizeof a);
-  std::memcpy(h + kArgsSlot, rows, sizeof(RowParams) * n_rows);
-  help_ranks(rows, n_rows, reinterpret_cast<RowParams*>(h + kArgsSlot));
 
   hipEvent_t e0 = nullptr, e1 = nullptr, e2 = nullptr;
   if (c->profile && c->ev_used + 3 <= 3 * 4096) {
@@ -323,20 +309,14 @@ int run_rows(as_ctx* c, const Plan& pl, const RowParams* rows, const float* logi
     e2 = next_event(c);
   }
   if (e0) AS_HIP(c, hipEventRecord(e0, c->stream));
-  c->share_dirty = true;
-  if (pl.row_kernel) {
-    AS_HIP(c, as_launch::sample_rows(c->stream, vec, logits, c->d_zero, row_stride, n, n_rows, h, c->d_block,
-                                     c->d_share, hist_off, hist_ids, extra_ids, c->d_stats, c->d_cands, pl.stride,
-                                     a));
-    c->share_dirty = false;
-    if (e1) AS_HIP(c, hipEventRecord(e1, c->stream));
-    if (e2) AS_HIP(c, hipEventRecord(e2, c->stream));
-    return AS_OK;
-  }
   order_rows(rows, n_rows, &c->order, c->order_cost);
   AS_HIP(c, as_launch::scan(c->stream, vec, logits, c->d_zero, row_stride, n, n_rows, n_seg, pl.slice_len,
-                            h, c->d_block, c->d_share, hist_off, hist_ids, extra_ids, c->d_stats, c->d_cands,
-                            pl.stride, a.tail_list, c->order));
+                            c->d_params, a, c->d_args, c->d_share, hist_off, hist_ids, extra_ids, c->d_stats,
+                            c->d_cands, pl.stride, a.tail_list, c->order));
+  // The scan is queued: from here the call's numbers are the context's.
+  c->calls = call;
+  c->deep_rows_done = deep_target;
+  c->share_dirty = true;
   if (e1) AS_HIP(c, hipEventRecord(e1, c->stream));
   // Only rows without a top-k that have min-p's floor can be flagged for S's sums: with any, the
   // finish kernel runs enough workgroups to take their parts at once.
@@ -414,7 +394,6 @@ int as_destroy(as_ctx* c) {
   (void)hipFree(c->d_zero);
   (void)hipFree(c->d_lp);
   (void)hipFree(c->d_mv_partials);
-  (void)hipFree(c->d_fused_count);
   for (hipEvent_t e : c->ev) (void)hipEventDestroy(e);
   for (int b = 0; b < 2; ++b)
     if (c->h_block[b]) (void)hipHostFree(c->h_block[b]);
@@ -439,6 +418,7 @@ int as_create(int device, void* hip_stream, uint32_t max_rows, uint32_t max_voca
   c->max_seg = max_seg;
   c->order_cost.reserve(std::min(max_rows, as_launch::kOrderMax));
   c->rows.resize(max_rows);
+  c->dev_rows.resize(max_rows);
   c->scratch_stride = as_launch::scratch_words(max_vocab);
   hipError_t e = hipSetDevice(device);
   if (e == hipSuccess) e = hipMalloc(&c->d_block, kArgsSlot + sizeof(RowParams) * max_rows);
@@ -469,12 +449,10 @@ int as_create(int device, void* hip_stream, uint32_t max_rows, uint32_t max_voca
   if (e == hipSuccess) e = hipMalloc(&c->d_mv_partials, sizeof(uint64_t) * as_launch::kMatvecGroups);
   if (e == hipSuccess)
     e = hipMalloc(&c->d_lp, sizeof(as_launch::LpPart) * as_launch::lp_capacity(max_rows, max_vocab));
-  if (e == hipSuccess) e = hipMalloc(&c->d_fused_count, sizeof(uint32_t));
-  if (e == hipSuccess) e = hipMemset(c->d_fused_count, 0, sizeof(uint32_t));
   if (e == hipSuccess) e = hipMalloc(&c->d_zero, sizeof(float) * 1024);
   if (e == hipSuccess) e = hipMemset(c->d_zero, 0, sizeof(float) * 1024);
   for (int b = 0; b < 2 && e == hipSuccess; ++b)
-    e = hipHostMalloc(&c->h_block[b], kArgsSlot + sizeof(RowParams) * max_rows, hipHostMallocDefault);
+    e = hipHostMalloc(&c->h_block[b], sizeof(RowParams) * max_rows, hipHostMallocDefault);
   if (e == hipSuccess) e = hipHostMalloc((void**)&c->h_done, 64, hipHostMallocCoherent);
   if (e == hipSuccess) *c->h_done = 0;
   if (e != hipSuccess) {
@@ -513,7 +491,7 @@ int as_sample(as_ctx* c, const as_batch* b, const as_sampling* params) {
       return fail(c, AS_ERR_PARAMS, "row " + std::to_string(r) + ": " + msg);
     c_max = std::max(c_max, wanted_cand(params[r], b->n_vocab));
   }
-  const Plan pl = choose_plan(c->force_path, b->n_vocab, b->n_rows, c_max);
+  const Plan pl = plan_slices(b->n_vocab, b->n_rows, c_max);
   RowParams* h = c->rows.data();
   for (uint32_t r = 0; r < b->n_rows; ++r) {
     h[r] = make_row(params[r], b->n_vocab, pl);
@@ -544,7 +522,7 @@ int as_verify(as_ctx* c, const float* rows, uint64_t row_stride, uint32_t n_voca
     return fail(c, AS_ERR_CAPACITY, "as_verify: the history and the drafts hold more ids than the context's max_history");
   char msg[160];
   if (as_check(params, msg, sizeof msg) != AS_OK) return fail(c, AS_ERR_PARAMS, msg);
-  const Plan pl = choose_plan(c->force_path, n_vocab, k + 1, wanted_cand(*params, n_vocab));
+  const Plan pl = plan_slices(n_vocab, k + 1, wanted_cand(*params, n_vocab));
   const bool draws = params->temp > 0.0f;
   RowParams* h = c->rows.data();
   for (uint32_t i = 0; i <= k; ++i) {
@@ -694,12 +672,6 @@ int as_logprobs(as_ctx* c, const float* logits, uint64_t row_stride, uint32_t n_
   AS_HIP(c, hipSetDevice(c->device));
   AS_HIP(c, as_launch::logprobs(c->stream, vec, logits, row_stride, n_vocab, n_rows, c->d_lp, tokens, top, logprob,
                                 top_ids, top_logprobs, status));
-  return AS_OK;
-}
-
-int as_debug_path(as_ctx* c, int path) {
-  if (!c || path < 0 || path > 2) return AS_ERR_INVALID;
-  c->force_path = path;
   return AS_OK;
 }
 

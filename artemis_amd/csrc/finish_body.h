@@ -3,8 +3,7 @@
 //   AS_FIN_NS       the namespace of this copy,
 //   AS_FIN_THREADS  threads per workgroup (a power of two, 256 to 1024),
 //   AS_FIN_MAX_SEG  the most slices a row may have,
-// and, for a kernel that shares its LDS with another body, AS_DYNAMIC_LDS with the kernel's dynamic
-// LDS declared as `as_dyn_lds`. The entry point is AS_FIN_NS::finish_row.
+// The entry point is AS_FIN_NS::finish_row.
 namespace {
 namespace AS_FIN_NS {
 
@@ -40,6 +39,7 @@ struct Shared {
   uint32_t bstart[1024];
   uint32_t red_u[kWaves];
   double red_d[kWaves];
+  double red_d2[kWaves];
   // Row scalars.
   uint32_t hist_over;
   uint32_t bad, gi, mk, total, trunc, keep, pick, done, exact, prefix, stats_bad, nsk, tail_over, have_tail, tail_count,
@@ -53,14 +53,9 @@ struct Shared {
   uint32_t dp_pick, dp_stop, dp_q, dp_base, dp_staged, dp_mk, dp_r[2 * 3];
   uint32_t dp_pub;  // this row published its histogram pass early (deep_publish_hist)
 };
-// The workgroup's LDS, at file scope so that the out-of-line paths below address it as LDS: a static
-// array, or the kernel's dynamic LDS (AS_DYNAMIC_LDS) when another body shares it.
-#ifdef AS_DYNAMIC_LDS
-__device__ __forceinline__ Shared& shm() { return *reinterpret_cast<Shared*>(as_dyn_lds); }
-#else
+// The workgroup's LDS, at file scope so that the out-of-line paths below address it as LDS.
 __shared__ Shared g_sh_static;
 __device__ __forceinline__ Shared& shm() { return g_sh_static; }
-#endif
 
 // --- block helpers ------------------------------------------------------------------------------
 
@@ -783,6 +778,177 @@ __device__ __forceinline__ uint32_t decide_draw(Shared& sh, uint32_t m, const do
   const uint32_t jc = block_min_u32<kWaves>(fc, sh.red_u);
   if (jp == jc) return jc;  // jc < m, or both m: past every c_j
   return kNone;
+}
+
+// --- the fast decision for rows without a top-k ----------------------------------------------------
+//
+// draw_partial's cut and draw (sample.rs:208-272) from the sorted candidates with as few block-wide
+// steps as possible, for a row without kept lists: one pass computes every sorted value's weights at
+// T = 1 and at T, and the block sums them; wave 0 then certifies the cut from the sums and finds the
+// draw among the first kWaveMax ranks from a wave prefix. Every decision is taken from bounds that
+// cover the reference's own left folds, as the general path's are (the same bounds: the reference's
+// cumulative at rank j within gamma(2j + 4) of its exact quotient, a parallel sum within gamma(40)
+// of its terms' exact sum, a wave prefix within gamma(kWPer + 7)); when they cannot decide, or the
+// draw lies past the first kWaveMax ranks, it returns false and the general path decides.
+//   - Min-p's cut im is the first sorted rank below the floor (exact compares), or lies past the
+//     sorted values.
+//   - Top-p cannot stop before im when the reference's cumulative at rank im - 1 is certainly below
+//     top_p: the sum S1 of the im values' weights at T = 1 against top_p * total1, total1's lower
+//     bound from the slices' sums. Otherwise the cut may lie among the first kWaveMax ranks, where
+//     the wave's prefix places it (or cannot).
+//   - The draw: u = unit() * (the kept values' total at T), the kept set's total from the block sum
+//     (or the wave's own total when it holds every kept value). When the kept set runs past the
+//     sorted values, its weight lies between the sorted values' and that plus a bound on every value
+//     below them (draw_past's: the values below the last sorted one at T, or for T <= 1 their mass
+//     at T = 1 scaled by exp(d (1/T - 1)) of the last sorted one).
+// On success the row's kept count (or P, a lower bound, with AS_ROW_KEPT_PARTIAL) and status are
+// returned and sh.pick / sh.sum hold the rank drawn and the total.
+__device__ __forceinline__ bool fast_partial(const FinishArgs& a, Shared& sh, const RowParams& p, uint32_t P,
+                                             bool floor_cut, uint32_t* keep_out, uint32_t* status_out) {
+  const uint32_t tid = threadIdx.x, lane = tid & (kWave - 1), w = tid / kWave, n = a.n;
+  const double top = (double)key_value(sh.mk), temp = (double)p.temp, top_p = (double)p.top_p;
+  const bool has_floor = p.min_p > 0.0f, topp = p.top_p < 1.0f;
+  const double floor = __dadd_rn(top, p.ln_min_p);
+  const uint64_t* tab = sh.tab;
+  auto val = [&](uint32_t i) -> double { return (double)packed_value(sh.sk[i]); };
+  uint32_t first = P;
+  if (has_floor && !floor_cut)
+    for (uint32_t i = tid; i < P; i += kThreads)
+      if (!(val(i) >= floor)) first = min(first, i);
+  const uint32_t im = block_min_u32<kWaves>(first, sh.red_u);
+  // min-p's cut is known when it falls among the sorted values or right after them (floor_cut).
+  const bool im_exact = (has_floor && im < P) || floor_cut;
+  double X = 0.0, eps = 0.0;
+  if (topp) {
+    slices_total(a, sh, top, temp, false, &X, &eps);
+    if (!(X - eps > 0.0 && eps == eps)) return false;
+  }
+  // The weights of the values before min-p's cut (all P when it lies past them): at T in sh.wd, at
+  // T = 1 for the first kWaveMax past the end of sh.wd's used part.
+  const uint32_t m = im;
+  double* w1s = sh.wd + (kCap - kWaveMax);
+  double s1 = 0.0, sT = 0.0;
+  for (uint32_t i = tid; i < m; i += kThreads) {
+    const double v = val(i);
+    const double wt = as_exp::exp_with(tab, __ddiv_rn(__dsub_rn(v, top), temp));
+    sh.wd[i] = wt;
+    sT = __dadd_rn(sT, wt);
+    if (topp) {
+      const double w1 = as_exp::exp_with(tab, __dsub_rn(v, top));
+      s1 = __dadd_rn(s1, w1);
+      if (i < kWaveMax) w1s[i] = w1;
+    }
+  }
+  s1 = wave_sum_f64(s1);
+  sT = wave_sum_f64(sT);
+  if (lane == 0) {
+    sh.red_d[w] = s1;
+    sh.red_d2[w] = sT;
+  }
+  __syncthreads();
+  if (tid < kWave) {
+    const double g40 = gamma_n(40.0);
+    double S1 = sh.red_d[0], ST = sh.red_d2[0];
+    for (int k = 1; k < kWaves; ++k) {
+      S1 = __dadd_rn(S1, sh.red_d[k]);
+      ST = __dadd_rn(ST, sh.red_d2[k]);
+    }
+    const uint32_t i0 = lane * kWPer;
+    const double g = gamma_ub(2.0 * kWPer + 16.0);
+    uint32_t kk = kNone;  // the kept count, when known
+    bool past = false;    // the kept set runs past the sorted values
+    if (topp) {
+      const double tp_lo = top_p * (X - eps), tp_hi = top_p * (X + eps);
+      if (S1 * (1.0 + 2.0 * g40 + gamma_ub(2.0 * (double)m + 2.0) + 10.0 * kU) < tp_lo) {
+        if (im_exact) kk = im;
+        else if (P == n) kk = n;
+        else past = true;
+      } else {
+        const uint32_t mw = min(m, kWaveMax);
+        double wv[kWPer], pre[kWPer];
+#pragma unroll
+        for (int q = 0; q < kWPer; ++q) wv[q] = (i0 + q < mw) ? w1s[i0 + q] : 0.0;
+        wave_prefix(wv, pre);
+        bool lo[kWPer], hi[kWPer];
+#pragma unroll
+        for (int q = 0; q < kWPer; ++q) {
+          const double rel = 2.0 * g + gamma_ub(2.0 * (double)(i0 + q) + 4.0) + 10.0 * kU;
+          lo[q] = pre[q] * (1.0 + rel) >= tp_lo;  // the reference's cumulative may have reached top_p
+          hi[q] = pre[q] * (1.0 - rel) >= tp_hi;  // it certainly has
+        }
+        const uint32_t jl = wave_first(lo, mw), jh = wave_first(hi, mw);
+        if (jl == jh && jh < mw) kk = jh + 1;
+      }
+    } else {
+      if (im_exact) kk = im;
+      else if (P == n) kk = n;
+      else past = true;
+    }
+    uint32_t pick = kNone;
+    double tot = 0.0, ulo = 0.0, uhi = 0.0;
+    uint32_t mw = 0;
+    if (kk != kNone) {
+      mw = min(kk, kWaveMax);
+      // The kept total: the wave's own when it holds every kept value, else the block's sum (kk == m).
+      double S = ST, dS = g40;
+      if (kk <= kWaveMax) {
+        double wv[kWPer], pre[kWPer];
+#pragma unroll
+        for (int q = 0; q < kWPer; ++q) wv[q] = (i0 + q < mw) ? sh.wd[i0 + q] : 0.0;
+        S = wave_prefix(wv, pre);
+        dS = g;
+      }
+      const double d = gamma_ub((double)kk + 1.0) + dS + 4.0 * kU;
+      ulo = sh.u01 * S * (1.0 - d) * (1.0 - 3.0 * kU);
+      uhi = sh.u01 * S * (1.0 + d) * (1.0 + 3.0 * kU);
+      tot = S;
+    } else if (past) {
+      mw = min(P, kWaveMax);
+      double tail = (double)(n - P) * sh.wd[P - 1] * (1.0 + 4.0 * kU);
+      if (topp && p.temp <= 1.0f) {
+        const double d = __dsub_rn(val(P - 1), top);
+        const double rest = (X + eps) - S1 * (1.0 - 2.0 * g40);
+        const double t2 = as_exp::exp_with(tab, d * (1.0 / temp - 1.0)) * (1.0 + 1e-9) * (rest > 0.0 ? rest : 0.0);
+        if (t2 < tail) tail = t2;
+      }
+      const double gn = gamma_n((double)n);
+      const double slo = ST * (1.0 - g40 - 4.0 * kU) * (1.0 - gn);
+      const double shi = (ST * (1.0 + g40 + 4.0 * kU) + tail) * (1.0 + gn);
+      ulo = sh.u01 * slo * (1.0 - 3.0 * kU);
+      uhi = sh.u01 * shi * (1.0 + 3.0 * kU);
+      tot = ST;
+    }
+    if (mw > 0) {
+      // The first rank among the first mw whose cumulative passes u, when the bounds agree.
+      double wv[kWPer], pre[kWPer];
+#pragma unroll
+      for (int q = 0; q < kWPer; ++q) wv[q] = (i0 + q < mw) ? sh.wd[i0 + q] : 0.0;
+      wave_prefix(wv, pre);
+      bool may[kWPer], sure[kWPer];
+#pragma unroll
+      for (int q = 0; q < kWPer; ++q) {
+        const double rel = gamma_ub((double)(i0 + q) + 1.0) + g + 4.0 * kU;
+        may[q] = pre[q] * (1.0 + rel) > ulo;
+        sure[q] = pre[q] * (1.0 - rel) > uhi;
+      }
+      const uint32_t jp = wave_first(may, mw), jc = wave_first(sure, mw);
+      if (jp == jc) {
+        if (jc < mw) pick = jc;
+        else if (kk != kNone && kk == mw) pick = kk - 1;  // past every cumulative: the last kept
+      }
+    }
+    if (lane == 0) {
+      sh.pick = pick;
+      sh.sum = tot;
+      sh.keep = pick == kNone ? kNone : (kk != kNone ? kk : P);
+    }
+  }
+  __syncthreads();
+  const uint32_t keep = sh.keep;
+  if (keep == kNone) return false;
+  *keep_out = keep;
+  *status_out = keep == P && !(im_exact || P == n) ? (uint32_t)AS_ROW_KEPT_PARTIAL : (uint32_t)AS_ROW_OK;
+  return true;
 }
 
 // --- the deep path ------------------------------------------------------------------------------
@@ -2852,10 +3018,11 @@ __device__ __forceinline__ void finish_row(const FinishArgs& a, uint32_t row) {
   const SegStats* gst = a.stats + (uint64_t)row * a.n_seg;
   const uint32_t n = a.n;
   if (tid < 256) sh.tab[tid] = as_exp::kTable[tid];
-  // The host learns that the scan no longer reads the call's parameter block; the next call's list
-  // of flagged rows empties (this call's scan and the call before it have ended).
+  // The host learns that the call's parameter upload (which ran before its scan) no longer reads its
+  // staging block; the next call's list of flagged rows empties (this call's scan and the call
+  // before it have ended).
   if (row == 0 && tid == 0) {
-    if (!a.fused) __hip_atomic_store(a.done, a.call, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+    __hip_atomic_store(a.done, a.call, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
     a.tail_next->count = 0u;
   }
   // S's sums: none until a flagged row waits for them (tail_wait).
@@ -2989,7 +3156,7 @@ __device__ __forceinline__ void finish_row(const FinishArgs& a, uint32_t row) {
   // candidates: it publishes its deep histogram pass now, so that the workgroups with no row left
   // sum it while this one sorts and tries its candidates (when they settle the row, the pass goes
   // unused).
-  if (a.deep_help && !a.fused && !a.kept_ids && p.mode == kModePartial && !sh.stats_bad && sh.tail_slot == kNone) {
+  if (a.deep_help && !a.kept_ids && p.mode == kModePartial && !sh.stats_bad && sh.tail_slot == kNone) {
     deep_publish_hist(a, row, sh.mk);
     if (tid == 0) sh.dp_pub = 1;  // read after later barriers
   }
@@ -3059,230 +3226,239 @@ __device__ __forceinline__ void finish_row(const FinishArgs& a, uint32_t row) {
     // The candidates in rank order; a flagged row's parts of S are summed meanwhile, and its sums
     // are read after (tail_wait).
     uint32_t P = sort_candidates(sh, total, R, sh.mk, p.mode == kModeTopK ? p.top_k : kNone);
-    if (!a.fused && sh.tail_slot != kNone) tail_wait(a, row);
-    // A row whose floor set S's parts listed (S: every value below R and at or above the floor),
-    // and whose whole floor set's mass at T = 1 is short of top-p's target: top-p never stops inside it
-    // and min-p's floor cuts first (sample.rs:237-251), so the kept set is the candidates and all of S.
-    // Every value of S ranks below every candidate: S sorted on its own follows them. The
-    // candidates' mass needs no order: a parallel sum of positive terms, within gamma(40) of exact,
-    // and the margins below are far wider.
-    bool floor_set = false;
-    if (p.mode == kModePartial && has_floor && !floor_cut && !too_many && sh.have_tail && sh.tail_listed &&
-        P + sh.tail_count <= (uint32_t)kCap) {
-      bool cuts_first = true;
-      if (p.top_p < 1.0f) {
-        double X, eps;
-        slices_total(a, sh, top, temp, false, &X, &eps);
-        double mc = 0.0;
-        for (uint32_t i = tid; i < P; i += kThreads) mc += w_one(val(i));
-        mc = block_sum_f64<kWaves>(mc, sh.red_d);
-        cuts_first = (X - eps > 0.0) && (eps == eps) &&
-                     sh.m_hi < top_p * (X - eps) * (1.0 - 1e-9) - mc * (1.0 + 1e-9);
-      }
-      if (cuts_first) {
-        const uint64_t* list = reinterpret_cast<const uint64_t*>(a.scratch + (uint64_t)row * a.scratch_stride);
-        const uint32_t cnt = sh.tail_count;
-        for (uint32_t i = tid; i < cnt; i += kThreads) sh.sk[P + i] = ld_agent(list + i);
-        __syncthreads();
-        P += sort_candidates(sh, cnt, 0ull, (uint32_t)(R >> 32), kNone, P);
-        floor_set = true;
-      }
-    }
     if (tid == 0) sh.prefix = P;
-    const bool complete = (P == n);  // every value of the row is sorted
-    // A top-k row's k best are among the sorted values only when at least k rank at or above R.
-    const bool short_topk = p.mode == kModeTopK && P < p.top_k;
-
     uint32_t keep = kNone;
     uint32_t status = AS_ROW_OK;
     bool drawn = false;
-    double r_prefix = 0.0;  // the top-p scan's sum of exp(l - top) over the P sorted values
-    double x1 = 0.0, eps1 = 0.0;  // total1 and its bound
-    if (floor_set) {
-      keep = P;  // every value at or above the floor
-      status |= AS_ROW_TAIL_PASS;
-    } else if (short_topk || too_many) {
-      keep = kNone;
-    } else if (p.mode == kModeTopK) {
-      // draw_full_sort over the k best (sample.rs:157-197), on wave 0 from registers: top-p's cut,
-      // min-p's floor (the ranks are sorted, so it keeps a prefix) and the draw, each decided by
-      // bounds and by the reference's sequential folds only when the bounds cannot.
-      static_assert(as_launch::kTopKMax <= kWaveMax, "one wave holds a top-k");
-      static_assert(2 * as_launch::kTopKMax <= (uint32_t)kCap && as_launch::kTopKMax <= (uint32_t)kThreads,
-                    "the weights of a top-k, one per thread");
-      const uint32_t k = p.top_k;
-      // Every weight first, one value per thread: sh.wd[i] = w at T, sh.wd[kTopKMax + i] = w at T = 1.
-      double* w1s = sh.wd + as_launch::kTopKMax;
-      if (tid < k) {
-        const double v = val(tid);
-        sh.wd[tid] = w_temp(v);
-        if (p.top_p < 1.0f) w1s[tid] = w_one(v);
-      }
-      __syncthreads();
-      if (tid < kWave) {
-        const uint32_t i0 = tid * kWPer;
-        uint32_t kk = k;
+    // A row without a top-k and without kept lists first takes the fast decision; a flagged row
+    // waits for S's sums only when that does not settle it.
+    if (p.mode == kModePartial && (p.top_p < 1.0f || has_floor) && !a.kept_ids && !too_many && P > 0 &&
+        P + kWaveMax <= (uint32_t)kCap)
+      drawn = fast_partial(a, sh, p, P, floor_cut, &keep, &status);
+    if (!drawn) {
+      if (sh.tail_slot != kNone) tail_wait(a, row);
+      // A row whose floor set S's parts listed (S: every value below R and at or above the floor),
+      // and whose whole floor set's mass at T = 1 is short of top-p's target: top-p never stops inside it
+      // and min-p's floor cuts first (sample.rs:237-251), so the kept set is the candidates and all of S.
+      // Every value of S ranks below every candidate: S sorted on its own follows them. The
+      // candidates' mass needs no order: a parallel sum of positive terms, within gamma(40) of exact,
+      // and the margins below are far wider.
+      bool floor_set = false;
+      if (p.mode == kModePartial && has_floor && !floor_cut && !too_many && sh.have_tail && sh.tail_listed &&
+          P + sh.tail_count <= (uint32_t)kCap) {
+        bool cuts_first = true;
         if (p.top_p < 1.0f) {
-          double w[kWPer];
-#pragma unroll
-          for (int q = 0; q < kWPer; ++q) w[q] = (i0 + q < k) ? w1s[i0 + q] : 0.0;
-          kk = wave_topp_cut(w, k, top_p);
-          if (kk == kNone) kk = wave_seq_cut(w1s, k, top_p);
+          double X, eps;
+          slices_total(a, sh, top, temp, false, &X, &eps);
+          double mc = 0.0;
+          for (uint32_t i = tid; i < P; i += kThreads) mc += w_one(val(i));
+          mc = block_sum_f64<kWaves>(mc, sh.red_d);
+          cuts_first = (X - eps > 0.0) && (eps == eps) &&
+                       sh.m_hi < top_p * (X - eps) * (1.0 - 1e-9) - mc * (1.0 + 1e-9);
         }
-        if (has_floor) {
-          bool below[kWPer];
-#pragma unroll
-          for (int q = 0; q < kWPer; ++q) below[q] = (i0 + q < kk) && !(val(i0 + q) >= floor);
-          kk = wave_first(below, kk);
-        }
-        double w[kWPer], tot = 0.0;
-#pragma unroll
-        for (int q = 0; q < kWPer; ++q) w[q] = (i0 + q < kk) ? sh.wd[i0 + q] : 0.0;  // also the kept weights
-        uint32_t pick = wave_draw(w, kk, sh.u01, &tot);
-        if (pick == kNone) pick = wave_seq_draw(sh.wd, kk, sh.u01, &tot);
-        if (tid == 0) {
-          sh.keep = kk;
-          sh.pick = pick;
-          sh.sum = tot;
-        }
-      }
-      __syncthreads();
-      keep = sh.keep;
-      drawn = true;
-    } else if (p.top_p < 1.0f || has_floor) {
-      // draw_partial's cut (sample.rs:230-259): the first rank below min-p's floor, or the rank at
-      // which the top-p cumulative reaches top_p, whichever comes first.
-      uint32_t im = P;  // first sorted rank below the floor (P: none among the sorted)
-      if (has_floor && !floor_cut) {
-        uint32_t first = P;
-        for (uint32_t i = tid; i < P; i += kThreads)
-          if (!(val(i) >= floor)) first = min(first, i);
-        im = block_min_u32<kWaves>(first, sh.red_u);
-      }
-      // min-p's cut is known exactly when it falls among the sorted values, or right after them.
-      const bool im_exact = (im < P) || floor_cut;
-      uint32_t jl = P, jh = P;  // top-p: possible and certain trigger ranks among the sorted
-      bool ok = true;
-      if (p.top_p < 1.0f) {
-        // total1 = sum of exp(l - top) over the row in index order (sample.rs:218-222): the
-        // segments' sums rescaled, with |result - reference's left fold| <= eps.
-        double X, eps;
-        slices_total(a, sh, top, temp, false, &X, &eps);
-        x1 = X;
-        eps1 = eps;
-        ok = (X - eps > 0.0) && (eps == eps);
-        if (ok) {
-          for (uint32_t i = tid; i < P; i += kThreads) sh.wd[i] = w_one(val(i));
+        if (cuts_first) {
+          const uint64_t* list = reinterpret_cast<const uint64_t*>(a.scratch + (uint64_t)row * a.scratch_stride);
+          const uint32_t cnt = sh.tail_count;
+          for (uint32_t i = tid; i < cnt; i += kThreads) sh.sk[P + i] = ld_agent(list + i);
           __syncthreads();
-          double loc[kScanPer], off;
-          r_prefix = prefix_scan(sh, P, loc, &off);
-          const double g40 = 2.0 * gamma_n(40.0);
-          const double tp_lo = top_p * (X - eps), tp_hi = top_p * (X + eps);
-          uint32_t fl = P, fh = P;
-          const uint32_t i0 = tid * kScanPer;
-#pragma unroll
-          for (int q = 0; q < kScanPer; ++q) {
-            const uint32_t i = i0 + q;
-            if (i < P) {
-              const double Rv = __dadd_rn(off, loc[q]);
-              const double rel = g40 + gamma_ub(2.0 * (double)i + 4.0) + 10.0 * kU;
-              // Rv / (X -+ eps) against top_p as Rv against top_p * (X -+ eps): the products'
-              // roundings are within the 10 u of rel.
-              if (Rv * (1.0 + rel) >= tp_lo) fl = min(fl, i);
-              if (Rv * (1.0 - rel) >= tp_hi) fh = min(fh, i);
+          P += sort_candidates(sh, cnt, 0ull, (uint32_t)(R >> 32), kNone, P);
+          floor_set = true;
+        }
+      }
+      if (tid == 0) sh.prefix = P;
+      const bool complete = (P == n);  // every value of the row is sorted
+      // A top-k row's k best are among the sorted values only when at least k rank at or above R.
+      const bool short_topk = p.mode == kModeTopK && P < p.top_k;
+
+      double r_prefix = 0.0;  // the top-p scan's sum of exp(l - top) over the P sorted values
+      double x1 = 0.0, eps1 = 0.0;  // total1 and its bound
+      if (floor_set) {
+        keep = P;  // every value at or above the floor
+        status |= AS_ROW_TAIL_PASS;
+      } else if (short_topk || too_many) {
+        keep = kNone;
+      } else if (p.mode == kModeTopK) {
+        // draw_full_sort over the k best (sample.rs:157-197), on wave 0 from registers: top-p's cut,
+        // min-p's floor (the ranks are sorted, so it keeps a prefix) and the draw, each decided by
+        // bounds and by the reference's sequential folds only when the bounds cannot.
+        static_assert(as_launch::kTopKMax <= kWaveMax, "one wave holds a top-k");
+        static_assert(2 * as_launch::kTopKMax <= (uint32_t)kCap && as_launch::kTopKMax <= (uint32_t)kThreads,
+                      "the weights of a top-k, one per thread");
+        const uint32_t k = p.top_k;
+        // Every weight first, one value per thread: sh.wd[i] = w at T, sh.wd[kTopKMax + i] = w at T = 1.
+        double* w1s = sh.wd + as_launch::kTopKMax;
+        if (tid < k) {
+          const double v = val(tid);
+          sh.wd[tid] = w_temp(v);
+          if (p.top_p < 1.0f) w1s[tid] = w_one(v);
+        }
+        __syncthreads();
+        if (tid < kWave) {
+          const uint32_t i0 = tid * kWPer;
+          uint32_t kk = k;
+          if (p.top_p < 1.0f) {
+            double w[kWPer];
+  #pragma unroll
+            for (int q = 0; q < kWPer; ++q) w[q] = (i0 + q < k) ? w1s[i0 + q] : 0.0;
+            kk = wave_topp_cut(w, k, top_p);
+            if (kk == kNone) kk = wave_seq_cut(w1s, k, top_p);
+          }
+          if (has_floor) {
+            bool below[kWPer];
+  #pragma unroll
+            for (int q = 0; q < kWPer; ++q) below[q] = (i0 + q < kk) && !(val(i0 + q) >= floor);
+            kk = wave_first(below, kk);
+          }
+          double w[kWPer], tot = 0.0;
+  #pragma unroll
+          for (int q = 0; q < kWPer; ++q) w[q] = (i0 + q < kk) ? sh.wd[i0 + q] : 0.0;  // also the kept weights
+          uint32_t pick = wave_draw(w, kk, sh.u01, &tot);
+          if (pick == kNone) pick = wave_seq_draw(sh.wd, kk, sh.u01, &tot);
+          if (tid == 0) {
+            sh.keep = kk;
+            sh.pick = pick;
+            sh.sum = tot;
+          }
+        }
+        __syncthreads();
+        keep = sh.keep;
+        drawn = true;
+      } else if (p.top_p < 1.0f || has_floor) {
+        // draw_partial's cut (sample.rs:230-259): the first rank below min-p's floor, or the rank at
+        // which the top-p cumulative reaches top_p, whichever comes first.
+        uint32_t im = P;  // first sorted rank below the floor (P: none among the sorted)
+        if (has_floor && !floor_cut) {
+          uint32_t first = P;
+          for (uint32_t i = tid; i < P; i += kThreads)
+            if (!(val(i) >= floor)) first = min(first, i);
+          im = block_min_u32<kWaves>(first, sh.red_u);
+        }
+        // min-p's cut is known exactly when it falls among the sorted values, or right after them.
+        const bool im_exact = (im < P) || floor_cut;
+        uint32_t jl = P, jh = P;  // top-p: possible and certain trigger ranks among the sorted
+        bool ok = true;
+        if (p.top_p < 1.0f) {
+          // total1 = sum of exp(l - top) over the row in index order (sample.rs:218-222): the
+          // segments' sums rescaled, with |result - reference's left fold| <= eps.
+          double X, eps;
+          slices_total(a, sh, top, temp, false, &X, &eps);
+          x1 = X;
+          eps1 = eps;
+          ok = (X - eps > 0.0) && (eps == eps);
+          if (ok) {
+            for (uint32_t i = tid; i < P; i += kThreads) sh.wd[i] = w_one(val(i));
+            __syncthreads();
+            double loc[kScanPer], off;
+            r_prefix = prefix_scan(sh, P, loc, &off);
+            const double g40 = 2.0 * gamma_n(40.0);
+            const double tp_lo = top_p * (X - eps), tp_hi = top_p * (X + eps);
+            uint32_t fl = P, fh = P;
+            const uint32_t i0 = tid * kScanPer;
+  #pragma unroll
+            for (int q = 0; q < kScanPer; ++q) {
+              const uint32_t i = i0 + q;
+              if (i < P) {
+                const double Rv = __dadd_rn(off, loc[q]);
+                const double rel = g40 + gamma_ub(2.0 * (double)i + 4.0) + 10.0 * kU;
+                // Rv / (X -+ eps) against top_p as Rv against top_p * (X -+ eps): the products'
+                // roundings are within the 10 u of rel.
+                if (Rv * (1.0 + rel) >= tp_lo) fl = min(fl, i);
+                if (Rv * (1.0 - rel) >= tp_hi) fh = min(fh, i);
+              }
+            }
+            jl = block_min_u32<kWaves>(fl, sh.red_u);
+            jh = block_min_u32<kWaves>(fh, sh.red_u);
+          }
+        }
+        if (!ok) {
+          keep = kNone;
+        } else if (im_exact && im <= jl) {
+          keep = im;  // min-p's cut, at or before any rank top-p could stop at
+        } else if (jl < P && jl == jh) {
+          keep = jh + 1;  // top-p's cut, certainly, and min-p's comes later
+        } else if (jl == P && complete) {
+          keep = n;  // neither filter stops: every value
+        } else if (jl == P && !im_exact && sh.have_tail && sh.tail_listed && P + sh.tail_count <= (uint32_t)kCap &&
+                   sh.m_hi < (p.top_p < 1.0f ? top_p * (x1 - eps1) * (1.0 - 1e-9) - r_prefix * (1.0 + 1e-9)
+                                             : __builtin_inf())) {
+          // Neither filter stops among the sorted values, and S's whole mass is short of top-p's
+          // target past them, so the floor cuts first: the kept set is the sorted values and all of
+          // S, which S's parts listed. Sorted in with the candidates, they take the exact draw.
+          const uint64_t* list = reinterpret_cast<const uint64_t*>(a.scratch + (uint64_t)row * a.scratch_stride);
+          const uint32_t cnt = sh.tail_count;
+          for (uint32_t i = tid; i < cnt; i += kThreads) sh.sk[P + i] = ld_agent(list + i);
+          __syncthreads();
+          // S ranks below every candidate: sorted on its own, it follows them.
+          const uint32_t P2 = P + sort_candidates(sh, cnt, 0ull, (uint32_t)(R >> 32), kNone, P);
+          if (tid == 0) sh.prefix = P2;
+          keep = P2;
+          status |= AS_ROW_TAIL_PASS;
+          __syncthreads();
+        } else if (jl == P && !im_exact && !a.kept_ids) {
+          // Neither filter stops among the P sorted values: the kept set runs past them.
+          if (tid == 0) {
+            sh.x1 = x1;
+            sh.eps1 = eps1;
+            sh.r_prefix = r_prefix;
+          }
+          __syncthreads();
+          // S's sums when the row was flagged; else the sorted values alone first, and one
+          // pass over the row when they cannot settle the draw.
+          uint32_t j;
+          if (sh.have_tail) {
+            status |= AS_ROW_TAIL_PASS;
+            j = draw_past(a, a.params[row], row, P, true, true);
+          } else {
+            j = draw_past(a, a.params[row], row, P, false, false);
+            // With the deep passes shared (a small batch), a row they would settle takes them at once
+            // rather than one workgroup's pass over the row first.
+            if (j == kNone && !a.deep_help &&
+                tail_sums(a, a.params[row], row, R, has_floor ? floor_f32(floor) : -__builtin_inff(),
+                          key_value(sh.mk))) {
+              status |= AS_ROW_TAIL_PASS;
+              j = draw_past(a, a.params[row], row, P, true, false);
             }
           }
-          jl = block_min_u32<kWaves>(fl, sh.red_u);
-          jh = block_min_u32<kWaves>(fh, sh.red_u);
-        }
-      }
-      if (!ok) {
-        keep = kNone;
-      } else if (im_exact && im <= jl) {
-        keep = im;  // min-p's cut, at or before any rank top-p could stop at
-      } else if (jl < P && jl == jh) {
-        keep = jh + 1;  // top-p's cut, certainly, and min-p's comes later
-      } else if (jl == P && complete) {
-        keep = n;  // neither filter stops: every value
-      } else if (jl == P && !im_exact && sh.have_tail && sh.tail_listed && P + sh.tail_count <= (uint32_t)kCap &&
-                 sh.m_hi < (p.top_p < 1.0f ? top_p * (x1 - eps1) * (1.0 - 1e-9) - r_prefix * (1.0 + 1e-9)
-                                           : __builtin_inf())) {
-        // Neither filter stops among the sorted values, and S's whole mass is short of top-p's
-        // target past them, so the floor cuts first: the kept set is the sorted values and all of
-        // S, which S's parts listed. Sorted in with the candidates, they take the exact draw.
-        const uint64_t* list = reinterpret_cast<const uint64_t*>(a.scratch + (uint64_t)row * a.scratch_stride);
-        const uint32_t cnt = sh.tail_count;
-        for (uint32_t i = tid; i < cnt; i += kThreads) sh.sk[P + i] = ld_agent(list + i);
-        __syncthreads();
-        // S ranks below every candidate: sorted on its own, it follows them.
-        const uint32_t P2 = P + sort_candidates(sh, cnt, 0ull, (uint32_t)(R >> 32), kNone, P);
-        if (tid == 0) sh.prefix = P2;
-        keep = P2;
-        status |= AS_ROW_TAIL_PASS;
-        __syncthreads();
-      } else if (jl == P && !im_exact && !a.kept_ids) {
-        // Neither filter stops among the P sorted values: the kept set runs past them.
-        if (tid == 0) {
-          sh.x1 = x1;
-          sh.eps1 = eps1;
-          sh.r_prefix = r_prefix;
-        }
-        __syncthreads();
-        // S's sums when the row was flagged; else the sorted values alone first, and one
-        // pass over the row when they cannot settle the draw.
-        uint32_t j;
-        if (sh.have_tail) {
-          status |= AS_ROW_TAIL_PASS;
-          j = draw_past(a, a.params[row], row, P, true, true);
-        } else {
-          j = draw_past(a, a.params[row], row, P, false, false);
-          // With the deep passes shared (a small batch), a row they would settle takes them at once
-          // rather than one workgroup's pass over the row first.
-          if (j == kNone && !a.deep_help &&
-              tail_sums(a, a.params[row], row, R, has_floor ? floor_f32(floor) : -__builtin_inff(),
-                        key_value(sh.mk))) {
-            status |= AS_ROW_TAIL_PASS;
-            j = draw_past(a, a.params[row], row, P, true, false);
+          if (j != kNone && j < P) {
+            if (tid == 0) sh.pick = j;  // sh.sum holds the sorted weight
+            drawn = true;
+            keep = P;  // a lower bound: the kept set's full size is not known
+            status |= AS_ROW_KEPT_PARTIAL;
+          } else {
+            keep = kNone;
           }
-        }
-        if (j != kNone && j < P) {
-          if (tid == 0) sh.pick = j;  // sh.sum holds the sorted weight
-          drawn = true;
-          keep = P;  // a lower bound: the kept set's full size is not known
-          status |= AS_ROW_KEPT_PARTIAL;
+          __syncthreads();
         } else {
           keep = kNone;
         }
-        __syncthreads();
       } else {
-        keep = kNone;
-      }
-    } else {
-      // No filter (sample.rs:274-292): the total over the row in index order, from the segments'
-      // sums with an error bound, then the first rank whose cumulative weight passes u.
-      double X, eps;
-      slices_total(a, sh, top, temp, true, &X, &eps);
-      for (uint32_t i = tid; i < P; i += kThreads) sh.wd[i] = w_temp(val(i));
-      __syncthreads();
-      keep = kNone;
-      if (X - eps > 0.0 && eps == eps) {
-        double loc[kScanPer], off;
-        prefix_scan(sh, P, loc, &off);
-        const uint32_t j = decide_draw(sh, P, loc, off, sh.u01 * (X - eps) * (1.0 - 3.0 * kU),
-                                       sh.u01 * (X + eps) * (1.0 + 3.0 * kU));
-        uint32_t pick = kNone;
-        if (j != kNone && j < P) pick = j;
-        else if (j == P && complete) pick = n - 1;  // u past every cumulative: the last value
-        if (pick != kNone) {
-          if (tid == 0) {
-            sh.pick = pick;
-            sh.sum = X;
-          }
-          drawn = true;
-          keep = n;
-        }
+        // No filter (sample.rs:274-292): the total over the row in index order, from the segments'
+        // sums with an error bound, then the first rank whose cumulative weight passes u.
+        double X, eps;
+        slices_total(a, sh, top, temp, true, &X, &eps);
+        for (uint32_t i = tid; i < P; i += kThreads) sh.wd[i] = w_temp(val(i));
         __syncthreads();
+        keep = kNone;
+        if (X - eps > 0.0 && eps == eps) {
+          double loc[kScanPer], off;
+          prefix_scan(sh, P, loc, &off);
+          const uint32_t j = decide_draw(sh, P, loc, off, sh.u01 * (X - eps) * (1.0 - 3.0 * kU),
+                                         sh.u01 * (X + eps) * (1.0 + 3.0 * kU));
+          uint32_t pick = kNone;
+          if (j != kNone && j < P) pick = j;
+          else if (j == P && complete) pick = n - 1;  // u past every cumulative: the last value
+          if (pick != kNone) {
+            if (tid == 0) {
+              sh.pick = pick;
+              sh.sum = X;
+            }
+            drawn = true;
+            keep = n;
+          }
+          __syncthreads();
+        }
       }
+
     }
 
     if (keep != kNone && !drawn) {
@@ -3361,7 +3537,7 @@ __device__ __forceinline__ void finish_row(const FinishArgs& a, uint32_t row) {
     // the same depth, so that the kernel's stack is the largest of theirs, not their sum.
     __syncthreads();
     // A flagged row's parts write its scratch: they have all ended before the passes below use it.
-    if (!a.fused && sh.tail_slot != kNone && !sh.tail_waited) tail_wait(a, row);
+    if (sh.tail_slot != kNone && !sh.tail_waited) tail_wait(a, row);
     const RowParams& pr = a.params[row];
     const bool pen = deep_prep(a, pr, row);
     bool done = false;

@@ -44,9 +44,11 @@ __host__ __device__ constexpr uint64_t scratch_words(uint32_t n) {
   return (head + (bufs > shared ? bufs : shared) + 3) & ~3ull;
 }
 
-// The finish kernel's arguments and the rows' parameter blocks travel together, in one pinned host
-// block: FinishArgs in the first kArgsSlot bytes, then RowParams per row. The scan reads it where
-// the host wrote it and copies it to device memory for the finish kernel.
+// The finish kernel's arguments reach the GPU as the scan's kernel argument; the scan's first
+// workgroup stores them in device memory, where every finish workgroup reads them. The rows'
+// parameter blocks live in device memory across calls: the host uploads a call's blocks only when
+// they differ from the ones already there (a request's settings rarely change between steps), and
+// the scan reads them with scalar loads.
 constexpr uint32_t kArgsSlot = 320;
 
 struct FinishArgs {
@@ -72,24 +74,23 @@ struct FinishArgs {
   uint32_t vec;             // the rows are 16-byte aligned (float4 loads)
   uint32_t* scratch;        // deep and exact paths: scratch_words(n) u32 per row
   uint64_t scratch_stride;  // u32 per row
-  uint64_t* done;           // pinned host word: the call number whose scan has ended (the host
-  uint64_t call;            //   reuses a parameter block once its call's scan is over)
+  uint64_t* done;           // pinned host word: the number of the last call whose finish kernel
+  uint64_t call;            //   has started (the host reuses an upload's staging block after it)
   as_dev::RowTail* tail;    // per row: S's sums (min-p rows whose scan gave up)
   as_dev::TailBins* tail_bins;  // per row: S's histogram
   as_dev::TailList* tail_list;  // the rows this call's scan flagged for S's sums
   as_dev::TailList* tail_next;  // the next call's list (cleared by this call's finish kernel)
   uint64_t* tail_claims;    // per helper of S's sums: the number of the last call that claimed its set
   uint32_t max_history;     // a row with more history ids than this is refused (AS_ROW_HISTORY)
-  uint32_t fused;           // the row kernel: each workgroup scans and finishes its own row
-  uint32_t* fused_count;    // the row kernel: workgroups that have ended (the last writes `done`)
   uint32_t n_rows;          // rows of the call
   uint32_t deep_help;       // the deep path's passes are shared with idle workgroups (small batches)
   as_dev::DeepJob* deep_jobs;  // per row
   uint64_t* deep_done;      // rows finished, over every call of the context
   uint64_t deep_target;     // deep_done once this call's rows are finished
   uint32_t rng_rows;        // row r draws from RNG state r (as_sample): its state loads without its parameters
-  uint32_t pad2_;
+  uint32_t pad2_[3];
 };
+static_assert(sizeof(FinishArgs) <= kArgsSlot && kArgsSlot % 16 == 0, "FinishArgs slot");
 
 // The row's history ids are hist_ids[*hb, return value), from the CSR offsets or the row's range.
 __device__ __forceinline__ uint32_t history_bounds(const FinishArgs& a, const as_dev::RowParams& p,
@@ -130,12 +131,13 @@ struct RowOrder {
 
 // n_seg slices of slice_len values per row (the last one shorter).
 // zero: 1,024 readable floats (the loads of a wave with no full chunk of its slice read there).
-// block_in: the pinned host block (arguments, then n_rows RowParams); block_out: its device copy.
+// params: the rows' parameter blocks (device memory); args: the finish kernel's arguments, which the
+// first workgroup stores at args_out.
 hipError_t scan(hipStream_t stream, bool vec, const float* logits, const float* zero, uint64_t row_stride,
-                uint32_t n, uint32_t n_rows, uint32_t n_seg, uint32_t slice_len, const void* block_in,
-                void* block_out, as_dev::RowShare* share, const uint32_t* hist_off, const uint32_t* hist_ids,
-                const uint32_t* extra_ids, as_dev::SegStats* stats, uint64_t* cands, uint32_t cand_stride,
-                as_dev::TailList* tail_list, const RowOrder& order);
+                uint32_t n, uint32_t n_rows, uint32_t n_seg, uint32_t slice_len, const as_dev::RowParams* params,
+                const FinishArgs& args, FinishArgs* args_out, as_dev::RowShare* share, const uint32_t* hist_off,
+                const uint32_t* hist_ids, const uint32_t* extra_ids, as_dev::SegStats* stats, uint64_t* cands,
+                uint32_t cand_stride, as_dev::TailList* tail_list, const RowOrder& order);
 
 // A call of at most kDeepHelpRows rows, any of which may take the deep path, runs kTailGroups
 // workgroups: those past its rows, and each row's once its row is done, take parts of the rows' deep
@@ -144,19 +146,6 @@ constexpr uint32_t kDeepHelpRows = 16;
 // groups: the call's rows, or more (the workgroups past them only take parts of S's sums and of the
 // deep passes).
 hipError_t finish(hipStream_t stream, uint32_t groups, const FinishArgs* a);
-
-// The row kernel (fused.hip): one 512-thread workgroup scans a whole row and chooses its token, for
-// rows of at most kRowMaxVocab values (its history bitmap lives in LDS). Batches of at least
-// kRowMinRows rows would take it by default; that is off (the sliced scan is faster on mixed batches,
-// where rows whose draw runs past their sorted values need a second pass that one workgroup makes
-// slowly), so it runs when a caller asks for it (as_debug_path).
-constexpr uint32_t kRowMaxVocab = 262144;
-constexpr uint32_t kRowMinRows = 0xFFFFFFFFu;
-hipError_t sample_rows(hipStream_t stream, bool vec, const float* logits, const float* zero, uint64_t row_stride,
-                       uint32_t n, uint32_t n_rows, const void* block_in, void* block_out, as_dev::RowShare* share,
-                       const uint32_t* hist_off, const uint32_t* hist_ids, const uint32_t* extra_ids,
-                       as_dev::SegStats* stats, uint64_t* cands, uint32_t cand_stride, const FinishArgs& a);
-size_t row_kernel_lds();
 
 // Log-probabilities (logprobs.hip): rows in parts, each part's 20 best and sums. Parts of kLpPart
 // values spread a part kernel's per-wave work over the most values its registers hold; a call whose

@@ -71,8 +71,9 @@ struct RowParams {
   uint32_t extra;       // ids of the extra list appended to the history (verify drafts)
   uint32_t cap;         // candidate slots per slice (slices x cap fit the finish LDS)
   uint32_t help;        // the row's place among the finish kernel's helpers of S's sums (cheapest first)
+  uint32_t pad_;        // zero: the host compares blocks byte for byte
 };
-static_assert(sizeof(RowParams) % 16 == 0, "whole 16-byte words");
+static_assert(sizeof(RowParams) == 80 && sizeof(RowParams) % 16 == 0, "whole 16-byte words, no implicit padding");
 
 // A row's words that its slices share during a scan, in device memory; zero before the scan (the
 // context clears them once, and the finish kernel clears its row's after each scan).

@@ -41,18 +41,27 @@ using namespace as_dev;
 
 namespace {
 
-// The sliced scan: workgroup (x, y) scans slice x of row r[y] (rows in the host's order).
+// The sliced scan: workgroup (x, y) scans slice x of row r[y] (rows in the host's order). The
+// finish kernel's arguments arrive here by value (the scan reads none of them) and the first
+// workgroup stores them where the finish kernel reads them.
 template <bool kVec>
 __global__ __launch_bounds__(256, 3) void scan_kernel(
     const float* __restrict__ logits, const float* __restrict__ zero, uint64_t row_stride, uint32_t n,
-    uint32_t n_seg, uint32_t slice_len, const uint32_t* block_in, uint32_t* __restrict__ block_out,
-    RowShare* share, const uint32_t* __restrict__ hist_off, const uint32_t* __restrict__ hist_ids,
+    uint32_t n_seg, uint32_t slice_len, const RowParams* __restrict__ params, RowShare* share,
+    const uint32_t* __restrict__ hist_off, const uint32_t* __restrict__ hist_ids,
     const uint32_t* __restrict__ extra_ids, SegStats* __restrict__ stats, uint64_t* __restrict__ cands,
-    uint32_t cand_stride, TailList* tail_list, as_launch::RowOrder order) {
+    uint32_t cand_stride, TailList* tail_list, as_launch::FinishArgs* __restrict__ args_out,
+    const as_launch::FinishArgs args, const as_launch::RowOrder order) {
   const uint32_t row = order.on ? (uint32_t)order.r[blockIdx.y] : blockIdx.y;
-  as_scan_sliced::scan_slice<kVec>(logits, zero, row_stride, n, n_seg, slice_len, block_in, block_out, share,
-                                   hist_off, hist_ids, extra_ids, stats, cands, cand_stride, tail_list, row,
-                                   blockIdx.x);
+  as_scan_sliced::scan_slice<kVec>(logits, zero, row_stride, n, n_seg, slice_len, params, share, hist_off, hist_ids,
+                                   extra_ids, stats, cands, cand_stride, tail_list, row, blockIdx.x);
+  // After the slice, so that reading the argument delays none of the slice's loads.
+  if (blockIdx.x == 0 && blockIdx.y == 0) {
+    constexpr uint32_t kWords = sizeof(as_launch::FinishArgs) / 4;
+    static_assert(kWords <= 256, "one word per thread");
+    if (threadIdx.x < kWords)
+      reinterpret_cast<uint32_t*>(args_out)[threadIdx.x] = reinterpret_cast<const uint32_t*>(&args)[threadIdx.x];
+  }
 }
 
 }  // namespace
@@ -60,19 +69,19 @@ __global__ __launch_bounds__(256, 3) void scan_kernel(
 namespace as_launch {
 
 hipError_t scan(hipStream_t stream, bool vec, const float* logits, const float* zero, uint64_t row_stride,
-                uint32_t n, uint32_t n_rows, uint32_t n_seg, uint32_t slice_len, const void* block_in,
-                void* block_out, as_dev::RowShare* share, const uint32_t* hist_off, const uint32_t* hist_ids,
-                const uint32_t* extra_ids, as_dev::SegStats* stats, uint64_t* cands, uint32_t cand_stride,
-                as_dev::TailList* tail_list, const RowOrder& order) {
+                uint32_t n, uint32_t n_rows, uint32_t n_seg, uint32_t slice_len, const RowParams* params,
+                const FinishArgs& args, FinishArgs* args_out, RowShare* share, const uint32_t* hist_off,
+                const uint32_t* hist_ids, const uint32_t* extra_ids, SegStats* stats, uint64_t* cands,
+                uint32_t cand_stride, TailList* tail_list, const RowOrder& order) {
   dim3 grid(n_seg, n_rows);
-  const uint32_t* in = static_cast<const uint32_t*>(block_in);
-  uint32_t* out = static_cast<uint32_t*>(block_out);
   if (vec)
-    hipLaunchKernelGGL(scan_kernel<true>, grid, dim3(256), 0, stream, logits, zero, row_stride, n, n_seg,
-                       slice_len, in, out, share, hist_off, hist_ids, extra_ids, stats, cands, cand_stride, tail_list, order);
+    hipLaunchKernelGGL(scan_kernel<true>, grid, dim3(256), 0, stream, logits, zero, row_stride, n, n_seg, slice_len,
+                       params, share, hist_off, hist_ids, extra_ids, stats, cands, cand_stride, tail_list, args_out,
+                       args, order);
   else
-    hipLaunchKernelGGL(scan_kernel<false>, grid, dim3(256), 0, stream, logits, zero, row_stride, n, n_seg,
-                       slice_len, in, out, share, hist_off, hist_ids, extra_ids, stats, cands, cand_stride, tail_list, order);
+    hipLaunchKernelGGL(scan_kernel<false>, grid, dim3(256), 0, stream, logits, zero, row_stride, n, n_seg, slice_len,
+                       params, share, hist_off, hist_ids, extra_ids, stats, cands, cand_stride, tail_list, args_out,
+                       args, order);
   return hipGetLastError();
 }
 

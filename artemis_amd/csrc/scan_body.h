@@ -5,9 +5,7 @@
 //   AS_SCAN_HASH       LDS hash slots for the slice's distinct history ids (a multiple of the threads),
 //   AS_SCAN_SLICE_MAX  the longest slice (its history bitmap lives in LDS),
 //   AS_SCAN_DEPTH      chunk buffers per wave (the loads of all but one are in flight),
-// optionally AS_SCAN_SHARE_LDS (one workgroup per row: the row's shared words live in its LDS),
-// and, for a kernel that shares its LDS with another body, AS_DYNAMIC_LDS with the kernel's dynamic
-// LDS declared as `as_dyn_lds`. The entry point is AS_SCAN_NS::scan_slice.
+// The entry point is AS_SCAN_NS::scan_slice.
 namespace {
 namespace AS_SCAN_NS {
 
@@ -29,11 +27,7 @@ constexpr uint32_t kFirstRankPartial = 16;
 // Waves read the row's shared words once per kShareEvery chunks (an even number): the read is an
 // agent-scope load, slower than the stream's own, and loads complete in order, so each read delays
 // the chunk loaded after it (measured: every two chunks cost ~7 us per top-k slice over every eight).
-#ifdef AS_SCAN_SHARE_EVERY
-constexpr uint32_t kShareEvery = AS_SCAN_SHARE_EVERY;
-#else
 constexpr uint32_t kShareEvery = 8;
-#endif
 static_assert(kShareEvery % 2 == 0, "reads fall on the loop's odd chunks");
 constexpr uint32_t kHash = AS_SCAN_HASH;
 constexpr int kHashPer = (kHash + kThreads - 1) / kThreads;  // hash slots per thread (the last may be short)
@@ -70,19 +64,11 @@ struct Shared {
   uint32_t hist_out;
   uint32_t overflow;
   uint32_t out_n;  // candidates the waves have written to HBM during the stream
-  RowParams prm;   // the row's parameters, as read from the host block
-#ifdef AS_SCAN_SHARE_LDS
-  RowShare lshare;  // the row's shared words, when this workgroup scans the whole row
-#endif
+  RowParams prm;   // the row's parameters
 };
-// The workgroup's LDS, at file scope so that the out-of-line helpers below address it directly: a
-// static array, or the kernel's dynamic LDS (AS_DYNAMIC_LDS) when another body shares it.
-#ifdef AS_DYNAMIC_LDS
-__device__ __forceinline__ Shared& shm() { return *reinterpret_cast<Shared*>(as_dyn_lds); }
-#else
+// The workgroup's LDS, at file scope so that the out-of-line helpers below address it directly.
 __shared__ Shared g_sh_static;
 __device__ __forceinline__ Shared& shm() { return g_sh_static; }
-#endif
 
 __device__ __forceinline__ uint32_t lanes_below(uint64_t m) {
   return __builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0u));
@@ -95,14 +81,9 @@ __device__ __forceinline__ uint64_t wave_min_u64(uint64_t v) {
   return v;
 }
 
-// The row's shared words (RowShare::bound, top, the slots): at device scope in HBM when a row's
-// slices run on different XCDs; in the workgroup's LDS (AS_SCAN_SHARE_LDS) when one workgroup scans
-// the whole row, where they cost an LDS access instead of a trip to memory.
-#ifdef AS_SCAN_SHARE_LDS
-constexpr int kShareScope = __HIP_MEMORY_SCOPE_WORKGROUP;
-#else
+// The row's shared words (RowShare::bound, top, the slots) live in device memory and are accessed at
+// agent scope: a row's slices run on different XCDs.
 constexpr int kShareScope = __HIP_MEMORY_SCOPE_AGENT;
-#endif
 __device__ __forceinline__ void publish(uint32_t* word, uint32_t key) {
   if (word && (threadIdx.x & (kWave - 1)) == 0) __hip_atomic_fetch_max(word, key, __ATOMIC_RELAXED, kShareScope);
 }
@@ -366,9 +347,10 @@ __device__ __forceinline__ uint32_t wave_qth(uint32_t x, uint32_t q) {
 }
 
 // The largest unmasked value of the wave's first chunk sets min-p's first floor. When more than one
-// in a hundred of the chunk's values pass it (a floor set of thousands: appending each value above
-// it would cost more than keeping the best few hundred), the wave keeps its best kPartialRank like a
-// row without min-p instead of every value above the floor (which still applies).
+// in a hundred of the chunk's values pass it (a floor set of thousands, or a first chunk whose
+// largest value lies far below the row's: appending each value above it would cost more than
+// keeping the best few hundred), the wave keeps its best kPartialRank like a row without min-p
+// instead of every value above the floor (which still applies).
 __device__ __forceinline__ WaveState first_floor(WaveState ws, f32x4 v0, f32x4 v1, f32x4 v2, f32x4 v3,
                                               uint32_t masked, uint32_t e0, double ln_min_p, uint32_t* share) {
   const f32x4 v[kU] = {v0, v1, v2, v3};
@@ -607,10 +589,24 @@ struct Walk {
   uint32_t c0, nfull;
 };
 
+// One set of load instructions whatever the case (the base address is selected): two sets writing
+// different registers would be merged by copies, which wait for every load in flight.
 template <bool kVec>
 __device__ __forceinline__ void load_at(f32x4 (&q)[kU], const Slice& sl, const Walk& wk, uint32_t i) {
-  if (wk.nfull) load_chunk<kVec>(q, sl.x, wk.c0 + min(i, wk.nfull - 1) * kGroupStep);
-  else load_chunk<kVec>(q, sl.zero, 0);
+  const float* base = wk.nfull ? sl.x + (wk.c0 + min(i, wk.nfull - 1) * kGroupStep) : sl.zero;
+  load_chunk<kVec>(q, base, 0);
+}
+
+// The row's parameter block by scalar loads (a constant-address-space view of device memory): they
+// count against their own wait counter, so reading them does not wait for the chunk loads in flight.
+__device__ __forceinline__ RowParams load_params(const RowParams* p) {
+  struct Words {
+    uint32_t w[sizeof(RowParams) / 4];
+  } r;
+  const __attribute__((address_space(4))) uint32_t* q = (const __attribute__((address_space(4))) uint32_t*)p;
+#pragma unroll
+  for (uint32_t i = 0; i < sizeof(RowParams) / 4; ++i) r.w[i] = q[i];
+  return __builtin_bit_cast(RowParams, r);
 }
 
 // Lane i < n_slots reads the row's slot i (others: all ones, so that the wave's minimum is the slots').
@@ -679,13 +675,13 @@ __device__ __forceinline__ void stream(Lane& ln, WaveState& ws, const Slice& sl,
   }
 }
 
-// One slice (seg) of one row: the body of the scan kernels. tail_list may be null (the rows whose
+// One slice (seg) of one row: the body of the scan kernel. tail_list may be null (the rows whose
 // slices give up keeping min-p's floor set are then not listed).
 template <bool kVec>
 __device__ __forceinline__ void scan_slice(
     const float* __restrict__ logits, const float* __restrict__ zero, uint64_t row_stride, uint32_t n,
-    uint32_t n_seg, uint32_t slice_len, const uint32_t* block_in, uint32_t* __restrict__ block_out,
-    RowShare* share, const uint32_t* __restrict__ hist_off, const uint32_t* __restrict__ hist_ids,
+    uint32_t n_seg, uint32_t slice_len, const RowParams* __restrict__ params, RowShare* share,
+    const uint32_t* __restrict__ hist_off, const uint32_t* __restrict__ hist_ids,
     const uint32_t* __restrict__ extra_ids, SegStats* __restrict__ stats, uint64_t* __restrict__ cands,
     uint32_t cand_stride, TailList* tail_list, uint32_t row, uint32_t seg) {
   Shared& sh = shm();
@@ -694,83 +690,60 @@ __device__ __forceinline__ void scan_slice(
   // keeps the stream's loop control in scalar registers only when it knows them uniform.
   const uint32_t lane = tid & (kWave - 1), w = __builtin_amdgcn_readfirstlane(tid / kWave);
 
-  // The row's parameters, read where the host wrote them (pinned memory, read with system-scope
-  // loads so that no cache serves an earlier call's), into LDS; the row's first slice also copies
-  // them to device memory for the finish kernel, and the first workgroup copies its arguments.
-  constexpr uint32_t kArgWords = as_launch::kArgsSlot / 4, kRowWords = sizeof(RowParams) / 4;
-  static_assert(kRowWords <= kThreads && kArgWords <= kThreads, "one word per thread");
-  {
-    const uint32_t base = kArgWords + row * kRowWords;
-    if (tid < kRowWords) {
-      const uint32_t v = __hip_atomic_load(block_in + base + tid, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
-      reinterpret_cast<uint32_t*>(&sh.prm)[tid] = v;
-      if (seg == 0) block_out[base + tid] = v;
-    }
-    if (seg == 0 && row == 0 && tid < kArgWords)
-      block_out[tid] = __hip_atomic_load(block_in + tid, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
-  }
-
   Slice sl;
   sl.x = logits + (uint64_t)row * row_stride;
   sl.zero = zero;
-#ifdef AS_SCAN_SHARE_LDS
-  sl.share = &sh.lshare.bound;
-#else
   sl.share = &share[row].bound;
-#endif
   sl.b0 = seg * slice_len;
   sl.out = cands + ((uint64_t)row * n_seg + seg) * cand_stride;
   sl.room = cand_stride > as_launch::kHistReserve ? cand_stride - as_launch::kHistReserve : 0u;
   sl.b1 = min(sl.b0 + slice_len, n);
   const uint32_t len = sl.b1 - sl.b0;
+  Walk wk;
+  wk.c0 = sl.b0 + w * kChunk;
+  wk.nfull = (wk.c0 + kChunk <= sl.b1) ? (sl.b1 - wk.c0 - kChunk) / kGroupStep + 1 : 0;
 
-  // In flight with the parameters: the first history ids (kHistRegs per thread; a CSR history is
-  // read before the parameters say whether penalties act), then the wave's first two chunks; the
-  // ids come back first and the LDS tables are built while the chunks arrive.
+  // The set-up, in the order its loads are issued. Every wave's first chunk goes first: at the
+  // start of a call the whole GPU's first chunks take a few microseconds to arrive, and everything
+  // below happens meanwhile. The parameters and the history's bounds come by scalar loads, which do
+  // not wait for the chunk. The history ids follow the first chunk and come back before the second,
+  // so that the LDS tables are built while the second is on its way.
+  f32x4 q[kDepth][kU];
+  load_at<kVec>(q[0], sl, wk, 0u);
+  const RowParams p = load_params(params + row);
   uint32_t hb = 0, he = 0;
-  if (hist_ids && hist_off) {
-    hb = hist_off[row];
-    he = hist_off[row + 1];
+  if (hist_ids) {
+    if (hist_off) {
+      hb = hist_off[row];
+      he = hist_off[row + 1];
+    } else {
+      hb = p.hist_begin;
+      he = p.hist_begin + p.hist_len;
+    }
   }
+  const uint32_t extra = extra_ids ? p.extra : 0;
+  sl.pen = (p.flags & kFlagPenalties) && (he > hb || extra > 0);
   constexpr int kHistRegs = 8;
   uint32_t hreg[kHistRegs];
 #pragma unroll
   for (int k = 0; k < kHistRegs; ++k) {
     const uint32_t h = hb + tid + k * kThreads;
-    hreg[k] = (h < he) ? hist_ids[h] : kEmpty;
+    hreg[k] = (sl.pen && h < he) ? hist_ids[h] : kEmpty;
   }
-  Walk wk;
-  wk.c0 = sl.b0 + w * kChunk;
-  wk.nfull = (wk.c0 + kChunk <= sl.b1) ? (sl.b1 - wk.c0 - kChunk) / kGroupStep + 1 : 0;
-  f32x4 q[kDepth][kU];
 #pragma unroll
-  for (int d = 0; d < kDepth; ++d) load_at<kVec>(q[d], sl, wk, (uint32_t)d);
+  for (int d = 1; d < kDepth; ++d) load_at<kVec>(q[d], sl, wk, (uint32_t)d);
   if (tid == 0) {
+    sh.prm = p;
     sh.hist_out = 0;
     sh.overflow = 0;
     sh.out_n = 0;
   }
-#ifdef AS_SCAN_SHARE_LDS
-  if (tid < sizeof(RowShare) / 4) reinterpret_cast<uint32_t*>(&sh.lshare)[tid] = 0u;
-#endif
-  // The history tables start empty (cleared while the parameters are on their way).
-  if (hist_ids || extra_ids) {
+  // The history tables start empty.
+  if (sl.pen) {
     for (uint32_t i = tid; i < (len + 31) / 32; i += kThreads) sh.bitmap[i] = 0;
     for (uint32_t i = tid; i < kHash; i += kThreads) {
       sh.hid[i] = kEmpty;
       sh.hcnt[i] = 0;
-    }
-  }
-  __syncthreads();  // the parameters are in LDS, the tables clear
-
-  const RowParams& p = sh.prm;
-  if (hist_ids && !hist_off) {
-    hb = p.hist_begin;
-    he = p.hist_begin + p.hist_len;
-#pragma unroll
-    for (int k = 0; k < kHistRegs; ++k) {
-      const uint32_t h = hb + tid + k * kThreads;
-      hreg[k] = (h < he) ? hist_ids[h] : kEmpty;
     }
   }
   const uint32_t mode = p.mode, flags = p.flags;
@@ -787,16 +760,11 @@ __device__ __forceinline__ void scan_slice(
   sl.first = mode == kModeTopK ? sl.C <= 2u * kWave : true;
   sl.first_rank = mode == kModeTopK ? sl.C : kFirstRankPartial;
   // Top-k rows: the first min(waves of the row, kShareSlots) waves each own a slot.
-#ifdef AS_SCAN_SHARE_LDS
-  sl.slots = sh.lshare.slot;
-#else
   sl.slots = share[row].slot;
-#endif
   sl.n_slots = (mode == kModeTopK && sl.first) ? min(n_seg * kWaves, kShareSlots) : 0u;
   sl.q = sl.n_slots ? (p.top_k + sl.n_slots - 1) / sl.n_slots : 0u;
   sl.my_slot = (seg * kWaves + w < sl.n_slots) ? sl.slots + seg * kWaves + w : nullptr;
-  const uint32_t extra = extra_ids ? p.extra : 0;
-  sl.pen = (flags & kFlagPenalties) && (he > hb || extra > 0);
+  __syncthreads();  // the tables clear, the parameters in LDS
 
   if (sl.pen) {
     auto mark = [&](uint32_t id) {
@@ -875,7 +843,7 @@ __device__ __forceinline__ void scan_slice(
     hpk[k] = 0;
     hidv[k] = (sl.pen && own_slot(tid, k)) ? sh.hid[tid + k * kThreads] : kEmpty;
     if (hidv[k] != kEmpty) {
-      const float v = penalize(hx[k], sh.hcnt[tid + k * kThreads], p);
+      const float v = penalize(hx[k], sh.hcnt[tid + k * kThreads], sh.prm);
       const uint32_t key = total_key(v);
       hpk[k] = pack(key, hidv[k]);
       hkey_max = max(hkey_max, key);

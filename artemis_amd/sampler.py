@@ -110,7 +110,6 @@ def lib() -> C.CDLL:
         L.as_head_argmax.argtypes = [vp, vp, u32, u32, u32, vp, vp, vp, vp, u64, u32, u32]
         L.as_debug_exp.argtypes = [vp, vp, vp, u32]
         L.as_debug_exp2f.argtypes = [vp, vp, vp, u32]
-        L.as_debug_path.argtypes = [vp, C.c_int]
         L.as_logprobs.argtypes = [vp, vp, u64, u32, u32, vp, u32, vp, vp, vp, vp]
         L.as_logprobs_static.argtypes = [vp, vp, u64, u32, u32, vp, u32, vp, vp, vp, vp, C.c_char_p, C.c_size_t]
         L.as_profile.argtypes = [vp, C.c_int]
@@ -367,11 +366,6 @@ class Context:
         a, b, k = C.c_double(), C.c_double(), C.c_uint32()
         self._ok(lib().as_profile_read(self.h, C.byref(a), C.byref(b), C.byref(k)))
         return a.value, b.value, k.value
-
-    def debug_path(self, path: int):
-        """Forces as_sample / as_verify's kernels: 0 the default, 1 rows spread over several
-        workgroups, 2 one workgroup per row (as_debug_path)."""
-        self._ok(lib().as_debug_path(self.h, path))
 
     def debug_exp(self, x: torch.Tensor) -> torch.Tensor:
         y = torch.empty_like(x)

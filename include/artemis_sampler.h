@@ -224,11 +224,6 @@ int as_profile_read(as_ctx* ctx, double* scan_ms, double* finish_ms, uint32_t* c
 
 /* Diagnostics: y[i] = exp(x[i]) on the GPU with the sampler's f64 exp (device arrays). */
 int as_debug_exp(as_ctx* ctx, const double* x, double* y, uint32_t n);
-/* Diagnostics: which kernels as_sample and as_verify take on this context: 0 the default (rows
- * spread over several workgroups), 1 the same, forced, 2 one workgroup per row that scans and
- * finishes it in one launch (rows of at most 262,144 values). The tokens are the same either way;
- * the tests run both. */
-int as_debug_path(as_ctx* ctx, int path);
 /* Diagnostics: y[i] = 2^x[i] by the GPU instruction the scan's error-bounded sums use. */
 int as_debug_exp2f(as_ctx* ctx, const float* x, float* y, uint32_t n);
 

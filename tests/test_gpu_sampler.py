@@ -19,19 +19,12 @@ PROB_RTOL = 1e-5
 VOCAB = 248_320
 
 
-# Every test runs on both kernel paths: rows spread over several workgroups (the sliced scan, then
-# the finish kernel) and one workgroup per row (the row kernel), whatever the batch size.
-PATHS = {"sliced": 1, "row": 2}
-
-
-@pytest.fixture(scope="module", params=list(PATHS), ids=list(PATHS))
-def ctx(request):
+@pytest.fixture(scope="module")
+def ctx():
     if not torch.cuda.is_available():
         pytest.skip("no GPU")
     from artemis_amd import Context
     c = Context(max_rows=1024, max_vocab=VOCAB)
-    c.debug_path(PATHS[request.param])
-    c.test_path = request.param
     yield c
     c.close()
 
@@ -232,9 +225,10 @@ def test_config5_batch(ctx):
 
 def test_draws_past_the_sorted_values_match_the_oracle(ctx):
     # A row whose kept set runs far past the values the finish kernel sorts (top-p keeps ~16,500
-    # values, min-p's floor ~111,000), drawn under many seeds: some draws fall within the tail's
-    # first bound and take the pass that bounds the unsorted weight, others the deep path; every
-    # token and stream must be the oracle's. Also with only the floor cutting, and with T > 1.
+    # values, min-p's floor ~111,000), drawn under many seeds: most draws are settled from the sorted
+    # values and a bound on the rest (the fast decision), some take S's sums, others the deep path;
+    # every token and stream must be the oracle's. Also with only the floor cutting (no row total for
+    # the fast decision: S's sums bound the tail), and with T > 1.
     from artemis_amd import AS_ROW_TAIL_PASS, workloads
     w = workloads.config5()
     r = 111
@@ -256,15 +250,16 @@ def test_draws_past_the_sorted_values_match_the_oracle(ctx):
     bad = np.nonzero(g["tokens"] != want)[0]
     assert len(bad) == 0, [(int(i), params[i], int(g["tokens"][i]), int(want[i]), int(g["status"][i])) for i in bad[:5]]
     assert (g["rng"] == rng).all()
-    assert (g["status"][:48] & AS_ROW_TAIL_PASS).any(), g["status"][:48]
+    assert (g["status"][48:96] & AS_ROW_TAIL_PASS).any(), g["status"][48:96]
 
 
 def test_tail_histogram_draws_match_the_oracle(ctx):
     # The finish kernel sums S for the first 16 flagged rows of a call and bins S by value;
     # the finish kernel places top-p's cut within one bin and draws past the sorted values from
-    # those bounds. Config 5's row 111 (top-p keeps ~16,500 values, min-p's floor ~111,000) under
-    # many seeds, 16 rows a call so that every row takes that path (and with T > 1, where the bins
-    # alone bound the kept tail from below): tokens and streams must be the oracle's.
+    # those bounds when the fast decision (the sorted values and a bound on the rest) cannot.
+    # Config 5's row 111 (top-p keeps ~16,500 values, min-p's floor ~111,000) under many seeds, 16
+    # rows a call so that every row is flagged (and with T > 1, where the bins alone bound the kept
+    # tail from below): tokens and streams must be the oracle's.
     from artemis_amd import AS_ROW_DEEP_PATH, AS_ROW_KEPT_PARTIAL, AS_ROW_TAIL_PASS, workloads
     w = workloads.config5()
     r = 111
@@ -291,24 +286,22 @@ def test_tail_histogram_draws_match_the_oracle(ctx):
                                    for i in bad[:5]]
             assert (g["rng"] == rng).all()
             st = g["status"]
-            seen[key] += int(((st & AS_ROW_TAIL_PASS) != 0).sum())
+            settled = ((st & (AS_ROW_TAIL_PASS | AS_ROW_KEPT_PARTIAL)) != 0) & ((st & AS_ROW_DEEP_PATH) == 0)
+            seen[key] += int(settled.sum())
             deep[key] += int(((st & AS_ROW_DEEP_PATH) != 0).sum())
-    # At the row's own T (0.36) every draw took S's sums and bins, and the bins
-    # settle nearly all of them (the first bound alone left about 1 in 20 to the deep path). At
+    # At the row's own T (0.36) every draw is settled past the sorted values, by the fast decision or
+    # by S's sums and bins (the first bound alone once left about 1 in 20 to the deep path). At
     # T = 1.3 the draw usually lands past the sorted values, which only the deep path can take.
-    # The row kernel does not sum S in parts: its rows bound the unsorted tail with the finish's own
-    # pass when the sorted values alone cannot (the tokens above are checked on both paths).
-    if ctx.test_path == "sliced":
-        assert seen[()] == 128, seen
-        assert deep[()] <= 3, deep
+    assert seen[()] + deep[()] == 128, (seen, deep)
+    assert deep[()] <= 3, deep
 
 
 def test_more_flagged_rows_than_the_list_holds(ctx):
     # 32 rows that the scan flags for S's sums (config 5's row 111 under many seeds), no kept lists:
     # more than the 16 the list holds, so nothing is shared. Each row draws from its sorted values
-    # when they settle the draw, else sums S in its own pass over the row (some rows under these
-    # seeds do). Tokens and streams must be the oracle's, and no row may need the deep path.
-    from artemis_amd import AS_ROW_DEEP_PATH, AS_ROW_TAIL_PASS, workloads
+    # when they settle the draw, else sums S in its own pass over the row. Tokens and streams must be
+    # the oracle's, and no row may need the deep path.
+    from artemis_amd import AS_ROW_DEEP_PATH, workloads
     w = workloads.config5()
     r = 111
     base = w.params[r]
@@ -323,9 +316,8 @@ def test_more_flagged_rows_than_the_list_holds(ctx):
     bad = np.nonzero(g["tokens"] != want)[0]
     assert len(bad) == 0, [(int(i), int(g["tokens"][i]), int(want[i]), int(g["status"][i])) for i in bad[:5]]
     assert (g["rng"] == rng).all()
-    if ctx.test_path == "sliced":
-        st = g["status"]
-        assert ((st & AS_ROW_TAIL_PASS) != 0).any() and not ((st & AS_ROW_DEEP_PATH) != 0).any(), st
+    st = g["status"]
+    assert not ((st & AS_ROW_DEEP_PATH) != 0).any(), st
 
 
 def test_large_floor_sets_match_the_oracle(ctx):
@@ -349,9 +341,8 @@ def test_large_floor_sets_match_the_oracle(ctx):
     want = oracle_rows(rows, params, seeds, hists, kept_cap=16)
     check_rows(g, want, params, kept_cap=16, label="floor sets")
     # S is summed in parts for the first 16 rows the scan flags (in the order it flags them); the finish
-    # kernel settles the rest. (The row kernel's sixteen waves keep such floor sets whole.)
-    if ctx.test_path == "sliced":
-        assert ((g["status"] & AS_ROW_TAIL_PASS) != 0).sum() >= 16, g["status"]
+    # kernel settles the rest.
+    assert ((g["status"] & AS_ROW_TAIL_PASS) != 0).sum() >= 16, g["status"]
 
 
 def test_whole_vocabulary_plants(ctx):

@@ -11,17 +11,12 @@ from oracle_lib import DEFAULT, GREEDY, Sampler
 pytestmark = pytest.mark.gpu
 
 
-# Both kernel paths: rows spread over several workgroups, and one workgroup per row.
-PATHS = {"sliced": 1, "row": 2}
-
-
-@pytest.fixture(scope="module", params=list(PATHS), ids=list(PATHS))
-def ctx(request):
+@pytest.fixture(scope="module")
+def ctx():
     if not torch.cuda.is_available():
         pytest.skip("no GPU")
     from artemis_amd import Context
     c = Context(max_rows=16, max_vocab=S.VOCAB)
-    c.debug_path(PATHS[request.param])
     yield c
     c.close()
 

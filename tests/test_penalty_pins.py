@@ -197,13 +197,12 @@ def test_oracle_history_order_duplicates_and_ids_past_the_row_do_not_matter(si):
 
 # ---- the same probes on the GPU, through the C ABI ------------------------------------------------
 
-def _gpu_ctx(path):
+def _gpu_ctx():
     torch = pytest.importorskip("torch")
     if not torch.cuda.is_available():
         pytest.skip("no GPU")
     from artemis_amd import Context
     ctx = Context(max_rows=512, max_vocab=N + 8)
-    ctx.debug_path(path)  # 1: rows spread over several workgroups, 2: one workgroup per row
     return torch, ctx
 
 
@@ -223,9 +222,8 @@ def _gpu_sample(torch, ctx, rows, params, hists, seeds):
 
 
 @pytest.mark.gpu
-@pytest.mark.parametrize("path", [1, 2], ids=["sliced", "row"])
-def test_gpu_penalised_values_are_the_fixed_ones(path):
-    torch, ctx = _gpu_ctx(path)
+def test_gpu_penalised_values_are_the_fixed_ones():
+    torch, ctx = _gpu_ctx()
     cases = all_cases()
     rows, params, hists, want = [], [], [], []
     for case in cases:
@@ -244,9 +242,8 @@ def test_gpu_penalised_values_are_the_fixed_ones(path):
 
 
 @pytest.mark.gpu
-@pytest.mark.parametrize("path", [1, 2], ids=["sliced", "row"])
-def test_gpu_history_order_duplicates_and_ids_past_the_row_match_the_oracle(path):
-    torch, ctx = _gpu_ctx(path)
+def test_gpu_history_order_duplicates_and_ids_past_the_row_match_the_oracle():
+    torch, ctx = _gpu_ctx()
     base, hists = invariance_rows()
     rows, params, hs, seeds = [], [], [], []
     for s in SETTINGS:
