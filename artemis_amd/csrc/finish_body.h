@@ -52,6 +52,11 @@ struct Shared {
   // The shared deep passes (deep_run, deep_help, deep_part).
   uint32_t dp_pick, dp_stop, dp_q, dp_base, dp_staged, dp_mk, dp_r[2 * 3];
   uint32_t dp_pub;  // this row published its histogram pass early (deep_publish_hist)
+  // The fast decision's hand-over from wave 0 to the block: how many weights to scan (0: none),
+  // whether the kept set runs past them, and the bounds on u.
+  uint32_t fp_m, fp_past;
+  uint32_t vast;  // a slice found min-p's floor set vast
+  double fp_lo, fp_hi;
 };
 // The workgroup's LDS, at file scope so that the out-of-line paths below address it as LDS.
 __shared__ Shared g_sh_static;
@@ -887,6 +892,7 @@ __device__ __forceinline__ bool fast_partial(const FinishArgs& a, Shared& sh, co
     uint32_t pick = kNone;
     double tot = 0.0, ulo = 0.0, uhi = 0.0;
     uint32_t mw = 0;
+    bool past_mw = false;  // u certainly passes every cumulative of the first mw
     if (kk != kNone) {
       mw = min(kk, kWaveMax);
       // The kept total: the wave's own when it holds every kept value, else the block's sum (kk == m).
@@ -935,16 +941,39 @@ __device__ __forceinline__ bool fast_partial(const FinishArgs& a, Shared& sh, co
       if (jp == jc) {
         if (jc < mw) pick = jc;
         else if (kk != kNone && kk == mw) pick = kk - 1;  // past every cumulative: the last kept
+        past_mw = jc == mw;
       }
     }
     if (lane == 0) {
       sh.pick = pick;
       sh.sum = tot;
       sh.keep = pick == kNone ? kNone : (kk != kNone ? kk : P);
+      // u certainly past the first kWaveMax: the whole block scans the weights in place when the
+      // kept set is every one of them, or runs past them (a bracket that straddles a cumulative among
+      // the first kWaveMax would straddle it there too).
+      const bool more = pick == kNone && past_mw && ((kk != kNone && kk == m) || past) && m > kWaveMax;
+      sh.fp_m = more ? m : 0u;
+      sh.fp_past = past ? 1u : 0u;
+      sh.fp_lo = ulo;
+      sh.fp_hi = uhi;
     }
   }
   __syncthreads();
-  const uint32_t keep = sh.keep;
+  uint32_t keep = sh.keep;
+  const uint32_t scan_m = sh.fp_m;
+  if (keep == kNone && scan_m > 0) {
+    double loc[kScanPer], off;
+    prefix_scan(sh, scan_m, loc, &off);
+    const uint32_t j = decide_draw(sh, scan_m, loc, off, sh.fp_lo, sh.fp_hi);
+    // j == scan_m: u passes every cumulative, so the draw is the last kept value, unless the kept
+    // set runs past the scanned values.
+    if (j != kNone && (j < scan_m || !sh.fp_past) && tid == 0) {
+      sh.pick = j < scan_m ? j : scan_m - 1;
+      sh.keep = sh.fp_past ? P : scan_m;
+    }
+    __syncthreads();
+    keep = sh.keep;
+  }
   if (keep == kNone) return false;
   *keep_out = keep;
   *status_out = keep == P && !(im_exact || P == n) ? (uint32_t)AS_ROW_KEPT_PARTIAL : (uint32_t)AS_ROW_OK;
@@ -3063,7 +3092,7 @@ __device__ __forceinline__ void finish_row(const FinishArgs& a, uint32_t row) {
     // holding a NaN or an infinity is refused before that pick matters), and each slice's first
     // candidate's place by a prefix of the counts in slice order.
     const uint32_t lane = tid;
-    uint32_t bad = kNone, gi = kNone, mk = 0, trunc = 0, long_hist = 0, run = 0;
+    uint32_t bad = kNone, gi = kNone, mk = 0, trunc = 0, long_hist = 0, run = 0, vast = 0;
     float gv = 0.0f;
     uint64_t bound = 0;
     for (uint32_t b0 = 0; b0 < a.n_seg; b0 += kWave) {
@@ -3080,6 +3109,7 @@ __device__ __forceinline__ void finish_row(const FinishArgs& a, uint32_t row) {
           bound = max(bound, t.bound);
         }
         if (t.truncated & 2u) long_hist = 1;
+        vast |= t.vast;
       }
       uint32_t incl = c;
       for (int o = 1; o < kWave; o <<= 1) {
@@ -3093,6 +3123,7 @@ __device__ __forceinline__ void finish_row(const FinishArgs& a, uint32_t row) {
     mk = wave_max_u32(mk);
     trunc = wave_max_u32(trunc);
     long_hist = wave_max_u32(long_hist);
+    vast = wave_max_u32(vast);
     bound = wave_max_u64(bound);
     wave_greedy(gv, gi);
     if (lane == 0) {
@@ -3104,6 +3135,7 @@ __device__ __forceinline__ void finish_row(const FinishArgs& a, uint32_t row) {
       sh.trunc = trunc;
       sh.bound_key = bound;
       sh.exact = long_hist;
+      sh.vast = vast;
       sh.stats_bad = long_hist;
       sh.nsk = 0;
       sh.u01 = 0.0;
@@ -3230,10 +3262,11 @@ __device__ __forceinline__ void finish_row(const FinishArgs& a, uint32_t row) {
     uint32_t keep = kNone;
     uint32_t status = AS_ROW_OK;
     bool drawn = false;
-    // A row without a top-k and without kept lists first takes the fast decision; a flagged row
-    // waits for S's sums only when that does not settle it.
+    // A row without a top-k and without kept lists first takes the fast decision, and a flagged row
+    // waits for S's sums only when that does not settle it. A flagged row whose floor set is not vast
+    // skips it: min-p cuts first within S, and the draw needs S's values.
     if (p.mode == kModePartial && (p.top_p < 1.0f || has_floor) && !a.kept_ids && !too_many && P > 0 &&
-        P + kWaveMax <= (uint32_t)kCap)
+        P + kWaveMax <= (uint32_t)kCap && (sh.tail_slot == kNone || sh.vast))
       drawn = fast_partial(a, sh, p, P, floor_cut, &keep, &status);
     if (!drawn) {
       if (sh.tail_slot != kNone) tail_wait(a, row);

@@ -153,7 +153,7 @@ struct SegStats {
   double sum;           // sum of exp(d), d = l - m (or (l - m) / T), m = sum_ref
   double sum_abs;       // sum of exp(d) * |d|
   float sum_ref;        // the sums' reference m: at least every value they hold
-  uint32_t pad_;
+  uint32_t vast;        // min-p rows: the slice found the floor set vast (tens of thousands of values)
 };
 
 // f32::total_cmp as an unsigned key (sample.rs:106-108): larger key = higher rank; +0 above -0.

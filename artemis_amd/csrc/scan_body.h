@@ -39,7 +39,9 @@ static_assert(kCapW % kWave == 0, "sizes");
 // Thread tid holds hash slots tid + k * kThreads, k < kHashPer, those below kHash.
 __device__ __forceinline__ bool own_slot(uint32_t tid, int k) { return kHash % kThreads == 0 || tid + k * kThreads < kHash; }
 static_assert(as_launch::kSliceAlign % kChunk == 0, "slices start on a chunk");
-static_assert(as_launch::kTopKMax + kRoom <= kCapW, "a select always frees room");
+static_assert(as_launch::kTopKMax + as_launch::kTopKMax / 4 + kRoom <= kCapW &&
+                  as_launch::kFloorRank + as_launch::kFloorRank / 4 + kRoom <= kCapW,
+              "a select always leaves room for one group");
 
 // What a slice computes besides the non-finite check.
 enum Kind : int {
@@ -64,6 +66,7 @@ struct Shared {
   uint32_t hist_out;
   uint32_t overflow;
   uint32_t out_n;  // candidates the waves have written to HBM during the stream
+  uint32_t vast;   // a wave found min-p's floor set vast (two in five of its first chunk)
   RowParams prm;   // the row's parameters
 };
 // The workgroup's LDS, at file scope so that the out-of-line helpers below address it directly.
@@ -121,8 +124,9 @@ __device__ __forceinline__ WaveState uniform(WaveState ws) {
   return ws;
 }
 
-// Selects run once the buffer holds twice C (at least C + 64), and whenever it might overflow.
-__device__ __forceinline__ uint32_t select_at(uint32_t C) { return min(max(2 * C, C + 64), kCapW - kRoom); }
+// Selects run once the buffer holds twice C (at least C + 64, at most all but one wave's worth of
+// entries), and whenever a group's values would not fit.
+__device__ __forceinline__ uint32_t select_at(uint32_t C) { return min(max(2 * C, C + 64), kCapW - kWave); }
 
 __device__ __forceinline__ void raise_tau(WaveState& ws, uint64_t t) {
   if (t > ws.tau) {
@@ -348,9 +352,10 @@ __device__ __forceinline__ uint32_t wave_qth(uint32_t x, uint32_t q) {
 
 // The largest unmasked value of the wave's first chunk sets min-p's first floor. When more than one
 // in a hundred of the chunk's values pass it (a floor set of thousands, or a first chunk whose
-// largest value lies far below the row's: appending each value above it would cost more than
-// keeping the best few hundred), the wave keeps its best kPartialRank like a row without min-p
-// instead of every value above the floor (which still applies).
+// largest value lies far below the row's: appending and spilling each value above it would cost
+// more than keeping the best few hundred), the wave keeps its best kPartialRank like a row without
+// min-p instead of every value above the floor (which still applies). When two in five pass, the
+// slice notes the floor set as vast (tens of thousands of values).
 __device__ __forceinline__ WaveState first_floor(WaveState ws, f32x4 v0, f32x4 v1, f32x4 v2, f32x4 v3,
                                               uint32_t masked, uint32_t e0, double ln_min_p, uint32_t* share) {
   const f32x4 v[kU] = {v0, v1, v2, v3};
@@ -375,9 +380,12 @@ __device__ __forceinline__ WaveState first_floor(WaveState ws, f32x4 v0, f32x4 v
       n_v += (uint32_t)__popcll(__ballot(valid));
       n_f += (uint32_t)__popcll(__ballot(valid && v[j][c] >= ws.tau_f));
     }
-  if (100 * n_f > n_v && ws.C > as_launch::kPartialRank) {
+  if (100 * n_f > n_v && ws.spill) {
     ws.spill = false;
+    // Past two in five, the floor set is tens of thousands: it cannot stay whole, and the wave keeps
+    // the depth of a row without min-p.
     ws.C = as_launch::kPartialRank;
+    if (5 * n_f > 2 * n_v && (threadIdx.x & (kWave - 1)) == 0) shm().vast = 1;
     ws.sel = select_at(ws.C);
     ws = first_tau(ws, v0, v1, v2, v3, masked, e0, kFirstRankPartial, share, nullptr, 0u);
   }
@@ -434,13 +442,18 @@ struct Lane {
 };
 
 // Appends the values e0 .. e0+3 of one 16-byte group that reach tau's value and are not masked to
-// the wave's buffer, first making room when it might not take four more per lane. A value's test is
-// one compare; the mask is looked at only when some lane passes it.
+// the wave's buffer, first making room when the values reaching tau would not fit. A value's test
+// is one compare; the mask is looked at only when some lane passes it.
 __device__ __forceinline__ void append4(WaveState& ws, Lane& ln, const f32x4& v, uint32_t e0, uint32_t mask,
                                         const Slice& sl) {
   if (ws.cnt > kCapW - kRoom) {
-    if (ws.spill) ws = uniform(spill(ws, sl.out, sl.room, sl.share));
-    else select_now(ws, ws.C, ws.C / 4, sl.share);
+    uint32_t need = 0;
+#pragma unroll
+    for (int c = 0; c < 4; ++c) need += (uint32_t)__popcll(__ballot(v[c] >= ws.tau_f));
+    if (ws.cnt + need > kCapW) {
+      if (ws.spill) ws = uniform(spill(ws, sl.out, sl.room, sl.share));
+      else select_now(ws, ws.C, ws.C / 4, sl.share);
+    }
   }
   uint64_t* buf = shm().buf[__builtin_amdgcn_readfirstlane(threadIdx.x / kWave)];
   const uint32_t nid = ~e0;  // e0 + c packs as nid - c
@@ -737,6 +750,7 @@ __device__ __forceinline__ void scan_slice(
     sh.hist_out = 0;
     sh.overflow = 0;
     sh.out_n = 0;
+    sh.vast = 0;
   }
   // The history tables start empty.
   if (sl.pen) {
@@ -871,7 +885,7 @@ __device__ __forceinline__ void scan_slice(
   st.sum = 0.0;
   st.sum_abs = 0.0;
   st.sum_ref = 0.0f;
-  st.pad_ = 0;
+  st.vast = 0;
 
   if (kind == kKindPlain) {
     wave_greedy(ln.gv, ln.gi);
@@ -910,6 +924,7 @@ __device__ __forceinline__ void scan_slice(
       rkey = max(rkey, sh.red_u[k]);
     }
     st.max_key = mk;
+    st.vast = sh.vast;
     // A min-p row's slice whose bound lies above its floor (from the largest value it knows the row
     // to hold) did not keep every value above the floor: the row is flagged for S's sums.
     // The first slice to flag the row lists it.
