@@ -39,10 +39,12 @@ struct ExpPoly {
     for (int i = 1; i < kPolyLen; ++i) p = __builtin_fma(p, f, c[i]);
     return __builtin_amdgcn_ldexp(p, (int32_t)k);
   }
-  // exp(d) for finite d <= 0 without the clamp: below d = -708 the result is 2^f 2^k rounded to a
-  // subnormal or 0 (k saturates at the least int), under 2^-1021 like exp(d) itself.
+  // exp(d) for finite d <= 0 without exp_neg's clamp at -708: below it the result is 2^f 2^k rounded
+  // to a subnormal or 0, under 2^-1021 like exp(d) itself. t is bounded at -1100 first, so that k
+  // converts to an int exactly (a double far outside the int range has no defined conversion); every
+  // d it moves lies below -762, where exp(d) and the result are both 0.
   __device__ __forceinline__ double exp_le0(double d) const {
-    const double t = d * 1.4426950408889634;
+    const double t = fmax(d * 1.4426950408889634, -1100.0);
     const double k = __builtin_rint(t);
     const double f = t - k;
     double p = c[0];

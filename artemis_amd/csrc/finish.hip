@@ -20,6 +20,7 @@
 // reference's sequential folds, so its token is the reference's in every case.
 #include "sampler_device.h"
 #include "launch.h"
+#include "fold.h"
 #include "../../include/artemis_sampler.h"
 
 #define AS_FIN_NS as_fin_sliced
@@ -32,13 +33,20 @@ using as_launch::FinishArgs;
 
 namespace {
 
-// The arguments are read from device memory (the scan's copy of the pinned block), which costs each
-// workgroup less than a large kernel-argument block. Workgroup b finishes row b; those past the
+// The arguments are read from device memory (the scan's copy of its kernel argument), which costs
+// each workgroup less than a large kernel-argument block. Workgroup b finishes row b; those past the
 // call's rows only take parts of S's sums (tail_help), which every workgroup whose row is not
 // flagged does first.
 __global__ __launch_bounds__(1024) void finish_kernel(const FinishArgs* __restrict__ ap) {
   const FinishArgs& a = *ap;
   const uint32_t row = blockIdx.x;
+  // The host learns that the call's parameter upload (which ran before its scan) no longer reads its
+  // staging block; the next call's list of flagged rows empties (this call's scan and the call
+  // before it have ended).
+  if (row == 0 && threadIdx.x == 0) {
+    __hip_atomic_store(a.done, a.call, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+    a.tail_next->count = 0u;
+  }
   as_fin_sliced::tail_list_load(a, row);
   __syncthreads();
   as_fin_sliced::tail_help(a, row, gridDim.x);

@@ -18,14 +18,6 @@ constexpr int kScanPer = kCap / kThreads;
 static_assert(kCap % kThreads == 0 && kThreads >= 256 && (kThreads & (kThreads - 1)) == 0, "a power of two");
 constexpr int kMaxSeg = AS_FIN_MAX_SEG;
 constexpr int kStage = 4096;
-constexpr double kU = 1.1102230246251565e-16;  // 2^-53, the unit roundoff
-
-__device__ __forceinline__ double gamma_n(double n) { return n * kU / (1.0 - n * kU); }
-// An upper bound of gamma_n with no division, for n * kU below 2^-30 (n below 2^22 here):
-// gamma_n = n u (1 + n u + ...) <= n u (1 + 2 n u), and the margin 1e-9 also covers the products'
-// own roundings.
-__device__ __forceinline__ double gamma_ub(double n) { return n * (kU * (1.0 + 1e-9)); }
-
 struct Shared {
   uint64_t sk[kCap];  // candidates (exact path: per-wave digit counts)
   double wd[kCap];    // weights and prefix sums (exact path: staging for sequential folds)
@@ -64,29 +56,6 @@ __device__ __forceinline__ Shared& shm() { return g_sh_static; }
 
 // --- block helpers ------------------------------------------------------------------------------
 
-// A pointer to global memory as such (gload explains why: flat instructions would share the LDS wait
-// counter). Every atomic and device-coherent access of the kernel's HBM goes through one.
-template <class T>
-__device__ __forceinline__ __attribute__((address_space(1))) T* gp(T* p) {
-  return (__attribute__((address_space(1))) T*)p;
-}
-
-// Device-coherent loads and stores (relaxed, agent scope): what other workgroups of the kernel write
-// with device atomics or such stores, whatever this XCD's L2 holds.
-__device__ __forceinline__ uint32_t ld_agent(const uint32_t* p) {
-  return __hip_atomic_load(gp(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ uint64_t ld_agent(const uint64_t* p) {
-  return __hip_atomic_load(gp(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ double ld_agent(const double* p) {
-  return __hip_atomic_load(gp(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ void st_agent(uint64_t* p, uint64_t v) {
-  __hip_atomic_store(gp(p), v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-
-
 // Exclusive prefix sum of one f64 per thread over the block.
 __device__ double block_exclusive_scan_f64(double x, double* wave_tot) {
   const int lane = threadIdx.x & (kWave - 1), w = threadIdx.x / kWave;
@@ -104,166 +73,6 @@ __device__ double block_exclusive_scan_f64(double x, double* wave_tot) {
   double excl_in_wave = __shfl_up(incl, 1, kWave);
   if (lane == 0) excl_in_wave = 0.0;
   return __dadd_rn(before, excl_in_wave);
-}
-
-// --- sequential folds on one wave --------------------------------------------------------------
-//
-// The reference folds a few hundred f64 terms left to right (draw_full_sort's totals and
-// cumulatives, sample.rs:169-197; draw_partial's draw, 260-272). One wave does it from registers, 64
-// terms a step: every lane adds lane 0's term, then lane 1's, and so on (through readlane), which
-// are the reference's roundings in the reference's order, and lane j keeps the running sum once its
-// own term is in. The terms' divisions (cum += w / total) do not depend on the running sum, so the
-// lanes compute them at once beforehand. Only wave 0 (tid < 64) calls these.
-
-// Lane j of the wave: carry + x_0 + ... + x_j, added left to right.
-__device__ __forceinline__ double wave_seq_prefix(double x, double carry) {
-  const uint32_t lane = threadIdx.x & (kWave - 1);
-  const uint64_t b = (uint64_t)__double_as_longlong(x);
-  const int lo = (int)(uint32_t)b, hi = (int)(uint32_t)(b >> 32);
-  double s = carry, mine = carry;
-#pragma unroll
-  for (int j = 0; j < kWave; ++j) {
-    const uint32_t l = (uint32_t)__builtin_amdgcn_readlane(lo, j), h = (uint32_t)__builtin_amdgcn_readlane(hi, j);
-    s = __dadd_rn(s, __longlong_as_double((long long)(((uint64_t)h << 32) | l)));
-    if (lane == (uint32_t)j) mine = s;
-  }
-  return mine;
-}
-__device__ __forceinline__ double wave_lane63(double x) {
-  const uint64_t b = (uint64_t)__double_as_longlong(x);
-  const uint32_t l = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)b, kWave - 1);
-  const uint32_t h = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(b >> 32), kWave - 1);
-  return __longlong_as_double((long long)(((uint64_t)h << 32) | l));
-}
-// The left fold of w[0..m) (zeros past m change no sum of positive terms).
-__device__ __forceinline__ double wave_seq_total(const double* w, uint32_t m) {
-  const uint32_t lane = threadIdx.x & (kWave - 1);
-  double carry = 0.0;
-  for (uint32_t b0 = 0; b0 < m; b0 += kWave) {
-    const double x = (b0 + lane < m) ? w[b0 + lane] : 0.0;
-    carry = wave_lane63(wave_seq_prefix(x, carry));
-  }
-  return carry;
-}
-
-// draw_full_sort's top-p cut (sample.rs:166-179) over w[0..m) in the reference's order: the total,
-// then cum += w_i / total until cum reaches top_p; returns the kept count (m when it never does).
-__device__ __forceinline__ uint32_t wave_seq_cut(const double* w, uint32_t m, double top_p) {
-  const uint32_t lane = threadIdx.x & (kWave - 1);
-  const double tot = wave_seq_total(w, m);
-  double carry = 0.0;
-  for (uint32_t b0 = 0; b0 < m; b0 += kWave) {
-    const uint32_t i = b0 + lane;
-    const double q = (i < m) ? __ddiv_rn(w[i], tot) : 0.0;
-    const double cum = wave_seq_prefix(q, carry);
-    const uint64_t hit = __ballot(i < m && cum >= top_p);
-    if (hit) return b0 + (uint32_t)__builtin_ctzll(hit) + 1;
-    carry = wave_lane63(cum);
-  }
-  return m;
-}
-// The draw over w[0..m) in the reference's order (sample.rs:184-197, 260-272): u = u01 * total,
-// then the first rank whose cumulative weight passes u (the last when none does). *tot gets the total.
-__device__ __forceinline__ uint32_t wave_seq_draw(const double* w, uint32_t m, double u01, double* tot) {
-  const uint32_t lane = threadIdx.x & (kWave - 1);
-  const double t = wave_seq_total(w, m);
-  const double u = __dmul_rn(u01, t);
-  *tot = t;
-  double carry = 0.0;
-  for (uint32_t b0 = 0; b0 < m; b0 += kWave) {
-    const uint32_t i = b0 + lane;
-    const double cum = wave_seq_prefix((i < m) ? w[i] : 0.0, carry);
-    const uint64_t hit = __ballot(i < m && u < cum);
-    if (hit) return b0 + (uint32_t)__builtin_ctzll(hit);
-    carry = wave_lane63(cum);
-  }
-  return m - 1;
-}
-
-// --- certified decisions on one wave ----------------------------------------------------------
-//
-// Up to kWPer * 64 sorted values, lane l holding ranks kWPer*l .. kWPer*l + kWPer-1 in registers.
-// Their prefix sums come from a fold of kWPer in the lane and a scan over the lanes: each is a sum
-// of positive terms through at most kWPer + 7 roundings, within gamma(kWPer + 7) of its exact value,
-// as the reference's left fold of j + 1 terms is within gamma(j) of it. A decision the two bounds
-// agree on is the reference's; otherwise the caller takes the sequential fold above.
-constexpr int kWPer = 4;
-constexpr uint32_t kWaveMax = kWPer * kWave;
-
-// Inclusive prefix sums pre[] of the values w[] in rank order; returns the total to every lane.
-__device__ __forceinline__ double wave_prefix(const double (&w)[kWPer], double (&pre)[kWPer]) {
-  const uint32_t lane = threadIdx.x & (kWave - 1);
-  double run = 0.0;
-#pragma unroll
-  for (int q = 0; q < kWPer; ++q) {
-    run = __dadd_rn(run, w[q]);
-    pre[q] = run;
-  }
-  double incl = run;
-#pragma unroll
-  for (int o = 1; o < kWave; o <<= 1) {
-    const double y = __shfl_up(incl, o, kWave);
-    if (lane >= (uint32_t)o) incl = __dadd_rn(incl, y);
-  }
-  double excl = __shfl_up(incl, 1, kWave);
-  if (lane == 0) excl = 0.0;
-#pragma unroll
-  for (int q = 0; q < kWPer; ++q) pre[q] = __dadd_rn(excl, pre[q]);
-  return __shfl(incl, kWave - 1, kWave);
-}
-// The first rank below m whose flag is set (m when none).
-__device__ __forceinline__ uint32_t wave_first(const bool (&f)[kWPer], uint32_t m) {
-  const uint32_t i0 = (threadIdx.x & (kWave - 1)) * kWPer;
-  uint32_t first = m;
-#pragma unroll
-  for (int q = kWPer - 1; q >= 0; --q)
-    if (f[q] && i0 + q < m) first = i0 + q;
-  return wave_min_u32(first);
-}
-// draw_full_sort's top-p cut over the m values' weights w (zero past m): the kept count, or kNone
-// when the bounds cannot decide. The reference's cumulative at rank j, its left fold of
-// fl(w_i / total), lies within gamma(j + 1) of exact / its total, which is within gamma(m) of exact;
-// ours (prefix / total) within gamma(kWPer + 8) of exact.
-__device__ __forceinline__ uint32_t wave_topp_cut(const double (&w)[kWPer], uint32_t m, double top_p) {
-  double pre[kWPer];
-  const double S = wave_prefix(w, pre);
-  const uint32_t i0 = (threadIdx.x & (kWave - 1)) * kWPer;
-  const double base = 2.0 * gamma_ub(2.0 * kWPer + 16.0) + gamma_ub(2.0 * (double)m + 4.0) + 10.0 * kU;
-  // pre / S against top_p as pre against top_p * S (S > 0): the products' roundings are within the
-  // 10 u of base.
-  const double t = top_p * S;
-  bool lo[kWPer], hi[kWPer];
-#pragma unroll
-  for (int q = 0; q < kWPer; ++q) {
-    const double rel = base + gamma_ub(2.0 * (double)(i0 + q) + 4.0);
-    lo[q] = pre[q] * (1.0 + rel) >= t;  // the reference's cumulative may have reached top_p
-    hi[q] = pre[q] * (1.0 - rel) >= t;  // it certainly has
-  }
-  const uint32_t jl = wave_first(lo, m), jh = wave_first(hi, m);
-  if (jl != jh) return kNone;
-  return jh < m ? jh + 1 : m;
-}
-// The draw over the m values' weights w (zero past m) with u = u01 * total (sample.rs:184-197,
-// 260-272): the first rank whose cumulative passes u (m - 1 when none does), or kNone when the
-// bounds cannot decide. *tot gets our total (within gamma(m) + gamma(kWPer + 8) of the reference's).
-__device__ __forceinline__ uint32_t wave_draw(const double (&w)[kWPer], uint32_t m, double u01, double* tot) {
-  double pre[kWPer];
-  const double S = wave_prefix(w, pre);
-  *tot = S;
-  const uint32_t i0 = (threadIdx.x & (kWave - 1)) * kWPer;
-  const double g = gamma_ub(2.0 * kWPer + 16.0);
-  const double d = gamma_ub((double)m + 1.0) + g + 4.0 * kU;
-  const double ulo = u01 * S * (1.0 - d) * (1.0 - 3.0 * kU), uhi = u01 * S * (1.0 + d) * (1.0 + 3.0 * kU);
-  bool may[kWPer], sure[kWPer];
-#pragma unroll
-  for (int q = 0; q < kWPer; ++q) {
-    const double rel = gamma_ub((double)(i0 + q) + 1.0) + g + 4.0 * kU;
-    may[q] = pre[q] * (1.0 + rel) > ulo;
-    sure[q] = pre[q] * (1.0 - rel) > uhi;
-  }
-  const uint32_t jp = wave_first(may, m), jc = wave_first(sure, m);
-  if (jp != jc) return kNone;
-  return jc < m ? jc : m - 1;
 }
 
 // --- the exact-order path ---------------------------------------------------------------------
@@ -3047,13 +2856,6 @@ __device__ __forceinline__ void finish_row(const FinishArgs& a, uint32_t row) {
   const SegStats* gst = a.stats + (uint64_t)row * a.n_seg;
   const uint32_t n = a.n;
   if (tid < 256) sh.tab[tid] = as_exp::kTable[tid];
-  // The host learns that the call's parameter upload (which ran before its scan) no longer reads its
-  // staging block; the next call's list of flagged rows empties (this call's scan and the call
-  // before it have ended).
-  if (row == 0 && tid == 0) {
-    __hip_atomic_store(a.done, a.call, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
-    a.tail_next->count = 0u;
-  }
   // S's sums: none until a flagged row waits for them (tail_wait).
   if (tid == 0) {
     sh.have_tail = 0;
@@ -3315,38 +3117,15 @@ __device__ __forceinline__ void finish_row(const FinishArgs& a, uint32_t row) {
         // min-p's floor (the ranks are sorted, so it keeps a prefix) and the draw, each decided by
         // bounds and by the reference's sequential folds only when the bounds cannot.
         static_assert(as_launch::kTopKMax <= kWaveMax, "one wave holds a top-k");
-        static_assert(2 * as_launch::kTopKMax <= (uint32_t)kCap && as_launch::kTopKMax <= (uint32_t)kThreads,
+        static_assert(2 * kWaveMax <= (uint32_t)kCap && as_launch::kTopKMax <= (uint32_t)kThreads,
                       "the weights of a top-k, one per thread");
         const uint32_t k = p.top_k;
-        // Every weight first, one value per thread: sh.wd[i] = w at T, sh.wd[kTopKMax + i] = w at T = 1.
-        double* w1s = sh.wd + as_launch::kTopKMax;
-        if (tid < k) {
-          const double v = val(tid);
-          sh.wd[tid] = w_temp(v);
-          if (p.top_p < 1.0f) w1s[tid] = w_one(v);
-        }
+        topk_weights(sh.sk, k, top, temp, p.top_p < 1.0f, tab, sh.wd);
         __syncthreads();
         if (tid < kWave) {
-          const uint32_t i0 = tid * kWPer;
-          uint32_t kk = k;
-          if (p.top_p < 1.0f) {
-            double w[kWPer];
-  #pragma unroll
-            for (int q = 0; q < kWPer; ++q) w[q] = (i0 + q < k) ? w1s[i0 + q] : 0.0;
-            kk = wave_topp_cut(w, k, top_p);
-            if (kk == kNone) kk = wave_seq_cut(w1s, k, top_p);
-          }
-          if (has_floor) {
-            bool below[kWPer];
-  #pragma unroll
-            for (int q = 0; q < kWPer; ++q) below[q] = (i0 + q < kk) && !(val(i0 + q) >= floor);
-            kk = wave_first(below, kk);
-          }
-          double w[kWPer], tot = 0.0;
-  #pragma unroll
-          for (int q = 0; q < kWPer; ++q) w[q] = (i0 + q < kk) ? sh.wd[i0 + q] : 0.0;  // also the kept weights
-          uint32_t pick = wave_draw(w, kk, sh.u01, &tot);
-          if (pick == kNone) pick = wave_seq_draw(sh.wd, kk, sh.u01, &tot);
+          uint32_t kk, pick;
+          double tot;
+          topk_decide(sh.sk, k, top_p, p.top_p < 1.0f, has_floor, floor, sh.u01, sh.wd, &kk, &pick, &tot);
           if (tid == 0) {
             sh.keep = kk;
             sh.pick = pick;

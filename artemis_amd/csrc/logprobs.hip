@@ -433,9 +433,10 @@ extern "C" int as_logprobs_static(void* hip_stream, const float* logits, uint64_
   if ((uint64_t)n_rows * parts > kStaticParts) {
     char msg[200];
     std::snprintf(msg, sizeof msg,
-                  "as_logprobs_static: %u rows of %u values need %llu parts; the static scratch holds %u "
-                  "(n_rows x ceil(n_vocab / %u) <= %u)",
-                  n_rows, n_vocab, (unsigned long long)n_rows * parts, kStaticParts, as_launch::kLpPart, kStaticParts);
+                  "as_logprobs_static: %u rows of %u values need %llu parts of %u values; the static scratch "
+                  "holds %u (n_rows x parts per row <= %u)",
+                  n_rows, n_vocab, (unsigned long long)n_rows * parts, as_launch::lp_part_len(n_vocab, n_rows),
+                  kStaticParts, kStaticParts);
     return static_fail(err, err_cap, AS_ERR_CAPACITY, msg);
   }
   int dev = 0;

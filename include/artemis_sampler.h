@@ -194,8 +194,10 @@ int as_head_argmax(as_ctx* ctx, const void* w, uint32_t wtype, uint32_t rows, ui
  * value's rounding to f32, or a token is out of range (its logprob is NaN). The bound is absolute:
  * |lse - lse_ref| <= e = gamma(n + 64) + 1.5e-12 + 2^-51 |ln total| + 2^-52 |lse| (gamma(m) =
  * m 2^-53 / (1 - m 2^-53); about 2.8e-11 at the model's vocabulary), so an inexact value is within
- * e + one f32 ulp of the reference's, and its exp within about e relative. Near lp = 0 (a
- * near-certain token) that can be many f32 ulps. */
+ * e + 2^-51 |lp| + one f32 ulp of the reference's (2^-51 |lp| covering the roundings of the two f64
+ * differences x - lse, ours and the reference's), and its exp within about e relative. Near lp = 0
+ * (a near-certain token) that can be many f32 ulps: compare log-probabilities bit for bit only on
+ * rows whose status is AS_LP_OK. */
 #define AS_LP_OK 0u
 #define AS_LP_INEXACT 1u
 int as_logprobs(as_ctx* ctx, const float* logits, uint64_t row_stride, uint32_t n_vocab, uint32_t n_rows,
@@ -209,8 +211,9 @@ int as_logprobs(as_ctx* ctx, const float* logits, uint64_t row_stride, uint32_t 
  * n_rows x ceil(n_vocab / 16384) must be at most 2,048 (128 rows at 248,320), else AS_ERR_CAPACITY.
  * Every call on one GPU shares that array: calls that overlap on one GPU (other streams, other host
  * threads) race and must be ordered by the caller. Nothing is allocated and nothing is freed; the
- * device's first call looks the array's address up. err (host, may be NULL) gets a one-line message
- * on failure. */
+ * device's first call looks the array's address up (hipGetSymbolAddress), so it must be made before
+ * any graph capture on that device; later calls only launch the two kernels and may be captured and
+ * replayed. err (host, may be NULL) gets a one-line message on failure. */
 int as_logprobs_static(void* hip_stream, const float* logits, uint64_t row_stride, uint32_t n_vocab,
                        uint32_t n_rows, const uint32_t* tokens, uint32_t top, float* logprob,
                        uint32_t* top_ids, float* top_logprobs, uint32_t* status, char* err,

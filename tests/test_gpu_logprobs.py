@@ -51,6 +51,8 @@ def lse_bound(row, lse):
 
 
 def same_or_within(got, want, exact, e):
+    """Bit-exact on an AS_LP_OK row; otherwise within the header's bound e + 2^-51 |lp| + one f32 ulp
+    (2^-51 |lp| = 4 U |lp| covers the two f64 differences x - lse, ours and the reference's)."""
     got, want = np.float32(got), np.float32(want)
     if exact:
         return got.tobytes() == want.tobytes()

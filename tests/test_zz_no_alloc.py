@@ -74,3 +74,45 @@ def test_static_logprobs_refuse_a_batch_past_the_scratch():
     assert rc == AS_ERR_CAPACITY and "2048" in msg.replace(",", ""), (rc, msg)
     torch.cuda.synchronize()
     assert torch.isnan(lp).all()  # nothing ran
+
+
+def test_static_logprobs_replay_under_graph_capture():
+    # After one eager call (which looks the static scratch up), as_logprobs_static is captured into a
+    # graph and replayed on new logits written into the captured input, with eager work and
+    # synchronisations between the replays; every replay must give as_logprobs' outputs bit for bit.
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU")
+    from artemis_amd import Context
+    dev = torch.device("cuda:0")
+    gen = np.random.default_rng(23)
+    n, rows, top = 248_320, 8, 20
+    x = torch.from_numpy((gen.standard_normal((rows, n)) * 2.5).astype(np.float32)).to(dev)
+    tok = torch.from_numpy(gen.integers(0, n, rows).astype(np.int32)).to(dev)
+    rc, msg, *_ = static_call(x, tok, top, n, n)
+    assert rc == 0, msg
+    torch.cuda.synchronize()
+    from artemis_amd import sampler as S
+    lp = torch.empty(rows, dtype=torch.float32, device=dev)
+    ids = torch.empty((rows, top), dtype=torch.int32, device=dev)
+    lps = torch.empty((rows, top), dtype=torch.float32, device=dev)
+    st = torch.empty(rows, dtype=torch.int32, device=dev)
+    err = C.create_string_buffer(256)
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        s = torch.cuda.current_stream()
+        rc = S.lib().as_logprobs_static(C.c_void_p(s.cuda_stream), x.data_ptr(), n, n, rows, tok.data_ptr(), top,
+                                        lp.data_ptr(), ids.data_ptr(), lps.data_ptr(), st.data_ptr(), err, 256)
+    assert rc == 0, err.value.decode()
+    ctx = Context(max_rows=rows, max_vocab=n)
+    for rep in range(3):
+        fresh = torch.from_numpy((gen.standard_normal((rows, n)) * (2.0 + rep)).astype(np.float32)).to(dev)
+        x.copy_(fresh)
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        want = ctx.logprobs(fresh, tok, top)
+        torch.cuda.synchronize()
+        for w, got in zip(want, (lp, ids, lps, st)):
+            assert same(w, got), rep
+        _ = (fresh * 2.0).sum().item()  # eager work between replays
+    ctx.close()
