@@ -30,8 +30,9 @@ constexpr uint32_t kPartialRank = 192;
 constexpr uint32_t kFloorRank = 384;
 constexpr uint32_t kTopKMax = 256;
 constexpr uint32_t kHistReserve = 64;
-// Distinct history ids a slice can count (an LDS hash); more send the row to the exact path.
-constexpr uint32_t kHistSlots = 512;
+// Distinct history ids a slice can count (an LDS hash; a 16,000-id history of generated text holds
+// about 3,200 distinct ids, 1,100 per slice at batch 256); more send the row to the exact path.
+constexpr uint32_t kHistSlots = 2048;
 // The deep passes shared with idle workgroups histogram a row into kDistBins bins.
 constexpr uint32_t kDistBins = 1024;
 // u32 words of scratch per row for rows of n values: the history counts [n], then (8-byte aligned)

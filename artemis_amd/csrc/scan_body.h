@@ -31,7 +31,13 @@ constexpr uint32_t kShareEvery = 8;
 static_assert(kShareEvery % 2 == 0, "reads fall on the loop's odd chunks");
 constexpr uint32_t kHash = AS_SCAN_HASH;
 constexpr int kHashPer = (kHash + kThreads - 1) / kThreads;  // hash slots per thread (the last may be short)
-constexpr int kHashShift = 32 - __builtin_ctz(kHash);  // the multiplicative hash's top bits
+constexpr int kHxEarly = 2;  // slots per thread whose raw values load before the stream
+// The table's first kHashPrimary slots are those of each thread's first kHxEarly (raw values loaded
+// before the stream): a short history's ids all go there.
+constexpr uint32_t kHashPrimary = (uint32_t)kThreads * 2u < kHash ? (uint32_t)kThreads * 2u : kHash;
+constexpr int kPrimaryShift = 32 - __builtin_ctz(kHashPrimary);  // the multiplicative hash's top bits
+constexpr uint32_t kPrimaryProbes = 16;
+static_assert((kHashPrimary & (kHashPrimary - 1)) == 0 && kHashPrimary < kHash, "a power-of-two first part");
 static_assert((kHash & (kHash - 1)) == 0, "a power of two");
 constexpr uint32_t kEmpty = 0xFFFFFFFFu;
 typedef float f32x4 __attribute__((ext_vector_type(4)));
@@ -785,14 +791,27 @@ __device__ __forceinline__ void scan_slice(
       const uint32_t off = id - sl.b0;
       if (off >= len) return;
       atomicOr(&sh.bitmap[off >> 5], 1u << (off & 31u));
-      uint32_t h = (id * 0x9E3779B1u) >> kHashShift;
-      for (uint32_t probe = 0; probe < kHash; ++probe) {
+      // The first kHashPrimary slots (those whose raw values load before the stream) take an id
+      // within kPrimaryProbes probes; the rest of the table takes the others. An id's probe sequence
+      // is fixed and slots are never freed, so every thread marking it reaches the same slot.
+      uint32_t h = (id * 0x9E3779B1u) >> kPrimaryShift;
+      for (uint32_t probe = 0; probe < kPrimaryProbes; ++probe) {
         const uint32_t prev = atomicCAS(&sh.hid[h], kEmpty, id);
         if (prev == kEmpty || prev == id) {
           atomicAdd(&sh.hcnt[h], 1u);
           return;
         }
-        h = (h + 1) & (kHash - 1);
+        h = (h + 1) & (kHashPrimary - 1);
+      }
+      constexpr uint32_t kRest = kHash - kHashPrimary;
+      h = (uint32_t)(((uint64_t)(id * 0x85EBCA77u) * kRest) >> 32);
+      for (uint32_t probe = 0; probe < kRest; ++probe) {
+        const uint32_t prev = atomicCAS(&sh.hid[kHashPrimary + h], kEmpty, id);
+        if (prev == kEmpty || prev == id) {
+          atomicAdd(&sh.hcnt[kHashPrimary + h], 1u);
+          return;
+        }
+        h = h + 1 == kRest ? 0u : h + 1;
       }
       sh.overflow = 1;
     };
@@ -804,10 +823,12 @@ __device__ __forceinline__ void scan_slice(
   }
   __syncthreads();
 
-  // The raw values of the slice's history ids, in flight during the stream.
-  float hx[kHashPer];
+  // The raw values of the slice's history ids in each thread's first kHxEarly slots, in flight
+  // during the stream; those in its other slots (a long history's) are read after the stream, where
+  // their registers cost the stream nothing.
+  float hx[kHxEarly];
 #pragma unroll
-  for (int k = 0; k < kHashPer; ++k) {
+  for (int k = 0; k < kHxEarly; ++k) {
     const uint32_t id = (sl.pen && own_slot(tid, k)) ? sh.hid[tid + k * kThreads] : kEmpty;
     hx[k] = (id != kEmpty) ? sl.x[id] : 0.0f;
   }
@@ -857,7 +878,8 @@ __device__ __forceinline__ void scan_slice(
     hpk[k] = 0;
     hidv[k] = (sl.pen && own_slot(tid, k)) ? sh.hid[tid + k * kThreads] : kEmpty;
     if (hidv[k] != kEmpty) {
-      const float v = penalize(hx[k], sh.hcnt[tid + k * kThreads], sh.prm);
+      const float raw = k < kHxEarly ? hx[k < kHxEarly ? k : 0] : sl.x[hidv[k]];
+      const float v = penalize(raw, sh.hcnt[tid + k * kThreads], sh.prm);
       const uint32_t key = total_key(v);
       hpk[k] = pack(key, hidv[k]);
       hkey_max = max(hkey_max, key);

@@ -200,6 +200,63 @@ def gpu_worst(reps=10):
     return out
 
 
+def gpu_cliffs(reps=5):
+    """The paths config 5 does not take, timed. Top-k past the one-pass limit (k = 1,000, 10,000 and
+    248,319; sample.rs:296-299 gives the reference's CPU times for these), at T = 1 with no other
+    filter and no penalties, for one row (config 5's row 0) and for config 5's 256 rows; beside each,
+    the CPU oracle's µs for one row at the same k, one core. And config 5's workload drawn with
+    16,000-id histories (more distinct ids per slice than the scan's hash holds). Kernel µs per call (HIP events on the
+    library's stream) and the rows that took the exact path."""
+    import torch
+
+    sys.path.insert(0, os.path.join(ROOT, "tests"))
+    import oracle_lib as O
+
+    from artemis_amd import Context, PackedSampling, Sampling, states_tensor, workloads
+
+    w = workloads.config5()
+    dev = torch.device("cuda:0")
+    rows, n = w.logits.shape
+    host = torch.from_numpy(w.logits)
+    lg = host.to(dev)
+
+    def timed(ctx, logits, packed, rng, res, off=None, ids=None):
+        for _ in range(2):
+            ctx.sample_batch(logits, packed, rng, off, ids, out=res)
+        _, st, *_ = ctx.sample_batch(logits, packed, rng, off, ids, out=res)
+        status = st.cpu().numpy()
+        ctx.profile(True)
+        for _ in range(reps):
+            ctx.sample_batch(logits, packed, rng, off, ids, out=res)
+        scan_ms, rest_ms, calls = ctx.profile_read()
+        ctx.profile(False)
+        return dict(us_per_call=round((scan_ms + rest_ms) / calls * 1e3, 2), scan_us=round(scan_ms / calls * 1e3, 2),
+                    exact_rows=int(((status & 0x100) != 0).sum()), deep_rows=int(((status & 0x400) != 0).sum()))
+
+    out = {}
+    ctx1, ctx = Context(max_rows=1, max_vocab=n), Context(max_rows=rows, max_vocab=n)
+    row0 = np.ascontiguousarray(w.logits[0])
+    for k in (1000, 10000, 248319):
+        s = Sampling(1.0, k, 1.0, 0.0)
+        one = timed(ctx1, lg[:1], PackedSampling([s]), states_tensor([w.seeds[0]], dev), ctx1.outputs(1))
+        batch = timed(ctx, lg, PackedSampling([s] * rows), states_tensor(w.seeds, dev), ctx.outputs(rows))
+        cpu = []
+        for i in range(3 if k > 10000 else 10):
+            smp = O.Sampler(w.seeds[0], temp=1.0, top_k=k, top_p=1.0, min_p=0.0)
+            cpu.append(smp.sample_timed(row0)[1] / 1e3)
+        out[f"topk_{k}"] = dict(batch1=one, batch256=batch, cpu_oracle_us_one_row=round(float(np.median(cpu)), 1))
+    ctx1.close()
+    wh = workloads.config5(hist=16000)
+    off, ids = wh.hist_csr()
+    params = PackedSampling([Sampling(p.temp, p.top_k, p.top_p, p.min_p, p.presence, p.frequency, p.repetition)
+                             for p in wh.params])
+    lgh = torch.from_numpy(wh.logits).to(dev)
+    out["history_16000"] = timed(ctx, lgh, params, states_tensor(wh.seeds, dev), ctx.outputs(rows),
+                                 torch.from_numpy(off).to(dev), torch.from_numpy(ids).to(dev))
+    ctx.close()
+    return out
+
+
 def gpu_logprobs(reps=50):
     """as_logprobs (logprobs.rs:12-38) at top 20: kernel time per call for config 5's 256 rows
     (HIP events on the library's stream, inputs rotated over three copies) and the wall time of one
@@ -367,11 +424,20 @@ def cpu_baseline(reps=100):
     w = workloads.config5()
     off, ids = w.hist_csr()
     params = [settings(p) for p in w.params]
-    threads = min(os.cpu_count() or 1, 16)
+    # The box gives one GPU's job a 16-core share of its host (whatever os.cpu_count() shows).
+    threads = min(len(os.sched_getaffinity(0)), 16)
     t1 = time.perf_counter()
     O.sample_rows(params, w.seeds, w.logits, off, ids, threads=threads)
     many = time.perf_counter() - t1
-    return dict(per_config=per, all_cores_rows_per_s=w.logits.shape[0] / many, threads=threads)
+    model = ""
+    try:
+        with open("/proc/cpuinfo") as f:
+            model = next((ln.split(":", 1)[1].strip() for ln in f if ln.startswith("model name")), "")
+    except OSError:
+        pass
+    host = dict(cpu_model=model, os_cpu_count=os.cpu_count(), affinity=len(os.sched_getaffinity(0)),
+                omp_num_threads=os.environ.get("OMP_NUM_THREADS"))
+    return dict(per_config=per, all_cores_rows_per_s=w.logits.shape[0] / many, threads=threads, host=host)
 
 
 def main():
@@ -393,12 +459,14 @@ def main():
         sys.exit(2)
 
     g = gpu_config5(a.steps, a.warmup)
-    b1 = lpb = head = worst = None
+    b1 = lpb = head = worst = cliffs = None
     if not a.only_config5:
         log("bench: batch-1 latency")
         b1 = gpu_batch1()
         log("bench: worst-case batches")
         worst = gpu_worst()
+        log("bench: top-k past 256 and long histories")
+        cliffs = gpu_cliffs()
         log("bench: log-probabilities")
         lpb = gpu_logprobs()
         log("bench: output head")
@@ -424,7 +492,9 @@ def main():
                          "sample timed, one core",
                "per_config_us": c["per_config"],
                "all_cores": {"value": round(c["all_cores_rows_per_s"], 2), "cores": c["threads"],
-                             "sample": "all 256 config-5 rows, one row per task"}}
+                             "sample": "all 256 config-5 rows, one row per task, on the job's share of "
+                                       "the host (16 cores for one GPU)"},
+               "host": c["host"]}
     out = {
         "metric": "sampled rows/s (248,320-vocab f32, 256-row batch, full penalty+top-k+top-p+min-p chain)",
         "value": round(rows_per_s, 1),
@@ -450,6 +520,7 @@ def main():
         "deep_path_rows": g["deep_rows"],
         "batch1": b1,
         "worst_case_batches": worst,
+        "cliffs": cliffs,
         "logprobs_top20": lpb,
         "head_q6k_248320x2048": head,
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
