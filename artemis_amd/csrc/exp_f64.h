@@ -11,7 +11,7 @@
 //   result = scale + scale * (T_i + exp(r) - 1).
 // Which multiply-adds are fused matters for the last bit; the pattern below was matched bitwise
 // against the host exp on 4e7 arguments over [-745, 0], [-1, 1], random exponents and the subnormal
-// range, and is rechecked by tests/test_exp_f64.py. Everything else must compile with
+// range, and is rechecked by tests/test_gpu_sampler.py::test_gpu_exp_is_the_hosts. Everything else must compile with
 // -ffp-contract=off so that no other product is fused.
 #pragma once
 #include <stdint.h>

@@ -48,6 +48,24 @@ def test_matvec_every_type_and_shape_bit_for_bit(ctx, name):
         assert differ == 0, f"{name} {rows}x{k}: {differ} of {rows} outputs differ from the twin"
 
 
+def test_matvec_order_plants_match_the_twin(ctx):
+    # The oracle's order pins (test_oracle_quant.py) on the GPU: a unit's products folded in order
+    # (2^24 stays 2^24), a lane's units folded in unit order (likewise) and units strided over the
+    # lanes (2^24 + 2), in F32 rows.
+    cases = [(1024, {0: 2.0 ** 24, 2: 1.0, 3: 1.0}, 2.0 ** 24),
+             (3072, {0: 2.0 ** 24, 32 * 32: 1.0, 64 * 32: 1.0}, 2.0 ** 24),
+             (3072, {16 * 32: 2.0 ** 24, 32 * 32: 1.0, 64 * 32: 1.0}, 2.0 ** 24 + 2)]
+    for k, plants, want in cases:
+        w = np.zeros(k, np.float32)
+        for i, v in plants.items():
+            w[i] = v
+        x = np.ones(k, np.float32)
+        table = np.frombuffer(w.tobytes(), np.uint8).copy()
+        got = gpu_matvec(ctx, "F32", table, 1, k, x)
+        assert float(got[0]) == want, (k, float(got[0]), want)
+        assert np.array_equal(bits(got), bits(O.matvec(O.WTYPES["F32"], w.tobytes(), 1, k, x)))
+
+
 def test_matvec_q8_0_rows_of_one_unit_per_lane(ctx):
     # k = 32 * 33: lane 0 sums two units, the others one; k = 64: lanes 2..31 add nothing.
     rng = np.random.default_rng(3)

@@ -246,6 +246,84 @@ def test_matvec_adds_the_lanes_in_the_twins_tree():
     assert seq != y[0]
 
 
+def _f32_row_dot_model(w, x, lane_of_unit, unit_order, within):
+    """A model of one row's matvec in f32 for an F32 row: units of 32 products, each unit's products
+    folded by `within` ("seq": left to right from 0; "pairs": pairwise), unit u to lane
+    lane_of_unit(u), each lane's units folded from 0 in `unit_order`, then the 32 lanes by the twins'
+    tree (twin/mod.rs:15-25). The reference is ("seq", lane = u mod 32, ascending)."""
+    f = np.float32
+    prods = (w.astype(f) * x.astype(f)).astype(f).reshape(-1, 32)
+
+    def unit(u):
+        v = [f(t) for t in prods[u]]
+        if within == "seq":
+            acc = f(0)
+            for t in v:
+                acc = f(acc + t)
+            return acc
+        while len(v) > 1:
+            v = [f(v[i] + v[i + 1]) for i in range(0, len(v), 2)]
+        return v[0]
+
+    lanes = [[] for _ in range(32)]
+    for u in range(prods.shape[0]):
+        lanes[lane_of_unit(u)].append(u)
+    p = np.zeros(32, f)
+    for l in range(32):
+        acc = f(0)
+        for u in (lanes[l] if unit_order == "asc" else lanes[l][::-1]):
+            acc = f(acc + unit(u))
+        p[l] = acc
+    s = 16
+    while s:
+        p[:s] = (p[:s] + p[s:2 * s]).astype(f)
+        s //= 2
+    return float(p[0])
+
+
+def test_matvec_folds_a_units_products_left_to_right():
+    # twin/matvec.rs:22-30: unit_dot folds its 32 products from 0 in order. 2^24, 0, 1, 1 in one
+    # unit: in order each 1 rounds away (2^24 + 1 ties to 2^24); paired (or from the end), 1 + 1 = 2
+    # meets 2^24 and survives.
+    k = 1024
+    w = np.zeros(k, np.float32)
+    w[0], w[2], w[3] = 2.0 ** 24, 1.0, 1.0
+    x = np.ones(k, np.float32)
+    y = O.matvec(O.WTYPES["F32"], w.tobytes(), 1, k, x)
+    ref = _f32_row_dot_model(w, x, lambda u: u % 32, "asc", "seq")
+    assert ref == 2.0 ** 24 and y[0] == ref
+    assert _f32_row_dot_model(w, x, lambda u: u % 32, "asc", "pairs") == 2.0 ** 24 + 2
+
+
+def test_matvec_folds_a_lanes_units_in_unit_order():
+    # twin/matvec.rs:87-98: lane l folds units l, l + 32, l + 64, ... from 0 in that order. Units 0, 32
+    # and 64 (lane 0's, at k = 3,072) summing to 2^24, 1 and 1: in order the 1s round away; folded
+    # from the last unit first they add to 2 before 2^24.
+    k = 3072
+    w = np.zeros(k, np.float32)
+    w[0], w[32 * 32], w[64 * 32] = 2.0 ** 24, 1.0, 1.0
+    x = np.ones(k, np.float32)
+    y = O.matvec(O.WTYPES["F32"], w.tobytes(), 1, k, x)
+    ref = _f32_row_dot_model(w, x, lambda u: u % 32, "asc", "seq")
+    assert ref == 2.0 ** 24 and y[0] == ref
+    assert _f32_row_dot_model(w, x, lambda u: u % 32, "desc", "seq") == 2.0 ** 24 + 2
+
+
+def test_matvec_strides_units_over_the_lanes():
+    # twin/matvec.rs:87-98: unit u belongs to lane u mod 32. Units 32 and 64 (both lane 0's) at 1 and
+    # unit 16 (lane 16's) at 2^24: lane 0 holds 2 before the tree's first step adds lane 16 into it,
+    # 2^24 + 2 exactly. Units given to lanes in contiguous runs (lane = u / 3 at 96 units) would meet
+    # 2^24 one at a time in the tree, and each 1 would round away.
+    k = 3072
+    w = np.zeros(k, np.float32)
+    w[16 * 32], w[32 * 32], w[64 * 32] = 2.0 ** 24, 1.0, 1.0
+    x = np.ones(k, np.float32)
+    y = O.matvec(O.WTYPES["F32"], w.tobytes(), 1, k, x)
+    ref = _f32_row_dot_model(w, x, lambda u: u % 32, "asc", "seq")
+    assert ref == 2.0 ** 24 + 2 and y[0] == ref
+    assert _f32_row_dot_model(w, x, lambda u: u // 3, "asc", "seq") == 2.0 ** 24
+
+
 def test_matvec_refuses_partial_units():
     with pytest.raises(ValueError):
         O.matvec(O.WTYPES["F32"], bytes(4 * 40), 1, 40, np.zeros(40, np.float32))
