@@ -3070,6 +3070,9 @@ __device__ __forceinline__ void finish_row(const FinishArgs& a, uint32_t row) {
     if (p.mode == kModePartial && (p.top_p < 1.0f || has_floor) && !a.kept_ids && !too_many && P > 0 &&
         P + kWaveMax <= (uint32_t)kCap && (sh.tail_slot == kNone || sh.vast))
       drawn = fast_partial(a, sh, p, P, floor_cut, &keep, &status);
+    // S's listed values past the sorted candidates, not yet sorted (sorted only when the draw lands
+    // past the candidates, or kept lists need them): how many, and where they start.
+    uint32_t tail_unsorted = 0, sorted_p = 0;
     if (!drawn) {
       if (sh.tail_slot != kNone) tail_wait(a, row);
       // A row whose floor set S's parts listed (S: every value below R and at or above the floor),
@@ -3096,7 +3099,13 @@ __device__ __forceinline__ void finish_row(const FinishArgs& a, uint32_t row) {
           const uint32_t cnt = sh.tail_count;
           for (uint32_t i = tid; i < cnt; i += kThreads) sh.sk[P + i] = ld_agent(list + i);
           __syncthreads();
-          P += sort_candidates(sh, cnt, 0ull, (uint32_t)(R >> 32), kNone, P);
+          if (a.kept_ids && a.kept_cap > P) {
+            P += sort_candidates(sh, cnt, 0ull, (uint32_t)(R >> 32), kNone, P);
+          } else {
+            sorted_p = P;
+            tail_unsorted = cnt;
+            P += cnt;
+          }
           floor_set = true;
         }
       }
@@ -3277,14 +3286,37 @@ __device__ __forceinline__ void finish_row(const FinishArgs& a, uint32_t row) {
       // The draw over the kept prefix (sample.rs:184-197, 260-272): u = unit() * sum(w), then the
       // first rank whose cumulative weight exceeds u. Both sums are the reference's left folds in
       // rank order; past a few hundred tokens they come from a parallel scan with an error bound,
-      // and the sequential folds run only when the bound cannot decide.
+      // and the sequential folds run only when the bound cannot decide. S's listed values past the
+      // sorted candidates add to the total in any order (the scan's bound holds for any order of
+      // positive terms); they are sorted only when u lies past the candidates.
+      if (tail_unsorted && keep <= 256) {
+        sort_candidates(sh, tail_unsorted, 0ull, (uint32_t)(R >> 32), kNone, sorted_p);
+        tail_unsorted = 0;
+      }
       for (uint32_t i = tid; i < keep; i += kThreads) sh.wd[i] = w_temp(val(i));
       __syncthreads();
       if (keep > 256) {
         double loc[kScanPer], off;
-        const double S = prefix_scan(sh, keep, loc, &off);
+        double S = prefix_scan(sh, keep, loc, &off);
         const double d = gamma_n((double)keep) + gamma_n(40.0) + 4.0 * kU;
-        const uint32_t j = decide_draw(sh, keep, loc, off, sh.u01 * S * (1.0 - d), sh.u01 * S * (1.0 + d));
+        const uint32_t m = tail_unsorted ? sorted_p : keep;
+        uint32_t j = decide_draw(sh, m, loc, off, sh.u01 * S * (1.0 - d), sh.u01 * S * (1.0 + d));
+        if (tail_unsorted && j == m) {
+          // u lies past every candidate: S in rank order (the sort works in sh.wd), then the draw
+          // over all of it.
+          sort_candidates(sh, tail_unsorted, 0ull, (uint32_t)(R >> 32), kNone, sorted_p);
+          for (uint32_t i = tid; i < keep; i += kThreads) sh.wd[i] = w_temp(val(i));
+          __syncthreads();
+          S = prefix_scan(sh, keep, loc, &off);
+          j = decide_draw(sh, keep, loc, off, sh.u01 * S * (1.0 - d), sh.u01 * S * (1.0 + d));
+          tail_unsorted = 0;
+        } else if (tail_unsorted && j == kNone) {
+          // Undecided near a candidate: the sequential folds below need every weight in rank order.
+          sort_candidates(sh, tail_unsorted, 0ull, (uint32_t)(R >> 32), kNone, sorted_p);
+          for (uint32_t i = tid; i < keep; i += kThreads) sh.wd[i] = w_temp(val(i));
+          __syncthreads();
+          tail_unsorted = 0;
+        }
         if (j != kNone) {
           if (tid == 0) {
             sh.pick = (j < keep) ? j : keep - 1;  // past every cumulative: the last kept
