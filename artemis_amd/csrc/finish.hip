@@ -48,6 +48,7 @@ __global__ __launch_bounds__(1024) void finish_kernel(const FinishArgs* __restri
     a.tail_next->count = 0u;
   }
   as_fin_sliced::tail_list_load(a, row);
+  as_fin_sliced::row_prefetch(a, row);
   __syncthreads();
   as_fin_sliced::tail_help(a, row, gridDim.x);
   if (row < a.n_rows) {

@@ -48,6 +48,11 @@ struct Shared {
   // whether the kept set runs past them, and the bounds on u.
   uint32_t fp_m, fp_past;
   uint32_t vast;  // a slice found min-p's floor set vast
+  // The row's parameters, RNG state and history bounds, loaded with the list of flagged rows at the
+  // kernel's start (row_prefetch), so that a row that first takes parts of S finds them in LDS.
+  RowParams prm;
+  uint64_t rng4[4];
+  uint32_t pf_hb, pf_he;
   double fp_lo, fp_hi;
 };
 // The workgroup's LDS, at file scope so that the out-of-line paths below address it as LDS.
@@ -2849,13 +2854,46 @@ __device__ __noinline__ __attribute__((unused)) void tail_end(const FinishArgs& 
 
 // --- the kernel ---------------------------------------------------------------------------------
 
+// The first loads of a row's workgroup, issued with the list of flagged rows (tail_list_load) before
+// the barrier that follows it, so that they arrive in the same round trip: the slices' statistics,
+// the exp table, the row's parameters and history bounds, and its RNG state when it draws from its
+// own (a.rng_rows). A row that first takes parts of S (tail_help) then starts on them at once.
+__device__ __forceinline__ void row_prefetch(const FinishArgs& a, uint32_t row) {
+  Shared& sh = shm();
+  const uint32_t tid = threadIdx.x;
+  if (tid < 256) sh.tab[tid] = as_exp::kTable[tid];
+  if (row >= a.n_rows) return;
+  const SegStats* gst = a.stats + (uint64_t)row * a.n_seg;
+  for (uint32_t s = tid; s < a.n_seg; s += kThreads) sh.seg[s] = gload(gst + s);
+  static_assert(sizeof(RowParams) % 4 == 0 && sizeof(RowParams) / 4 <= (uint32_t)kThreads, "a word per thread");
+  if (tid < sizeof(RowParams) / 4)
+    reinterpret_cast<uint32_t*>(&sh.prm)[tid] = gload(reinterpret_cast<const uint32_t*>(a.params + row) + tid);
+  if (a.rng_rows && tid >= 64 && tid < 68) sh.rng4[tid - 64] = gload(a.rng_state + 4ull * row + (tid - 64));
+  if (tid == 96) {
+    // history_bounds, without the row's parameters when the CSR offsets are given.
+    uint32_t b = 0, e = 0;
+    if (a.hist_ids) {
+      if (a.hist_off) {
+        b = a.hist_off[row];
+        e = a.hist_off[row + 1];
+      } else {
+        const RowParams& pg = a.params[row];
+        b = pg.hist_begin;
+        e = pg.hist_begin + pg.hist_len;
+      }
+    }
+    sh.pf_hb = b;
+    sh.pf_he = e;
+  }
+}
+
 __device__ __forceinline__ void finish_row(const FinishArgs& a, uint32_t row) {
   Shared& sh = shm();
   const uint32_t tid = threadIdx.x;
-  const RowParams p = gload(a.params + row);
-  const SegStats* gst = a.stats + (uint64_t)row * a.n_seg;
+  // The slices' statistics, the exp table, the row's parameters, its history bounds and (drawing
+  // from its own state) its RNG state are in LDS already (row_prefetch).
+  const RowParams p = sh.prm;
   const uint32_t n = a.n;
-  if (tid < 256) sh.tab[tid] = as_exp::kTable[tid];
   // S's sums: none until a flagged row waits for them (tail_wait).
   if (tid == 0) {
     sh.have_tail = 0;
@@ -2864,23 +2902,18 @@ __device__ __forceinline__ void finish_row(const FinishArgs& a, uint32_t row) {
     sh.tail_parts = 0;
     sh.dp_pub = 0;
   }
-  // The slices' results, all loads in flight at once, with the row's RNG state and history bounds
-  // (thread 0 keeps them in registers for the merge below).
-  // The slices' statistics first (they need nothing loaded), then what needs the row's parameters,
-  // so that waiting for the statistics does not wait for the RNG state too.
-  for (uint32_t s = tid; s < a.n_seg; s += kThreads) sh.seg[s] = gload(gst + s);
   const bool draws = p.mode != kModeGreedy;
   uint64_t s4[4] = {0ull, 0ull, 0ull, 0ull};
   uint64_t* src = a.rng_state + 4ull * p.rng_index;
   uint32_t hb = 0, he = 0;
   if (tid == 0) {
-    // A row drawing from its own state (a.rng_rows) loads it beside its parameters rather than after.
     if (a.rng_rows) {
-      for (int k = 0; k < 4; ++k) s4[k] = gload(a.rng_state + 4ull * row + k);
+      for (int k = 0; k < 4; ++k) s4[k] = sh.rng4[k];
     } else if (draws) {
       for (int k = 0; k < 4; ++k) s4[k] = gload(src + k);
     }
-    he = as_launch::history_bounds(a, p, row, &hb);
+    hb = sh.pf_hb;
+    he = sh.pf_he;
   }
   __syncthreads();
   // The row's shared words go back to zero for the next call (this call's scan has ended, and their
