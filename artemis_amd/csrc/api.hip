@@ -264,11 +264,13 @@ int run_rows(as_ctx* c, const Plan& pl, RowParams* rows, const float* logits, ui
   bool own_states = true;
   for (uint32_t r = 0; r < n_rows && own_states; ++r) own_states = rows[r].rng_index == r;
   a.rng_rows = own_states ? 1u : 0u;
-  // Small batches share the deep passes with idle workgroups: any row without a top-k may take them
-  // (rows with kept lists take the full deep path, which is not shared).
-  bool partial = false;
-  for (uint32_t r = 0; r < n_rows; ++r) partial = partial || rows[r].mode == as_dev::kModePartial;
-  a.deep_help = (n_rows <= as_launch::kDeepHelpRows && !kept_ids && partial) ? 1u : 0u;
+  // Small batches share the deep passes with idle workgroups: any row without a top-k, or with one
+  // too large for the slices' candidates, may take them (rows with kept lists take the full deep
+  // path, which is not shared).
+  bool deep_rows = false;
+  for (uint32_t r = 0; r < n_rows; ++r)
+    deep_rows = deep_rows || rows[r].mode == as_dev::kModePartial || rows[r].mode == as_dev::kModeExactTopK;
+  a.deep_help = (n_rows <= as_launch::kDeepHelpRows && !kept_ids && deep_rows) ? 1u : 0u;
   const uint64_t deep_target = c->deep_rows_done + (a.deep_help ? n_rows : 0u);
   a.deep_target = deep_target;
 

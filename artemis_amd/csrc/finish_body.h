@@ -1364,7 +1364,11 @@ __device__ __noinline__ bool deep_bins(const FinishArgs& a, const RowParams& p, 
   const double top = (double)key_value(mk), temp = (double)p.temp, top_p = (double)p.top_p;
   const float topf = key_value(mk);
   const bool has_floor = p.min_p > 0.0f, by_top_p = p.top_p < 1.0f;
-  const bool unfiltered = !by_top_p && !has_floor;
+  // A top-k row keeps its k best ranks before top-p and min-p cut (sample.rs:157-161), and top-p's
+  // total is theirs.
+  const bool topk = p.mode == kModeTopK || p.mode == kModeExactTopK;
+  const uint32_t kk = topk ? p.top_k : n;
+  const bool unfiltered = !by_top_p && !has_floor && !topk;
   const float floorf = floor_f32(__dadd_rn(top, p.ln_min_p));
   // Bins of distance below the largest value, kNB over span, everything further down in the
   // last: below span a weight is under e^-32 of the largest's (span is 32 T above T = 1).
@@ -1475,10 +1479,32 @@ __device__ __noinline__ bool deep_bins(const FinishArgs& a, const RowParams& p, 
   auto Wc = [&](uint32_t b) -> double { return b == kNone ? 0.0 : hw[b]; };
   auto before = [](uint32_t b) -> uint32_t { return b == 0 ? kNone : b - 1; };
 
+  // top-k's count cut: rank k - 1 lies in bin bk, the first whose count reaches k.
+  uint32_t bk = kNB - 1;
+  if (topk) {
+    uint32_t a0 = kNone;
+#pragma unroll
+    for (int q = 0; q < kDPer; ++q) {
+      const uint32_t b = tid * kDPer + q;
+      if (hc[b] >= kk) a0 = min(a0, b);
+    }
+    bk = block_min_u32<kWaves>(a0, sh.red_u);
+    if (bk == kNone) return false;
+  }
+  // top-p's total1: the row's, or the top-k ranks' (those of the bins before bk and some of bk's:
+  // bounded here, summed from bk's sorted values below; each bound three times the error of that
+  // sum apart, so that the targets only narrow once it is known).
+  const double Em2 = Em + 2.0 * gamma_n(64.0) * M_all;
+  double M_lo = M_all - Em, M_hi = M_all + Em;
+  if (topk) {
+    M_lo = Mc(before(bk)) - 3.0 * Em2;
+    M_hi = Mc(bk) + 3.0 * Em2;
+  }
   // top-p's cut: the first rank whose reference cumulative reaches top_p, i.e. whose prefix S_j
   // reaches top_p * total1. Bins before c_lo cannot hold it (their prefixes cannot reach the least
-  // target); at the end of c_hi it has surely been reached.
-  const double tp_lo = top_p * (M_all - Em), tp_hi = top_p * (M_all + Em);
+  // target); at the end of c_hi it has surely been reached (for a top-k row, at bk's end at the
+  // latest: past rank k - 1 nothing is kept).
+  double tp_lo = top_p * M_lo, tp_hi = top_p * M_hi;
   uint32_t c_lo = kNone, c_hi = kNone;
   if (by_top_p) {
     uint32_t a0 = kNone, a1 = kNone;
@@ -1492,11 +1518,17 @@ __device__ __noinline__ bool deep_bins(const FinishArgs& a, const RowParams& p, 
     c_hi = block_min_u32<kWaves>(a1, sh.red_u);
     if (c_hi == kNone) c_hi = kNB - 1;
     if (c_lo == kNone) c_lo = c_hi;
+    c_lo = min(c_lo, bk);
+    c_hi = min(c_hi, bk);
   }
   // min-p's cut, the first rank below the floor, lies in the floor value's bin f (or at its ends).
   const uint32_t f = has_floor ? bin_of(floorf) : kNone;
   const bool need_c = by_top_p && !(has_floor && f < c_lo);  // else min-p surely cuts first
-  const bool need_f = has_floor && !(by_top_p && f > c_hi);  // else top-p surely cuts first
+  const bool need_f = has_floor && !(by_top_p && f > c_hi) && !(topk && f > bk);  // else another does
+  // The count cut, unless min-p surely cuts first; bk's values are collected for it and for top-p's
+  // total1.
+  const bool need_k = topk && !(has_floor && f < bk);
+  const bool need_bk = need_k || (topk && need_c);
   // The kept set ends in bins [k_lo, k_hi] (the last bin when nothing cuts).
   uint32_t k_lo = kNB - 1, k_hi = kNB - 1;
   if (need_c) {
@@ -1505,7 +1537,11 @@ __device__ __noinline__ bool deep_bins(const FinishArgs& a, const RowParams& p, 
   }
   if (need_f) {
     k_lo = min(k_lo, f);
-    k_hi = need_c ? min(k_hi, f) : f;
+    k_hi = min(k_hi, f);
+  }
+  if (need_k) {
+    k_lo = min(k_lo, bk);
+    k_hi = min(k_hi, bk);
   }
   // The draw: u = unit() * W, W the kept weight at T, in [Wc(k_lo - 1), Wc(k_hi)] (all of it when
   // nothing cuts); the bins that can hold the first cumulative above u, at most the kept set's.
@@ -1524,13 +1560,15 @@ __device__ __noinline__ bool deep_bins(const FinishArgs& a, const RowParams& p, 
     d_lo = min(block_min_u32<kWaves>(a0, sh.red_u), k_hi);
     d_hi = min(block_min_u32<kWaves>(a1, sh.red_u), k_hi);  // past the kept set: its last value
   }
-  // The runs of bins to collect, in bin order, merged where they touch.
+  // The runs of bins to collect, in bin order, merged where they touch (more than kBinRanges runs:
+  // the full deep path).
   uint32_t r0[kBinRanges], r1[kBinRanges], nr = 0;
   {
-    // The draw's, the cut's and the floor's (kNone: not needed), sorted by start with three
+    // The draw's, the cut's, the floor's and bk (kNone: not needed), sorted by start with five
     // compare-exchanges (kNone last), then merged.
-    uint32_t lo[kBinRanges] = {d_lo, need_c ? c_lo : kNone, need_f ? f : kNone};
-    uint32_t hi[kBinRanges] = {d_hi, need_c ? c_hi : kNone, need_f ? f : kNone};
+    constexpr uint32_t kIn = kBinRanges + 1;
+    uint32_t lo[kIn] = {d_lo, need_c ? c_lo : kNone, need_f ? f : kNone, need_bk ? bk : kNone};
+    uint32_t hi[kIn] = {d_hi, need_c ? c_hi : kNone, need_f ? f : kNone, need_bk ? bk : kNone};
     auto cx = [&](int i, int j) {
       if (lo[j] < lo[i]) {
         const uint32_t t0 = lo[i], t1 = hi[i];
@@ -1540,22 +1578,28 @@ __device__ __noinline__ bool deep_bins(const FinishArgs& a, const RowParams& p, 
         hi[j] = t1;
       }
     };
+    static_assert(kIn == 4, "a sorting network of four");
     cx(0, 1);
+    cx(2, 3);
+    cx(0, 2);
+    cx(1, 3);
     cx(1, 2);
-    cx(0, 1);
 #pragma unroll
     for (uint32_t i = 0; i < kBinRanges; ++i) {
       r0[i] = kNone;
       r1[i] = kNone;
     }
+    bool over = false;
 #pragma unroll
-    for (uint32_t i = 0; i < kBinRanges; ++i) {
+    for (uint32_t i = 0; i < kIn; ++i) {
       if (lo[i] == kNone) continue;
       if (nr > 0 && lo[i] <= sel3(nr - 1, r1[0], r1[1], r1[2]) + 1) {
         const uint32_t e = max(sel3(nr - 1, r1[0], r1[1], r1[2]), hi[i]);
 #pragma unroll
         for (uint32_t k = 0; k < kBinRanges; ++k)
           if (k + 1 == nr) r1[k] = e;
+      } else if (nr == kBinRanges) {
+        over = true;
       } else {
 #pragma unroll
         for (uint32_t k = 0; k < kBinRanges; ++k)
@@ -1566,6 +1610,7 @@ __device__ __noinline__ bool deep_bins(const FinishArgs& a, const RowParams& p, 
         ++nr;
       }
     }
+    if (over) return false;
   }
   // Per run: the count and weights before it, and where its values start among the collected ones.
   uint32_t cbr[kBinRanges], first[kBinRanges];
@@ -1678,11 +1723,33 @@ __device__ __noinline__ bool deep_bins(const FinishArgs& a, const RowParams& p, 
 
   // The cut (sample.rs:230-252): at the first rank below the floor, or one past the first whose
   // cumulative reaches top_p, whichever comes first.
+  // The run that holds rank r (kNone: not collected).
+  auto home_of = [&](uint32_t r) -> uint32_t {
+    uint32_t home = kNone;
+    for (uint32_t i = tid; i < P; i += kThreads) {
+      const uint32_t k = run_of(i);
+      if (rank_of(i, k) == r) home = k;
+    }
+    return block_min_u32<kWaves>(home, sh.red_u);
+  };
   uint32_t keep = n;
   double Wkeep = W_all, Wkeep_err = Ew;
-  if (need_c || need_f) {
+  if (need_c || need_f || topk) {
     for (uint32_t i = tid; i < P; i += kThreads) sh.wd[i] = need_c ? w1(val(i)) : 0.0;
     __syncthreads();
+    if (topk && need_c) {
+      // top-p's total1 over the top-k ranks: the prefix before rank k - 1's run plus that run's
+      // terms through it, within Em2 of the exact sum; the targets narrow to it.
+      const uint32_t home = home_of(kk - 1);
+      if (home == kNone) return false;
+      double part = 0.0;
+      for (uint32_t i = tid; i < P; i += kThreads)
+        if (run_of(i) == home && rank_of(i, home) < kk) part += sh.wd[i];
+      part = block_sum_f64<kWaves>(part, sh.red_d);
+      const double Mk = __dadd_rn(sel3(home, mbr[0], mbr[1], mbr[2]), part);
+      tp_lo = top_p * (Mk - Em2);
+      tp_hi = top_p * (Mk + Em2);
+    }
     scan_runs();
     uint32_t jl = kNone, jh = kNone, jf = kNone;
     const double err = Em + g40 * M_all;
@@ -1691,6 +1758,7 @@ __device__ __noinline__ bool deep_bins(const FinishArgs& a, const RowParams& p, 
       const uint32_t i = tid * kScanPer + q;
       if (i >= P) continue;
       const uint32_t k = run_of(i), r = rank_of(i, k);
+      if (r >= kk) continue;  // past top-k's cut
       if (need_f && !(val(i) >= floorf)) jf = min(jf, r);
       if (need_c) {
         const double S = __dadd_rn(sel3(k, mbr[0], mbr[1], mbr[2]), __dsub_rn(__dadd_rn(off, loc[q]), run_base[k]));
@@ -1703,12 +1771,18 @@ __device__ __noinline__ bool deep_bins(const FinishArgs& a, const RowParams& p, 
     jf = block_min_u32<kWaves>(jf, sh.red_u);
     uint32_t k_topp = kNone, k_floor = kNone;
     if (need_c) {
-      if (jl != jh || jh == kNone) return false;
-      k_topp = jh + 1;
+      // A top-k row's cumulative may not reach top_p by rank k - 1 (its terms' rounding): then
+      // top-p keeps all k (sample.rs:169-176).
+      if (topk && jl == kNone) {
+        k_topp = kNone;
+      } else {
+        if (jl != jh || jh == kNone) return false;
+        k_topp = jh + 1;
+      }
     }
     // The first value past the floor's bin is below the floor: min-p cuts there at the latest.
     if (need_f) k_floor = min(jf, cf_through);
-    keep = min(k_topp, k_floor);
+    keep = min(min(k_topp, k_floor), kk);
     // The kept weight at T: a prefix of whole bins when min-p cuts at its bin's ends, else a run's
     // prefix plus its terms through rank keep - 1.
     __syncthreads();
@@ -1719,12 +1793,7 @@ __device__ __noinline__ bool deep_bins(const FinishArgs& a, const RowParams& p, 
     } else if (need_f && keep == k_floor && keep == cf_before) {
       Wkeep = wf_before;
     } else {
-      uint32_t home = kNone;
-      for (uint32_t i = tid; i < P; i += kThreads) {
-        const uint32_t k = run_of(i);
-        if (rank_of(i, k) + 1 == keep) home = k;
-      }
-      home = block_min_u32<kWaves>(home, sh.red_u);
+      const uint32_t home = home_of(keep - 1);
       if (home == kNone) return false;
       double part = 0.0;
       for (uint32_t i = tid; i < P; i += kThreads)
@@ -3020,10 +3089,11 @@ __device__ __forceinline__ void finish_row(const FinishArgs& a, uint32_t row) {
     return;
   }
   // A small batch's row without a top-k (and not flagged for S's sums) may have to draw past its
-  // candidates: it publishes its deep histogram pass now, so that the workgroups with no row left
-  // sum it while this one sorts and tries its candidates (when they settle the row, the pass goes
-  // unused).
-  if (a.deep_help && !a.kept_ids && p.mode == kModePartial && !sh.stats_bad && sh.tail_slot == kNone) {
+  // candidates, and one whose top-k is too large for them surely does: it publishes its deep
+  // histogram pass now, so that the workgroups with no row left sum it while this one sorts and
+  // tries its candidates (when they settle the row, the pass goes unused).
+  if (a.deep_help && !a.kept_ids && (p.mode == kModePartial || p.mode == kModeExactTopK) && !sh.stats_bad &&
+      sh.tail_slot == kNone) {
     deep_publish_hist(a, row, sh.mk);
     if (tid == 0) sh.dp_pub = 1;  // read after later barriers
   }
@@ -3409,16 +3479,16 @@ __device__ __forceinline__ void finish_row(const FinishArgs& a, uint32_t row) {
   }
 
   if (sh.exact) {
-    // Rows without a top-k first try collecting only the bins their decisions fall in (kept lists
-    // need every kept value in order: those rows take the full deep path). Each path is called at
-    // the same depth, so that the kernel's stack is the largest of theirs, not their sum.
+    // Rows first try collecting only the bins their decisions fall in (kept lists need every kept
+    // value in order: those rows take the full deep path). Each path is called at the same depth,
+    // so that the kernel's stack is the largest of theirs, not their sum.
     __syncthreads();
     // A flagged row's parts write its scratch: they have all ended before the passes below use it.
     if (sh.tail_slot != kNone && !sh.tail_waited) tail_wait(a, row);
     const RowParams& pr = a.params[row];
     const bool pen = deep_prep(a, pr, row);
     bool done = false;
-    if (!sh.stats_bad && pr.mode != kModeTopK && pr.mode != kModeExactTopK && !a.kept_ids) {
+    if (!sh.stats_bad && !a.kept_ids) {
       done = a.deep_help ? deep_bins<true>(a, pr, row, pen) : deep_bins<false>(a, pr, row, pen);
       __syncthreads();
     }

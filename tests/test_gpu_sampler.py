@@ -166,6 +166,15 @@ def test_small_rows_match_the_oracle(ctx, n):
     g = gpu_batch(ctx, logits, params, seeds, hists, kept_cap=64)
     want = oracle_rows(logits, params, seeds, hists, kept_cap=64)
     check_rows(g, want, params, kept_cap=64, label=f"n={n}")
+    if n >= 300:
+        # Without kept lists rows past their candidates first try the histogram bins' decisions (top-k
+        # 300 rows among them); in batches of 12 the idle workgroups share those passes.
+        k300 = [i for i, p in enumerate(GRID) if p["top_k"] == 300 and p["temp"] in (0.6, 1.0)]
+        drawn = [i for i, p in enumerate(GRID) if p["temp"] > 0]
+        for sub in (k300, drawn):
+            pr = [params[i] for i in sub]
+            g = gpu_batch(ctx, logits[sub], pr, [seeds[i] for i in sub], [hists[i] for i in sub])
+            check_rows(g, [want[i] for i in sub], pr, label=f"n={n}, no kept lists, {len(sub)} rows")
 
 
 def test_nonfinite_rows_report_their_first_index_and_keep_the_stream(ctx):
@@ -318,6 +327,51 @@ def test_more_flagged_rows_than_the_list_holds(ctx):
     assert (g["rng"] == rng).all()
     st = g["status"]
     assert not ((st & AS_ROW_DEEP_PATH) != 0).any(), st
+
+
+@pytest.mark.parametrize("n_rows", [12, 40])
+def test_large_top_k_rows_match_the_oracle(ctx, n_rows):
+    # Top-k rows whose k is past the slices' candidates (sample.rs:157-198 with k > 256) at the
+    # model's vocabulary, without kept lists: the count cut, top-p's total over the k best, min-p's
+    # floor and the draw are decided from the row's histogram bins where they can be. 12 rows share
+    # the deep passes with idle workgroups, 40 take them alone. Logits: a spread like a model's,
+    # heavy ties (the k-th best inside a tie run) and a narrow band with spread highs.
+    from artemis_amd import AS_ROW_DEEP_PATH, AS_ROW_EXACT_PATH
+    N = VOCAB
+    gen = np.random.default_rng(900 + n_rows)
+    ks = [257, 300, 1000, 10_000, 100_000, N - 2, N - 1]
+    settings = [(1.0, 1.0, 0.0), (0.6, 0.95, 0.0), (1.0, 0.5, 0.05), (3.0, 1.0, 0.001), (0.7, 0.9, 0.02),
+                (1.0, 0.99999, 0.0), (0.8, 1.0, 0.0)]
+    params, logits, seeds, hists = [], [], [], []
+    for r in range(n_rows):
+        k = ks[r % len(ks)]
+        t, tp, mp = settings[(r // len(ks) + 3 * r) % len(settings)]
+        p = dict(temp=t, top_k=k, top_p=tp, min_p=mp)
+        if r % 3 == 1:
+            p.update(presence=1.5)
+        elif r % 3 == 2:
+            p.update(presence=0.5, frequency=0.3, repetition=1.05)
+        shape = (r // 2) % 3
+        if shape == 0:
+            l = (gen.standard_normal(N) * 2.5).astype(np.float32)
+        elif shape == 1:
+            l = (np.round(gen.standard_normal(N) * 8) / 4).astype(np.float32)
+        else:
+            l = (gen.random(N) * 4 - 8).astype(np.float32)
+            l[::1009] = 5.0 + gen.random(len(l[::1009])).astype(np.float32)
+        params.append(p)
+        logits.append(l)
+        seeds.append(4100 + r)
+        hists.append(gen.integers(0, N, size=40).astype(np.uint32) if r % 3 else np.zeros(0, np.uint32))
+    logits = np.stack(logits)
+    g = gpu_batch(ctx, logits, params, seeds, hists)
+    want = oracle_rows(logits, params, seeds, hists)
+    check_rows(g, want, params, label=f"large top-k, {n_rows} rows")
+    # Every row is settled past the candidates; a top-p of 0.99999 over nearly the whole row may cut
+    # where no bin's bounds decide, and goes on to the exact-order path.
+    st = g["status"]
+    assert ((st & (AS_ROW_DEEP_PATH | AS_ROW_EXACT_PATH)) != 0).all(), st
+    assert all(st[r] & AS_ROW_DEEP_PATH for r in range(n_rows) if params[r]["top_p"] != 0.99999), st
 
 
 def test_large_floor_sets_match_the_oracle(ctx):
