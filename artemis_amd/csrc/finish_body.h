@@ -61,23 +61,18 @@ __device__ __forceinline__ Shared& shm() { return g_sh_static; }
 
 // --- block helpers ------------------------------------------------------------------------------
 
-// Exclusive prefix sum of one f64 per thread over the block.
+// Exclusive prefix sum of one f64 per thread over the block: a wave scan, then every wave scans the
+// waves' totals (depth 6 + 4 + 1 over any thread's terms).
 __device__ double block_exclusive_scan_f64(double x, double* wave_tot) {
   const int lane = threadIdx.x & (kWave - 1), w = threadIdx.x / kWave;
-  double incl = x;
-  for (int o = 1; o < kWave; o <<= 1) {
-    const double y = __shfl_up(incl, o, kWave);
-    if (lane >= o) incl = __dadd_rn(incl, y);
-  }
+  const double incl = wave_scan_f64(x);
   __syncthreads();
   if (lane == kWave - 1) wave_tot[w] = incl;
   __syncthreads();
-  double before = 0.0;
-  for (int k = 0; k < w; ++k) before = __dadd_rn(before, wave_tot[k]);
-  // incl - x is not exact; recompute the exclusive value from the wave's shifted inclusive scan.
-  double excl_in_wave = __shfl_up(incl, 1, kWave);
-  if (lane == 0) excl_in_wave = 0.0;
-  return __dadd_rn(before, excl_in_wave);
+  const double waves = wave_scan_f64(lane < kWaves ? wave_tot[lane] : 0.0);
+  const double before = w == 0 ? 0.0 : wave_lane_f64(waves, (uint32_t)(w - 1));
+  // incl - x is not exact; the exclusive value is the wave's inclusive scan shifted by a lane.
+  return __dadd_rn(before, wave_prev_f64(incl));
 }
 
 // --- the exact-order path ---------------------------------------------------------------------
@@ -355,21 +350,13 @@ static_assert(kBuckets % kThreads == 0 && kBuckets <= sizeof(Shared::bcnt) / 4, 
 // Exclusive prefix sum of one u32 per thread over the block; *total gets the sum.
 __device__ uint32_t block_exclusive_scan_u32(uint32_t x, uint32_t* wave_tot, uint32_t* total) {
   const int lane = threadIdx.x & (kWave - 1), w = threadIdx.x / kWave;
-  uint32_t incl = x;
-  for (int o = 1; o < kWave; o <<= 1) {
-    const uint32_t y = (uint32_t)__shfl_up((int)incl, o, kWave);
-    if (lane >= o) incl += y;
-  }
+  const uint32_t incl = wave_scan_u32(x);
   __syncthreads();
   if (lane == kWave - 1) wave_tot[w] = incl;
   __syncthreads();
-  uint32_t before = 0, all = 0;
-  for (int k = 0; k < kWaves; ++k) {
-    if (k < w) before += wave_tot[k];
-    all += wave_tot[k];
-  }
-  *total = all;
-  return before + incl - x;
+  const uint32_t waves = wave_scan_u32(lane < kWaves ? wave_tot[lane] : 0u);
+  *total = wave_lane_u32(waves, kWaves - 1);
+  return (w == 0 ? 0u : wave_lane_u32(waves, (uint32_t)(w - 1))) + incl - x;
 }
 
 // The row's total from the slices' sums: total1 (by_temp false: sum of exp(l - top)) or the
@@ -513,13 +500,7 @@ __device__ __forceinline__ uint32_t sort_candidates(Shared& sh, uint32_t total, 
       cs[q] = sh.bcnt[tid * kB + q];
       run += cs[q];
     }
-    uint32_t incl = run;
-#pragma unroll
-    for (int o = 1; o < kWave; o <<= 1) {
-      const uint32_t y = (uint32_t)__shfl_up((int)incl, o, kWave);
-      if (tid >= (uint32_t)o) incl += y;
-    }
-    uint32_t off = incl - run;
+    uint32_t off = wave_scan_u32(run) - run;
 #pragma unroll
     for (uint32_t q = 0; q < kB; ++q) {
       sh.bstart[tid * kB + q] = off;
@@ -2499,16 +2480,8 @@ __device__ __noinline__ uint32_t draw_past(const FinishArgs& a, const RowParams&
           mlo[q] = rl;
         }
         // The lanes before this one, by an inclusive scan over the lanes.
-        double ih = rh, il = rl;
-        for (int o = 1; o < kWave; o <<= 1) {
-          const double yh = __shfl_up(ih, o, kWave), yl = __shfl_up(il, o, kWave);
-          if (tid >= (uint32_t)o) {
-            ih = __dadd_rn(ih, yh);
-            il = __dadd_rn(il, yl);
-          }
-        }
-        const double ph = __shfl_up(ih, 1, kWave), pl = __shfl_up(il, 1, kWave);
-        const double eh = tid == 0 ? 0.0 : ph, el = tid == 0 ? 0.0 : pl;
+        const double ih = wave_scan_f64(rh), il = wave_scan_f64(rl);
+        const double eh = wave_prev_f64(ih), el = wave_prev_f64(il);
         uint32_t a_min = kNone, a_max = kNone;
 #pragma unroll
         for (uint32_t q = 0; q < kBPer; ++q) {
@@ -3015,13 +2988,9 @@ __device__ __forceinline__ void finish_row(const FinishArgs& a, uint32_t row) {
         if (t.truncated & 2u) long_hist = 1;
         vast |= t.vast;
       }
-      uint32_t incl = c;
-      for (int o = 1; o < kWave; o <<= 1) {
-        const uint32_t y = (uint32_t)__shfl_up((int)incl, o, kWave);
-        if (lane >= (uint32_t)o) incl += y;
-      }
+      const uint32_t incl = wave_scan_u32(c);
       if (s < a.n_seg) sh.seg_off[s] = run + incl - c;
-      run += (uint32_t)__shfl((int)incl, kWave - 1, kWave);
+      run += wave_lane_u32(incl, kWave - 1);
     }
     bad = wave_min_u32(bad);
     mk = wave_max_u32(mk);

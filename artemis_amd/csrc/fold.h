@@ -125,24 +125,17 @@ constexpr uint32_t kWaveMax = kWPer * kWave;
 
 // Inclusive prefix sums pre[] of the values w[] in rank order; returns the total to every lane.
 __device__ __forceinline__ double wave_prefix(const double (&w)[kWPer], double (&pre)[kWPer]) {
-  const uint32_t lane = threadIdx.x & (kWave - 1);
   double run = 0.0;
 #pragma unroll
   for (int q = 0; q < kWPer; ++q) {
     run = __dadd_rn(run, w[q]);
     pre[q] = run;
   }
-  double incl = run;
-#pragma unroll
-  for (int o = 1; o < kWave; o <<= 1) {
-    const double y = __shfl_up(incl, o, kWave);
-    if (lane >= (uint32_t)o) incl = __dadd_rn(incl, y);
-  }
-  double excl = __shfl_up(incl, 1, kWave);
-  if (lane == 0) excl = 0.0;
+  const double incl = wave_scan_f64(run);
+  const double excl = wave_prev_f64(incl);
 #pragma unroll
   for (int q = 0; q < kWPer; ++q) pre[q] = __dadd_rn(excl, pre[q]);
-  return __shfl(incl, kWave - 1, kWave);
+  return wave_lane_f64(incl, kWave - 1);
 }
 // The first rank below m whose flag is set (m when none).
 __device__ __forceinline__ uint32_t wave_first(const bool (&f)[kWPer], uint32_t m) {

@@ -227,6 +227,54 @@ __device__ __forceinline__ uint32_t wave_sum_u32(uint32_t v) { return __ockl_wfr
 __device__ __forceinline__ double wave_sum_f64(double v) { return __ockl_wfred_add_f64(v); }
 __device__ __forceinline__ uint64_t wave_max_u64(uint64_t v) { return __ockl_wfred_max_u64(v); }
 
+// ---- wave64 scans by DPP lane moves -----------------------------------------------------------
+// Lane i's inclusive sum of lanes 0..i by Hillis-Steele steps inside each row of 16 lanes (row_shr
+// 1, 2, 4, 8), then across rows (row_bcast:15 carries a row's last lane into rows 1 and 3,
+// row_bcast:31 lane 31 into rows 2 and 3): every lane's sum is a tree of depth 6 over its terms, as
+// a shuffle-based Hillis-Steele scan's is, without the shuffles' trips through the LDS crossbar. A
+// lane with no source lane, or outside the row mask, reads 0.
+constexpr int kDppRowShr = 0x110, kDppWaveShr1 = 0x138, kDppRowBcast15 = 0x142, kDppRowBcast31 = 0x143;
+template <int kCtrl, int kRowMask = 0xf>
+__device__ __forceinline__ uint32_t dpp_u32(uint32_t x) {
+  return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, kCtrl, kRowMask, 0xf, true);
+}
+template <int kCtrl, int kRowMask = 0xf>
+__device__ __forceinline__ double dpp_f64(double x) {
+  const uint64_t b = __builtin_bit_cast(uint64_t, x);
+  const uint64_t lo = dpp_u32<kCtrl, kRowMask>((uint32_t)b), hi = dpp_u32<kCtrl, kRowMask>((uint32_t)(b >> 32));
+  return __builtin_bit_cast(double, lo | (hi << 32));
+}
+__device__ __forceinline__ uint32_t wave_scan_u32(uint32_t x) {
+  x += dpp_u32<kDppRowShr + 1>(x);
+  x += dpp_u32<kDppRowShr + 2>(x);
+  x += dpp_u32<kDppRowShr + 4>(x);
+  x += dpp_u32<kDppRowShr + 8>(x);
+  x += dpp_u32<kDppRowBcast15, 0xa>(x);
+  x += dpp_u32<kDppRowBcast31, 0xc>(x);
+  return x;
+}
+__device__ __forceinline__ double wave_scan_f64(double x) {
+  x = __dadd_rn(x, dpp_f64<kDppRowShr + 1>(x));
+  x = __dadd_rn(x, dpp_f64<kDppRowShr + 2>(x));
+  x = __dadd_rn(x, dpp_f64<kDppRowShr + 4>(x));
+  x = __dadd_rn(x, dpp_f64<kDppRowShr + 8>(x));
+  x = __dadd_rn(x, dpp_f64<kDppRowBcast15, 0xa>(x));
+  x = __dadd_rn(x, dpp_f64<kDppRowBcast31, 0xc>(x));
+  return x;
+}
+// Lane i - 1's value (0 on lane 0), e.g. the exclusive sum from the inclusive one.
+__device__ __forceinline__ uint32_t wave_prev_u32(uint32_t x) { return dpp_u32<kDppWaveShr1>(x); }
+__device__ __forceinline__ double wave_prev_f64(double x) { return dpp_f64<kDppWaveShr1>(x); }
+// Lane k's value in every lane (k the same in the whole wave).
+__device__ __forceinline__ uint32_t wave_lane_u32(uint32_t x, uint32_t k) {
+  return (uint32_t)__builtin_amdgcn_readlane((int)x, (int)__builtin_amdgcn_readfirstlane(k));
+}
+__device__ __forceinline__ double wave_lane_f64(double x, uint32_t k) {
+  const uint64_t b = __builtin_bit_cast(uint64_t, x);
+  const uint64_t lo = wave_lane_u32((uint32_t)b, k), hi = wave_lane_u32((uint32_t)(b >> 32), k);
+  return __builtin_bit_cast(double, lo | (hi << 32));
+}
+
 // Greedy's order (sample.rs:9-17): a larger value by IEEE `>`, equal values to the lower index;
 // kNone loses to anything.
 __device__ __forceinline__ void greedy_merge(float& v, uint32_t& i, float v2, uint32_t i2) {

@@ -787,38 +787,81 @@ __device__ __forceinline__ void scan_slice(
   __syncthreads();  // the tables clear, the parameters in LDS
 
   if (sl.pen) {
-    auto mark = [&](uint32_t id) {
+    // A history of at most kHistRegs ids per thread is short: its ids go to the table's first
+    // kHashPrimary slots (those whose raw values load before the stream) within kPrimaryProbes
+    // probes, the rest of the table takes the others. A longer one's ids hash over the whole table:
+    // once its distinct ids fill the first part, every id past it would first probe all of it. An
+    // id's probe sequence is fixed for the call and slots are never freed, so every thread marking
+    // it reaches the same slot.
+    const bool long_hist = he - hb > (uint32_t)(kHistRegs * kThreads);
+    auto count = [&](uint32_t slot, uint32_t id) {
+      const uint32_t prev = atomicCAS(&sh.hid[slot], kEmpty, id);
+      if (prev == kEmpty || prev == id) {
+        atomicAdd(&sh.hcnt[slot], 1u);
+        return true;
+      }
+      return false;
+    };
+    auto mark_in = [&](uint32_t id) {  // id in the slice
       const uint32_t off = id - sl.b0;
-      if (off >= len) return;
       atomicOr(&sh.bitmap[off >> 5], 1u << (off & 31u));
-      // The first kHashPrimary slots (those whose raw values load before the stream) take an id
-      // within kPrimaryProbes probes; the rest of the table takes the others. An id's probe sequence
-      // is fixed and slots are never freed, so every thread marking it reaches the same slot.
+      if (long_hist) {
+        uint32_t h = (uint32_t)(((uint64_t)(id * 0x85EBCA77u) * kHash) >> 32);
+        for (uint32_t probe = 0; probe < kHash; ++probe) {
+          if (count(h, id)) return;
+          h = (h + 1) & (kHash - 1);
+        }
+        sh.overflow = 1;
+        return;
+      }
       uint32_t h = (id * 0x9E3779B1u) >> kPrimaryShift;
       for (uint32_t probe = 0; probe < kPrimaryProbes; ++probe) {
-        const uint32_t prev = atomicCAS(&sh.hid[h], kEmpty, id);
-        if (prev == kEmpty || prev == id) {
-          atomicAdd(&sh.hcnt[h], 1u);
-          return;
-        }
+        if (count(h, id)) return;
         h = (h + 1) & (kHashPrimary - 1);
       }
       constexpr uint32_t kRest = kHash - kHashPrimary;
       h = (uint32_t)(((uint64_t)(id * 0x85EBCA77u) * kRest) >> 32);
       for (uint32_t probe = 0; probe < kRest; ++probe) {
-        const uint32_t prev = atomicCAS(&sh.hid[kHashPrimary + h], kEmpty, id);
-        if (prev == kEmpty || prev == id) {
-          atomicAdd(&sh.hcnt[kHashPrimary + h], 1u);
-          return;
-        }
+        if (count(kHashPrimary + h, id)) return;
         h = h + 1 == kRest ? 0u : h + 1;
       }
       sh.overflow = 1;
     };
+    auto mark = [&](uint32_t id) {
+      if (id - sl.b0 < len) mark_in(id);
+    };
+    if (!long_hist) {
 #pragma unroll
-    for (int k = 0; k < kHistRegs; ++k)
-      if (hreg[k] != kEmpty) mark(hreg[k]);
-    for (uint32_t h = hb + tid + kHistRegs * kThreads; h < he; h += kThreads) mark(hist_ids[h]);
+      for (int k = 0; k < kHistRegs; ++k)
+        if (hreg[k] != kEmpty) mark(hreg[k]);
+    } else {
+      // kHistRegs ids per thread a step, their loads in flight together; each wave packs the ids in
+      // the slice (about one in n_seg) into its candidate buffer, which the stream has not begun to
+      // use, and marks them with every lane busy.
+      uint32_t* pack = reinterpret_cast<uint32_t*>(sh.buf[w]);
+      static_assert(kHistRegs * kWave <= 2 * kCapW, "a step's ids fit a wave's buffer");
+      for (uint32_t h0 = hb;; h0 += kHistRegs * kThreads) {
+        if (h0 != hb) {
+#pragma unroll
+          for (int k = 0; k < kHistRegs; ++k) {
+            const uint32_t h = h0 + tid + k * kThreads;
+            hreg[k] = h < he ? hist_ids[h] : kEmpty;
+          }
+        }
+        uint32_t m = 0;
+#pragma unroll
+        for (int k = 0; k < kHistRegs; ++k) {
+          const bool in = hreg[k] - sl.b0 < len;  // kEmpty is past every slice
+          const uint64_t bal = __ballot(in);
+          if (in) pack[m + lanes_below(bal)] = hreg[k];
+          m += (uint32_t)__builtin_popcountll(bal);
+        }
+        __builtin_amdgcn_wave_barrier();
+        for (uint32_t i = lane; i < m; i += kWave) mark_in(pack[i]);
+        __builtin_amdgcn_wave_barrier();
+        if (h0 + kHistRegs * kThreads >= he) break;
+      }
+    }
     for (uint32_t h = tid; h < extra; h += kThreads) mark(extra_ids[h]);
   }
   __syncthreads();
