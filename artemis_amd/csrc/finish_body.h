@@ -1702,6 +1702,177 @@ __device__ __noinline__ bool deep_bins(const FinishArgs& a, const RowParams& p, 
   };
   const double g40 = 2.0 * gamma_n(40.0);
 
+  // Up to kWaveMax collected values: wave 0 takes the decisions below from registers (lane l holds
+  // collected values kWPer l .. kWPer l + kWPer - 1, their prefixes come from a wave scan) with the
+  // same bounds and no block-wide step, and the other waves wait at one barrier. A prefix through
+  // collected value i is within gamma(kWPer + 7) of its exact sum, inside the block path's gamma(40).
+  if (P <= kWaveMax) {
+    if (tid < kWave) {
+      const uint32_t i0 = tid * kWPer;
+      float v[kWPer];
+      uint32_t rn[kWPer], rk[kWPer];
+#pragma unroll
+      for (int q = 0; q < kWPer; ++q) {
+        const uint32_t i = i0 + q;
+        v[q] = i < P ? val(i) : 0.0f;
+        rn[q] = run_of(i);
+        rk[q] = i < P ? rank_of(i, rn[q]) : kNone;
+      }
+      // Where a rank's value lies among the collected ones (kNone: not collected), and the run that
+      // holds it: run k holds ranks cbr[k] .. and collected values first[k] .., up to the next run's.
+      auto index_of = [&](uint32_t r, uint32_t* home) -> uint32_t {
+        uint32_t j = kNone;
+#pragma unroll
+        for (uint32_t k = 0; k < kBinRanges; ++k) {
+          if (k >= nr) continue;
+          const uint32_t f0 = sel3(k, first[0], first[1], first[2]);
+          const uint32_t f1 = k + 1 < nr ? sel3(k + 1, first[0], first[1], first[2]) : P;
+          const uint32_t c0 = sel3(k, cbr[0], cbr[1], cbr[2]);
+          if (r >= c0 && r - c0 < f1 - f0) {
+            j = f0 + (r - c0);
+            *home = k;
+          }
+        }
+        return j;
+      };
+      double w[kWPer], pre[kWPer], rb[kBinRanges];
+      // The prefixes of w in pre, and per run the prefix just before it in rb.
+      auto prefixes = [&]() {
+        wave_prefix(w, pre);
+#pragma unroll
+        for (uint32_t k = 0; k < kBinRanges; ++k) {
+          const uint32_t f = sel3(k, first[0], first[1], first[2]);
+          double x = 0.0;
+          if (k > 0 && k < nr && f > 0) {
+            const uint32_t j = f - 1, qj = j % kWPer;
+            double y = pre[0];
+#pragma unroll
+            for (int q = 1; q < kWPer; ++q)
+              if ((uint32_t)q == qj) y = pre[q];
+            x = wave_lane_f64(y, j / kWPer);
+          }
+          rb[k] = x;
+        }
+      };
+      // The prefix through collected value j in run k, above the run's start.
+      auto run_part = [&](uint32_t j, uint32_t k) -> double {
+        const uint32_t qj = j % kWPer;
+        double y = pre[0];
+#pragma unroll
+        for (int q = 1; q < kWPer; ++q)
+          if ((uint32_t)q == qj) y = pre[q];
+        return __dsub_rn(wave_lane_f64(y, j / kWPer), sel3(k, rb[0], rb[1], rb[2]));
+      };
+      bool ok = true;
+      uint32_t keep_w = n, k_floor = kNone;
+      double Wk = W_all, Wk_err = Ew;
+      if (need_c || need_f || topk) {
+        uint32_t jl = kNone, jh = kNone, jf = kNone;
+        if (need_c) {
+#pragma unroll
+          for (int q = 0; q < kWPer; ++q) w[q] = i0 + q < P ? w1(v[q]) : 0.0;
+          prefixes();
+          double tlo = tp_lo, thi = tp_hi;
+          if (topk) {
+            uint32_t home = kNone;
+            const uint32_t j = index_of(kk - 1, &home);
+            if (j == kNone) {
+              ok = false;
+            } else {
+              const double Mk = __dadd_rn(sel3(home, mbr[0], mbr[1], mbr[2]), run_part(j, home));
+              tlo = top_p * (Mk - Em2);
+              thi = top_p * (Mk + Em2);
+            }
+          }
+          const double err = Em + g40 * M_all;
+#pragma unroll
+          for (int q = 0; q < kWPer; ++q) {
+            if (i0 + q >= P || rk[q] >= kk) continue;
+            const uint32_t k = rn[q];
+            const double S = __dadd_rn(sel3(k, mbr[0], mbr[1], mbr[2]), __dsub_rn(pre[q], sel3(k, rb[0], rb[1], rb[2])));
+            if ((S + err) * (1.0 + gj) >= tlo) jl = min(jl, rk[q]);
+            if ((S - err) * (1.0 - gj) >= thi) jh = min(jh, rk[q]);
+          }
+        }
+#pragma unroll
+        for (int q = 0; q < kWPer; ++q)
+          if (need_f && i0 + q < P && rk[q] < kk && !(v[q] >= floorf)) jf = min(jf, rk[q]);
+        jl = wave_min_u32(jl);
+        jh = wave_min_u32(jh);
+        jf = wave_min_u32(jf);
+        uint32_t k_topp = kNone;
+        if (need_c) {
+          if (topk && jl == kNone) {
+            k_topp = kNone;
+          } else if (jl != jh || jh == kNone) {
+            ok = false;
+          } else {
+            k_topp = jh + 1;
+          }
+        }
+        if (need_f) k_floor = min(jf, cf_through);
+        keep_w = min(min(k_topp, k_floor), kk);
+        Wk_err = Ew + 2.0 * gamma_n(64.0) * W_all;
+      }
+      // The weights at T and their prefixes; the kept weight, a prefix of whole bins when min-p cuts
+      // at its bin's ends, else a run's prefix plus its terms through rank keep - 1.
+#pragma unroll
+      for (int q = 0; q < kWPer; ++q) w[q] = i0 + q < P ? wt(v[q]) : 0.0;
+      prefixes();
+      if (need_c || need_f || topk) {
+        if (need_f && keep_w == k_floor && keep_w == cf_through) {
+          Wk = wf_through;
+        } else if (need_f && keep_w == k_floor && keep_w == cf_before) {
+          Wk = wf_before;
+        } else {
+          uint32_t home = kNone;
+          const uint32_t j = keep_w > 0 ? index_of(keep_w - 1, &home) : kNone;
+          if (j == kNone) ok = false;
+          else Wk = __dadd_rn(sel3(home, wbr[0], wbr[1], wbr[2]), run_part(j, home));
+        }
+      }
+      // The draw, as below.
+      const double ulo = sh.u01 * (Wk - Wk_err) * (1.0 - gj) * (1.0 - 4.0 * kU);
+      const double uhi = sh.u01 * (Wk + Wk_err) * (1.0 + gj) * (1.0 + 4.0 * kU);
+      const double err = Ew + g40 * W_all;
+      uint32_t jp = kNone, jc = kNone, last = kNone;
+#pragma unroll
+      for (int q = 0; q < kWPer; ++q) {
+        if (i0 + q >= P || rk[q] >= keep_w) continue;
+        if (rk[q] + 1 == keep_w) last = i0 + q;
+        const uint32_t k = rn[q];
+        const double S = __dadd_rn(sel3(k, wbr[0], wbr[1], wbr[2]), __dsub_rn(pre[q], sel3(k, rb[0], rb[1], rb[2])));
+        if ((S + err) * (1.0 + gj) > ulo) jp = min(jp, rk[q]);
+        if ((S - err) * (1.0 - gj) > uhi) jc = min(jc, rk[q]);
+      }
+      jp = wave_min_u32(jp);
+      jc = wave_min_u32(jc);
+      last = wave_min_u32(last);
+      uint32_t pick_rank = kNone;
+      if (jp == kNone) {
+        if (last == kNone) ok = false;
+        else pick_rank = keep_w - 1;
+      } else if (jp == jc) {
+        pick_rank = jc;
+      } else {
+        ok = false;
+      }
+      uint32_t home = kNone;
+      const uint32_t pi = ok ? index_of(pick_rank, &home) : kNone;
+      if (pi == kNone) ok = false;
+      if (tid == 0) {
+        if (ok) {
+          a.tokens[row] = packed_id(sh.sk[pi]);
+          a.status[row] = AS_ROW_OK | AS_ROW_DEEP_PATH;
+          if (a.kept_count) a.kept_count[row] = keep_w;
+        }
+        sh.pick = ok ? 1u : 0u;
+      }
+    }
+    __syncthreads();
+    return sh.pick != 0;
+  }
+
   // The cut (sample.rs:230-252): at the first rank below the floor, or one past the first whose
   // cumulative reaches top_p, whichever comes first.
   // The run that holds rank r (kNone: not collected).
