@@ -264,6 +264,10 @@ int run_rows(as_ctx* c, const Plan& pl, RowParams* rows, const float* logits, ui
   bool own_states = true;
   for (uint32_t r = 0; r < n_rows && own_states; ++r) own_states = rows[r].rng_index == r;
   a.rng_rows = own_states ? 1u : 0u;
+  // Every row greedy and no history: each row's last slice finishes it, and no finish kernel runs.
+  bool all_greedy = !hist_ids && !extra_ids;
+  for (uint32_t r = 0; r < n_rows && all_greedy; ++r) all_greedy = rows[r].mode == as_dev::kModeGreedy;
+  a.scan_finishes = all_greedy ? 1u : 0u;
   // Small batches share the deep passes with idle workgroups: any row without a top-k, or with one
   // too large for the slices' candidates, may take them (rows with kept lists take the full deep
   // path, which is not shared).
@@ -318,8 +322,12 @@ int run_rows(as_ctx* c, const Plan& pl, RowParams* rows, const float* logits, ui
   // The scan is queued: from here the call's numbers are the context's.
   c->calls = call;
   c->deep_rows_done = deep_target;
-  c->share_dirty = true;
+  if (!a.scan_finishes) c->share_dirty = true;
   if (e1) AS_HIP(c, hipEventRecord(e1, c->stream));
+  if (a.scan_finishes) {
+    if (e2) AS_HIP(c, hipEventRecord(e2, c->stream));
+    return AS_OK;
+  }
   // Only rows without a top-k that have min-p's floor can be flagged for S's sums: with any, the
   // finish kernel runs enough workgroups to take their parts at once.
   uint32_t floor_rows = 0;

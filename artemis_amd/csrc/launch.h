@@ -89,7 +89,9 @@ struct FinishArgs {
   uint64_t* deep_done;      // rows finished, over every call of the context
   uint64_t deep_target;     // deep_done once this call's rows are finished
   uint32_t rng_rows;        // row r draws from RNG state r (as_sample): its state loads without its parameters
-  uint32_t pad2_[3];
+  uint32_t scan_finishes;   // every row greedy and no history: each row's last slice finishes it, and
+                            // no finish kernel runs
+  uint32_t pad2_[2];
 };
 static_assert(sizeof(FinishArgs) <= kArgsSlot && kArgsSlot % 16 == 0, "FinishArgs slot");
 

@@ -76,7 +76,8 @@ struct RowParams {
 static_assert(sizeof(RowParams) == 80 && sizeof(RowParams) % 16 == 0, "whole 16-byte words, no implicit padding");
 
 // A row's words that its slices share during a scan, in device memory; zero before the scan (the
-// context clears them once, and the finish kernel clears its row's after each scan).
+// context clears them once, and the finish kernel clears its row's after each scan; in a call the
+// scan finishes, the rows' slices touch only `arrived`, which the row's last slice clears).
 constexpr uint32_t kShareSlots = 16;
 struct RowShare {
   uint32_t bound;  // the largest wave threshold's key any slice of the row has published
@@ -85,7 +86,7 @@ struct RowShare {
   // q = ceil(k / slots); once every slot is set, their minimum has at least k values at or above it.
   uint32_t slot[kShareSlots];
   uint32_t gave_up;  // min-p rows: a slice's bound lay above its floor (not every value above it kept)
-  uint32_t pad_;
+  uint32_t arrived;  // calls the scan finishes: the row's slices that have ended (the last one clears it)
 };
 
 // A min-p row whose candidates do not hold its whole floor set: the weights of S, the row's values

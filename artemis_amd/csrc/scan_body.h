@@ -697,7 +697,8 @@ __device__ __forceinline__ void stream(Lane& ln, WaveState& ws, const Slice& sl,
 // One slice (seg) of one row: the body of the scan kernel. tail_list may be null (the rows whose
 // slices give up keeping min-p's floor set are then not listed).
 template <bool kVec>
-__device__ __forceinline__ void scan_slice(
+// Returns the slice's statistics (in thread 0; as stored).
+__device__ __forceinline__ SegStats scan_slice(
     const float* __restrict__ logits, const float* __restrict__ zero, uint64_t row_stride, uint32_t n,
     uint32_t n_seg, uint32_t slice_len, const RowParams* __restrict__ params, RowShare* share,
     const uint32_t* __restrict__ hist_off, const uint32_t* __restrict__ hist_ids,
@@ -1102,6 +1103,7 @@ __device__ __forceinline__ void scan_slice(
     }
   }
   if (tid == 0) stats[(uint64_t)row * n_seg + seg] = st;
+  return st;
 }
 
 }  // namespace AS_SCAN_NS

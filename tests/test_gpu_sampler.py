@@ -194,6 +194,32 @@ def test_nonfinite_rows_report_their_first_index_and_keep_the_stream(ctx):
     assert g["status"][5] == 0
 
 
+@pytest.mark.parametrize("n_rows", [1, 7, 300])
+def test_greedy_calls_the_scan_finishes(ctx, n_rows):
+    # A call whose rows are all greedy with no history runs no finish kernel: each row's last slice
+    # merges its slices (sample.rs:9-17, 22-34). Ties, non-finite plants, kept lists, and calls of the
+    # other kind in between (their slices' shared words and the flagged-row lists must stay clean).
+    N = VOCAB
+    gen = np.random.default_rng(50 + n_rows)
+    rows = (np.round(gen.standard_normal((n_rows, N)) * 4) / 4).astype(np.float32)
+    for r in range(n_rows):
+        if r % 5 == 1:
+            rows[r, gen.integers(N)] = np.nan
+        if r % 5 == 2:
+            rows[r, [N - 1, 3]] = [np.inf, -np.inf]
+        if r % 5 == 3:
+            rows[r, :] = -1.0  # all tied: the lowest index
+    greedy = [dict(temp=0.0, top_k=0, top_p=1.0, min_p=0.0)] * n_rows
+    mixed = [dict(temp=0.8, top_k=0, top_p=1.0, min_p=0.01)] * n_rows
+    want = oracle_rows(rows, greedy, list(range(n_rows)), kept_cap=4)
+    want_m = oracle_rows(rows, mixed, list(range(n_rows)))
+    for rep in range(3):
+        g = gpu_batch(ctx, rows, greedy, list(range(n_rows)), kept_cap=4 if rep == 1 else 0)
+        check_rows(g, want, greedy, kept_cap=4 if rep == 1 else 0, label=f"greedy {n_rows} rows, call {rep}")
+        g = gpu_batch(ctx, rows, mixed, list(range(n_rows)))
+        check_rows(g, want_m, mixed, label=f"min-p {n_rows} rows after greedy, call {rep}")
+
+
 def test_config1_greedy(ctx):
     from artemis_amd import workloads
     w = workloads.config1()
