@@ -92,15 +92,17 @@ uint32_t wanted_cand(const as_sampling& s, uint32_t n) {
 }
 
 // How a call splits its rows: n_seg slices of slice_len values, and `stride` candidate slots per
-// slice. Enough slices to give the GPU about kTargetGroups workgroups, no more than the finish
-// kernel's candidate room allows for the largest per-wave count, and slices of at most kSliceMax.
+// slice. Enough slices to give the GPU about kTargetGroups workgroups (a small batch's slices hold
+// at least two chunks of 1,024 values: at batch 1, 2,048-value slices gave the call 1 us less than
+// 4,096-value ones, and 16,384-value ones 2 us more), no more than the finish kernel's candidate
+// room allows for the largest per-wave count, and slices of at most kSliceMax.
 struct Plan {
   uint32_t n_seg, slice_len, stride, limit;
 };
 Plan plan_slices(uint32_t n, uint32_t n_rows, uint32_t c_max) {
   const uint32_t s_min = (n + as_launch::kSliceMax - 1) / as_launch::kSliceMax;
   uint32_t s = (as_launch::kTargetGroups + n_rows - 1) / n_rows;
-  s = std::min(s, std::max(1u, n / (4 * as_launch::kSliceAlign)));
+  s = std::min(s, std::max(1u, n / (2 * as_launch::kSliceAlign)));
   if (c_max > 0) s = std::min(s, as_launch::kCandCap / (4 * c_max + as_launch::kHistReserve));
   s = std::min(s, as_launch::kMaxSlices);
   s = std::max(s, std::max(s_min, 1u));

@@ -81,9 +81,10 @@ def test_histories_past_the_slice_hash_take_the_exact_path(ctx, rows):
     n = 248_320
     rng = np.random.default_rng(20 + rows)
     logits = (rng.standard_normal((rows, n)) * 2.5).astype(np.float32)
-    # 20,000 history ids over the first 30,000 ids (about 14,000 distinct, each seen one to a few
-    # times): every slice that covers that range holds far more than 512 distinct ids.
-    hists = [rng.integers(0, 30_000, size=20_000).astype(np.uint32) for _ in range(rows)]
+    # 20,000 history ids over the first 12,000 ids (about 9,700 distinct, each seen one to a few
+    # times): every slice that covers that range holds more distinct ids than its 2,048-slot hash
+    # (these rows' slices hold at least 4,096 values).
+    hists = [rng.integers(0, 12_000, size=20_000).astype(np.uint32) for _ in range(rows)]
     for r, h in enumerate(hists):
         logits[r, int(h[0])] += 6.0  # a history id among the best
     kinds = [dict(temp=0.7, top_k=40, top_p=0.9, min_p=0.05, presence=0.5, frequency=0.3, repetition=1.05),
