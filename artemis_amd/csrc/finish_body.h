@@ -998,6 +998,14 @@ __device__ __forceinline__ T sel3(uint32_t k, T v0, T v1, T v2) {
   return k == 0 ? v0 : (k == 1 ? v1 : v2);
 }
 
+// The deep passes' lower cut: min-p's floor (as an f32: v >= it exactly when v is at or above the
+// reference's f64 floor) when it is the row's only cut, else -inf. Below it nothing is kept and no
+// total the row's decisions use counts a value.
+__device__ __forceinline__ float deep_cut(const RowParams& p, float topf) {
+  const bool only_floor = p.mode == kModePartial && p.min_p > 0.0f && !(p.top_p < 1.0f);
+  return only_floor ? floor_f32(__dadd_rn((double)topf, p.ln_min_p)) : -__builtin_inff();
+}
+
 // --- the deep passes shared with idle workgroups ----------------------------------------------
 //
 // In a small batch most of the finish kernel's workgroups have no row, or are done with theirs, while
@@ -1092,11 +1100,14 @@ __device__ __noinline__ void deep_part(const FinishArgs& a, uint32_t row, uint32
   const float topf = key_value(mk);
   const double top = (double)topf, temp = (double)p.temp;
   const float bsc = (float)kNB / (32.0f * fmaxf(1.0f, p.temp));
+  const float cut = deep_cut(p, topf);
   auto bin_of = [&](float val) -> uint32_t {
     const float t = (topf - val) * bsc;
     return t < (float)(kNB - 1) ? (uint32_t)t : kNB - 1;
   };
-  auto own = [&](uint32_t k) { return at(k) < len && !(pen && ((bm[at(k) >> 5] >> (at(k) & 31u)) & 1u)); };
+  auto own = [&](uint32_t k) {
+    return at(k) < len && !(pen && ((bm[at(k) >> 5] >> (at(k) & 31u)) & 1u)) && v[k] >= cut;
+  };
   uint32_t* sh_g = deep_shared(a, row);
   if (pass == 0) {
     const bool by_top_p = p.top_p < 1.0f;
@@ -1258,15 +1269,15 @@ __device__ __forceinline__ uint32_t deep_bin(float topf, float bsc, uint32_t nb,
   return t < (float)(nb - 1) ? (uint32_t)t : nb - 1;
 }
 
-// Pass 1: each value's count and weights into the LDS histogram (hc counts, hm the weights at T = 1
-// when by_top_p, hw the weights at T).
+// Pass 1: each value at or above cut, its count and weights into the LDS histogram (hc counts, hm the
+// weights at T = 1 when by_top_p, hw the weights at T).
 __device__ __forceinline__ void deep_hist(const float* x, const uint32_t* pcnt, uint32_t n, bool vec, uint32_t nb,
-                                       float topf, float bsc, double top, double temp, bool by_top_p, uint32_t* hc,
-                                       double* hm, double* hw) {
+                                       float topf, float bsc, double top, double temp, bool by_top_p, float cut,
+                                       uint32_t* hc, double* hm, double* hw) {
   PassWeights pw;
   pw.init(top, temp);
   for_each_value<true, 3>(x, pcnt, n, vec, [&](uint32_t, float v, uint32_t c) {
-    if (__builtin_expect(c == 0, 1)) {
+    if (__builtin_expect(c == 0, 1) && v >= cut) {
       const uint32_t b = deep_bin(topf, bsc, nb, v);
       const double d = pw.d(v);
       atomicAdd(&hc[b], 1u);
@@ -1276,8 +1287,9 @@ __device__ __forceinline__ void deep_hist(const float* x, const uint32_t* pcnt, 
   });
 }
 
-// Pass 2: the values of the bins in the runs [a0, e0], [a1, e1], [a2, e2] (kNone: no run) into sk,
-// packed, in any order; *pick counts them (past cap they are counted, not kept). kb: 6 words of LDS.
+// Pass 2: the values of the bins in the runs [a0, e0], [a1, e1], [a2, e2] (kNone: no run) whose key is
+// at least kcut into sk, packed, in any order; *pick counts them (past cap they are counted, not
+// kept). kb: 6 words of LDS.
 // The bin is a non-increasing function of the value, so the values whose bin lies in a run [a, e]
 // are those whose key lies in an interval [lo, hi]. Lanes 0-5 find the six bounds by bisection over
 // the keys at or below the largest value's (no value of the row lies above it; the keys below the
@@ -1286,7 +1298,7 @@ __device__ __forceinline__ void deep_hist(const float* x, const uint32_t* pcnt, 
 __device__ __forceinline__ void deep_collect(const float* x, const uint32_t* pcnt, uint32_t n, bool vec, uint32_t nb,
                                           float topf, float bsc, uint32_t a0, uint32_t e0, uint32_t a1, uint32_t e1,
                                           uint32_t a2, uint32_t e2, uint32_t* pick, uint64_t* sk, uint32_t cap,
-                                          uint32_t* kb) {
+                                          uint32_t* kb, uint32_t kcut) {
   static_assert(kBinRanges == 3, "three runs");
   const uint32_t tid = threadIdx.x;
   if (tid < 2 * kBinRanges) {
@@ -1303,7 +1315,7 @@ __device__ __forceinline__ void deep_collect(const float* x, const uint32_t* pcn
         if (bin(mid) <= e) hi = mid;
         else lo = mid + 1;
       }
-      out = lo;
+      out = max(lo, kcut);
     } else {
       // hi: the greatest key at or below ktop whose bin is at least a (key 0's, the last bin, is).
       uint32_t lo = 0, hi = ktop;
@@ -1351,6 +1363,9 @@ __device__ __noinline__ bool deep_bins(const FinishArgs& a, const RowParams& p, 
   const uint32_t kk = topk ? p.top_k : n;
   const bool unfiltered = !by_top_p && !has_floor && !topk;
   const float floorf = floor_f32(__dadd_rn(top, p.ln_min_p));
+  // With min-p's floor the only cut (no top-p, no top-k), values below the floor are never kept and
+  // no total counts them: both passes leave them out.
+  const float cut = deep_cut(p, topf);
   // Bins of distance below the largest value, kNB over span, everything further down in the
   // last: below span a weight is under e^-32 of the largest's (span is 32 T above T = 1).
   const float span = 32.0f * fmaxf(1.0f, p.temp);
@@ -1402,7 +1417,7 @@ __device__ __noinline__ bool deep_bins(const FinishArgs& a, const RowParams& p, 
     }
     __syncthreads();  // the bins are whole before the history's values add to them
   } else {
-    deep_hist(x, pcnt, n, vec, kNB, topf, bsc, top, temp, by_top_p, hc, hm, hw);
+    deep_hist(x, pcnt, n, vec, kNB, topf, bsc, top, temp, by_top_p, cut, hc, hm, hw);
   }
   if (pen) {
     // Each history id once, penalised, by the thread that sets its count's top bit first (pass 2
@@ -1410,7 +1425,10 @@ __device__ __noinline__ bool deep_bins(const FinishArgs& a, const RowParams& p, 
     auto hist_one = [&](uint32_t id) {
       if (id >= n) return;
       const uint32_t old = atomicOr(&cnt[id], 0x80000000u);
-      if (!(old & 0x80000000u)) count(penalize(x[id], old, p));
+      if (!(old & 0x80000000u)) {
+        const float v = penalize(x[id], old, p);
+        if (v >= cut) count(v);
+      }
     };
     for (uint32_t h = hb + tid; h < he; h += kThreads) hist_one(gload(a.hist_ids + h));
     for (uint32_t h = tid; h < extra; h += kThreads) hist_one(gload(a.extra_ids + h));
@@ -1652,7 +1670,7 @@ __device__ __noinline__ bool deep_bins(const FinishArgs& a, const RowParams& p, 
     __syncthreads();
   } else if (fits) {
     deep_collect(x, pcnt, n, vec, kNB, topf, bsc, r0[0], r1[0], r0[1], r1[1], r0[2], r1[2], &sh.pick, sh.sk,
-                 (uint32_t)kCap, sh.base);
+                 (uint32_t)kCap, sh.base, cut > -__builtin_inff() ? total_key(cut) : 0u);
   }
   if (pen) {
     auto hist_two = [&](uint32_t id) {
@@ -1660,7 +1678,7 @@ __device__ __noinline__ bool deep_bins(const FinishArgs& a, const RowParams& p, 
       const uint32_t old = atomicAnd(&cnt[id], 0x7fffffffu);
       if (!(old & 0x80000000u) || !fits) return;
       const float v = penalize(x[id], old & 0x7fffffffu, p);
-      if (in_runs(bin_of(v))) {
+      if (v >= cut && in_runs(bin_of(v))) {
         const uint32_t s = atomicAdd(&sh.pick, 1u);
         if (s < (uint32_t)kCap) sh.sk[s] = pack(total_key(v), id);
       }

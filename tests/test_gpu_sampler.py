@@ -400,6 +400,25 @@ def test_large_top_k_rows_match_the_oracle(ctx, n_rows):
     assert all(st[r] & AS_ROW_DEEP_PATH for r in range(n_rows) if params[r]["top_p"] != 0.99999), st
 
 
+def test_min_p_only_rows_past_their_candidates_match_the_oracle(ctx):
+    # min-p 0.002 with no top-p and no top-k on config 5's logits (floor sets of thousands of values):
+    # some draws land past every candidate, and those rows take the deep passes, which then leave
+    # out every value below the floor (sample.rs:181, 237: nothing below it is kept or counted). 64
+    # rows take the passes alone, 12 share them with idle workgroups.
+    from artemis_amd import AS_ROW_DEEP_PATH, workloads
+    w = workloads.config5()
+    deep = 0
+    for n_rows, base in [(64, 0), (64, 64), (12, 128)]:
+        params = [dict(temp=0.7, top_k=0, top_p=1.0, min_p=0.002)] * n_rows
+        rows = np.ascontiguousarray(w.logits[base:base + n_rows])
+        seeds = [900 + base + r for r in range(n_rows)]
+        g = gpu_batch(ctx, rows, params, seeds)
+        want = oracle_rows(rows, params, seeds)
+        check_rows(g, want, params, label=f"min-p only, rows {base}:{base + n_rows}")
+        deep += int(((g["status"] & AS_ROW_DEEP_PATH) != 0).sum())
+    assert deep > 0, "no row took the deep passes: the case is not covered"
+
+
 def test_large_floor_sets_match_the_oracle(ctx):
     # min-p rows whose floor set holds thousands of values (config 5's rows 254 and 151: 4,302 and
     # 3,365 values above the floor, top-p far deeper): the scan keeps a few thousand candidates and
