@@ -218,6 +218,12 @@ def test_greedy_calls_the_scan_finishes(ctx, n_rows):
         check_rows(g, want, greedy, kept_cap=4 if rep == 1 else 0, label=f"greedy {n_rows} rows, call {rep}")
         g = gpu_batch(ctx, rows, mixed, list(range(n_rows)))
         check_rows(g, want_m, mixed, label=f"min-p {n_rows} rows after greedy, call {rep}")
+    # Rows of one slice (the only slice is the last) and of a few.
+    for n in (1, 7, 3000, 9000):
+        small = np.ascontiguousarray(rows[:, :n])
+        small[0, n // 2] = small[0].max()  # a tie with an earlier maximum, or the maximum itself
+        g = gpu_batch(ctx, small, greedy, list(range(n_rows)))
+        check_rows(g, oracle_rows(small, greedy, list(range(n_rows))), greedy, label=f"greedy {n_rows} rows of {n}")
 
 
 def test_config1_greedy(ctx):
