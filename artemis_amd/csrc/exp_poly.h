@@ -24,6 +24,24 @@ static __constant__ double kExp2Poly[kPolyLen] = {
     0.009618129159402558,   0.05550410941205933,    0.2402265069581299,     0.6931471805459335,
     1.0};
 
+// k (an integral double) to an int by v_cvt_i32_f64, which clamps values past the int range to it (a
+// C++ conversion of such a double is undefined). With it a far negative argument needs no clamp of its
+// own: its k converts to INT_MIN and ldexp(p, INT_MIN) is 0.
+__device__ __forceinline__ int32_t cvt_i32_sat(double k) {
+  int32_t r;
+  __asm__("v_cvt_i32_f64 %0, %1" : "=v"(r) : "v"(k));
+  return r;
+}
+
+// The fused argument below: t = x log2(e) + c in one rounding, with c = -m log2(e) rounded, for
+// |m| <= kFusedMax. Its distance to (x - m) log2(e) is at most (|x| + 2.45 |m| + |t|) 2^-53 (the
+// rounding of log2(e), of c and of the sum); where the term is above 2^-1100, |t| <= 1100 and
+// |x| <= |m| + 763, so at most 3.05e-13, which moves 2^t by at most 2.2e-13 relative (times ln 2).
+constexpr double kFusedMax = 256.0;
+constexpr double kFusedArgRel = 2.2e-13;
+static_assert(1.07e-12 + kFusedArgRel + 1e-15 <= kExpPolyRel, "the fused argument's terms within kExpPolyRel");
+constexpr double kLog2e = 1.4426950408889634;
+
 struct ExpPoly {
   double c[kPolyLen];
   __device__ __forceinline__ void load() {
@@ -38,6 +56,26 @@ struct ExpPoly {
 #pragma unroll
     for (int i = 1; i < kPolyLen; ++i) p = __builtin_fma(p, f, c[i]);
     return __builtin_amdgcn_ldexp(p, (int32_t)k);
+  }
+  __device__ __forceinline__ double horner(double f) const {
+    double p = c[0];
+#pragma unroll
+    for (int i = 1; i < kPolyLen; ++i) p = __builtin_fma(p, f, c[i]);
+    return p;
+  }
+  // exp(x - m) for x <= m, both finite, |m| <= kFusedMax, given c = fused_offset(m): within
+  // kExpPolyRel relative where the result is above 2^-1021, and 0 or a subnormal below.
+  static __device__ __forceinline__ double fused_offset(double m) { return -m * kLog2e; }
+  __device__ __forceinline__ double exp_fused(double x, double cm) const {
+    const double t = __builtin_fma(x, kLog2e, cm);
+    const double k = __builtin_rint(t);
+    return __builtin_amdgcn_ldexp(horner(t - k), cvt_i32_sat(k));
+  }
+  // exp(d) for finite d <= 0, as exp_le0, with the clamp left to cvt_i32_sat.
+  __device__ __forceinline__ double exp_sat(double d) const {
+    const double t = d * kLog2e;
+    const double k = __builtin_rint(t);
+    return __builtin_amdgcn_ldexp(horner(t - k), cvt_i32_sat(k));
   }
   // exp(d) for finite d <= 0 without exp_neg's clamp at -708: below it the result is 2^f 2^k rounded
   // to a subnormal or 0, under 2^-1021 like exp(d) itself. t is bounded at -1100 first, so that k

@@ -7,7 +7,7 @@
 //   - lp_part_kernel: one 256-thread workgroup per part of a row (kLpPart values, or kLpPartSmall
 //     for a call whose grid of those fills at most one round of the chip: lp_part_len). Its largest value m_p,
 //     S_p = sum of exp(x - m_p) in f64 (each term within kExpRel of the reference's exp, from a
-//     table-free polynomial: exp_le0), and its 20 best by the reference's order: each wave's 5th
+//     table-free polynomial: exp_fused), and its 20 best by the reference's order: each wave's 5th
 //     largest lane maximum (by value), the smallest of the four, is a threshold with at least 20
 //     values of the part at or above it; the few values there go into LDS (each wave's into a
 //     segment of its own, at places a ballot per value gives), where a rank count of their (value,
@@ -64,7 +64,7 @@ __device__ __forceinline__ uint32_t wave_qth_u32(uint32_t x, uint32_t m0, uint32
 
 __device__ __forceinline__ double gamma_n(double n) { return n * kU / (1.0 - n * kU); }
 
-// Each term's relative error against the reference's exp (ExpPoly::exp_le0, exp_poly.h).
+// Each term's relative error against the reference's exp (ExpPoly::exp_fused and exp_sat, exp_poly.h).
 constexpr double kExpRel = kExpPolyRel;
 
 // The value part of lp_key.
@@ -129,13 +129,28 @@ __device__ __forceinline__ void lp_part(PartShared& sh, const float* __restrict_
 
   // S_p, each term within kExpRel of the reference's exp(f64(x) - m). Each half of the thread's
   // values has its own running sum (at most 32 roundings deep, as the bound on the row's sum counts).
+  // A part whose maximum is at most kFusedMax in size takes each term's argument in one fused
+  // multiply-add (exp_fused); others subtract m first (exp_sat). Both are within kExpPolyRel.
   ExpPoly ep;
   ep.load();
   double s = 0.0, s2 = 0.0;
+  if (fabs(md) <= kFusedMax) {
+    const double cm = ExpPoly::fused_offset(md);
 #pragma unroll
-  for (uint32_t q = 0; q < kPer / 2; ++q) {
-    if (valid(q)) s += ep.exp_le0((double)v[q] - md);
-    if (valid(q + kPer / 2)) s2 += ep.exp_le0((double)v[q + kPer / 2] - md);
+    for (uint32_t q = 0; q < kPer / 2; ++q) {
+      if (valid(q)) s += ep.exp_fused((double)v[q], cm);
+      if (valid(q + kPer / 2)) s2 += ep.exp_fused((double)v[q + kPer / 2], cm);
+    }
+  } else {
+    // (Each value passes through an empty asm here, so that the compiler does not convert every value
+    // to f64 ahead of the branch, for both loops at once, and hold them all in registers.)
+#pragma unroll
+    for (uint32_t q = 0; q < kPer / 2; ++q) {
+      float a0 = v[q], a1 = v[q + kPer / 2];
+      __asm__("" : "+v"(a0), "+v"(a1));
+      if (valid(q)) s += ep.exp_sat((double)a0 - md);
+      if (valid(q + kPer / 2)) s2 += ep.exp_sat((double)a1 - md);
+    }
   }
   s += s2;
 

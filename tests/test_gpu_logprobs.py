@@ -204,6 +204,22 @@ def test_wide_ranges_within_a_wave(ctx):
         check(ctx, rows, [1, 8, 5000, n - 1], 20, f"wide n={n}")
 
 
+def test_parts_on_both_sides_of_the_fused_argument(ctx):
+    # A part whose maximum m has |m| <= 256 takes each term's argument as one fused multiply-add
+    # (exp_poly.h, exp_fused); a larger |m| subtracts first (exp_sat). Rows whose parts sit at and just
+    # past that edge, on both signs, with values spread over exp's whole range below m.
+    gen = np.random.default_rng(43)
+    n = 40000
+    for m in [256.0, -256.0, 256.03125, -256.03125, 300.0, -300.0, 255.5]:
+        rows = np.empty((3, n), np.float32)
+        rows[0] = m - np.abs(gen.standard_normal(n)) * 3.0
+        rows[1] = m - gen.random(n).astype(np.float32) * 800.0
+        rows[2] = m - np.abs(gen.standard_normal(n)) * 0.01
+        for r in range(3):
+            rows[r, gen.integers(0, n)] = m
+        check(ctx, rows, [0, 17, n - 1], 20, f"m={m}")
+
+
 def test_strided_and_shared_rows(ctx):
     # A padded row stride, and stride 0 (every row reads the same row).
     gen = np.random.default_rng(3)

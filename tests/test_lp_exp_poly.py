@@ -8,6 +8,7 @@ shows up as an error many times larger."""
 import os
 import re
 
+import numpy as np
 import pytest
 
 mp = pytest.importorskip("mpmath")
@@ -36,3 +37,44 @@ def test_the_polynomial_of_2_to_the_f_is_within_its_documented_error():
     # The kernel's kExpRel adds the rounding of t = d log2(e) and of the Horner steps.
     kexprel = float(re.search(r"constexpr double kExpPolyRel = ([0-9.e-]+);", open(SRC).read()).group(1))
     assert worst + 1.6e-13 + 1e-15 <= kexprel
+
+
+def test_the_fused_argument_stays_within_its_documented_error():
+    # exp_fused takes t = fma(x, L, c) with L = f64(log2 e) and c = f64(-m L), one rounding, for parts
+    # whose maximum has |m| <= kFusedMax. Its distance to (x - m) log2 e, moved through 2^t, is the
+    # source's kFusedArgRel at most where the term is above 2^-1100 (|t| <= 1100, x >= m - 763). This
+    # computes the fused rounding exactly (Fraction, then one correctly rounded conversion) at the
+    # corners of that domain and at random points, and checks the polynomial error plus it against
+    # kExpPolyRel.
+    from fractions import Fraction
+    import random
+
+    text = open(SRC).read()
+    fmax = float(re.search(r"constexpr double kFusedMax = ([0-9.e-]+);", text).group(1))
+    arg_rel = float(re.search(r"constexpr double kFusedArgRel = ([0-9.e-]+);", text).group(1))
+    kexprel = float(re.search(r"constexpr double kExpPolyRel = ([0-9.e-]+);", text).group(1))
+    L = float(re.search(r"constexpr double kLog2e = ([0-9.e-]+);", text).group(1))
+    mp.mp.dps = 50
+    log2e = 1 / mp.log(2)
+    rng = random.Random(7)
+    cases = []
+    for m in [fmax, -fmax, fmax / 3, 0.0, -1.0]:
+        for d in [0.0, -1e-3, -1.0, -700.0, -762.0, -763.0]:
+            cases.append((m, d))
+    for _ in range(3000):
+        cases.append((rng.uniform(-fmax, fmax), -rng.uniform(0, 763)))
+    worst = 0.0
+    for m, d in cases:
+        m = float(np.float32(m))
+        x = float(np.float32(m + d))
+        if x > m:
+            continue
+        c = float(Fraction(-m) * Fraction(L))
+        t = float(Fraction(x) * Fraction(L) + Fraction(c))
+        exact = (mp.mpf(x) - mp.mpf(m)) * log2e
+        if exact < -1100:
+            continue
+        rel = abs(mp.mpf(t) - exact) * mp.log(2)
+        worst = max(worst, float(rel))
+    assert worst <= arg_rel, worst
+    assert 1.07e-12 + arg_rel + 1e-15 <= kexprel
