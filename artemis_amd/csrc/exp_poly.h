@@ -1,8 +1,9 @@
 // exp(d) for d <= 0 to within kExpPolyRel relative, without a table: for sums whose error is bounded
 // anyway (a table's gathers from LDS conflict across lanes, and the host-exact exp of exp_f64.h costs
 // about twice the instructions). e^d = 2^t, t = d log2(e) = k + f with k = rint(t) and |f| <= 1/2
-// (f = t - k exactly), 2^f by a polynomial of degree 8, 2^k by ldexp. Below d = -708 the argument is
-// clamped (the result, under 2^-1021, is then e^-708 rather than e^d).
+// (f = t - k exactly), 2^f by a polynomial of degree 8, 2^k by ldexp. exp_neg clamps the argument
+// below d = -708 (the result, under 2^-1021, is then e^-708 rather than e^d); exp_sat and exp_fused
+// need no clamp (cvt_i32_sat).
 //
 // The coefficients of 2^f, highest degree first: the Chebyshev interpolant of 2^f on [-1/2, 1/2] at
 // degree 8 (mpmath.chebyfit at 40 digits), rounded to f64; with the rounded coefficients its relative
@@ -71,24 +72,13 @@ struct ExpPoly {
     const double k = __builtin_rint(t);
     return __builtin_amdgcn_ldexp(horner(t - k), cvt_i32_sat(k));
   }
-  // exp(d) for finite d <= 0, as exp_le0, with the clamp left to cvt_i32_sat.
+  // exp(d) for finite d <= 0: within kExpPolyRel relative where the result is above 2^-1021, and 0 or
+  // a subnormal below (2^f 2^k rounded, under 2^-1021 like exp(d) itself); a far negative d needs no
+  // clamp (cvt_i32_sat).
   __device__ __forceinline__ double exp_sat(double d) const {
     const double t = d * kLog2e;
     const double k = __builtin_rint(t);
     return __builtin_amdgcn_ldexp(horner(t - k), cvt_i32_sat(k));
-  }
-  // exp(d) for finite d <= 0 without exp_neg's clamp at -708: below it the result is 2^f 2^k rounded
-  // to a subnormal or 0, under 2^-1021 like exp(d) itself. t is bounded at -1100 first, so that k
-  // converts to an int exactly (a double far outside the int range has no defined conversion); every
-  // d it moves lies below -762, where exp(d) and the result are both 0.
-  __device__ __forceinline__ double exp_le0(double d) const {
-    const double t = fmax(d * 1.4426950408889634, -1100.0);
-    const double k = __builtin_rint(t);
-    const double f = t - k;
-    double p = c[0];
-#pragma unroll
-    for (int i = 1; i < kPolyLen; ++i) p = __builtin_fma(p, f, c[i]);
-    return __builtin_amdgcn_ldexp(p, (int32_t)k);
   }
 };
 
