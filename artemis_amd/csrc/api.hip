@@ -54,9 +54,12 @@ struct as_ctx {
   std::vector<std::pair<double, uint32_t>> order_cost;  // its sort keys (kept: no allocation per call)
   std::vector<RowParams> rows;  // the call's parameter blocks as built on the host (max_rows, kept)
   std::string err;
-  // Profiling: events before the scan, between the kernels and after the finish, per call.
+  // Profiling: events before the scan, between the kernels and after the finish, per call, and
+  // whether the call ran a finish kernel (a call the scan finishes has nothing between its last two
+  // events but their own overhead, which counts as no finish time).
   bool profile = false;
   std::vector<hipEvent_t> ev;
+  std::vector<uint8_t> ev_fin;
   size_t ev_used = 0;
 };
 
@@ -328,6 +331,7 @@ int run_rows(as_ctx* c, const Plan& pl, RowParams* rows, const float* logits, ui
   c->deep_rows_done = deep_target;
   if (!a.scan_finishes) c->share_dirty = true;
   if (e1) AS_HIP(c, hipEventRecord(e1, c->stream));
+  if (e0) c->ev_fin[(c->ev_used - 3) / 3] = a.scan_finishes ? 0 : 1;
   if (a.scan_finishes) {
     if (e2) AS_HIP(c, hipEventRecord(e2, c->stream));
     return AS_OK;
@@ -433,6 +437,7 @@ int as_create(int device, void* hip_stream, uint32_t max_rows, uint32_t max_voca
   c->order_cost.reserve(std::min(max_rows, as_launch::kOrderMax));
   c->rows.resize(max_rows);
   c->dev_rows.resize(max_rows);
+  c->ev_fin.assign(4096, 1);
   c->scratch_stride = as_launch::scratch_words(max_vocab);
   hipError_t e = hipSetDevice(device);
   if (e == hipSuccess) e = hipMalloc(&c->d_block, kArgsSlot + sizeof(RowParams) * max_rows);
@@ -649,7 +654,7 @@ int as_profile_read(as_ctx* c, double* scan_ms, double* finish_ms, uint32_t* cal
   for (size_t i = 0; i + 2 < c->ev_used; i += 3) {
     float a = 0.0f, b = 0.0f;
     AS_HIP(c, hipEventElapsedTime(&a, c->ev[i], c->ev[i + 1]));
-    AS_HIP(c, hipEventElapsedTime(&b, c->ev[i + 1], c->ev[i + 2]));
+    if (c->ev_fin[i / 3]) AS_HIP(c, hipEventElapsedTime(&b, c->ev[i + 1], c->ev[i + 2]));
     s += a;
     f += b;
     ++k;
