@@ -221,7 +221,8 @@ int as_logprobs_static(void* hip_stream, const float* logits, uint64_t row_strid
 /* Profiling: while enabled, each as_sample / as_verify records HIP events on the context's stream
  * around its scan and finish kernels (no counterpart in the reference, which samples on the CPU;
  * for benchmarks). as_profile_read waits for the stream and returns the summed kernel times of the
- * calls since as_profile and how many calls there were, then starts a new count. */
+ * calls since as_profile and how many calls there were, then starts a new count; a call that runs no
+ * finish kernel (greedy rows without history) adds no finish time. */
 int as_profile(as_ctx* ctx, int enable);
 int as_profile_read(as_ctx* ctx, double* scan_ms, double* finish_ms, uint32_t* calls);
 
