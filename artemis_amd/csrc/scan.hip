@@ -1,6 +1,6 @@
-// Pass 1 over the logits, the only kernel that streams the rows from HBM: one 256-thread workgroup
-// per slice of a row (about a quarter of a 248,320-value row at batch 256, smaller slices for small
-// batches). Each wave walks its own 1,024-value chunks of the slice (chunks w, w+4, w+8, ...) with
+// Pass 1 over the logits, the kernel that streams the rows from HBM (greedy_kernel below takes calls
+// of greedy rows without history instead): one 256-thread workgroup per slice of a row (about a
+// third of a 248,320-value row at batch 256, smaller slices for small batches). Each wave walks its own 1,024-value chunks of the slice (chunks w, w+4, w+8, ...) with
 // the loads of the next chunk in flight while it works on the current one, and with no barrier until
 // the slice ends. Per value it does only what every value needs; what few values need is done when
 // they occur:
