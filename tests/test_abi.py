@@ -92,8 +92,9 @@ def _rust_block(text, start):
 
 
 def test_integration_binding_matches_the_header(L):
-    """INTEGRATION.md's Rust AsSampling has the header's fields in the header's order, its From impl
-    passes both new penalties through, and the check messages it quotes are as_check's."""
+    """The Rust AsSampling of the integration notes at the repository root has the header's fields in the
+    header's order, its From impl passes both new penalties through, and the check messages it quotes
+    are as_check's."""
     doc = open(os.path.join(ROOT, "INTEGRATION.md")).read()
     header = open(HEADER).read()
     c_struct = header[:header.index("} as_sampling;")]
